@@ -1,0 +1,324 @@
+// C-ABI entry points and the per-device workspace pool.
+//
+// Mirrors the reference's XLA FFI handlers and plain C exports
+// (src/cuda_zlib/native/codec_ffi.cu:132-273, 958-1182): ABI-shape errors are
+// returned, data errors go to the metadata buffer, scratch comes from one
+// stream-ordered hipMemPool per device, and no call synchronises with the host.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hip_zlib.h"
+#include "kernels.h"
+
+namespace hz {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct PoolEntry {
+  int device;
+  hipMemPool_t pool;
+};
+
+struct PoolRegistry {
+  std::mutex mutex;
+  std::vector<PoolEntry> pools;
+  u64 retention = 1ull << 30;
+};
+
+// Process-lifetime registry; deliberately leaked so no HIP call runs at exit.
+PoolRegistry& registry() {
+  static PoolRegistry* r = new PoolRegistry;
+  return *r;
+}
+
+hipError_t get_pool(int device, hipMemPool_t* out) {
+  PoolRegistry& reg = registry();
+  std::lock_guard<std::mutex> lock(reg.mutex);
+  for (const PoolEntry& e : reg.pools)
+    if (e.device == device) { *out = e.pool; return hipSuccess; }
+  hipMemPoolProps props = {};
+  props.allocType = hipMemAllocationTypePinned;
+  props.handleTypes = hipMemHandleTypeNone;
+  props.location.type = hipMemLocationTypeDevice;
+  props.location.id = device;
+  hipMemPool_t pool = nullptr;
+  hipError_t err = hipMemPoolCreate(&pool, &props);
+  if (err != hipSuccess) return err;
+  u64 threshold = reg.retention;
+  err = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
+  if (err != hipSuccess) return err;
+  reg.pools.push_back({device, pool});
+  *out = pool;
+  return hipSuccess;
+}
+
+bool find_pool(int device, hipMemPool_t* out) {
+  PoolRegistry& reg = registry();
+  std::lock_guard<std::mutex> lock(reg.mutex);
+  for (const PoolEntry& e : reg.pools)
+    if (e.device == device) { *out = e.pool; return true; }
+  return false;
+}
+
+// Makes the stream's device current for the duration of a call.
+class DeviceScope {
+ public:
+  hipError_t enter(hipStream_t stream) {
+    hipError_t err = hipGetDevice(&previous_);
+    if (err != hipSuccess) return err;
+    int device = previous_;
+    if (stream) {
+      err = hipStreamGetDevice(stream, &device);
+      if (err != hipSuccess) return err;
+    }
+    device_ = device;
+    if (device != previous_) {
+      err = hipSetDevice(device);
+      if (err != hipSuccess) return err;
+      switched_ = true;
+    }
+    return hipSuccess;
+  }
+  ~DeviceScope() {
+    if (switched_) hipSetDevice(previous_);
+  }
+  int device() const { return device_; }
+
+ private:
+  int previous_ = 0, device_ = 0;
+  bool switched_ = false;
+};
+
+// Stream-ordered scratch for one call; everything is freed (stream-ordered)
+// when the call ends, so results stay valid for later work on the stream.
+class Workspace final : public Scratch {
+ public:
+  Workspace(hipStream_t stream, hipMemPool_t pool) : stream_(stream), pool_(pool) {}
+  hipError_t alloc_bytes(void** p, u64 bytes) override {
+    *p = nullptr;
+    if (!bytes) bytes = 1;
+    bytes = (bytes + 255) & ~u64(255);
+    hipError_t err = hipMallocFromPoolAsync(p, bytes, pool_, stream_);
+    if (err != hipSuccess) return err;
+    allocations_.push_back(*p);
+    return hipSuccess;
+  }
+  hipError_t release() {
+    hipError_t first = hipSuccess;
+    for (void* p : allocations_) {
+      hipError_t err = hipFreeAsync(p, stream_);
+      if (first == hipSuccess) first = err;
+    }
+    allocations_.clear();
+    return first;
+  }
+  ~Workspace() override { release(); }
+
+ private:
+  hipStream_t stream_;
+  hipMemPool_t pool_;
+  std::vector<void*> allocations_;
+};
+
+int invalid(const char* message) {
+  g_last_error = message;
+  return HIP_ZLIB_INVALID_ARGUMENT;
+}
+
+template <typename Body>
+int execute(hipStream_t stream, Body&& body) {
+  try {
+    DeviceScope scope;
+    hipError_t err = scope.enter(stream);
+    if (err != hipSuccess) return int(err);
+    hipMemPool_t pool = nullptr;
+    err = get_pool(scope.device(), &pool);
+    if (err != hipSuccess) return int(err);
+    Workspace ws(stream, pool);
+    err = body(ws);
+    hipError_t rel = ws.release();
+    return int(err != hipSuccess ? err : rel);
+  } catch (...) {
+    g_last_error = "native HIP codec handler exception";
+    return HIP_ZLIB_INVALID_ARGUMENT;
+  }
+}
+
+u64 chunk_count(u64 size, u64 chunk) { return std::max<u64>(1, (size + chunk - 1) / chunk); }
+
+}  // namespace
+}  // namespace hz
+
+using namespace hz;
+
+extern "C" int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int64_t max_blocks,
+                                 const uint8_t* input, uint64_t input_size, uint8_t* output,
+                                 uint64_t output_size, uint32_t* metadata,
+                                 uint64_t metadata_count) {
+  if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
+  return execute(stream, [&](Workspace& ws) -> hipError_t {
+    if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, kInvalidBounds, 0);
+    auto fail = [&](u32 status) -> hipError_t {
+      hipError_t err = launch_fill(stream, output, 0, output_size);
+      if (err != hipSuccess) return err;
+      return launch_set_meta(stream, metadata, status, 0);
+    };
+    if (input_size > kMaxBytes || max_candidates < 1 || max_candidates > kMaxCandidates ||
+        max_blocks < 1 || max_blocks > kMaxBlocks)
+      return fail(kInvalidBounds);
+    if (input_size < 8) return fail(kTruncatedZlib);
+    const bool default_limits = max_candidates == kMaxCandidates && max_blocks == kMaxBlocks;
+    // Small streams decode serially in one wave (the reference's small route,
+    // codec_ffi.cu:681-693); everything else takes the parallel route.
+    if (default_limits && output_size <= 65536 && input_size <= 131072)
+      return launch_inflate_single(stream, input, input_size, output, output_size,
+                                   u32(max_blocks), metadata);
+    return run_inflate_general(stream, ws, input, input_size, output, output_size,
+                               u32(max_candidates), u32(max_blocks), metadata);
+  });
+}
+
+extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
+                               uint64_t input_size, uint8_t* output, uint64_t output_size,
+                               uint32_t* metadata, uint64_t metadata_count) {
+  if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
+  return execute(stream, [&](Workspace& ws) -> hipError_t {
+    if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, 0, kInvalidBounds);
+    hipError_t err = launch_fill(stream, output, 0, output_size);
+    if (err != hipSuccess) return err;
+    if (input_size > kMaxBytes || chunk_bytes < 256 || chunk_bytes > 65535)
+      return launch_set_meta(stream, metadata, 0, kInvalidBounds);
+    const u64 chunks = chunk_count(input_size, u64(chunk_bytes));
+    if (2 * chunks - 1 > kMaxBlocks || input_size + chunks * 5 + 6 > kMaxBytes ||
+        output_size != input_size + chunks * 5 + 6)
+      return launch_set_meta(stream, metadata, 0, kInvalidBounds);
+    return run_deflate(stream, ws, input, input_size, output, output_size, u32(chunk_bytes),
+                       metadata);
+  });
+}
+
+extern "C" int HipZlibCompressBatch(hipStream_t stream, int64_t chunk_bytes,
+                                    const int64_t* input_sizes, uint64_t files,
+                                    const uint8_t* input, uint64_t input_size, uint8_t* output,
+                                    uint64_t output_size, uint32_t* metadata,
+                                    uint64_t metadata_rows, uint64_t metadata_cols) {
+  if (!metadata || metadata_rows != files || metadata_cols != 2)
+    return invalid("batch codec metadata must have shape (files, 2)");
+  if (files && !input_sizes) return invalid("invalid argument: missing input sizes");
+  // Layout validation mirrors codec_ffi.cu:1002-1045.
+  std::vector<BatchFile> layout(files);
+  u64 in_total = 0, out_total = 0, total_chunks = 0;
+  bool bounds = chunk_bytes >= 256 && chunk_bytes <= 65535 && files <= kMaxBlocks;
+  for (u64 f = 0; f < files; ++f) {
+    if (input_sizes[f] < 0) return invalid("invalid argument: negative input size");
+    const u64 size = u64(input_sizes[f]);
+    const u64 chunks = bounds ? chunk_count(size, u64(chunk_bytes)) : 1;
+    const u64 capacity = size + 5 * chunks + 6;
+    layout[f] = {in_total, size, out_total, capacity};
+    in_total += size;
+    out_total += capacity;
+    total_chunks += chunks;
+    if (2 * chunks - 1 > kMaxBlocks) bounds = false;
+  }
+  if (in_total != input_size || out_total != output_size)
+    return invalid("invalid argument: batch layout differs from buffer sizes");
+  if (total_chunks > kMaxBlocks || in_total > kMaxBytes || out_total > kMaxBytes) bounds = false;
+  return execute(stream, [&](Workspace& ws) -> hipError_t {
+    hipError_t err = launch_fill(stream, output, 0, output_size);
+    if (err != hipSuccess) return err;
+    if (!bounds) return launch_set_meta_rows(stream, metadata, files, 0, kInvalidBounds);
+    return run_deflate_batch(stream, ws, input, input_size, layout.data(), u32(files), output,
+                             output_size, u32(chunk_bytes), metadata);
+  });
+}
+
+extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_sizes,
+                                      uint64_t input_count, const int64_t* output_sizes,
+                                      uint64_t output_count, const uint8_t* input,
+                                      uint64_t input_size, const uint32_t* encoded_metadata,
+                                      uint64_t encoded_rows, uint64_t encoded_cols,
+                                      uint8_t* output, uint64_t output_size, uint32_t* metadata,
+                                      uint64_t metadata_rows, uint64_t metadata_cols) {
+  if (!metadata || metadata_rows != input_count || metadata_cols != 2)
+    return invalid("batch codec metadata must have shape (files, 2)");
+  if (!input_count || input_count != output_count)
+    return invalid("input and output size lists must have matching nonempty lengths");
+  if (encoded_rows && (encoded_rows != input_count || encoded_cols != 2 || !encoded_metadata))
+    return invalid("encoded metadata must have shape (files, 2)");
+  if (!input_sizes || !output_sizes) return invalid("invalid argument: missing size lists");
+  std::vector<BatchFile> layout(input_count);
+  u64 in_total = 0, out_total = 0;
+  for (u64 f = 0; f < input_count; ++f) {
+    if (input_sizes[f] < 0 || output_sizes[f] < 0)
+      return invalid("invalid argument: negative size");
+    layout[f] = {in_total, u64(input_sizes[f]), out_total, u64(output_sizes[f])};
+    in_total += u64(input_sizes[f]);
+    out_total += u64(output_sizes[f]);
+  }
+  if (in_total != input_size || out_total != output_size)
+    return invalid("invalid argument: batch layout differs from buffer sizes");
+  const u64 files = input_count;
+  return execute(stream, [&](Workspace& ws) -> hipError_t {
+    hipError_t err = launch_fill(stream, output, 0, output_size);
+    if (err != hipSuccess) return err;
+    if (files > kMaxBlocks || in_total > kMaxBytes || out_total > kMaxBytes)
+      return launch_set_meta_rows(stream, metadata, files, kInvalidBounds, 0);
+    BatchFile* device_files = nullptr;
+    err = ws.alloc(&device_files, files);
+    if (err != hipSuccess) return err;
+    // Pageable source: the runtime stages it before returning, so the host
+    // vector may go out of scope immediately afterwards.
+    err = hipMemcpyAsync(device_files, layout.data(), files * sizeof(BatchFile),
+                         hipMemcpyHostToDevice, stream);
+    if (err != hipSuccess) return err;
+    return launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
+                                metadata, encoded_rows ? encoded_metadata : nullptr);
+  });
+}
+
+extern "C" int HipZlibSetWorkspaceRetention(uint64_t bytes) {
+  PoolRegistry& reg = registry();
+  std::lock_guard<std::mutex> lock(reg.mutex);
+  if (!reg.pools.empty()) return invalid("workspace retention must be set before first use");
+  reg.retention = bytes;
+  return 0;
+}
+
+extern "C" int HipZlibWorkspacePoolStats(int device, uint64_t* stats) {
+  if (!stats) return invalid("invalid argument: null stats");
+  PoolRegistry& reg = registry();
+  u64 retention, reserved = 0, used = 0, count = 0;
+  {
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    retention = reg.retention;
+  }
+  hipMemPool_t pool;
+  if (find_pool(device, &pool)) {
+    count = 1;
+    hipError_t err = hipMemPoolGetAttribute(pool, hipMemPoolAttrReservedMemCurrent, &reserved);
+    if (err != hipSuccess) return int(err);
+    err = hipMemPoolGetAttribute(pool, hipMemPoolAttrUsedMemCurrent, &used);
+    if (err != hipSuccess) return int(err);
+  }
+  stats[0] = retention;
+  stats[1] = reserved;
+  stats[2] = used;
+  stats[3] = count;
+  return 0;
+}
+
+extern "C" int HipZlibTrimWorkspacePool(int device) {
+  hipMemPool_t pool;
+  if (!find_pool(device, &pool)) return 0;
+  return int(hipMemPoolTrimTo(pool, 0));
+}
+
+extern "C" const char* HipZlibErrorString(int code) {
+  if (code == HIP_ZLIB_INVALID_ARGUMENT) return g_last_error.c_str();
+  return hipGetErrorString(hipError_t(code));
+}

@@ -1,0 +1,329 @@
+// Shared device-side building blocks of the HIP zlib/DEFLATE codec (gfx950).
+//
+// Everything here is header-only and included by each kernel translation unit.
+// Status codes are the codec's metadata contract (src/cuda_zlib/_decode_kernels.py:36-50
+// and native/codec_ffi.cu:51-62 in the reference); bit/Huffman semantics follow
+// RFC 1951 plus the reference's exact error rules (_decode_kernels.py:69-296).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hz {
+
+typedef uint8_t u8;
+typedef uint16_t u16;
+typedef uint32_t u32;
+typedef uint64_t u64;
+typedef int32_t i32;
+
+// ---- status contract -------------------------------------------------------
+enum Status : u32 {
+  kOk = 0,
+  kTruncated = 1,          // bits ran out inside a header, symbol or payload
+  kReservedBlock = 2,      // BTYPE == 3
+  kBadTree = 3,            // over/under-subscribed code, HLIT > 286, EOB length 0
+  kBadSymbol = 4,          // LL 286/287, distance 30/31, invalid code, LEN/NLEN
+  kBadRepeat = 5,          // code-length repeat before a length or past the end
+  kBadDistance = 6,        // distance beyond history or the declared window
+  kOutputOverflow = 7,     // decoded output exceeds the declared size
+  kBlockCapacity = 9,      // more blocks than max_blocks
+  kUndiscovered = 10,      // dynamic block boundary not among the candidates
+  kSizeMismatch = 11,      // final decoded size differs from the declared size
+  kExtent = 12,            // block end/trailing-byte mismatch
+  kTruncatedZlib = 14,
+  kInvalidHeader = 15,
+  kUnsupportedGzip = 16,
+  kUnsupportedDictionary = 17,
+  kCandidateOverflow = 18,
+  kInitialBlockMissing = 19,
+  kReferenceDepth = 20,
+  kAdlerMismatch = 21,
+  kCompressionOverflow = 22,
+  kInvalidBounds = 23,
+};
+
+constexpr u64 kMaxBytes = 0xffffffffull;   // per-buffer bound (4 GiB - 1)
+constexpr u32 kMaxCandidates = 262144;
+constexpr u32 kMaxBlocks = 262144;
+constexpr u32 kAdlerMod = 65521;
+
+// ---- RFC 1951 length/distance alphabets (closed forms) ----------------------
+// Length symbol 257+i: base and extra bits.  i<8: 3+i, 0 extra; i==28: 258.
+__host__ __device__ __forceinline__ u32 length_extra(u32 i) {
+  return (i < 8 || i == 28) ? 0u : (i >> 2) - 1u;
+}
+__host__ __device__ __forceinline__ u32 length_base(u32 i) {
+  return i < 8 ? i + 3u : (i == 28 ? 258u : 3u + ((4u + (i & 3u)) << ((i >> 2) - 1u)));
+}
+// Distance symbol d (0..29).
+__host__ __device__ __forceinline__ u32 dist_extra(u32 d) {
+  return d < 4 ? 0u : (d >> 1) - 1u;
+}
+__host__ __device__ __forceinline__ u32 dist_base(u32 d) {
+  return d < 4 ? d + 1u : 1u + ((2u + (d & 1u)) << ((d >> 1) - 1u));
+}
+
+__host__ __device__ __forceinline__ u32 bit_reverse(u32 code, u32 len) {
+  return __builtin_bitreverse32(code) >> (32 - len);
+}
+
+// ---- bit input --------------------------------------------------------------
+// LSB-first reader over a byte range [data, data + bytes).  The reader loads
+// aligned dwords only, and only dwords that hold at least one byte of the
+// range, so it never touches a page outside the caller's buffer.  `pos` counts
+// consumed bits from the start of the range; `avail()` is what remains.  Bits
+// past the range may be garbage inside `buf`; every consumer checks avail()
+// before committing, which reproduces the reference's "error 1 on over-read".
+struct BitIn {
+  const u32* words;
+  u64 base_bit;   // bit offset of data[0] inside words[0]
+  u64 total;      // valid bits in the range
+  u64 pos;        // consumed bits
+  u64 buf;        // bits [pos, pos + cnt)
+  u32 cnt;
+  u64 wnext;      // next dword index to load
+  u64 wlimit;     // dwords holding range bytes
+
+  __device__ __forceinline__ void init(const u8* data, u64 bytes, u64 start_bit) {
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(data);
+    words = reinterpret_cast<const u32*>(addr & ~uintptr_t(3));
+    base_bit = u64(addr & 3u) * 8u;
+    total = bytes * 8u;
+    wlimit = (u64(addr & 3u) + bytes + 3u) >> 2;
+    seek(start_bit);
+  }
+  __device__ __forceinline__ void refill() {
+    while (cnt <= 32) {
+      const u64 v = wnext < wlimit ? u64(words[wnext]) : 0ull;
+      buf |= v << cnt;
+      cnt += 32;
+      ++wnext;
+    }
+  }
+  __device__ __forceinline__ void seek(u64 p) {
+    pos = p;
+    const u64 a = base_bit + p;
+    wnext = a >> 5;
+    buf = 0;
+    cnt = 0;
+    refill();
+    const u32 skip = u32(a & 31u);
+    buf >>= skip;
+    cnt -= skip;
+    refill();
+  }
+  __device__ __forceinline__ u64 avail() const { return pos <= total ? total - pos : 0; }
+  // Callers guarantee n <= 32 and have checked avail() where it matters.
+  __device__ __forceinline__ u32 peek(u32 n) const {
+    return n ? u32(buf & ((1ull << n) - 1ull)) : 0u;
+  }
+  __device__ __forceinline__ void drop(u32 n) {
+    buf >>= n;
+    cnt -= n;
+    pos += n;
+    if (cnt <= 32) refill();
+  }
+  // take(n): returns false (truncation) when fewer than n bits remain.
+  __device__ __forceinline__ bool take(u32 n, u32& v) {
+    if (u64(n) > avail()) return false;
+    v = peek(n);
+    drop(n);
+    return true;
+  }
+};
+
+// ---- canonical Huffman decode tables ---------------------------------------
+// Primary LUT entry (u32): bits 0..3 code length (0 = no short code here),
+// bits 16..31 symbol.  Codes longer than the primary width use the canonical
+// count/first walk.  `maximum` is the longest code length (0 for an empty tree).
+template <int N, int P>
+struct HuffTable {
+  u16 count[16];
+  u16 symbols[N];
+  u32 primary[1 << P];
+  u32 maximum;
+};
+
+// Build from code lengths.  empty_ok: all-zero lengths allowed (distance tree).
+// single_ok: an incomplete code consisting of one length-1 code is allowed.
+// Returns 0 or kBadTree.  Must be called by one thread.  Semantics follow the
+// reference's Huffman::build (_decode_kernels.py:141-183).
+template <int N, int P>
+__device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_ok,
+                          bool single_ok, u32 limit) {
+  for (u32 i = 0; i < 16; ++i) t.count[i] = 0;
+  t.maximum = 0;
+  if (n > u32(N)) return kBadTree;
+  for (u32 i = 0; i < n; ++i) {
+    const u32 l = lens[i];
+    if (l > limit) return kBadTree;
+    ++t.count[l];
+    if (l > t.maximum) t.maximum = l;
+  }
+  if (!t.maximum) return empty_ok ? 0u : u32(kBadTree);
+  i32 left = 1;
+  for (u32 l = 1; l <= limit; ++l) {
+    left = (left << 1) - i32(t.count[l]);
+    if (left < 0) return kBadTree;
+  }
+  if (left && !(single_ok && t.maximum == 1 && t.count[1] == 1)) return kBadTree;
+  u16 offs[16];
+  offs[1] = 0;
+  for (u32 l = 1; l < 15; ++l) offs[l + 1] = offs[l] + t.count[l];
+  for (u32 i = 0; i < n; ++i)
+    if (lens[i]) t.symbols[offs[lens[i]]++] = u16(i);
+  for (u32 i = 0; i < (1u << P); ++i) t.primary[i] = 0;
+  u32 code = 0, index = 0;
+  for (u32 l = 1; l <= u32(P); ++l) {
+    for (u32 j = 0; j < t.count[l]; ++j) {
+      const u32 rev = bit_reverse(code + j, l);
+      const u32 e = (u32(t.symbols[index + j]) << 16) | l;
+      for (u32 k = rev; k < (1u << P); k += 1u << l) t.primary[k] = e;
+    }
+    index += t.count[l];
+    code = (code + t.count[l]) << 1;
+  }
+  return 0;
+}
+
+// Decode one symbol.  Returns the symbol (>= 0), or -1 with `err` set to
+// kTruncated (bits ran out first) or kBadSymbol (no code matches within
+// `maximum` bits).  Matches the reference's LUT-plus-canonical decode exactly,
+// including its behaviour at the end of the bit range.
+template <int N, int P>
+__device__ __forceinline__ i32 huff_decode(const HuffTable<N, P>& t, BitIn& r, u32& err) {
+  const u32 e = t.primary[r.peek(P)];
+  const u32 l = e & 15u;
+  if (l) {
+    if (u64(l) > r.avail()) { err = kTruncated; return -1; }
+    r.drop(l);
+    return i32(e >> 16);
+  }
+  // Canonical walk for long codes and invalid prefixes.
+  u32 code = 0, first = 0, index = 0;
+  const u64 avail = r.avail();
+  for (u32 len = 1; len <= t.maximum; ++len) {
+    if (u64(len) > avail) { err = kTruncated; return -1; }
+    code |= u32((r.buf >> (len - 1)) & 1ull);
+    const u32 c = t.count[len];
+    if (code < first + c) {
+      r.drop(len);
+      return i32(t.symbols[index + code - first]);
+    }
+    index += c;
+    first = (first + c) << 1;
+    code <<= 1;
+  }
+  err = kBadSymbol;
+  return -1;
+}
+
+struct DecodeTables {
+  HuffTable<288, 10> ll;
+  HuffTable<32, 8> dd;
+  HuffTable<19, 7> cl;
+  u8 lens[320];
+};
+
+// Fixed Huffman tables (RFC 1951 3.2.6).
+__device__ inline u32 build_fixed_tables(DecodeTables& t) {
+  for (u32 i = 0; i < 288; ++i) t.lens[i] = i < 144 ? 8 : i < 256 ? 9 : i < 280 ? 7 : 8;
+  u32 err = huff_build(t.ll, t.lens, 288, false, true, 15);
+  if (err) return err;
+  for (u32 i = 0; i < 32; ++i) t.lens[i] = 5;
+  return huff_build(t.dd, t.lens, 32, false, true, 15);
+}
+
+// Dynamic block header (RFC 1951 3.2.7), reader positioned after BTYPE.
+// Error order follows the reference's dynamic_tables (_decode_kernels.py:240-287).
+__device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
+  u32 hlit, hdist, hclen;
+  if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return kTruncated;
+  const u32 nl = hlit + 257, nd = hdist + 1, nc = hclen + 4;
+  if (nl > 286) return kBadTree;
+  const u8 order[19] = {16, 17, 18, 0, 8, 7, 9, 6, 10, 5, 11, 4, 12, 3, 13, 2, 14, 1, 15};
+  u8 clens[19];
+  for (u32 i = 0; i < 19; ++i) clens[i] = 0;
+  for (u32 i = 0; i < nc; ++i) {
+    u32 v;
+    if (!r.take(3, v)) return kTruncated;
+    clens[order[i]] = u8(v);
+  }
+  u32 err = huff_build(t.cl, clens, 19, false, false, 7);
+  if (err) return err;
+  u32 i = 0;
+  while (i < nl + nd) {
+    u32 e = 0;
+    const i32 sym = huff_decode(t.cl, r, e);
+    if (sym < 0) return e;
+    if (sym < 16) { t.lens[i++] = u8(sym); continue; }
+    u32 repeat, value, x;
+    if (sym == 16) {
+      if (!i) return kBadRepeat;
+      if (!r.take(2, x)) return kTruncated;
+      repeat = x + 3;
+      value = t.lens[i - 1];
+    } else if (sym == 17) {
+      if (!r.take(3, x)) return kTruncated;
+      repeat = x + 3;
+      value = 0;
+    } else {
+      if (!r.take(7, x)) return kTruncated;
+      repeat = x + 11;
+      value = 0;
+    }
+    if (repeat > nl + nd - i) return kBadRepeat;
+    for (u32 j = 0; j < repeat; ++j) t.lens[i++] = u8(value);
+  }
+  if (!t.lens[256]) return kBadTree;
+  err = huff_build(t.ll, t.lens, nl, false, true, 15);
+  if (err) return err;
+  return huff_build(t.dd, t.lens + nl, nd, true, true, 15);
+}
+
+// One literal/length token after the LL symbol.  Returns kOk and sets
+// length/distance (length 0 = EOB, distance 0 = literal in `lit`), or an error.
+// Order of checks follows the reference's token decode (_decode_kernels.py:393-420).
+__device__ __forceinline__ u32 decode_token(DecodeTables& t, BitIn& r, u32 window, u32& lit,
+                                             u32& length, u32& distance) {
+  u32 err = 0;
+  const i32 sym = huff_decode(t.ll, r, err);
+  length = 0;
+  distance = 0;
+  if (sym < 0) return err;
+  if (sym < 256) { lit = u32(sym); length = 1; return kOk; }
+  if (sym == 256) return kOk;
+  if (sym > 285) return kBadSymbol;
+  const u32 li = u32(sym) - 257;
+  u32 x = 0;
+  if (!r.take(length_extra(li), x)) return kTruncated;
+  length = length_base(li) + x;
+  const i32 ds = huff_decode(t.dd, r, err);
+  if (ds < 0) return err;
+  if (ds > 29) return kBadSymbol;
+  if (!r.take(dist_extra(u32(ds)), x)) return kTruncated;
+  distance = dist_base(u32(ds)) + x;
+  if (distance > window) return kBadDistance;
+  return kOk;
+}
+
+// zlib wrapper (RFC 1950) checks, in the reference's precedence order.
+__host__ __device__ __forceinline__ u32 check_framing(const u8* in, u64 size, u32& window,
+                                                       u32& wanted) {
+  window = 0;
+  wanted = 0;
+  if (size < 8) return kTruncatedZlib;
+  const u32 cmf = in[0], flg = in[1];
+  if (cmf == 0x1f && flg == 0x8b) return kUnsupportedGzip;
+  if ((cmf & 15) != 8 || (cmf >> 4) > 7 || (cmf * 256 + flg) % 31) return kInvalidHeader;
+  if (flg & 32) return kUnsupportedDictionary;
+  window = 1u << ((cmf >> 4) + 8);
+  wanted = (u32(in[size - 4]) << 24) | (u32(in[size - 3]) << 16) | (u32(in[size - 2]) << 8) |
+           u32(in[size - 1]);
+  return kOk;
+}
+
+__device__ __forceinline__ u32 lane_id() { return __lane_id(); }
+
+}  // namespace hz

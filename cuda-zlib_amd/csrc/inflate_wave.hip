@@ -1,0 +1,241 @@
+// Single-wave serial inflate: one 64-lane wavefront decodes one whole zlib
+// stream.  Lane 0 walks the bit stream; the wave joins in for stored payload
+// copies and long matches; the wave computes the Adler-32 check at the end.
+//
+// Serves the small-stream route and every file of a batch.  Semantics restate
+// the reference's DecodeOneFile (native/batch_decode.cuh:123-296): statuses in
+// stream order, failed output = decoded prefix followed by zeros, exact output
+// size (11), no trailing body bytes (12), block cap (9), declared window (6).
+#include "deflate_common.h"
+#include "kernels.h"
+
+namespace hz {
+
+namespace {
+
+constexpr u32 kWave = 64;
+constexpr u32 kCoopMatch = 32;  // matches at least this long are copied by the wave
+
+struct WaveShared {
+  DecodeTables tables;
+  u32 action;  // 0 done, 1 match copy, 2 stored copy
+  u32 error;
+  u64 begin, length, distance, src;
+};
+
+// Copy a match of `length` bytes to out[begin..) from `d` bytes back.  Reads
+// only the d-byte seed preceding `begin`, so an overlapping match never
+// depends on this copy's own stores.
+__device__ __forceinline__ void wave_match(u8* out, u64 begin, u64 d, u64 length, u32 lane) {
+  const u64 first = begin - d;
+  if (d == 1) {
+    const u8 v = out[first];
+    for (u64 j = lane; j < length; j += kWave) out[begin + j] = v;
+    return;
+  }
+  u64 src = first + (lane % d);
+  const u64 stride = kWave % d;
+  for (u64 j = lane; j < length; j += kWave) {
+    out[begin + j] = out[src];
+    src += stride;
+    if (src >= begin) src -= d;
+  }
+}
+
+// Adler-32 of out[0..n) by one wave; result valid in lane 0.
+__device__ u32 wave_adler(const u8* out, u64 n, u32 lane) {
+  u64 s = 0, w = 0;
+  // weight of byte i is (n - i) mod 65521; it drops by 64 per step.
+  u64 weight = (n - lane) % kAdlerMod;
+  const u64 step = kWave % kAdlerMod;
+  u32 since = 0;
+  for (u64 i = lane; i < n; i += kWave) {
+    const u64 v = out[i];
+    s += v;
+    w += weight * v;
+    weight = weight >= step ? weight - step : weight + kAdlerMod - step;
+    if (++since == 4096) {  // keep sums far from overflow
+      s %= kAdlerMod;
+      w %= kAdlerMod;
+      since = 0;
+    }
+  }
+  s %= kAdlerMod;
+  w %= kAdlerMod;
+  for (u32 off = kWave / 2; off; off >>= 1) {
+    s += __shfl_down(s, off, kWave);
+    w += __shfl_down(w, off, kWave);
+  }
+  const u32 a = u32((s + 1) % kAdlerMod);
+  const u32 b = u32((w + n) % kAdlerMod);
+  return (b << 16) | a;
+}
+
+// Decodes one stream with a 64-thread workgroup and writes [status, 0].
+__device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_size,
+                                 u32 max_blocks, u32* meta, WaveShared& sh) {
+  const u32 lane = threadIdx.x;
+  if (in_size > kMaxBytes || out_size > kMaxBytes || !max_blocks || max_blocks > kMaxBlocks) {
+    if (!lane) { meta[0] = kInvalidBounds; meta[1] = 0; }
+    return;
+  }
+  for (u64 i = lane; i < out_size; i += kWave) out[i] = 0;
+  __syncthreads();
+
+  // Lane-0 private parser state.
+  u32 error = 0, final_block = 0, blocks = 0, window = 0, wanted = 0;
+  u64 produced = 0, body_bytes = 0;
+  bool need_header = true, complete = false;
+  BitIn r;
+  if (!lane) {
+    error = check_framing(in, in_size, window, wanted);
+    if (!error) {
+      body_bytes = in_size - 6;
+      r.init(in + 2, body_bytes, 0);
+    }
+  }
+
+  while (true) {
+    if (!lane) {
+      u32 action = 0;
+      while (!error && !complete) {
+        if (need_header) {
+          if (blocks >= max_blocks) { error = kBlockCapacity; break; }
+          ++blocks;
+          u32 type;
+          if (!r.take(1, final_block) || !r.take(2, type)) { error = kTruncated; break; }
+          if (type == 3) { error = kReservedBlock; break; }
+          if (type == 0) {
+            r.seek((r.pos + 7) & ~u64(7));
+            u32 n, comp;
+            if (!r.take(16, n) || !r.take(16, comp)) { error = kTruncated; break; }
+            if ((n ^ comp) != 0xffffu) { error = kBadSymbol; break; }
+            if (n > out_size - produced) { error = kOutputOverflow; break; }
+            if (u64(n) * 8 > r.avail()) { error = kTruncated; break; }
+            sh.begin = produced;
+            sh.length = n;
+            sh.src = (r.pos >> 3) + 2;
+            produced += n;
+            r.seek(r.pos + u64(n) * 8);
+            complete = final_block != 0;
+            action = 2;
+            break;
+          }
+          error = type == 1 ? build_fixed_tables(sh.tables) : build_dynamic_tables(sh.tables, r);
+          need_header = false;
+          if (error) break;
+        }
+        u32 lit = 0, length = 0, distance = 0;
+        error = decode_token(sh.tables, r, window, lit, length, distance);
+        if (error) break;
+        if (!length) {  // end of block
+          complete = final_block != 0;
+          need_header = true;
+          continue;
+        }
+        if (length > out_size - produced) { error = kOutputOverflow; break; }
+        if (!distance) { out[produced++] = u8(lit); continue; }
+        if (distance > produced) { error = kBadDistance; break; }
+        if (length >= kCoopMatch) {
+          sh.begin = produced;
+          sh.length = length;
+          sh.distance = distance;
+          produced += length;
+          action = 1;
+          break;
+        }
+        u64 src = produced - distance;
+        const u64 first = src;
+        for (u32 j = 0; j < length; ++j) {
+          out[produced + j] = out[src];
+          if (++src == produced) src = first;
+        }
+        produced += length;
+      }
+      if (!action && !error) {
+        if (produced != out_size) error = kSizeMismatch;
+        else if ((r.pos + 7) / 8 != body_bytes) error = kExtent;
+      }
+      sh.action = action;
+      sh.error = error;
+    }
+    __syncthreads();
+    const u32 action = sh.action;
+    if (!action) break;
+    if (action == 1) wave_match(out, sh.begin, sh.distance, sh.length, lane);
+    else
+      for (u64 j = lane; j < sh.length; j += kWave) out[sh.begin + j] = in[sh.src + j];
+    __syncthreads();
+  }
+
+  u32 status = sh.error;
+  if (!status) {
+    const u32 got = wave_adler(out, out_size, lane);
+    if (!lane && got != wanted) status = kAdlerMismatch;
+  }
+  if (!lane) {
+    meta[0] = status;
+    meta[1] = 0;
+  }
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(64) void inflate_single_kernel(const u8* in, u64 in_size, u8* out,
+                                                            u64 out_size, u32 max_blocks,
+                                                            u32* meta) {
+  __shared__ WaveShared sh;
+  inflate_one_wave(in, in_size, out, out_size, max_blocks, meta, sh);
+}
+
+// One workgroup per file.  With encoded metadata (compression's
+// [length, status] rows), a file's stream length comes from its row and a
+// failed or oversized slot is zeroed with status 22/23 (batch_decode.cuh:298-328).
+__global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out,
+                                                           const BatchFile* files, u32 count,
+                                                           u32 max_blocks, u32* meta,
+                                                           const u32* encoded) {
+  __shared__ WaveShared sh;
+  for (u32 f = blockIdx.x; f < count; f += gridDim.x) {
+    const BatchFile file = files[f];
+    u64 in_size = file.in_size;
+    if (encoded) {
+      const u32 enc_len = encoded[2 * u64(f)];
+      const u32 enc_status = encoded[2 * u64(f) + 1];
+      u32 error = enc_status ? u32(kCompressionOverflow) : (enc_len > file.in_size ? u32(kInvalidBounds) : 0u);
+      if (file.out_size > kMaxBytes) error = kInvalidBounds;
+      if (error) {
+        if (file.out_size <= kMaxBytes)
+          for (u64 i = threadIdx.x; i < file.out_size; i += kWave) out[file.out_offset + i] = 0;
+        if (!threadIdx.x) {
+          meta[2 * u64(f)] = error;
+          meta[2 * u64(f) + 1] = 0;
+        }
+        __syncthreads();
+        continue;
+      }
+      in_size = enc_len;
+    }
+    inflate_one_wave(in + file.in_offset, in_size, out + file.out_offset, file.out_size, max_blocks,
+                     meta + 2 * u64(f), sh);
+    __syncthreads();
+  }
+}
+
+hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
+                                 u64 out_size, u32 max_blocks, u32* meta) {
+  hipLaunchKernelGGL(inflate_single_kernel, dim3(1), dim3(kWave), 0, stream, in, in_size, out,
+                     out_size, max_blocks, meta);
+  return hipGetLastError();
+}
+
+hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const BatchFile* files,
+                                u32 count, u32 max_blocks, u32* meta, const u32* encoded) {
+  if (!count) return hipSuccess;
+  const u32 grid = count < 65536u ? count : 65536u;
+  hipLaunchKernelGGL(inflate_batch_kernel, dim3(grid), dim3(kWave), 0, stream, in, out, files, count,
+                     max_blocks, meta, encoded);
+  return hipGetLastError();
+}
+
+}  // namespace hz

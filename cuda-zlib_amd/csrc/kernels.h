@@ -1,0 +1,53 @@
+// Internal host-side launch interface between the C-ABI layer and the kernel
+// translation units.  Every launcher enqueues on `stream` and returns the
+// launch error; none of them synchronises with the host.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "deflate_common.h"
+
+namespace hz {
+
+struct BatchFile {
+  u64 in_offset;
+  u64 in_size;
+  u64 out_offset;
+  u64 out_size;
+};
+
+// util.hip
+hipError_t launch_fill(hipStream_t stream, void* dst, u8 value, u64 bytes);
+hipError_t launch_set_meta(hipStream_t stream, u32* meta, u32 first, u32 second);
+hipError_t launch_set_meta_rows(hipStream_t stream, u32* meta, u64 rows, u32 first, u32 second);
+
+// inflate_wave.hip: serial-route decode (one wave per stream).
+hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
+                                 u64 out_size, u32 max_blocks, u32* meta);
+hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const BatchFile* files,
+                                u32 count, u32 max_blocks, u32* meta, const u32* encoded);
+
+// Scratch allocation interface used by multi-kernel routes.
+struct Scratch {
+  virtual hipError_t alloc_bytes(void** p, u64 bytes) = 0;
+  template <typename T>
+  hipError_t alloc(T** p, u64 count) {
+    return alloc_bytes(reinterpret_cast<void**>(p), count * sizeof(T));
+  }
+  virtual ~Scratch() {}
+};
+
+// inflate_par.hip: general-route decode.
+hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
+                               u8* out, u64 out_size, u32 max_candidates, u32 max_blocks,
+                               u32* meta);
+
+// deflate.hip: chunked encode of one stream / a batch of streams.
+hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
+                       u64 capacity, u32 chunk_bytes, u32* meta);
+hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_total,
+                             const BatchFile* files_host, u32 count, u8* out, u64 out_total,
+                             u32 chunk_bytes, u32* meta);
+
+}  // namespace hz

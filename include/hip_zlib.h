@@ -1,0 +1,79 @@
+/* C-ABI of the MI355X (gfx950) zlib/DEFLATE codec.
+ *
+ * Every entry point takes device pointers, sizes and a HIP stream.  Work is
+ * enqueued on that stream; no entry point synchronises with the host except
+ * where noted.  Buffers are owned by the caller; scratch comes from a private
+ * per-device stream-ordered pool.
+ *
+ * Return value: 0 on success; a positive hipError_t for a HIP runtime failure;
+ * HIP_ZLIB_INVALID_ARGUMENT (-1) for a malformed call (wrong metadata shape,
+ * inconsistent batch layout).  HipZlibErrorString() describes either.  Data
+ * errors are never returned: they are written to the metadata buffer as codec
+ * statuses (0 ok, 1..23 as documented in the Python package), exactly like the
+ * reference's XLA FFI handlers, which return Success with an error status.
+ */
+#ifndef HIP_ZLIB_H_
+#define HIP_ZLIB_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HIP_ZLIB_INVALID_ARGUMENT (-1)
+
+/* Compress input[0..input_size) into a zero-padded zlib stream.
+ * output_size must equal input_size + 5 * max(1, ceil(input_size / chunk_bytes)) + 6.
+ * metadata (2 x u32, device): [encoded_length, status].
+ * Replaces the reference's CudaZlibCompress FFI handler
+ * (src/cuda_zlib/native/codec_ffi.cu:1144-1152, body Compress at 551-612). */
+int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
+                    uint64_t input_size, uint8_t* output, uint64_t output_size,
+                    uint32_t* metadata, uint64_t metadata_count);
+
+/* Decompress a zlib stream into exactly output_size bytes.
+ * metadata (2 x u32, device): [status, 0].  Output is zero-filled on failure
+ * (serial small-stream route: decoded prefix followed by zeros).
+ * Replaces CudaZlibDecompress (codec_ffi.cu:1153-1162, body Decompress at 662-950). */
+int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int64_t max_blocks,
+                      const uint8_t* input, uint64_t input_size, uint8_t* output,
+                      uint64_t output_size, uint32_t* metadata, uint64_t metadata_count);
+
+/* Compress `files` packed inputs (host array input_sizes) into consecutive
+ * padded slots; metadata (files x 2 u32, device) rows are [encoded_length, status].
+ * The host-side size list is copied to the device before the call returns.
+ * Replaces CudaZlibCompressBatch (codec_ffi.cu:1163-1172, body 1002-1063). */
+int HipZlibCompressBatch(hipStream_t stream, int64_t chunk_bytes, const int64_t* input_sizes,
+                         uint64_t files, const uint8_t* input, uint64_t input_size,
+                         uint8_t* output, uint64_t output_size, uint32_t* metadata,
+                         uint64_t metadata_rows, uint64_t metadata_cols);
+
+/* Decompress packed independent streams.  encoded_metadata is null (rows = 0)
+ * or compression's (files x 2) [length, status] rows on the device; then a
+ * file's stream length is read on the device.  metadata rows are [status, 0].
+ * Replaces CudaZlibDecompressBatch (codec_ffi.cu:1173-1182, body 1065-1107). */
+int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_sizes, uint64_t input_count,
+                           const int64_t* output_sizes, uint64_t output_count,
+                           const uint8_t* input, uint64_t input_size,
+                           const uint32_t* encoded_metadata, uint64_t encoded_rows,
+                           uint64_t encoded_cols, uint8_t* output, uint64_t output_size,
+                           uint32_t* metadata, uint64_t metadata_rows, uint64_t metadata_cols);
+
+/* Workspace pool controls.  Replace CudaZlibSetWorkspaceRetention,
+ * CudaZlibWorkspacePoolStats and CudaZlibTrimWorkspacePool (codec_ffi.cu:1113-1142).
+ * Retention may only change before the first pool is created.
+ * stats = {retention_bytes, reserved_bytes, used_bytes, pool_count}. */
+int HipZlibSetWorkspaceRetention(uint64_t bytes);
+int HipZlibWorkspacePoolStats(int device, uint64_t* stats);
+int HipZlibTrimWorkspacePool(int device);
+
+/* Text for a return code of any entry point above (thread-local for -1). */
+const char* HipZlibErrorString(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIP_ZLIB_H_ */
