@@ -1,9 +1,930 @@
-// General-route decode (parallel).  Under construction: returns an explicit
-// error until the parallel kernels land.
+// General-route decode: any valid zlib stream, parallel over Deflate blocks.
+//
+// Pipeline (all on one stream, no host synchronisation):
+//   frame      framing checks, declared window, wanted Adler-32
+//   discover   every bit offset: cheap bit-parallel prefilter, exact dynamic
+//              header validation; ordered compaction (per-workgroup lists,
+//              scan, gather) gives a sorted candidate list without a sort
+//   describe   one wave per candidate: parse its segment (the candidate's
+//              block plus following stored/fixed blocks up to the next
+//              candidate) -> end bit, output size, block count, status
+//   chain      one workgroup: path from bit 0 through the segment graph,
+//              output prefixes; any anomaly defers to the exact walk
+//   exact      serial walk with the reference's status precedence (runs only
+//              when the fast chain did not accept the stream)
+//   emit       one wave per accepted segment writes output bytes in place;
+//              bytes copied from earlier segments become (position, root)
+//              entries of an unresolved list
+//   resolve    pointer-jumping rounds over the unresolved list
+//   adler      tiled Adler-32 partials, then the final status
+//
+// Status semantics restate the reference's general route: framing
+// (native/codec_ffi.cu:304-329) > candidate overflow (344-360) > exact chain
+// (select_chain, _decode_kernels.py:1226-1408) > emission history/window
+// (parse_block<Emit>, 683-781; EmissionStatus codec_ffi.cu:405-435) > Adler-32
+// (467-483).  Failed output is all zeros except on an Adler-32 mismatch.
+#include "deflate_common.h"
 #include "kernels.h"
 
 namespace hz {
-hipError_t run_inflate_general(hipStream_t, Scratch&, const u8*, u64, u8*, u64, u32, u32, u32*) {
-  return hipErrorNotSupported;
+namespace {
+
+constexpr u32 kWave = 64;
+constexpr u32 kNone = 0xffffffffu;
+constexpr u32 kDiscThreads = 256;
+constexpr u32 kDiscBytesPerThread = 8;
+constexpr u32 kDiscRange = kDiscThreads * kDiscBytesPerThread;  // bytes per workgroup
+constexpr u32 kDiscCap = 64;                                      // local list capacity
+constexpr u32 kCoopMatch = 32;
+
+struct State {
+  u32 status;        // first error (framing, discovery, chain/exact)
+  u32 window;
+  u32 wanted;
+  u32 chain_ok;      // fast chain accepted the stream
+  u64 candidates;    // dynamic candidates + bit 0 (sorted list length)
+  u64 seeds;         // stored-endpoint seeds (counted for the overflow check)
+  u64 accepted;      // number of accepted segments
+  u32 emit_status;
+  u32 pad;
+  u64 unresolved[2]; // ping-pong list lengths for resolve rounds
+  u64 adler_s, adler_w;
+};
+
+struct Segment {
+  u64 start;   // bit offset of the first block
+  u64 end;     // bit offset after the last block
+  u64 prefix;  // output offset
+  u64 size;    // output bytes
+};
+
+__device__ __forceinline__ u64 load_window_word(const u8* body, u64 len, u64 byte) {
+  // Eight bytes starting at `byte`; bytes past the body read as zero.
+  u64 v = 0;
+  if (byte + 8 <= len) {
+#pragma unroll
+    for (u32 j = 0; j < 8; ++j) v |= u64(body[byte + j]) << (8 * j);
+  } else {
+    for (u32 j = 0; j < 8; ++j)
+      if (byte + j < len) v |= u64(body[byte + j]) << (8 * j);
+  }
+  return v;
 }
+
+__device__ __forceinline__ u64 funnel(u64 lo, u64 hi, u32 k) {
+  return k ? (lo >> k) | (hi << (64 - k)) : lo;
+}
+
+// Exact validity of a dynamic header whose BTYPE bits were already checked:
+// the same outcome as building all three tables (huff_build rules), computed
+// with Kraft sums instead of tables.  `lut` is 128 bytes of thread-private LDS.
+__device__ bool dynamic_header_valid(const u8* body, u64 len, u64 start, u8* lut) {
+  BitIn r;
+  r.init(body, len, start + 3);
+  u32 hlit, hdist, hclen;
+  if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return false;
+  const u32 nl = hlit + 257, nd = hdist + 1, nc = hclen + 4;
+  if (nl > 286) return false;
+  const u8 order[19] = {16, 17, 18, 0, 8, 7, 9, 6, 10, 5, 11, 4, 12, 3, 13, 2, 14, 1, 15};
+  u64 pack = 0;  // 3-bit length per code-length symbol
+  u32 kraft = 0;
+  for (u32 i = 0; i < nc; ++i) {
+    u32 v;
+    if (!r.take(3, v)) return false;
+    pack |= u64(v) << (3 * order[i]);
+    if (v) kraft += 128u >> v;
+  }
+  if (kraft != 128) return false;
+  // Canonical codes for the code-length alphabet into a 7-bit LUT: entry =
+  // symbol | length << 5.
+  u32 count[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (u32 s = 0; s < 19; ++s) ++count[(pack >> (3 * s)) & 7];
+  u32 next[8];
+  u32 code = 0;
+  count[0] = 0;
+  for (u32 l = 1; l < 8; ++l) {
+    code = (code + count[l - 1]) << 1;
+    next[l] = code;
+  }
+  for (u32 s = 0; s < 19; ++s) {
+    const u32 l = (pack >> (3 * s)) & 7;
+    if (!l) continue;
+    const u32 rev = bit_reverse(next[l]++, l);
+    for (u32 k = rev; k < 128; k += 1u << l) lut[k] = u8(s | (l << 5));
+  }
+  u32 ll_kraft = 0, ll_nnz = 0, d_kraft = 0, d_nnz = 0, eob = 0, prev = 0;
+  u32 i = 0;
+  const u32 total = nl + nd;
+  while (i < total) {
+    const u32 e = lut[r.peek(7)];
+    const u32 l = e >> 5, sym = e & 31;
+    if (u64(l) > r.avail()) return false;
+    r.drop(l);
+    u32 repeat, value, x;
+    if (sym < 16) {
+      repeat = 1;
+      value = sym;
+    } else if (sym == 16) {
+      if (!i) return false;
+      if (!r.take(2, x)) return false;
+      repeat = x + 3;
+      value = prev;
+    } else if (sym == 17) {
+      if (!r.take(3, x)) return false;
+      repeat = x + 3;
+      value = 0;
+    } else {
+      if (!r.take(7, x)) return false;
+      repeat = x + 11;
+      value = 0;
+    }
+    if (repeat > total - i) return false;
+    if (value) {
+      const u32 in_ll = i < nl ? min(repeat, nl - i) : 0u;
+      const u32 in_d = repeat - in_ll;
+      ll_kraft += in_ll << (15 - value);
+      ll_nnz += in_ll;
+      d_kraft += in_d << (15 - value);
+      d_nnz += in_d;
+      if (i <= 256 && 256 < i + repeat) eob = 1;
+    }
+    prev = value;
+    i += repeat;
+  }
+  if (!eob) return false;
+  const bool ll_ok = ll_kraft == (1u << 15) || (ll_nnz == 1 && ll_kraft == (1u << 14));
+  const bool d_ok = d_nnz == 0 || d_kraft == (1u << 15) || (d_nnz == 1 && d_kraft == (1u << 14));
+  return ll_ok && d_ok;
+}
+
+// Stored-block endpoint seed at `byte` (counted like the reference's discovery,
+// _decode_kernels.py:1019-1038).
+__device__ __forceinline__ bool stored_seed(const u8* body, u64 len, u64 byte) {
+  if (!byte || len - byte < 5) return false;
+  const u32 n = body[byte] | (u32(body[byte + 1]) << 8);
+  const u32 comp = body[byte + 2] | (u32(body[byte + 3]) << 8);
+  if ((n ^ comp) != 0xffffu || u64(n) + 4 >= len - byte) return false;
+  u32 before = u32(body[byte - 1]) << 8;
+  if (byte >= 2) before |= body[byte - 2];
+  bool possible = false;
+  for (u32 gap = 3; gap <= 10; ++gap)
+    if (byte * 8 >= gap && ((before >> (17 - gap)) & 3u) == 0) possible = true;
+  return possible && ((body[byte + 4 + n] >> 1) & 3u) == 1;
+}
+
+// Candidate mask for the 64 bit offsets of bytes [b0, b0 + 8).
+__device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, u8* lut) {
+  if (b0 >= len) return 0;
+  const u64 w0 = load_window_word(body, len, b0);
+  const u64 w1 = load_window_word(body, len, b0 + 8);
+  const u64 w2 = load_window_word(body, len, b0 + 16);
+  // Bit k of s_j is stream bit (8*b0 + k + j).
+  const u64 s1 = funnel(w0, w1, 1), s2 = funnel(w0, w1, 2);
+  const u64 s4 = funnel(w0, w1, 4), s5 = funnel(w0, w1, 5);
+  const u64 s6 = funnel(w0, w1, 6), s7 = funnel(w0, w1, 7);
+  u64 m = ~s1 & s2 & ~(s4 & s5 & s6 & s7);  // BTYPE == 2 and HLIT <= 29
+  const u64 bits_left = (len - b0) * 8;
+  if (bits_left < 64) m &= (1ull << bits_left) - 1;
+  u64 valid = 0;
+  while (m) {
+    const u32 k = __builtin_ctzll(m);
+    m &= m - 1;
+    const u64 a = funnel(w0, w1, k), b = funnel(w1, w2, k);
+    const u32 nc = u32((a >> 13) & 15) + 4;
+    const u64 lens = (a >> 17) | (b << 47);
+    u32 kraft = 0;
+    for (u32 i = 0; i < nc; ++i) {
+      const u32 l = u32(lens >> (3 * i)) & 7u;
+      if (l) kraft += 128u >> l;
+    }
+    if (kraft != 128) continue;
+    const u64 start = b0 * 8 + k;
+    if (start && dynamic_header_valid(body, len, start, lut)) valid |= 1ull << k;
+  }
+  return valid;
+}
+
+__device__ __forceinline__ u32 block_exclusive_scan(u32 v, u32* sh, u32& total) {
+  // 256-thread exclusive scan through LDS.
+  const u32 t = threadIdx.x;
+  sh[t] = v;
+  __syncthreads();
+  for (u32 off = 1; off < kDiscThreads; off <<= 1) {
+    const u32 x = t >= off ? sh[t - off] : 0u;
+    __syncthreads();
+    sh[t] += x;
+    __syncthreads();
+  }
+  total = sh[kDiscThreads - 1];
+  const u32 excl = sh[t] - v;
+  __syncthreads();
+  return excl;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* st) {
+  u32 window, wanted;
+  const u32 status = check_framing(in, in_size, window, wanted);
+  st->status = status;
+  st->window = window;
+  st->wanted = wanted;
+  st->chain_ok = 0;
+  st->candidates = 0;
+  st->seeds = 0;
+  st->accepted = 0;
+  st->emit_status = 0;
+  st->unresolved[0] = 0;
+  st->unresolved[1] = 0;
+  st->adler_s = 0;
+  st->adler_w = 0;
+}
+
+// Pass 1: per-workgroup candidate count and (up to kDiscCap) ordered entries.
+__global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State* st,
+                                                  u32* wg_count, u64* wg_list) {
+  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u32 scan[kDiscThreads];
+  if (st->status) return;
+  const u64 wg = blockIdx.x;
+  const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
+  u64 mask = candidate_mask(body, len, b0, luts[threadIdx.x]);
+  if (b0 == 0) mask |= 1;  // bit 0 is always a candidate
+  u32 seeds = 0;
+  for (u32 j = 0; j < kDiscBytesPerThread; ++j)
+    if (b0 + j < len && stored_seed(body, len, b0 + j)) ++seeds;
+  if (seeds) atomicAdd(reinterpret_cast<unsigned long long*>(&st->seeds), seeds);
+  u32 total;
+  const u32 base = block_exclusive_scan(__popcll(mask), scan, total);
+  if (!threadIdx.x) wg_count[wg] = total;
+  if (total <= kDiscCap) {
+    u32 at = base;
+    while (mask) {
+      const u32 k = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      wg_list[wg * kDiscCap + at++] = b0 * 8 + k;
+    }
+  }
+}
+
+// Pass 2: one workgroup scans the per-workgroup counts into offsets.
+__global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg_count,
+                                                        u64* wg_offset, u64 groups,
+                                                        u64 max_candidates) {
+  __shared__ u64 part[1024];
+  if (st->status) return;
+  const u32 t = threadIdx.x;
+  const u64 per = (groups + 1023) / 1024;
+  const u64 lo = min<u64>(groups, u64(t) * per), hi = min<u64>(groups, lo + per);
+  u64 sum = 0;
+  for (u64 i = lo; i < hi; ++i) sum += wg_count[i];
+  part[t] = sum;
+  __syncthreads();
+  for (u32 off = 1; off < 1024; off <<= 1) {
+    const u64 x = t >= off ? part[t - off] : 0ull;
+    __syncthreads();
+    part[t] += x;
+    __syncthreads();
+  }
+  u64 run = part[t] - sum;
+  for (u64 i = lo; i < hi; ++i) {
+    wg_offset[i] = run;
+    run += wg_count[i];
+  }
+  if (t == 1023) {
+    const u64 total = part[1023];
+    st->candidates = total;
+    if (total + st->seeds > max_candidates) st->status = kCandidateOverflow;
+  }
+}
+
+// Pass 3: gather local lists into the sorted candidate array; overflowing
+// workgroups recompute their masks and write directly.
+__global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len, const State* st,
+                                                         const u32* wg_count, const u64* wg_list,
+                                                         const u64* wg_offset, u64* cand) {
+  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u32 scan[kDiscThreads];
+  if (st->status) return;
+  const u64 wg = blockIdx.x;
+  const u32 count = wg_count[wg];
+  const u64 off = wg_offset[wg];
+  if (count <= kDiscCap) {
+    for (u32 i = threadIdx.x; i < count; i += kDiscThreads) cand[off + i] = wg_list[wg * kDiscCap + i];
+    return;
+  }
+  const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
+  u64 mask = candidate_mask(body, len, b0, luts[threadIdx.x]);
+  if (b0 == 0) mask |= 1;
+  u32 total;
+  u32 at = block_exclusive_scan(__popcll(mask), scan, total);
+  while (mask) {
+    const u32 k = __builtin_ctzll(mask);
+    mask &= mask - 1;
+    cand[off + at++] = b0 * 8 + k;
+  }
+}
+
+namespace {
+
+// Lower bound of `key` in the sorted candidate array.
+__device__ u64 lower_bound(const u64* cand, u64 n, u64 key) {
+  u64 lo = 0, hi = n;
+  while (lo < hi) {
+    const u64 mid = lo + (hi - lo) / 2;
+    if (cand[mid] < key) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Count-only parse of one block at r.pos (the reference's parse_block with
+// Emit=false): limit bounds this block's output, distances are checked
+// against the maximum window only.
+__device__ u32 describe_block(BitIn& r, DecodeTables& t, u64 limit, u32& final_block, u64& size) {
+  size = 0;
+  u32 type;
+  if (!r.take(1, final_block) || !r.take(2, type)) return kTruncated;
+  if (type == 3) return kReservedBlock;
+  if (type == 0) {
+    r.seek((r.pos + 7) & ~u64(7));
+    u32 n, comp;
+    if (!r.take(16, n) || !r.take(16, comp)) return kTruncated;
+    if ((n ^ comp) != 0xffffu) return kBadSymbol;
+    if (n > limit) return kOutputOverflow;
+    if (u64(n) * 8 > r.avail()) return kTruncated;
+    r.seek(r.pos + u64(n) * 8);
+    size = n;
+    return kOk;
+  }
+  u32 err = type == 1 ? build_fixed_tables(t) : build_dynamic_tables(t, r);
+  if (err) return err;
+  u64 produced = 0;
+  for (;;) {
+    u32 lit, length, distance;
+    err = decode_token(t, r, 32768u, lit, length, distance);
+    if (err) break;
+    if (!length) break;
+    if (!distance) {
+      if (produced >= limit) { err = kOutputOverflow; break; }
+      ++produced;
+      continue;
+    }
+    if (length > limit - produced) { err = kOutputOverflow; break; }
+    produced += length;
+  }
+  size = produced;
+  return err;
+}
+
+struct DescribeShared {
+  DecodeTables tables;
+  u8 lut[128];
+};
+
+}  // namespace
+
+// One wave per candidate; lane 0 parses the candidate's segment.
+__global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const u64* cand,
+                                                 const State* st, u64 out_size, u64* seg_end,
+                                                 u64* seg_size, u32* seg_blocks, u32* seg_next,
+                                                 u32* seg_flags) {
+  __shared__ DescribeShared sh;
+  if (st->status) return;
+  const u64 n = st->candidates;
+  for (u64 c = blockIdx.x; c < n; c += gridDim.x) {
+    if (threadIdx.x) continue;
+    BitIn r;
+    r.init(body, len, cand[c]);
+    u64 produced = 0;
+    u32 blocks = 0, status = 0, final_block = 0, next = kNone;
+    for (;;) {
+      u64 size;
+      status = describe_block(r, sh.tables, out_size, final_block, size);
+      ++blocks;
+      produced += size;
+      if (status) break;
+      if (produced > out_size) { status = kOutputOverflow; break; }
+      if (final_block) break;
+      const u64 pos = r.pos;
+      const u64 idx = lower_bound(cand, n, pos);
+      if (idx < n && cand[idx] == pos) { next = u32(idx); break; }
+      // A dynamic header here failed validation: the exact walk reports it.
+      BitIn h;
+      h.init(body, len, pos);
+      u32 f, type;
+      if (h.take(1, f) && h.take(2, type) && type == 2) { status = kUndiscovered; break; }
+      if (blocks >= kMaxBlocks) { status = kBlockCapacity; break; }
+    }
+    seg_end[c] = r.pos;
+    seg_size[c] = produced;
+    seg_blocks[c] = blocks;
+    seg_next[c] = next;
+    seg_flags[c] = status | (final_block ? 0x80000000u : 0u);
+  }
+}
+
+// One 1024-thread workgroup: path from candidate 0, output prefixes and
+// acceptance of the whole chain.
+__global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, const u64* seg_end,
+                                                const u64* seg_size, const u32* seg_blocks,
+                                                const u32* seg_next, const u32* seg_flags,
+                                                u32* exit_node, u64 len,
+                                                u64 out_size, u32 max_blocks, Segment* acc) {
+  __shared__ u32 entry[1024];
+  __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
+  __shared__ u32 last_node;
+  __shared__ u32 ok;
+  if (st->status) return;
+  const u32 t = threadIdx.x;
+  const u64 n = st->candidates;
+  const u64 per = (n + 1023) / 1024;
+  const u64 lo = min<u64>(n, u64(t) * per), hi = min<u64>(n, lo + per);
+  // 1. exits: first node outside [lo, hi) reached from each node.
+  for (u64 c = hi; c-- > lo;) {
+    const u32 nx = seg_next[c];
+    exit_node[c] = (nx == kNone || nx >= hi) ? nx : exit_node[nx];
+  }
+  entry[t] = kNone;
+  __syncthreads();
+  // 2. walk ranges from node 0.
+  if (!t) {
+    u32 cur = 0;
+    u32 last = 0;
+    while (cur != kNone) {
+      entry[per ? u32(cur / per) : 0] = cur;
+      last = cur;
+      cur = exit_node[cur];
+    }
+    last_node = last;
+  }
+  __syncthreads();
+  // 3. mark path nodes inside each range and sum their sizes.
+  u64 s = 0, b = 0, k = 0;
+  u32 cur = entry[t];
+  while (cur != kNone && cur < hi) {
+    s += seg_size[cur];
+    b += seg_blocks[cur];
+    ++k;
+    cur = seg_next[cur];
+  }
+  psize[t] = s;
+  pblocks[t] = b;
+  pcount[t] = k;
+  __syncthreads();
+  for (u32 off = 1; off < 1024; off <<= 1) {
+    const u64 xs = t >= off ? psize[t - off] : 0ull;
+    const u64 xb = t >= off ? pblocks[t - off] : 0ull;
+    const u64 xk = t >= off ? pcount[t - off] : 0ull;
+    __syncthreads();
+    psize[t] += xs;
+    pblocks[t] += xb;
+    pcount[t] += xk;
+    __syncthreads();
+  }
+  if (!t) {
+    // The path's last node: follow next pointers inside the last entered range.
+    u32 z = last_node;
+    while (seg_next[z] != kNone) z = seg_next[z];
+    const u32 flags = seg_flags[z];
+    const u64 total = psize[1023], blocks = pblocks[1023], count = pcount[1023];
+    const bool good = (flags & 0x7fffffffu) == 0 && (flags & 0x80000000u) && total == out_size &&
+                      blocks <= max_blocks && (seg_end[z] + 7) / 8 == len;
+    ok = good ? 1u : 0u;
+    st->chain_ok = ok;
+    st->accepted = good ? count : 0;
+  }
+  __syncthreads();
+  if (!ok) return;
+  // 4. write accepted segments in order.
+  u64 offset = psize[t] - s, index = pcount[t] - k;
+  cur = entry[t];
+  while (cur != kNone && cur < hi) {
+    acc[index].start = cand[cur];
+    acc[index].end = seg_end[cur];
+    acc[index].prefix = offset;
+    acc[index].size = seg_size[cur];
+    offset += seg_size[cur];
+    ++index;
+    cur = seg_next[cur];
+  }
+}
+
+namespace {
+struct WalkShared {
+  DecodeTables tables;
+  u8 lut[128];
+};
+}  // namespace
+
+// Exact serial walk (the reference's select_chain precedence); runs only when
+// the fast chain did not accept the stream.  On success it rebuilds the
+// accepted list one block per entry.
+__global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, State* st,
+                                                   u64 out_size, u32 max_blocks, Segment* acc) {
+  __shared__ WalkShared sh;
+  if (st->status || st->chain_ok || threadIdx.x) return;
+  u64 next = 0, output = 0, n = 0;
+  u32 status = 0;
+  for (;;) {
+    if (n >= max_blocks) { status = kBlockCapacity; break; }
+    BitIn h;
+    h.init(body, len, next);
+    u32 f, type;
+    if (!h.take(1, f) || !h.take(2, type)) { status = kTruncated; break; }
+    if (type == 3) { status = kReservedBlock; break; }
+    u64 limit = out_size - output;
+    if (next == 0 || type == 2) {
+      if (next && !dynamic_header_valid(body, len, next, sh.lut)) { status = kUndiscovered; break; }
+      limit = out_size;
+    }
+    BitIn r;
+    r.init(body, len, next);
+    u32 final_block;
+    u64 size;
+    status = describe_block(r, sh.tables, limit, final_block, size);
+    if (status) break;
+    const u64 end = r.pos;
+    if (end <= next || end > len * 8) { status = kExtent; break; }
+    if (size > out_size - output) { status = kOutputOverflow; break; }
+    acc[n].start = next;
+    acc[n].end = end;
+    acc[n].prefix = output;
+    acc[n].size = size;
+    ++n;
+    output += size;
+    next = end;
+    if (final_block) {
+      if (output != out_size) status = kSizeMismatch;
+      else if ((next + 7) / 8 != len) status = kExtent;
+      break;
+    }
+  }
+  st->status = status;
+  st->accepted = status ? 0 : n;
+}
+
+namespace {
+
+struct EmitShared {
+  DecodeTables tables;
+  u32 action;
+  u32 error;
+  u64 begin, length, distance, src;
+  u32 done;
+};
+
+__device__ __forceinline__ bool bit_get(const u32* bits, u64 i) {
+  const u32 w = __hip_atomic_load(bits + (i >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (w >> (i & 31)) & 1u;
+}
+__device__ __forceinline__ void bit_set(u32* bits, u64 i) {
+  atomicOr(bits + (i >> 5), 1u << (i & 31));
+}
+
+// Copies one output byte from `src` to `dst` inside a segment starting at
+// `seg`; sources outside the segment or still unresolved make the byte
+// unresolved.  Returns true when the byte was queued.
+__device__ __forceinline__ bool copy_byte(u8* out, u32* roots, u32* unres, u64 seg, u64 dst,
+                                          u64 src) {
+  if (src < seg) {
+    roots[dst] = u32(src);
+    bit_set(unres, dst);
+    return true;
+  }
+  if (bit_get(unres, src)) {
+    roots[dst] = roots[src];
+    bit_set(unres, dst);
+    return true;
+  }
+  out[dst] = out[src];
+  return false;
+}
+
+// Wave-aggregated append of positions to the unresolved list.
+__device__ __forceinline__ void append_unresolved(bool flag, u64 pos, u32* list, u64* count,
+                                                  u64 capacity) {
+  const u64 ballot = __ballot(flag);
+  if (!ballot) return;
+  const u32 lane = threadIdx.x & 63;
+  const u32 leader = __builtin_ctzll(ballot);
+  u64 base = 0;
+  if (lane == leader) base = atomicAdd(reinterpret_cast<unsigned long long*>(count), __popcll(ballot));
+  base = __shfl(base, leader, 64);
+  if (flag) {
+    const u64 at = base + __popcll(ballot & ((1ull << lane) - 1));
+    if (at < capacity) list[at] = u32(pos);
+  }
+}
+
+}  // namespace
+
+// One wave per accepted segment: lane 0 parses, the wave copies stored
+// payloads and long matches.  Output positions are absolute.
+__global__ __launch_bounds__(64) void g_emit(const u8* body, u64 len, State* st, const Segment* acc,
+                                             u8* out, u32* roots, u32* unres, u32* list,
+                                             u64 list_capacity) {
+  __shared__ EmitShared sh;
+  if (st->status) return;
+  const u32 lane = threadIdx.x;
+  const u64 segments = st->accepted;
+  const u32 window = st->window;
+  for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
+    const Segment seg = acc[si];
+    // Lane-0 parser state.
+    BitIn r;
+    u64 produced = 0;
+    u32 error = 0, final_block = 0;
+    bool need_header = true, complete = false;
+    if (!lane) r.init(body, len, seg.start);
+    while (true) {
+      if (!lane) {
+        u32 action = 0;
+        while (!error && !complete) {
+          if (need_header) {
+            // Deterministic re-parse of a described segment: it ends exactly at seg.end.
+            if (r.pos >= seg.end) { complete = true; break; }
+            u32 type;
+            if (!r.take(1, final_block) || !r.take(2, type) || type == 3) { error = kExtent; break; }
+            if (type == 0) {
+              r.seek((r.pos + 7) & ~u64(7));
+              u32 nlen, comp;
+              if (!r.take(16, nlen) || !r.take(16, comp) || u64(nlen) * 8 > r.avail()) {
+                error = kExtent;
+                break;
+              }
+              if (nlen > seg.size - produced) { error = kExtent; break; }
+              sh.begin = seg.prefix + produced;
+              sh.length = nlen;
+              sh.src = r.pos >> 3;
+              produced += nlen;
+              r.seek(r.pos + u64(nlen) * 8);
+              if (r.pos >= seg.end) complete = true;
+              action = 2;
+              break;
+            }
+            const u32 terr = type == 1 ? build_fixed_tables(sh.tables) : build_dynamic_tables(sh.tables, r);
+            if (terr) { error = kExtent; break; }
+            need_header = false;
+          }
+          u32 lit = 0, length = 0, distance = 0;
+          if (decode_token(sh.tables, r, 32768u, lit, length, distance)) { error = kExtent; break; }
+          if (!length) {
+            need_header = true;
+            continue;
+          }
+          const u64 dst = seg.prefix + produced;
+          // Described and emitted parses agree; the guard keeps writes inside
+          // the segment even if they did not.
+          if (length > seg.size - produced) { error = kExtent; break; }
+          if (!distance) {
+            out[dst] = u8(lit);
+            ++produced;
+            continue;
+          }
+          if (distance > window || distance > dst) { error = kBadDistance; break; }
+          if (length >= kCoopMatch) {
+            sh.begin = dst;
+            sh.length = length;
+            sh.distance = distance;
+            produced += length;
+            action = 1;
+            break;
+          }
+          for (u32 j = 0; j < length; ++j) {
+            const u64 src = dst - distance + (j % distance);
+            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src)) {
+              const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), 1ull);
+              if (at < list_capacity) list[at] = u32(dst + j);
+            }
+          }
+          produced += length;
+        }
+        sh.action = action;
+        sh.error = error;
+      }
+      __syncthreads();
+      const u32 action = sh.action;
+      if (!action) break;
+      const u64 begin = sh.begin, length = sh.length;
+      if (action == 1) {
+        const u64 d = sh.distance;
+        for (u64 j0 = 0; j0 < length; j0 += kWave) {
+          const u64 j = j0 + lane;
+          bool queued = false;
+          if (j < length) queued = copy_byte(out, roots, unres, seg.prefix, begin + j, begin - d + (j % d));
+          append_unresolved(queued, begin + j, list, &st->unresolved[0], list_capacity);
+        }
+      } else {
+        for (u64 j = lane; j < length; j += kWave) out[begin + j] = body[sh.src + j];
+      }
+      __syncthreads();
+    }
+    if (!lane && sh.error) atomicMax(&st->emit_status, sh.error);
+    __syncthreads();
+  }
+}
+
+// One pointer-jumping round over the unresolved list `round & 1`.
+__global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
+                                                 u32* bits1, u32* list0, u32* list1, u32 round,
+                                                 u64 capacity) {
+  if (st->status || st->emit_status) return;
+  const u32 cur = round & 1, nxt = cur ^ 1;
+  const u64 count = min<u64>(st->unresolved[cur], capacity);
+  if (!count) return;
+  const u32* bits = cur ? bits1 : bits0;
+  u32* next_bits = cur ? bits0 : bits1;
+  const u32* list = cur ? list1 : list0;
+  u32* next_list = cur ? list0 : list1;
+  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
+  const u64 stride = u64(gridDim.x) * blockDim.x;
+  const u64 rounds_total = (count + stride - 1) / stride;
+  for (u64 it = 0; it < rounds_total; ++it) {
+    const u64 i = tid + it * stride;
+    bool keep = false;
+    u32 u = 0;
+    if (i < count) {
+      u = list[i];
+      const u32 r = roots[u];
+      const bool r_unres = (__hip_atomic_load(bits + (r >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> (r & 31)) & 1u;
+      if (!r_unres) {
+        out[u] = out[r];
+        atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
+      } else {
+        roots[u] = roots[r];
+        atomicOr(next_bits + (u >> 5), 1u << (u & 31));
+        keep = true;
+      }
+    }
+    append_unresolved(keep, u, next_list, &st->unresolved[nxt], capacity);
+  }
+}
+
+// Resets the next round's list length before round `round` runs.
+__global__ __launch_bounds__(1) void g_resolve_reset(State* st, u32 round) {
+  st->unresolved[(round & 1) ^ 1] = 0;
+}
+
+// Adler-32 partial sums over 4096-byte tiles, accumulated into the state.
+__global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n) {
+  __shared__ u64 rs[256], rw[256];
+  if (st->status || st->emit_status) return;
+  const u64 tiles = (n + 4095) / 4096;
+  u64 acc_s = 0, acc_w = 0;
+  for (u64 tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const u64 a = tile * 4096;
+    u32 s = 0, l = 0;
+    for (u32 j = threadIdx.x; j < 4096 && a + j < n; j += 256) {
+      const u32 v = out[a + j];
+      s += v;
+      l += j * v;
+    }
+    rs[threadIdx.x] = s;
+    rw[threadIdx.x] = l;
+    __syncthreads();
+    for (u32 off = 128; off; off >>= 1) {
+      if (threadIdx.x < off) {
+        rs[threadIdx.x] += rs[threadIdx.x + off];
+        rw[threadIdx.x] += rw[threadIdx.x + off];
+      }
+      __syncthreads();
+    }
+    if (!threadIdx.x) {
+      const u64 S = rs[0] % kAdlerMod, L = rw[0] % kAdlerMod;
+      // sum over tile of (n - i) x_i = (n - a) S - L
+      const u64 w = (((n - a) % kAdlerMod) * S + kAdlerMod - L) % kAdlerMod;
+      acc_s += S;
+      acc_w += w;
+    }
+    __syncthreads();
+  }
+  if (!threadIdx.x && (acc_s || acc_w)) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_s), acc_s % kAdlerMod);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_w), acc_w % kAdlerMod);
+  }
+}
+
+__global__ __launch_bounds__(1) void g_finish(State* st, u64 n, u32 rounds, u32* meta) {
+  u32 status = st->status;
+  if (!status) status = st->emit_status;
+  // References still unresolved after every pointer-jumping round.
+  if (!status && st->unresolved[rounds & 1]) status = kReferenceDepth;
+  if (!status) {
+    const u32 a = u32((st->adler_s + 1) % kAdlerMod);
+    const u32 b = u32((st->adler_w + n) % kAdlerMod);
+    if (((b << 16) | a) != st->wanted) status = kAdlerMismatch;
+  }
+  st->status = status;
+  meta[0] = status;
+  meta[1] = 0;
+}
+
+// Zero the output unless the stream decoded (status 0) or only its checksum failed.
+__global__ __launch_bounds__(256) void g_zero_on_failure(const State* st, u8* out, u64 n) {
+  const u32 status = st->status;
+  if (!status || status == kAdlerMismatch) return;
+  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
+  const u64 stride = u64(gridDim.x) * blockDim.x;
+  for (u64 i = tid; i < n; i += stride) out[i] = 0;
+}
+
+namespace {
+u32 clamp_grid(u64 want, u32 cap) { return u32(want < 1 ? 1 : (want > cap ? cap : want)); }
+
+#define HZ_TRY(expr)                          \
+  do {                                        \
+    hipError_t _e = (expr);                   \
+    if (_e != hipSuccess) return _e;          \
+  } while (0)
+}  // namespace
+
+hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
+                               u8* out, u64 out_size, u32 max_candidates, u32 max_blocks,
+                               u32* meta) {
+  const u8* body = in + 2;
+  const u64 len = in_size - 6;
+  State* st = nullptr;
+  HZ_TRY(scratch.alloc(&st, 1));
+  hipLaunchKernelGGL(g_frame, dim3(1), dim3(1), 0, stream, in, in_size, st);
+  HZ_TRY(hipGetLastError());
+
+  // Discovery.
+  const u64 groups = len ? (len + kDiscRange - 1) / kDiscRange : 1;
+  u32* wg_count = nullptr;
+  u64 *wg_list = nullptr, *wg_offset = nullptr, *cand = nullptr;
+  HZ_TRY(scratch.alloc(&wg_count, groups));
+  HZ_TRY(scratch.alloc(&wg_list, groups * kDiscCap));
+  HZ_TRY(scratch.alloc(&wg_offset, groups));
+  const u64 cand_capacity = u64(max_candidates) + 1;
+  HZ_TRY(scratch.alloc(&cand, cand_capacity));
+  hipLaunchKernelGGL(g_discover, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
+                     wg_count, wg_list);
+  HZ_TRY(hipGetLastError());
+  hipLaunchKernelGGL(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset,
+                     groups, u64(max_candidates));
+  HZ_TRY(hipGetLastError());
+  hipLaunchKernelGGL(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len,
+                     st, wg_count, wg_list, wg_offset, cand);
+  HZ_TRY(hipGetLastError());
+
+  // Describe every candidate's segment.
+  u64 *seg_end = nullptr, *seg_size = nullptr;
+  u32 *seg_blocks = nullptr, *seg_next = nullptr, *seg_flags = nullptr, *exit_node = nullptr;
+  HZ_TRY(scratch.alloc(&seg_end, cand_capacity));
+  HZ_TRY(scratch.alloc(&seg_size, cand_capacity));
+  HZ_TRY(scratch.alloc(&seg_blocks, cand_capacity));
+  HZ_TRY(scratch.alloc(&seg_next, cand_capacity));
+  HZ_TRY(scratch.alloc(&seg_flags, cand_capacity));
+  HZ_TRY(scratch.alloc(&exit_node, cand_capacity));
+  hipLaunchKernelGGL(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kWave), 0, stream, body,
+                     len, cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags);
+  HZ_TRY(hipGetLastError());
+
+  // Chain selection, then the exact walk if the fast chain declined.
+  Segment* acc = nullptr;
+  HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
+  hipLaunchKernelGGL(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size,
+                     seg_blocks, seg_next, seg_flags, exit_node, len, out_size, max_blocks,
+                     acc);
+  HZ_TRY(hipGetLastError());
+  hipLaunchKernelGGL(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size,
+                     max_blocks, acc);
+  HZ_TRY(hipGetLastError());
+
+  // Emission and cross-segment resolution.
+  const u64 words = (out_size + 31) / 32 + 1;
+  u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr, *list0 = nullptr, *list1 = nullptr;
+  const u64 list_capacity = out_size ? out_size : 1;
+  HZ_TRY(scratch.alloc(&roots, list_capacity));
+  HZ_TRY(scratch.alloc(&bits0, words));
+  HZ_TRY(scratch.alloc(&bits1, words));
+  HZ_TRY(scratch.alloc(&list0, list_capacity));
+  HZ_TRY(scratch.alloc(&list1, list_capacity));
+  HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
+  HZ_TRY(launch_fill(stream, bits1, 0, words * 4));
+  hipLaunchKernelGGL(g_emit, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
+                     st, acc, out, roots, bits0, list0, list_capacity);
+  HZ_TRY(hipGetLastError());
+  // Pointer jumping halves every reference chain per round; chains span at
+  // most max_blocks segments.
+  u32 rounds = 2;
+  for (u64 span = 1; span < u64(max_blocks); span <<= 1) ++rounds;
+  for (u32 round = 0; round < rounds; ++round) {
+    hipLaunchKernelGGL(g_resolve_reset, dim3(1), dim3(1), 0, stream, st, round);
+    HZ_TRY(hipGetLastError());
+    hipLaunchKernelGGL(g_resolve, dim3(1024), dim3(256), 0, stream, st, out, roots, bits0, bits1,
+                       list0, list1, round, list_capacity);
+    HZ_TRY(hipGetLastError());
+  }
+  hipLaunchKernelGGL(g_adler, dim3(clamp_grid((out_size + 4095) / 4096, 8192)), dim3(256), 0, stream,
+                     st, out, out_size);
+  HZ_TRY(hipGetLastError());
+  hipLaunchKernelGGL(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, rounds, meta);
+  HZ_TRY(hipGetLastError());
+  hipLaunchKernelGGL(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
+                     stream, st, out, out_size);
+  return hipGetLastError();
+}
+
 }  // namespace hz
