@@ -318,6 +318,26 @@ extern "C" int HipZlibTrimWorkspacePool(int device) {
   return int(hipMemPoolTrimTo(pool, 0));
 }
 
+namespace hz {
+std::string profile_collect(bool reset);
+void profile_enable(bool on);
+}  // namespace hz
+
+extern "C" int HipZlibProfileEnable(int enabled) {
+  hz::profile_enable(enabled != 0);
+  return 0;
+}
+
+extern "C" uint64_t HipZlibProfileCollect(char* buffer, uint64_t capacity, int reset) {
+  const std::string text = hz::profile_collect(reset != 0);
+  if (buffer && capacity) {
+    const uint64_t n = std::min<uint64_t>(capacity - 1, text.size());
+    std::copy(text.data(), text.data() + n, buffer);
+    buffer[n] = 0;
+  }
+  return text.size();
+}
+
 extern "C" const char* HipZlibErrorString(int code) {
   if (code == HIP_ZLIB_INVALID_ARGUMENT) return g_last_error.c_str();
   return hipGetErrorString(hipError_t(code));

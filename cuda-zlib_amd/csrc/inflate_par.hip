@@ -846,7 +846,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 len = in_size - 6;
   State* st = nullptr;
   HZ_TRY(scratch.alloc(&st, 1));
-  hipLaunchKernelGGL(g_frame, dim3(1), dim3(1), 0, stream, in, in_size, st);
+  HZ_LAUNCH(g_frame, dim3(1), dim3(1), 0, stream, in, in_size, st);
   HZ_TRY(hipGetLastError());
 
   // Discovery.
@@ -858,13 +858,13 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&wg_offset, groups));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
-  hipLaunchKernelGGL(g_discover, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
+  HZ_LAUNCH(g_discover, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
                      wg_count, wg_list);
   HZ_TRY(hipGetLastError());
-  hipLaunchKernelGGL(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset,
+  HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset,
                      groups, u64(max_candidates));
   HZ_TRY(hipGetLastError());
-  hipLaunchKernelGGL(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len,
+  HZ_LAUNCH(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len,
                      st, wg_count, wg_list, wg_offset, cand);
   HZ_TRY(hipGetLastError());
 
@@ -877,18 +877,18 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&seg_next, cand_capacity));
   HZ_TRY(scratch.alloc(&seg_flags, cand_capacity));
   HZ_TRY(scratch.alloc(&exit_node, cand_capacity));
-  hipLaunchKernelGGL(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kWave), 0, stream, body,
+  HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kWave), 0, stream, body,
                      len, cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags);
   HZ_TRY(hipGetLastError());
 
   // Chain selection, then the exact walk if the fast chain declined.
   Segment* acc = nullptr;
   HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
-  hipLaunchKernelGGL(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size,
+  HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size,
                      seg_blocks, seg_next, seg_flags, exit_node, len, out_size, max_blocks,
                      acc);
   HZ_TRY(hipGetLastError());
-  hipLaunchKernelGGL(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size,
+  HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size,
                      max_blocks, acc);
   HZ_TRY(hipGetLastError());
 
@@ -903,7 +903,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&list1, list_capacity));
   HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
   HZ_TRY(launch_fill(stream, bits1, 0, words * 4));
-  hipLaunchKernelGGL(g_emit, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
+  HZ_LAUNCH(g_emit, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
                      st, acc, out, roots, bits0, list0, list_capacity);
   HZ_TRY(hipGetLastError());
   // Pointer jumping halves every reference chain per round; chains span at
@@ -911,18 +911,18 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   u32 rounds = 2;
   for (u64 span = 1; span < u64(max_blocks); span <<= 1) ++rounds;
   for (u32 round = 0; round < rounds; ++round) {
-    hipLaunchKernelGGL(g_resolve_reset, dim3(1), dim3(1), 0, stream, st, round);
+    HZ_LAUNCH(g_resolve_reset, dim3(1), dim3(1), 0, stream, st, round);
     HZ_TRY(hipGetLastError());
-    hipLaunchKernelGGL(g_resolve, dim3(1024), dim3(256), 0, stream, st, out, roots, bits0, bits1,
+    HZ_LAUNCH(g_resolve, dim3(1024), dim3(256), 0, stream, st, out, roots, bits0, bits1,
                        list0, list1, round, list_capacity);
     HZ_TRY(hipGetLastError());
   }
-  hipLaunchKernelGGL(g_adler, dim3(clamp_grid((out_size + 4095) / 4096, 8192)), dim3(256), 0, stream,
+  HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 4095) / 4096, 8192)), dim3(256), 0, stream,
                      st, out, out_size);
   HZ_TRY(hipGetLastError());
-  hipLaunchKernelGGL(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, rounds, meta);
+  HZ_LAUNCH(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, rounds, meta);
   HZ_TRY(hipGetLastError());
-  hipLaunchKernelGGL(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
+  HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
                      stream, st, out, out_size);
   return hipGetLastError();
 }

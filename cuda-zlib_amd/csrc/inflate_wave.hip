@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out
 
 hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
                                  u64 out_size, u32 max_blocks, u32* meta) {
-  hipLaunchKernelGGL(inflate_single_kernel, dim3(1), dim3(kWave), 0, stream, in, in_size, out,
+  HZ_LAUNCH(inflate_single_kernel, dim3(1), dim3(kWave), 0, stream, in, in_size, out,
                      out_size, max_blocks, meta);
   return hipGetLastError();
 }
@@ -233,7 +233,7 @@ hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const
                                 u32 count, u32 max_blocks, u32* meta, const u32* encoded) {
   if (!count) return hipSuccess;
   const u32 grid = count < 65536u ? count : 65536u;
-  hipLaunchKernelGGL(inflate_batch_kernel, dim3(grid), dim3(kWave), 0, stream, in, out, files, count,
+  HZ_LAUNCH(inflate_batch_kernel, dim3(grid), dim3(kWave), 0, stream, in, out, files, count,
                      max_blocks, meta, encoded);
   return hipGetLastError();
 }

@@ -17,7 +17,26 @@ struct BatchFile {
   u64 out_size;
 };
 
-// util.hip
+// util.hip: optional per-kernel timing.  When enabled, every launch made
+// through HZ_LAUNCH is bracketed by HIP events on its stream; totals are read
+// back (after the caller synchronises) through the C ABI.
+bool profiling_enabled();
+void profile_record(const char* name, hipEvent_t start, hipEvent_t stop);
+
+#define HZ_LAUNCH(kernel, grid, block, shmem, stream, ...)                       \
+  do {                                                                         \
+    hipEvent_t hz_start_ = nullptr, hz_stop_ = nullptr;                        \
+    const bool hz_prof_ = ::hz::profiling_enabled();                           \
+    if (hz_prof_ && hipEventCreate(&hz_start_) == hipSuccess &&                \
+        hipEventCreate(&hz_stop_) == hipSuccess)                               \
+      hipEventRecord(hz_start_, stream);                                       \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);       \
+    if (hz_prof_ && hz_stop_) {                                                \
+      hipEventRecord(hz_stop_, stream);                                        \
+      ::hz::profile_record(#kernel, hz_start_, hz_stop_);                      \
+    }                                                                          \
+  } while (0)
+
 hipError_t launch_fill(hipStream_t stream, void* dst, u8 value, u64 bytes);
 hipError_t launch_set_meta(hipStream_t stream, u32* meta, u32 first, u32 second);
 hipError_t launch_set_meta_rows(hipStream_t stream, u32* meta, u64 rows, u32 first, u32 second);

@@ -32,6 +32,8 @@ SIGNATURES = {
     "HipZlibWorkspacePoolStats": [ctypes.c_int, ctypes.POINTER(_U64)],
     "HipZlibTrimWorkspacePool": [ctypes.c_int],
     "HipZlibErrorString": [ctypes.c_int],
+    "HipZlibProfileEnable": [ctypes.c_int],
+    "HipZlibProfileCollect": [ctypes.c_char_p, _U64, ctypes.c_int],
 }
 
 
@@ -47,7 +49,8 @@ def _bind(library):
     for name, args in SIGNATURES.items():
         function = getattr(library, name)
         function.argtypes = args
-        function.restype = ctypes.c_char_p if name == "HipZlibErrorString" else ctypes.c_int
+        function.restype = (ctypes.c_char_p if name == "HipZlibErrorString" else
+                            _U64 if name == "HipZlibProfileCollect" else ctypes.c_int)
     return library
 
 
@@ -83,3 +86,15 @@ def check(library, code):
 def int64_array(values):
     array = (ctypes.c_int64 * max(1, len(values)))(*values)
     return array
+
+
+def profile_collect(library, reset=True):
+    """{kernel: (launches, total_ms)} recorded while profiling was enabled."""
+    size = library.HipZlibProfileCollect(None, 0, 0)
+    buffer = ctypes.create_string_buffer(int(size) + 1)
+    library.HipZlibProfileCollect(buffer, len(buffer), int(reset))
+    result = {}
+    for line in buffer.value.decode().splitlines():
+        name, count, ms = line.split()
+        result[name] = (int(count), float(ms))
+    return result

@@ -69,6 +69,13 @@ int HipZlibSetWorkspaceRetention(uint64_t bytes);
 int HipZlibWorkspacePoolStats(int device, uint64_t* stats);
 int HipZlibTrimWorkspacePool(int device);
 
+/* Measurement hooks.  While enabled, every kernel the library launches is
+ * bracketed by HIP events on the caller's stream.  Collect writes lines
+ * "kernel launches total_ms" (after the caller synchronised the stream) and
+ * returns the full text length; reset != 0 discards the records. */
+int HipZlibProfileEnable(int enabled);
+uint64_t HipZlibProfileCollect(char* buffer, uint64_t capacity, int reset);
+
 /* Text for a return code of any entry point above (thread-local for -1). */
 const char* HipZlibErrorString(int code);
 
