@@ -140,10 +140,18 @@ struct BitIn {
 template <int N, int P>
 struct HuffTable {
   u16 count[16];
+  u16 offs[16];   // build scratch (kept in the table so builds use no private arrays)
   u16 symbols[N];
   u32 primary[1 << P];
   u32 maximum;
 };
+
+// Code-length alphabet order (RFC 1951 3.2.7), 5 bits per entry, packed so
+// device code indexes registers rather than a private array.
+__host__ __device__ __forceinline__ u32 cl_order(u32 i) {
+  return i < 12 ? u32((0x22caa324e804a30ull >> (5 * i)) & 31)
+                : u32((0x3c2e1346cull >> (5 * (i - 12))) & 31);
+}
 
 // Build from code lengths.  empty_ok: all-zero lengths allowed (distance tree).
 // single_ok: an incomplete code consisting of one length-1 code is allowed.
@@ -168,11 +176,10 @@ __device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_
     if (left < 0) return kBadTree;
   }
   if (left && !(single_ok && t.maximum == 1 && t.count[1] == 1)) return kBadTree;
-  u16 offs[16];
-  offs[1] = 0;
-  for (u32 l = 1; l < 15; ++l) offs[l + 1] = offs[l] + t.count[l];
+  t.offs[1] = 0;
+  for (u32 l = 1; l < 15; ++l) t.offs[l + 1] = t.offs[l] + t.count[l];
   for (u32 i = 0; i < n; ++i)
-    if (lens[i]) t.symbols[offs[lens[i]]++] = u16(i);
+    if (lens[i]) t.symbols[t.offs[lens[i]]++] = u16(i);
   for (u32 i = 0; i < (1u << P); ++i) t.primary[i] = 0;
   u32 code = 0, index = 0;
   for (u32 l = 1; l <= u32(P); ++l) {
@@ -235,22 +242,60 @@ __device__ inline u32 build_fixed_tables(DecodeTables& t) {
   return huff_build(t.dd, t.lens, 32, false, true, 15);
 }
 
-// Dynamic block header (RFC 1951 3.2.7), reader positioned after BTYPE.
-// Error order follows the reference's dynamic_tables (_decode_kernels.py:240-287).
-__device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
+// Code-length code table from 19 packed 3-bit lengths (symbol s at bits 3s):
+// counts and next codes live in packed registers, so no private arrays.
+// The code must be complete (RFC 1951 allows no other).  Returns 0 or kBadTree.
+__device__ inline u32 build_cl_table(HuffTable<19, 7>& t, u64 pack) {
+  u64 cnt = 0;  // byte l = number of symbols of length l
+  for (u32 s = 0; s < 19; ++s) cnt += 1ull << (8 * ((pack >> (3 * s)) & 7));
+  u32 kraft = 0, maximum = 0;
+  for (u32 l = 1; l < 8; ++l) {
+    const u32 c = u32(cnt >> (8 * l)) & 0xff;
+    kraft += c << (7 - l);
+    if (c) maximum = l;
+  }
+  for (u32 l = 0; l < 16; ++l) t.count[l] = l < 8 ? u16((cnt >> (8 * l)) & 0xff) : 0;
+  t.maximum = maximum;
+  if (kraft != 128) return kBadTree;
+  u64 next = 0, offs = 0;  // byte l: next code / next symbol slot for length l
+  u32 code = 0, slot = 0;
+  for (u32 l = 1; l < 8; ++l) {
+    code = (code + (l > 1 ? u32(cnt >> (8 * (l - 1))) & 0xff : 0u)) << 1;
+    next |= u64(code) << (8 * l);
+    offs |= u64(slot) << (8 * l);
+    slot += u32(cnt >> (8 * l)) & 0xff;
+  }
+  for (u32 s = 0; s < 19; ++s) {
+    const u32 l = (pack >> (3 * s)) & 7;
+    if (!l) continue;
+    const u32 c = u32(next >> (8 * l)) & 0xff;
+    next += 1ull << (8 * l);
+    t.symbols[u32(offs >> (8 * l)) & 0xff] = u16(s);
+    offs += 1ull << (8 * l);
+    const u32 e = (s << 16) | l;
+    for (u32 k = bit_reverse(c, l); k < 128; k += 1u << l) t.primary[k] = e;
+  }
+  return kOk;
+}
+
+// Dynamic block header (RFC 1951 3.2.7) up to the code lengths: reads HLIT,
+// HDIST, HCLEN and the code-length code, then decodes the nl + nd lengths into
+// t.lens.  Reader positioned after BTYPE.  Error order follows the reference's
+// dynamic_tables (_decode_kernels.py:240-283).
+__device__ inline u32 parse_dynamic_lengths(DecodeTables& t, BitIn& r, u32& nl, u32& nd) {
   u32 hlit, hdist, hclen;
   if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return kTruncated;
-  const u32 nl = hlit + 257, nd = hdist + 1, nc = hclen + 4;
+  nl = hlit + 257;
+  nd = hdist + 1;
+  const u32 nc = hclen + 4;
   if (nl > 286) return kBadTree;
-  const u8 order[19] = {16, 17, 18, 0, 8, 7, 9, 6, 10, 5, 11, 4, 12, 3, 13, 2, 14, 1, 15};
-  u8 clens[19];
-  for (u32 i = 0; i < 19; ++i) clens[i] = 0;
+  u64 pack = 0;
   for (u32 i = 0; i < nc; ++i) {
     u32 v;
     if (!r.take(3, v)) return kTruncated;
-    clens[order[i]] = u8(v);
+    pack |= u64(v) << (3 * cl_order(i));
   }
-  u32 err = huff_build(t.cl, clens, 19, false, false, 7);
+  u32 err = build_cl_table(t.cl, pack);
   if (err) return err;
   u32 i = 0;
   while (i < nl + nd) {
@@ -277,9 +322,108 @@ __device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
     for (u32 j = 0; j < repeat; ++j) t.lens[i++] = u8(value);
   }
   if (!t.lens[256]) return kBadTree;
+  return kOk;
+}
+
+// Dynamic block header (RFC 1951 3.2.7), reader positioned after BTYPE.
+__device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
+  u32 nl, nd;
+  u32 err = parse_dynamic_lengths(t, r, nl, nd);
+  if (err) return err;
   err = huff_build(t.ll, t.lens, nl, false, true, 15);
   if (err) return err;
   return huff_build(t.dd, t.lens + nl, nd, true, true, 15);
+}
+
+// Wave-cooperative table build for a 64-thread workgroup (one wavefront).
+// Length counts, per-length ranks and canonical codes come from ballots over
+// 64-symbol chunks; lane 0 only checks the Kraft sum over 15 lengths.  Same
+// validity rules and table contents as huff_build.  `scratch` holds >= 320
+// u16 in LDS (codes, then offsets/next codes); every lane must call it and
+// every lane gets the status.
+template <int N, int P>
+__device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_ok,
+                               bool single_ok, u32 limit, u16* scratch, u32* status) {
+  const u32 lane = threadIdx.x;
+  u16* codes = scratch;
+  u16* offs = scratch + 288;
+  u16* next = scratch + 304;
+  // Counts: lane l (< 16) accumulates the number of symbols of length l.
+  u32 cnt = 0;
+  for (u32 base = 0; base < n; base += 64) {
+    const u32 sym = base + lane;
+    const u32 l = sym < n ? lens[sym] : 16u;
+    for (u32 len = 0; len < 16; ++len) {
+      const u64 b = __ballot(l == len);
+      if (lane == len) cnt += __popcll(b);
+    }
+  }
+  if (lane < 16) t.count[lane] = u16(cnt);
+  __syncthreads();
+  if (!lane) {
+    u32 st = kOk, maximum = 0;
+    if (n > u32(N)) st = kBadTree;
+    for (u32 l = limit + 1; l < 16 && !st; ++l)
+      if (t.count[l]) st = kBadTree;
+    for (u32 l = 1; l <= limit && l < 16; ++l)
+      if (t.count[l]) maximum = l;
+    t.maximum = maximum;
+    if (!st && !maximum && !empty_ok) st = kBadTree;
+    if (!st && maximum) {
+      i32 left = 1;
+      for (u32 l = 1; l <= limit && !st; ++l) {
+        left = (left << 1) - i32(t.count[l]);
+        if (left < 0) st = kBadTree;
+      }
+      if (!st && left && !(single_ok && maximum == 1 && t.count[1] == 1)) st = kBadTree;
+    }
+    if (!st && maximum) {
+      offs[1] = 0;
+      for (u32 l = 1; l < 15; ++l) offs[l + 1] = u16(offs[l] + t.count[l]);
+      u32 code = 0;
+      next[1] = 0;
+      for (u32 l = 2; l < 16; ++l) {
+        code = (code + t.count[l - 1]) << 1;
+        next[l] = u16(code);
+      }
+    }
+    *status = st;
+  }
+  for (u32 i = lane; i < (1u << P); i += 64) t.primary[i] = 0;
+  __syncthreads();
+  const u32 st = *status;
+  if (!st && t.maximum) {
+    // Symbols in (length, symbol) order and canonical codes; lane l (< 16)
+    // carries the running count of length-l symbols seen in earlier chunks.
+    u32 running = 0;
+    for (u32 base = 0; base < n; base += 64) {
+      const u32 sym = base + lane;
+      const u32 l = sym < n ? lens[sym] : 0u;
+      u32 rank = 0, chunk = 0;
+      for (u32 len = 1; len < 16; ++len) {
+        const u64 b = __ballot(l == len);
+        if (l == len) rank = __popcll(b & ((1ull << lane) - 1));
+        if (lane == len) chunk = __popcll(b);
+      }
+      const u32 before = __shfl(running, l, 64);
+      if (l) {
+        t.symbols[offs[l] + before + rank] = u16(sym);
+        codes[sym] = u16(next[l] + before + rank);
+      }
+      running += chunk;
+    }
+  }
+  __syncthreads();
+  if (!st) {
+    for (u32 s = lane; s < n; s += 64) {
+      const u32 l = lens[s];
+      if (!l || l > u32(P)) continue;
+      const u32 e = (s << 16) | l;
+      for (u32 k = bit_reverse(codes[s], l); k < (1u << P); k += 1u << l) t.primary[k] = e;
+    }
+  }
+  __syncthreads();
+  return st;
 }
 
 // One literal/length token after the LL symbol.  Returns kOk and sets

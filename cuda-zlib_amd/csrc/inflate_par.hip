@@ -49,14 +49,110 @@ struct State {
   u32 pad;
   u64 unresolved[2]; // ping-pong list lengths for resolve rounds
   u64 adler_s, adler_w;
+  u64 recs_used;     // block records handed out by describe
+  u64 groups_used;   // 64-slot slice groups handed out by describe
 };
 
 struct Segment {
-  u64 start;   // bit offset of the first block
-  u64 end;     // bit offset after the last block
-  u64 prefix;  // output offset
-  u64 size;    // output bytes
+  u64 start;      // bit offset of the first block
+  u64 end;        // bit offset after the last block
+  u64 prefix;     // output offset
+  u64 size;       // output bytes
+  u32 rec_first;  // first block record, or kNone: emit serially
+  u32 rec_count;
 };
+
+// One block of a described segment; records of a segment are linked through
+// `next`.  A fixed/dynamic block's token range is split into `lanes` slices
+// held in linked groups of 64 slots: slice i of a group decodes tokens from
+// slice_entry[64 * group + i] up to the next slice's entry (the last slice
+// ends at the EOB) and writes at block output offset slice_off[64 * group + i].
+struct BlockRec {
+  u64 start;      // bit offset of the block header
+  u64 data;       // first token bit (stored: first payload bit)
+  u64 end;        // bit after the block
+  u64 size;       // output bytes
+  u32 type;
+  u32 lanes;      // slices (fixed/dynamic)
+  u32 group;      // first slice group
+  u32 next;       // next record of the segment, or kNone
+};
+
+constexpr u32 kStageBytes = 16384;                 // LDS bitstream window per wave
+constexpr u32 kStageMargin = 64;                   // bytes staged past the last slice
+constexpr u32 kStageWords = (kStageBytes + kStageMargin) / 4 + 2;
+constexpr u64 kMinSlice = 64;                      // bits; > longest token (48 bits)
+constexpr u64 kMaxSlice = (u64(kStageBytes) * 8) / 64;
+constexpr u32 kWindowSlots = 32;                   // token starts recorded per slice window
+
+// LDS copy of a bitstream range: words[] are consecutive aligned dwords of
+// the input; body bit `bit0` is the first bit of words[0] (mod 2^64).
+template <u32 W>
+struct StageT {
+  u32 words[W];
+  u64 bit0;
+  u32 count;
+};
+using Stage = StageT<kStageWords>;
+
+// Stage the body bytes covering bits [bit0, bit1) plus `margin` bytes into LDS
+// (capped at the body end and at the stage capacity).  Every thread of the
+// workgroup takes part.
+template <u32 W>
+__device__ void stage_range(const u8* body, u64 len, u64 bit0, u64 bit1, StageT<W>& sg,
+                            u64 margin = kStageMargin) {
+  const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+  const u64 first_word = (base + (bit0 >> 3)) >> 2;
+  u64 last_byte = (bit1 + 7) / 8 + margin;
+  if (last_byte > len) last_byte = len;
+  const u64 end_word = (base + last_byte + 3) >> 2;  // words holding body bytes only
+  u64 words = end_word > first_word ? end_word - first_word : 0;
+  if (words > W) words = W;
+  const u32* g = reinterpret_cast<const u32*>(first_word << 2);
+  for (u64 i = threadIdx.x; i < words; i += blockDim.x) sg.words[i] = g[i];
+  if (!threadIdx.x) {
+    sg.count = u32(words);
+    sg.bit0 = (first_word << 5) - (u64(base) << 3);  // body bit of word 0, mod 2^64
+  }
+}
+
+// Reader over staged words whose positions are body bits; bits outside the
+// staged words read as zero and avail() still reflects the real body end.
+template <u32 W>
+__device__ __forceinline__ BitIn staged_reader(const StageT<W>& sg, u64 len, u64 pos) {
+  BitIn r;
+  r.words = sg.words;
+  r.base_bit = u64(0) - sg.bit0;
+  r.total = len * 8;
+  r.wlimit = sg.count;
+  r.seek(pos);
+  return r;
+}
+
+// True if the staged words hold every byte of bits [bit0, bit1) plus margin
+// (or up to the body end).
+template <u32 W>
+__device__ __forceinline__ bool staged_covers(const StageT<W>& sg, const u8* body, u64 len,
+                                              u64 bit0, u64 bit1, u64 margin = kStageMargin) {
+  const u64 lo = sg.bit0, have = u64(sg.count) * 32;
+  u64 need_end = ((bit1 + 7) / 8 + margin) * 8;
+  if (need_end > len * 8) need_end = len * 8;
+  return bit0 >= lo && bit0 - lo < have && need_end - lo <= have;
+}
+
+// 64 bits of the body starting at bit `pos` from the stage (zeros outside).
+template <u32 W>
+__device__ __forceinline__ u64 staged_u64(const StageT<W>& sg, u64 pos) {
+  const u64 a = pos - sg.bit0;
+  const u64 w = a >> 5;
+  const u32 sh = u32(a & 31);
+  const u64 w0 = w < sg.count ? sg.words[w] : 0u;
+  const u64 w1 = w + 1 < sg.count ? sg.words[w + 1] : 0u;
+  const u64 w2 = w + 2 < sg.count ? sg.words[w + 2] : 0u;
+  const u64 lo = w0 | (w1 << 32);
+  return sh ? (lo >> sh) | (w2 << (64 - sh)) : lo;
+}
+
 
 __device__ __forceinline__ u64 load_window_word(const u8* body, u64 len, u64 byte) {
   // Eight bytes starting at `byte`; bytes past the body read as zero.
@@ -78,39 +174,36 @@ __device__ __forceinline__ u64 funnel(u64 lo, u64 hi, u32 k) {
 // Exact validity of a dynamic header whose BTYPE bits were already checked:
 // the same outcome as building all three tables (huff_build rules), computed
 // with Kraft sums instead of tables.  `lut` is 128 bytes of thread-private LDS.
-__device__ bool dynamic_header_valid(const u8* body, u64 len, u64 start, u8* lut) {
-  BitIn r;
-  r.init(body, len, start + 3);
+__device__ __forceinline__ bool dynamic_header_fields_valid(BitIn& r, u8* lut) {
   u32 hlit, hdist, hclen;
   if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return false;
   const u32 nl = hlit + 257, nd = hdist + 1, nc = hclen + 4;
   if (nl > 286) return false;
-  const u8 order[19] = {16, 17, 18, 0, 8, 7, 9, 6, 10, 5, 11, 4, 12, 3, 13, 2, 14, 1, 15};
   u64 pack = 0;  // 3-bit length per code-length symbol
   u32 kraft = 0;
   for (u32 i = 0; i < nc; ++i) {
     u32 v;
     if (!r.take(3, v)) return false;
-    pack |= u64(v) << (3 * order[i]);
+    pack |= u64(v) << (3 * cl_order(i));
     if (v) kraft += 128u >> v;
   }
   if (kraft != 128) return false;
-  // Canonical codes for the code-length alphabet into a 7-bit LUT: entry =
-  // symbol | length << 5.
-  u32 count[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (u32 s = 0; s < 19; ++s) ++count[(pack >> (3 * s)) & 7];
-  u32 next[8];
+  // Canonical codes of the code-length alphabet into a 7-bit LUT (entry =
+  // symbol | length << 5); counts and next codes packed in registers.
+  u64 cnt = 0;
+  for (u32 s = 0; s < 19; ++s) cnt += 1ull << (8 * ((pack >> (3 * s)) & 7));
+  u64 next = 0;
   u32 code = 0;
-  count[0] = 0;
   for (u32 l = 1; l < 8; ++l) {
-    code = (code + count[l - 1]) << 1;
-    next[l] = code;
+    code = (code + (l > 1 ? u32(cnt >> (8 * (l - 1))) & 0xff : 0u)) << 1;
+    next |= u64(code) << (8 * l);
   }
   for (u32 s = 0; s < 19; ++s) {
     const u32 l = (pack >> (3 * s)) & 7;
     if (!l) continue;
-    const u32 rev = bit_reverse(next[l]++, l);
-    for (u32 k = rev; k < 128; k += 1u << l) lut[k] = u8(s | (l << 5));
+    const u32 c = u32(next >> (8 * l)) & 0xff;
+    next += 1ull << (8 * l);
+    for (u32 k = bit_reverse(c, l); k < 128; k += 1u << l) lut[k] = u8(s | (l << 5));
   }
   u32 ll_kraft = 0, ll_nnz = 0, d_kraft = 0, d_nnz = 0, eob = 0, prev = 0;
   u32 i = 0;
@@ -157,6 +250,14 @@ __device__ bool dynamic_header_valid(const u8* body, u64 len, u64 start, u8* lut
   return ll_ok && d_ok;
 }
 
+// Exact validity of the dynamic header at `start` (BTYPE already checked),
+// reading global memory.
+__device__ bool dynamic_header_valid(const u8* body, u64 len, u64 start, u8* lut) {
+  BitIn r;
+  r.init(body, len, start + 3);
+  return dynamic_header_fields_valid(r, lut);
+}
+
 // Stored-block endpoint seed at `byte` (counted like the reference's discovery,
 // _decode_kernels.py:1019-1038).
 __device__ __forceinline__ bool stored_seed(const u8* body, u64 len, u64 byte) {
@@ -172,12 +273,18 @@ __device__ __forceinline__ bool stored_seed(const u8* body, u64 len, u64 byte) {
   return possible && ((body[byte + 4 + n] >> 1) & 3u) == 1;
 }
 
-// Candidate mask for the 64 bit offsets of bytes [b0, b0 + 8).
-__device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, u8* lut) {
+// Bytes past a workgroup's range staged for header validation: the longest
+// dynamic header is 3 + 14 + 57 + 318 * 14 bits (< 566 bytes).
+constexpr u32 kDiscMargin = 640;
+constexpr u32 kDiscStageWords = (kDiscRange + kDiscMargin + 32) / 4;
+using DiscStage = StageT<kDiscStageWords>;
+
+// Candidate mask for the 64 bit offsets of bytes [b0, b0 + 8), reading the
+// workgroup's stage (headers that run past it are validated from global memory).
+__device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, const DiscStage& sg, u8* lut) {
   if (b0 >= len) return 0;
-  const u64 w0 = load_window_word(body, len, b0);
-  const u64 w1 = load_window_word(body, len, b0 + 8);
-  const u64 w2 = load_window_word(body, len, b0 + 16);
+  const u64 w0 = staged_u64(sg, b0 * 8), w1 = staged_u64(sg, b0 * 8 + 64),
+            w2 = staged_u64(sg, b0 * 8 + 128);
   // Bit k of s_j is stream bit (8*b0 + k + j).
   const u64 s1 = funnel(w0, w1, 1), s2 = funnel(w0, w1, 2);
   const u64 s4 = funnel(w0, w1, 4), s5 = funnel(w0, w1, 5);
@@ -185,6 +292,7 @@ __device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, u8* lut) {
   u64 m = ~s1 & s2 & ~(s4 & s5 & s6 & s7);  // BTYPE == 2 and HLIT <= 29
   const u64 bits_left = (len - b0) * 8;
   if (bits_left < 64) m &= (1ull << bits_left) - 1;
+  const u64 staged_end = sg.bit0 + u64(sg.count) * 32;
   u64 valid = 0;
   while (m) {
     const u32 k = __builtin_ctzll(m);
@@ -199,7 +307,15 @@ __device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, u8* lut) {
     }
     if (kraft != 128) continue;
     const u64 start = b0 * 8 + k;
-    if (start && dynamic_header_valid(body, len, start, lut)) valid |= 1ull << k;
+    if (!start) continue;
+    bool ok;
+    if (start + u64(kDiscMargin - 8) * 8 <= staged_end || staged_end >= len * 8) {
+      BitIn r = staged_reader(sg, len, start + 3);
+      ok = dynamic_header_fields_valid(r, lut);
+    } else {
+      ok = dynamic_header_valid(body, len, start, lut);
+    }
+    if (ok) valid |= 1ull << k;
   }
   return valid;
 }
@@ -238,6 +354,8 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
   st->unresolved[1] = 0;
   st->adler_s = 0;
   st->adler_w = 0;
+  st->recs_used = 0;
+  st->groups_used = 0;
 }
 
 // Pass 1: per-workgroup candidate count and (up to kDiscCap) ordered entries.
@@ -245,10 +363,13 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
                                                   u32* wg_count, u64* wg_list) {
   __shared__ u8 luts[kDiscThreads][128];
   __shared__ u32 scan[kDiscThreads];
+  __shared__ DiscStage sg;
   if (st->status) return;
   const u64 wg = blockIdx.x;
+  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kDiscMargin);
+  __syncthreads();
   const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = candidate_mask(body, len, b0, luts[threadIdx.x]);
+  u64 mask = candidate_mask(body, len, b0, sg, luts[threadIdx.x]);
   if (b0 == 0) mask |= 1;  // bit 0 is always a candidate
   u32 seeds = 0;
   for (u32 j = 0; j < kDiscBytesPerThread; ++j)
@@ -305,6 +426,7 @@ __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len
                                                          const u64* wg_offset, u64* cand) {
   __shared__ u8 luts[kDiscThreads][128];
   __shared__ u32 scan[kDiscThreads];
+  __shared__ DiscStage sg;
   if (st->status) return;
   const u64 wg = blockIdx.x;
   const u32 count = wg_count[wg];
@@ -313,8 +435,10 @@ __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len
     for (u32 i = threadIdx.x; i < count; i += kDiscThreads) cand[off + i] = wg_list[wg * kDiscCap + i];
     return;
   }
+  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kDiscMargin);
+  __syncthreads();
   const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = candidate_mask(body, len, b0, luts[threadIdx.x]);
+  u64 mask = candidate_mask(body, len, b0, sg, luts[threadIdx.x]);
   if (b0 == 0) mask |= 1;
   u32 total;
   u32 at = block_exclusive_scan(__popcll(mask), scan, total);
@@ -377,50 +501,372 @@ __device__ u32 describe_block(BitIn& r, DecodeTables& t, u64 limit, u32& final_b
   return err;
 }
 
-struct DescribeShared {
+constexpr u64 kSyncBits = 1024;   // window in which a slice records its token starts
+constexpr u32 kSyncWords = kSyncBits / 64;
+constexpr u32 kNoMerge = 0xffffffffu;
+
+// Per-wave LDS of the describe kernel.
+struct SpecShared {
   DecodeTables tables;
-  u8 lut[128];
+  Stage stage;
+  u16 codes[320];                     // scratch of cooperative table builds
+  u64 visit[64][kSyncWords];          // token starts in [slice start, + kSyncBits)
+  u64 xpos[64], evpos[64], evend[64];
+  u32 count[64], ev[64];
+  u32 merge[64];                      // offset (from slice start) where lane j-1's
+                                      // continuation met lane j's tokens, or kNoMerge
+  u32 tail[64];                       // bytes of lane j's continuation tokens
+  u32 before[64];                     // bytes lane j produced before its merge point
+  // control written by lane 0 (d0: block data start; r0: round start)
+  u64 pos, d0, r0, hint, end, size, slice;
+  u32 type, final_block, status, nl, nd, go, build_status, group, lanes;
 };
+
+__device__ __forceinline__ bool visited(const SpecShared& sh, u32 lane, u64 off) {
+  return off < kSyncBits && ((sh.visit[lane][off >> 6] >> (off & 63)) & 1);
+}
+
+// Token-level decode from r.pos until r.pos >= stop, an EOB or an error.
+// ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  With
+// `visit`, token starts in [win0, win0 + kSyncBits) are recorded.
+__device__ void slice_decode(const DecodeTables& t, BitIn& r, u64 stop, u64* visit, u64 win0,
+                             u64& xpos, u32& count, u32& ev, u64& evpos, u64& evend) {
+  u64 produced = 0;
+  ev = 0;
+  if (visit)
+    for (u32 w = 0; w < kSyncWords; ++w) visit[w] = 0;
+  for (;;) {
+    const u64 p = r.pos;
+    if (p >= stop) break;
+    if (visit) {
+      const u64 off = p - win0;
+      if (off < kSyncBits) visit[off >> 6] |= 1ull << (off & 63);
+    }
+    u32 lit, length, distance;
+    const u32 err = decode_token(const_cast<DecodeTables&>(t), r, 32768u, lit, length, distance);
+    if (err) { ev = 0x100u | err; evpos = p; break; }
+    if (!length) { ev = 1; evpos = p; evend = r.pos; break; }
+    produced += length;
+    if (produced >= 0xffff0000ull) { ev = 0x100u | kOutputOverflow; evpos = p; break; }
+  }
+  xpos = r.pos;
+  count = u32(produced);
+}
+
+// Bytes produced by decoding tokens from `from` up to token start `to`.
+__device__ u32 bytes_between(const DecodeTables& t, const Stage& sg, u64 len, u64 from, u64 to) {
+  BitIn r = staged_reader(sg, len, from);
+  u32 bytes = 0;
+  while (r.pos < to) {
+    u32 lit, length, distance;
+    if (decode_token(const_cast<DecodeTables&>(t), r, 32768u, lit, length, distance) || !length) break;
+    bytes += length;
+  }
+  return bytes;
+}
+
+// Reads a block header at sh.pos from the stage (lane 0): stored fields, or
+// dynamic code lengths; then the wave builds fixed/dynamic tables.  Sets
+// sh.type, sh.final_block, sh.status, sh.d0 (first token or payload bit) and,
+// for stored blocks, sh.end/sh.size.
+template <typename Shared>
+__device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
+  const u32 lane = threadIdx.x;
+  if (!staged_covers(sh.stage, body, len, sh.pos, sh.pos + 4096)) {
+    __syncthreads();
+    stage_range(body, len, sh.pos, sh.pos + 64 * kMaxSlice, sh.stage);
+  }
+  __syncthreads();
+  if (!lane) {
+    BitIn r = staged_reader(sh.stage, len, sh.pos);
+    u32 type = 0, fin = 0, err = 0;
+    sh.nl = sh.nd = 0;
+    if (!r.take(1, fin) || !r.take(2, type)) err = kTruncated;
+    else if (type == 3) err = kReservedBlock;
+    else if (type == 0) {
+      r.seek((r.pos + 7) & ~u64(7));
+      u32 nlen, comp;
+      if (!r.take(16, nlen) || !r.take(16, comp)) err = kTruncated;
+      else if ((nlen ^ comp) != 0xffffu) err = kBadSymbol;
+      else if (nlen > limit) err = kOutputOverflow;
+      else if (u64(nlen) * 8 > r.avail()) err = kTruncated;
+      else {
+        sh.end = r.pos + u64(nlen) * 8;
+        sh.size = nlen;
+      }
+    } else if (type == 1) {
+      for (u32 i = 0; i < 320; ++i) sh.tables.lens[i] = i < 144 ? 8 : i < 256 ? 9 : i < 280 ? 7 : i < 288 ? 8 : 5;
+      sh.nl = 288;
+      sh.nd = 32;
+    } else {
+      u32 nl = 0, nd = 0;
+      err = parse_dynamic_lengths(sh.tables, r, nl, nd);
+      sh.nl = nl;
+      sh.nd = nd;
+    }
+    sh.d0 = r.pos;
+    sh.type = type;
+    sh.final_block = fin;
+    sh.status = err;
+  }
+  __syncthreads();
+  if (sh.type && !sh.status) {
+    const bool fixed = sh.type == 1;
+    u32 err = huff_build_wave(sh.tables.ll, sh.tables.lens, sh.nl, false, true, 15, sh.codes,
+                              &sh.build_status);
+    if (!err)
+      err = huff_build_wave(sh.tables.dd, sh.tables.lens + sh.nl, sh.nd, !fixed, true, 15,
+                            sh.codes, &sh.build_status);
+    if (!lane) sh.status = err;
+    __syncthreads();
+  }
+}
+
+// Describe the tokens of the fixed/dynamic block whose tables are built and
+// whose tokens start at sh.d0.  Each round:
+//   1. the 64 lanes decode evenly spaced slices speculatively, each recording
+//      the token starts in the first kSyncBits of its slice;
+//   2. every lane continues past its slice end until it meets a token start
+//      of the next lane (a merge: from there the two decodings coincide);
+//   3. every lane counts the bytes it produced before its merge point;
+//   4. lane 0 chains the true slice entries from the round start, decoding
+//      serially only where a slice never merged.
+// Results: sh.status, sh.end (bit after the EOB), sh.size, and slice groups
+// (sh.group = kNone if capacity ran out; emission then decodes serially).
+__device__ void describe_tokens(const u8* body, u64 len, u64 limit, SpecShared& sh, State* st,
+                                u64* slice_entry, u32* slice_off, u32* group_link,
+                                u64 group_capacity) {
+  const u32 lane = threadIdx.x;
+  u64 e = sh.d0, total = 0;
+  bool done = false, keep = true;
+  u32 last_group = kNone, status = 0, lanes = 0, group = kNone;
+  u64 end = 0;
+  while (true) {
+    if (!lane) {
+      // Past the hint (a false candidate inside this block): full rounds.
+      const u64 span = sh.hint > e ? sh.hint - e : 64 * kMaxSlice;
+      u64 slice = (span + 63) / 64;
+      if (slice < kMinSlice) slice = kMinSlice;
+      if (slice > kMaxSlice) slice = kMaxSlice;
+      sh.r0 = e;
+      sh.slice = slice;
+      sh.go = done ? 0u : 1u;
+    }
+    __syncthreads();
+    if (!sh.go) break;
+    const u64 r0 = sh.r0, slice = sh.slice;
+    if (!staged_covers(sh.stage, body, len, r0, r0 + 64 * slice)) {
+      stage_range(body, len, r0, r0 + 64 * slice, sh.stage);
+      __syncthreads();
+    }
+    const u64 s0 = r0 + u64(lane) * slice;
+    {  // 1. speculative slices
+      BitIn r = staged_reader(sh.stage, len, s0);
+      slice_decode(sh.tables, r, s0 + slice, sh.visit[lane], s0, sh.xpos[lane], sh.count[lane],
+                   sh.ev[lane], sh.evpos[lane], sh.evend[lane]);
+    }
+    __syncthreads();
+    if (lane < 63) {  // 2. continuation into the next slice
+      u32 merge = kNoMerge, tail = 0;
+      if (!sh.ev[lane]) {
+        const u64 s1 = s0 + slice;
+        BitIn r = staged_reader(sh.stage, len, sh.xpos[lane]);
+        for (;;) {
+          const u64 off = r.pos - s1;
+          if (off >= kSyncBits || r.pos >= s1 + slice) break;
+          if (visited(sh, lane + 1, off)) { merge = u32(off); break; }
+          u32 lit, length, distance;
+          if (decode_token(sh.tables, r, 32768u, lit, length, distance) || !length) break;
+          tail += length;
+        }
+      }
+      sh.merge[lane + 1] = merge;
+      sh.tail[lane] = tail;
+    }
+    if (!lane) sh.merge[0] = kNoMerge;
+    __syncthreads();
+    // 3. bytes before the merge point of each lane's own decoding
+    sh.before[lane] = sh.merge[lane] != kNoMerge ? bytes_between(sh.tables, sh.stage, len, s0, s0 + sh.merge[lane]) : 0u;
+    __syncthreads();
+    if (!lane) {  // 4. chain the true entries
+      u32 g = kNone;
+      if (keep) {
+        const u64 gi = atomicAdd(reinterpret_cast<unsigned long long*>(&st->groups_used), 1ull);
+        if (gi < group_capacity) {
+          g = u32(gi);
+          group_link[g] = kNone;
+          if (last_group == kNone) group = g;
+          else group_link[last_group] = g;
+          last_group = g;
+        } else {
+          keep = false;
+          group = kNone;
+        }
+      }
+      bool via_merge = false;
+      for (u32 j = 0; j < 64 && !done; ++j) {
+        const u64 sj = r0 + u64(j) * slice;
+        u32 before = 0;
+        bool synced = j == 0;
+        if (!synced && via_merge && e == sj + sh.merge[j]) {
+          synced = true;
+          before = sh.before[j];
+        }
+        if (!synced) {
+          // Advance the true position until it meets lane j's tokens.
+          for (;;) {
+            const u64 off = e - sj;
+            if (visited(sh, j, off)) {
+              synced = true;
+              before = bytes_between(sh.tables, sh.stage, len, sj, e);
+              break;
+            }
+            if (off >= kSyncBits || e >= sj + slice) break;
+            BitIn r = staged_reader(sh.stage, len, e);
+            u32 lit, length, distance;
+            const u32 err = decode_token(sh.tables, r, 32768u, lit, length, distance);
+            if (err) { status = err; end = e; done = true; break; }
+            if (!length) { end = r.pos; done = true; break; }
+            total += length;
+            e = r.pos;
+          }
+          if (done) break;
+        }
+        if (keep) {
+          slice_entry[u64(g) * 64 + j] = e;
+          slice_off[u64(g) * 64 + j] = u32(total);
+        }
+        ++lanes;
+        u64 xpos, evpos, evend;
+        u32 count, ev;
+        if (synced) {
+          xpos = sh.xpos[j];
+          count = sh.count[j];
+          ev = sh.ev[j];
+          evpos = sh.evpos[j];
+          evend = sh.evend[j];
+        } else {
+          // Lane j never met the true tokens in its window: decode its slice.
+          BitIn r = staged_reader(sh.stage, len, e);
+          slice_decode(sh.tables, r, sj + slice, nullptr, 0, xpos, count, ev, evpos, evend);
+          before = 0;
+        }
+        total += count - before;
+        if (ev == 1) { end = evend; done = true; break; }
+        if (ev) { status = ev & 0xffu; end = evpos; done = true; break; }
+        e = xpos;
+        via_merge = false;
+        if (synced && j < 63 && sh.merge[j + 1] != kNoMerge) {
+          total += sh.tail[j];
+          e = r0 + u64(j + 1) * slice + sh.merge[j + 1];
+          via_merge = true;
+        }
+        if (total > limit) { status = kOutputOverflow; end = e; done = true; break; }
+      }
+      if (!done && e >= len * 8) { status = kTruncated; end = e; done = true; }
+      sh.status = status;
+      sh.end = end;
+      sh.size = total;
+      sh.group = keep ? group : kNone;
+      sh.lanes = lanes;
+    }
+    __syncthreads();
+  }
+}
 
 }  // namespace
 
-// One wave per candidate; lane 0 parses the candidate's segment.
-__global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const u64* cand,
-                                                 const State* st, u64 out_size, u64* seg_end,
-                                                 u64* seg_size, u32* seg_blocks, u32* seg_next,
-                                                 u32* seg_flags) {
-  __shared__ DescribeShared sh;
+// One wave per candidate: describe the candidate's segment (its block and the
+// following stored/fixed blocks up to the next candidate) with wave-parallel
+// token decoding, and record per-block slices for emission.
+__global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const u64* cand, State* st,
+                                                 u64 out_size, u64* seg_end, u64* seg_size,
+                                                 u32* seg_blocks, u32* seg_next, u32* seg_flags,
+                                                 u32* seg_rec, BlockRec* recs, u64 rec_capacity,
+                                                 u64* slice_entry, u32* slice_off, u32* group_link,
+                                                 u64 group_capacity) {
+  __shared__ SpecShared sh;
   if (st->status) return;
+  const u32 lane = threadIdx.x;
   const u64 n = st->candidates;
   for (u64 c = blockIdx.x; c < n; c += gridDim.x) {
-    if (threadIdx.x) continue;
-    BitIn r;
-    r.init(body, len, cand[c]);
     u64 produced = 0;
-    u32 blocks = 0, status = 0, final_block = 0, next = kNone;
-    for (;;) {
-      u64 size;
-      status = describe_block(r, sh.tables, out_size, final_block, size);
-      ++blocks;
-      produced += size;
-      if (status) break;
-      if (produced > out_size) { status = kOutputOverflow; break; }
-      if (final_block) break;
-      const u64 pos = r.pos;
-      const u64 idx = lower_bound(cand, n, pos);
-      if (idx < n && cand[idx] == pos) { next = u32(idx); break; }
-      // A dynamic header here failed validation: the exact walk reports it.
-      BitIn h;
-      h.init(body, len, pos);
-      u32 f, type;
-      if (h.take(1, f) && h.take(2, type) && type == 2) { status = kUndiscovered; break; }
-      if (blocks >= kMaxBlocks) { status = kBlockCapacity; break; }
+    u32 blocks = 0, status = 0, final_block = 0, next = kNone, first_rec = kNone, last_rec = kNone;
+    bool recs_ok = true;
+    if (!lane) {
+      sh.pos = cand[c];
+      sh.stage.count = 0;
+      sh.stage.bit0 = 0;
     }
-    seg_end[c] = r.pos;
-    seg_size[c] = produced;
-    seg_blocks[c] = blocks;
-    seg_next[c] = next;
-    seg_flags[c] = status | (final_block ? 0x80000000u : 0u);
+    __syncthreads();
+    for (;;) {
+      block_header(body, len, out_size, sh);
+      if (!lane && sh.type && !sh.status) {
+        const u64 idx = lower_bound(cand, n, sh.pos + 1);
+        sh.hint = idx < n ? cand[idx] : len * 8;
+        sh.group = kNone;
+        sh.lanes = 0;
+      }
+      __syncthreads();
+      if (sh.type && !sh.status)
+        describe_tokens(body, len, out_size, sh, st, slice_entry, slice_off, group_link,
+                        group_capacity);
+      if (!lane) {
+        ++blocks;
+        const u32 bstatus = sh.status;
+        if (bstatus) status = bstatus;
+        else {
+          produced += sh.size;
+          if (recs_ok) {
+            const u64 ri = atomicAdd(reinterpret_cast<unsigned long long*>(&st->recs_used), 1ull);
+            if (ri >= rec_capacity || ri >= kNone || (sh.type != 0 && sh.group == kNone)) {
+              recs_ok = false;
+            } else {
+              BlockRec rec;
+              rec.start = sh.pos;
+              rec.data = sh.d0;
+              rec.end = sh.end;
+              rec.size = sh.size;
+              rec.type = sh.type;
+              rec.lanes = sh.type ? sh.lanes : 0;
+              rec.group = sh.type ? sh.group : kNone;
+              rec.next = kNone;
+              recs[ri] = rec;
+              if (last_rec == kNone) first_rec = u32(ri);
+              else recs[last_rec].next = u32(ri);
+              last_rec = u32(ri);
+            }
+          }
+          if (produced > out_size) status = kOutputOverflow;
+          else if (sh.final_block) final_block = 1;
+          else {
+            const u64 p = sh.end;
+            const u64 idx = lower_bound(cand, n, p);
+            if (idx < n && cand[idx] == p) next = u32(idx);
+            else {
+              BitIn h;
+              h.init(body, len, p);
+              u32 f, type;
+              if (h.take(1, f) && h.take(2, type) && type == 2) status = kUndiscovered;
+              else if (blocks >= kMaxBlocks) status = kBlockCapacity;
+            }
+          }
+        }
+        sh.pos = sh.end;
+        sh.go = (status || final_block || next != kNone) ? 0u : 1u;
+      }
+      __syncthreads();
+      if (!sh.go) break;
+    }
+    if (!lane) {
+      seg_end[c] = sh.end;
+      seg_size[c] = produced;
+      seg_blocks[c] = blocks;
+      seg_next[c] = next;
+      seg_flags[c] = status | (final_block ? 0x80000000u : 0u);
+      seg_rec[c] = recs_ok ? first_rec : kNone;
+    }
+    __syncthreads();
   }
 }
 
@@ -429,6 +875,7 @@ __global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const 
 __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, const u64* seg_end,
                                                 const u64* seg_size, const u32* seg_blocks,
                                                 const u32* seg_next, const u32* seg_flags,
+                                                const u32* seg_rec,
                                                 u32* exit_node, u64 len,
                                                 u64 out_size, u32 max_blocks, Segment* acc) {
   __shared__ u32 entry[1024];
@@ -504,6 +951,8 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
     acc[index].end = seg_end[cur];
     acc[index].prefix = offset;
     acc[index].size = seg_size[cur];
+    acc[index].rec_first = seg_rec[cur];
+    acc[index].rec_count = seg_blocks[cur];
     offset += seg_size[cur];
     ++index;
     cur = seg_next[cur];
@@ -551,6 +1000,8 @@ __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, Stat
     acc[n].end = end;
     acc[n].prefix = output;
     acc[n].size = size;
+    acc[n].rec_first = kNone;
+    acc[n].rec_count = 1;
     ++n;
     output += size;
     next = end;
@@ -621,9 +1072,9 @@ __device__ __forceinline__ void append_unresolved(bool flag, u64 pos, u32* list,
 
 // One wave per accepted segment: lane 0 parses, the wave copies stored
 // payloads and long matches.  Output positions are absolute.
-__global__ __launch_bounds__(64) void g_emit(const u8* body, u64 len, State* st, const Segment* acc,
-                                             u8* out, u32* roots, u32* unres, u32* list,
-                                             u64 list_capacity) {
+__global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, State* st,
+                                                    const Segment* acc, u8* out, u32* roots,
+                                                    u32* unres, u32* list, u64 list_capacity) {
   __shared__ EmitShared sh;
   if (st->status) return;
   const u32 lane = threadIdx.x;
@@ -631,6 +1082,7 @@ __global__ __launch_bounds__(64) void g_emit(const u8* body, u64 len, State* st,
   const u32 window = st->window;
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
+    if (seg.rec_first != kNone) continue;
     // Lane-0 parser state.
     BitIn r;
     u64 produced = 0;
@@ -721,6 +1173,145 @@ __global__ __launch_bounds__(64) void g_emit(const u8* body, u64 len, State* st,
       __syncthreads();
     }
     if (!lane && sh.error) atomicMax(&st->emit_status, sh.error);
+    __syncthreads();
+  }
+}
+
+namespace {
+constexpr u32 kPushSlots = 16;
+
+struct LaneEmitShared {
+  DecodeTables tables;
+  Stage stage;
+  u16 codes[320];
+  u32 push[64][kPushSlots];
+  BlockRec rec;
+  // block_header interface
+  u64 pos, d0, end, size;
+  u32 type, final_block, status, nl, nd, build_status;
+};
+
+__device__ __forceinline__ void push_unresolved(u32* buf, u32& n, u32 pos, u32* list, u64* count,
+                                                u64 capacity) {
+  buf[n++] = pos;
+  if (n == kPushSlots) {
+    const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(count), u64(kPushSlots));
+    for (u32 i = 0; i < kPushSlots; ++i)
+      if (at + i < capacity) list[at + i] = buf[i];
+    n = 0;
+  }
+}
+
+__device__ __forceinline__ void flush_unresolved(u32* buf, u32& n, u32* list, u64* count,
+                                                 u64 capacity) {
+  if (!n) return;
+  const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(count), u64(n));
+  for (u32 i = 0; i < n; ++i)
+    if (at + i < capacity) list[at + i] = buf[i];
+  n = 0;
+}
+}  // namespace
+
+// One wave per accepted segment with block records: stored blocks are copied
+// by the wave; fixed/dynamic blocks decode their described slices in parallel,
+// one slice per lane, writing output in place.  A byte copied from before its
+// slice's output start is queued as unresolved (root = source position).
+__global__ __launch_bounds__(64) void g_emit_lanes(const u8* body, u64 len, State* st,
+                                                   const Segment* acc, const BlockRec* recs,
+                                                   const u64* slice_entry, const u32* slice_off,
+                                                   const u32* group_link, u8* out, u32* roots,
+                                                   u32* unres, u32* list, u64 list_capacity) {
+  __shared__ LaneEmitShared sh;
+  if (st->status) return;
+  const u32 lane = threadIdx.x;
+  const u64 segments = st->accepted;
+  const u32 window = st->window;
+  u64* list_count = &st->unresolved[0];
+  for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
+    const Segment seg = acc[si];
+    if (seg.rec_first == kNone) continue;
+    u32 ri = seg.rec_first;
+    u64 block_out = seg.prefix;
+    u32 error = 0;
+    if (!lane) {
+      sh.stage.count = 0;
+      sh.stage.bit0 = 0;
+    }
+    __syncthreads();
+    while (ri != kNone) {
+      if (!lane) {
+        sh.rec = recs[ri];
+        sh.pos = sh.rec.start;
+      }
+      __syncthreads();
+      const BlockRec rec = sh.rec;
+      if (rec.type == 0) {
+        const u64 src = rec.data >> 3;
+        for (u64 j = lane; j < rec.size; j += 64) out[block_out + j] = body[src + j];
+      } else {
+        block_header(body, len, ~0ull, sh);
+        if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
+        u32 g = rec.group;
+        u32 done = 0;
+        while (g != kNone && done < rec.lanes) {
+          const u32 count = rec.lanes - done < 64 ? rec.lanes - done : 64u;
+          const u32 next_g = group_link[g];
+          const u64 first = slice_entry[u64(g) * 64];
+          const u64 group_end =
+              next_g != kNone && count == 64 && done + 64 < rec.lanes ? slice_entry[u64(next_g) * 64]
+                                                                      : rec.end;
+          if (!staged_covers(sh.stage, body, len, first, group_end)) {
+            __syncthreads();
+            stage_range(body, len, first, group_end, sh.stage);
+          }
+          __syncthreads();
+          u32 lerr = 0;
+          if (lane < count) {
+            const u64 entry = slice_entry[u64(g) * 64 + lane];
+            const u64 stop = lane + 1 < count ? slice_entry[u64(g) * 64 + lane + 1] : group_end;
+            const u64 dst0 = block_out + slice_off[u64(g) * 64 + lane];
+            const u64 block_end = block_out + rec.size;
+            BitIn r = staged_reader(sh.stage, len, entry);
+            u64 dst = dst0;
+            bool any_unres = false;
+            u32 pushed = 0;
+            while (r.pos < stop) {
+              u32 lit, length, distance;
+              if (decode_token(sh.tables, r, 32768u, lit, length, distance)) { lerr = kExtent; break; }
+              if (!length) break;
+              if (length > block_end - dst) { lerr = kExtent; break; }
+              if (!distance) { out[dst++] = u8(lit); continue; }
+              if (distance > window || distance > dst) { lerr = kBadDistance; break; }
+              for (u32 j = 0; j < length; ++j) {
+                const u64 d = dst + j, src = d - distance;
+                if (src < dst0) {
+                  roots[d] = u32(src);
+                  bit_set(unres, d);
+                  push_unresolved(sh.push[lane], pushed, u32(d), list, list_count, list_capacity);
+                  any_unres = true;
+                } else if (any_unres && bit_get(unres, src)) {
+                  roots[d] = roots[src];
+                  bit_set(unres, d);
+                  push_unresolved(sh.push[lane], pushed, u32(d), list, list_count, list_capacity);
+                } else {
+                  out[d] = out[src];
+                }
+              }
+              dst += length;
+            }
+            flush_unresolved(sh.push[lane], pushed, list, list_count, list_capacity);
+          }
+          if (lerr) atomicMax(&st->emit_status, lerr);
+          done += count;
+          g = next_g;
+          __syncthreads();
+        }
+      }
+      block_out += rec.size;
+      ri = rec.next;
+      __syncthreads();
+    }
+    if (!lane && error) atomicMax(&st->emit_status, error);
     __syncthreads();
   }
 }
@@ -871,25 +1462,38 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   // Describe every candidate's segment.
   u64 *seg_end = nullptr, *seg_size = nullptr;
   u32 *seg_blocks = nullptr, *seg_next = nullptr, *seg_flags = nullptr, *exit_node = nullptr;
+  u32* seg_rec = nullptr;
   HZ_TRY(scratch.alloc(&seg_end, cand_capacity));
   HZ_TRY(scratch.alloc(&seg_size, cand_capacity));
   HZ_TRY(scratch.alloc(&seg_blocks, cand_capacity));
   HZ_TRY(scratch.alloc(&seg_next, cand_capacity));
   HZ_TRY(scratch.alloc(&seg_flags, cand_capacity));
+  HZ_TRY(scratch.alloc(&seg_rec, cand_capacity));
   HZ_TRY(scratch.alloc(&exit_node, cand_capacity));
-  HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kWave), 0, stream, body,
-                     len, cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags);
+  // Block records and slice groups; running out only sends a segment to the
+  // serial emitter.
+  const u64 rec_capacity = u64(max_blocks) + cand_capacity + 1024;
+  const u64 group_capacity = (len * 8) / 8192 + 65536;
+  BlockRec* recs = nullptr;
+  u64* slice_entry = nullptr;
+  u32 *slice_off = nullptr, *group_link = nullptr;
+  HZ_TRY(scratch.alloc(&recs, rec_capacity));
+  HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
+  HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
+  HZ_TRY(scratch.alloc(&group_link, group_capacity));
+  HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kWave), 0, stream, body, len,
+            cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
+            rec_capacity, slice_entry, slice_off, group_link, group_capacity);
   HZ_TRY(hipGetLastError());
 
   // Chain selection, then the exact walk if the fast chain declined.
   Segment* acc = nullptr;
   HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
-  HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size,
-                     seg_blocks, seg_next, seg_flags, exit_node, len, out_size, max_blocks,
-                     acc);
+  HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size, seg_blocks,
+            seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size,
-                     max_blocks, acc);
+  HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size, max_blocks,
+            acc);
   HZ_TRY(hipGetLastError());
 
   // Emission and cross-segment resolution.
@@ -903,13 +1507,18 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&list1, list_capacity));
   HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
   HZ_TRY(launch_fill(stream, bits1, 0, words * 4));
-  HZ_LAUNCH(g_emit, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
-                     st, acc, out, roots, bits0, list0, list_capacity);
+  HZ_LAUNCH(g_emit_lanes, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
+            st, acc, recs, slice_entry, slice_off, group_link, out, roots, bits0, list0,
+            list_capacity);
   HZ_TRY(hipGetLastError());
-  // Pointer jumping halves every reference chain per round; chains span at
-  // most max_blocks segments.
+  HZ_LAUNCH(g_emit_serial, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
+            st, acc, out, roots, bits0, list0, list_capacity);
+  HZ_TRY(hipGetLastError());
+  // Pointer jumping halves every reference chain per round.  A chain hops
+  // back across slices (or serially emitted segments), so its length is
+  // bounded by the number of slices plus segments.
   u32 rounds = 2;
-  for (u64 span = 1; span < u64(max_blocks); span <<= 1) ++rounds;
+  for (u64 span = 1; span < group_capacity * 64 + u64(max_blocks); span <<= 1) ++rounds;
   for (u32 round = 0; round < rounds; ++round) {
     HZ_LAUNCH(g_resolve_reset, dim3(1), dim3(1), 0, stream, st, round);
     HZ_TRY(hipGetLastError());
