@@ -117,6 +117,10 @@ def cpu_baselines(payload, raw, budget_s):
         times.append(time.perf_counter() - t0)
     single = n / statistics.median(times) / 1e9
     all_cores, cores, repeats = _all_cores(payload, "decompress", budget_s, single * 1e9, n)
+    t0 = time.perf_counter()
+    zlib.compress(raw, 1)
+    comp_single = n / (time.perf_counter() - t0) / 1e9
+    comp_all, _, comp_repeats = _all_cores(raw, "compress", budget_s, comp_single * 1e9, n)
     return {
         "cpu_baseline": {"value": round(n / port_s / 1e9, 4), "unit": "GB/s", "cores": 1,
                          "kind": "port",
@@ -125,10 +129,24 @@ def cpu_baselines(payload, raw, budget_s):
         "cpu_zlib": {"zlib_version": zlib.ZLIB_RUNTIME_VERSION,
                      "decompress_single_gbs": round(single, 4),
                      "decompress_all_cores_gbs": round(all_cores, 4),
-                     "all_cores_processes": cores, "repeats_per_process": repeats,
+                     "compress_l1_single_gbs": round(comp_single, 4),
+                     "compress_l1_all_cores_gbs": round(comp_all, 4),
+                     "all_cores_processes": cores,
+                     "repeats_per_process": {"decompress": repeats, "compress": comp_repeats},
+                     "cpu_model": _cpu_model(),
                      "libdeflate_single_gbs": (lambda v: round(v, 4) if v else None)(
                          _libdeflate_decode(payload, n))},
     }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 # ---- GPU measurement ----------------------------------------------------------
@@ -151,11 +169,13 @@ def traffic_from_profiles(kernel):
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--cpu-seconds", type=float, default=8.0,
-                        help="approximate budget of the all-cores CPU baseline")
+                        help="approximate budget of each all-cores CPU baseline")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--legs", choices=("both", "decode", "encode"), default="both",
+                        help="restrict the timed step to one leg (profiling runs)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this codec path runs on a single MI355X; "
@@ -173,42 +193,81 @@ def main():
     raw = workloads.c1()
     payload = zlib.compress(raw, 6)
     n = len(raw)
+    chunk = 32768
+    chunks = (n + chunk - 1) // chunk
+    capacity = n + 5 * chunks + 6
     src = torch.from_numpy(np.frombuffer(payload, np.uint8).copy()).to(dev)
     ref = torch.from_numpy(np.frombuffer(raw, np.uint8).copy()).to(dev)
     out = torch.empty(n, dtype=torch.uint8, device=dev)
     meta = torch.empty(2, dtype=torch.uint32, device=dev)
+    enc = torch.empty(capacity, dtype=torch.uint8, device=dev)
+    enc_meta = torch.empty(2, dtype=torch.uint32, device=dev)
     stream = torch.cuda.current_stream(dev)
     handle = ctypes.c_void_p(stream.cuda_stream)
+    do_decode = args.legs in ("both", "decode")
+    do_encode = args.legs in ("both", "encode")
 
-    def step():
+    def decode():
         rc = lib.HipZlibDecompress(handle, MAX, MAX, _ptr(src), len(payload), _ptr(out), n,
                                    _ptr(meta), 2)
         if rc:
             _native.check(lib, rc)
 
+    def encode():
+        rc = lib.HipZlibCompress(handle, chunk, _ptr(ref), n, _ptr(enc), capacity,
+                                 _ptr(enc_meta), 2)
+        if rc:
+            _native.check(lib, rc)
+
+    def step():
+        if do_decode:
+            decode()
+        if do_encode:
+            encode()
+
+    encoded = {}
+
     def verify(label):
         torch.cuda.synchronize(dev)
-        status = int(meta.cpu().numpy()[0])
-        assert status == 0, "%s: decode status %d" % (label, status)
-        assert torch.equal(out, ref), "%s: decoded bytes differ from the source" % label
+        if do_decode:
+            status = int(meta.cpu().numpy()[0])
+            assert status == 0, "%s: decode status %d" % (label, status)
+            assert torch.equal(out, ref), "%s: decoded bytes differ from the source" % label
+        if do_encode:
+            length, status = (int(v) for v in enc_meta.cpu().numpy())
+            assert status == 0, "%s: encode status %d" % (label, status)
+            stream_bytes = enc[:length].cpu().numpy().tobytes()
+            if "bytes" in encoded:
+                assert stream_bytes == encoded["bytes"], "%s: encoder is not deterministic" % label
+            else:
+                assert zlib.decompress(stream_bytes) == raw, "%s: encoded stream fails zlib" % label
+                encoded["bytes"] = stream_bytes
 
     for _ in range(max(1, args.warmup)):
         step()
     verify("warmup")
     out.zero_()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    stop.record(stream)
-    torch.cuda.synchronize(dev)
-    wall = time.perf_counter() - t0
+    enc.zero_()
+
+    def timed(fn, steps):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        stop.record(stream)
+        torch.cuda.synchronize(dev)
+        return (time.perf_counter() - t0) * 1000 / steps, start.elapsed_time(stop) / steps
+
+    ms_per_step, device_ms = timed(step, args.steps)
     verify("timed")
-    device_ms = start.elapsed_time(stop) / args.steps
-    ms_per_step = wall * 1000 / args.steps
     value = n / (ms_per_step / 1000) / 1e9
+    legs = {}
+    if do_decode:
+        legs["decode"] = timed(decode, max(3, args.steps // 2))
+    if do_encode:
+        legs["encode"] = timed(encode, max(3, args.steps // 2))
 
     # Per-kernel durations, HIP events around each launch on the codec's stream.
     lib.HipZlibProfileEnable(1)
@@ -220,8 +279,9 @@ def main():
     kernels = _native.profile_collect(lib)
     dominant, (launches, total_ms) = max(kernels.items(), key=lambda kv: kv[1][1])
     avg_ms = total_ms / launches
-    # Algorithmic bytes per launch: the uncompressed bytes one decode produces,
-    # counted once per launch of the dominant kernel (one launch per decode).
+    # Algorithmic bytes per launch: the uncompressed bytes of the stream the
+    # launch belongs to (one 64 MiB decode or encode per launch of every
+    # per-step kernel).
     per_launch = n * profile_steps / launches
     achieved = per_launch / (avg_ms / 1000) / 1e9
 
@@ -239,12 +299,16 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8",
-        "data": "synthetic (seeded float32 strain, zlib level 6 on the CPU)",
-        "config": {"workload": "decode 64 MiB float32 strain stream (16,777,216 samples, "
-                               "Gaussian sigma 1e-21 + 1e-22 chirp 20-500 Hz @ 4096 Hz, seed 1), "
-                               "zlib level 6, %d compressed bytes" % len(payload),
-                   "uncompressed_bytes": n, "compressed_bytes": len(payload),
-                   "route": "general (parallel)", "parallelism": "single GPU"},
+        "data": "synthetic (seeded float32 strain; decode input compressed by CPU zlib level 6)",
+        "config": {"workload": "64 MiB float32 strain stream (16,777,216 samples, Gaussian sigma "
+                               "1e-21 + 1e-22 chirp 20-500 Hz @ 4096 Hz, seed 1): one step = "
+                               "decode of its zlib level-6 stream + encode with 32 KiB chunks"
+                               if args.legs == "both" else
+                               "64 MiB float32 strain stream, %s leg only" % args.legs,
+                   "uncompressed_bytes": n, "compressed_bytes_l6": len(payload),
+                   "chunk_bytes": chunk, "parallelism": "single GPU"},
+        "legs": {k: {"gbs": round(n / (v[0] / 1000) / 1e9, 4), "ms": round(v[0], 4),
+                     "device_ms": round(v[1], 4)} for k, v in legs.items()},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 3),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 6),
@@ -252,6 +316,10 @@ def main():
                      "avg_launch_ms": round(avg_ms, 4)},
         "kernels_ms_per_step": {k: round(v[1] / profile_steps, 4) for k, v in kernels.items()},
     }
+    if "bytes" in encoded:
+        result["encode_ratio"] = {"gpu": round(len(encoded["bytes"]) / n, 6),
+                                  "zlib_l1": round(len(zlib.compress(raw, 1)) / n, 6),
+                                  "zlib_l6": round(len(payload) / n, 6)}
     if not args.no_cpu_baseline:
         result.update(cpu_baselines(payload, raw, args.cpu_seconds))
     print(json.dumps(result), flush=True)

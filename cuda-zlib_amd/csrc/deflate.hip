@@ -1,13 +1,940 @@
-// Chunked encoder.  Under construction: returns an explicit error until the
-// encoder kernels land.
+// Chunked zlib encoder: one 256-thread workgroup (4 waves) per chunk
+// (default 32 KiB).
+//
+// Stream layout (the reference's compress path, native/codec_ffi.cu:551-612,
+// encoder E:283-418): header 78 01; every chunk is one block of the cheapest
+// type (stored, fixed or dynamic Huffman); a non-final fixed/dynamic block is
+// followed by an empty stored block so every chunk ends byte aligned and
+// chunks concatenate at byte granularity; Adler-32 trailer, big endian.  The
+// worst chunk costs len + 5 bytes, so a stream always fits in
+// n + 5 * chunks + 6 bytes.
+//
+// Unlike the reference, a chunk's LZ77 window includes up to 32 KiB of the
+// same input before it (the decoder has already produced those bytes), which
+// keeps the ratio below whole-stream zlib level 1.  Per chunk:
+//   stage    window (history + chunk) into LDS as aligned dwords; Adler-32
+//            partial sums of the chunk bytes
+//   history  every history position enters the hash table
+//   parse    steps of 256 positions, one per thread: 4-byte hash into 4096
+//            buckets x 4 ways, candidates = the bucket plus the nearest of the
+//            8 previous positions of the same wave with an equal hash; longest
+//            match (ties: nearest); one-step lazy rule (a position yields to
+//            a longer match at the next position); a wave-uniform walk over
+//            the match mask picks the greedy token starts; tokens go to a
+//            global list, histograms by LDS atomics; the step's positions are
+//            inserted into way (step mod 4) by atomicMax, so the newest
+//            position wins independently of execution order
+//   huffman  wave 0: optimal code lengths (parallel rank sort, two-queue
+//            merge), limited to 15/7 bits by the JPEG count adjustment
+//   choose   exact bit costs of stored / fixed / dynamic
+//   emit     per 256 tokens: bit lengths, block-wide exclusive scan, atomicOr
+//            into an LDS bit buffer; one coalesced copy into the chunk's slot
+// Then a scan of chunk extents, per-file wrapper/metadata, and packing, all on
+// device (no host synchronisation).
+#include <algorithm>
+#include <vector>
+
+#include "deflate_common.h"
 #include "kernels.h"
 
 namespace hz {
-hipError_t run_deflate(hipStream_t, Scratch&, const u8*, u64, u8*, u64, u32, u32*) {
-  return hipErrorNotSupported;
+namespace {
+
+constexpr u32 kThreads = 256;
+constexpr u32 kWaves = kThreads / 64;
+constexpr u32 kStep = kThreads;  // parse positions per step
+constexpr u32 kHashBits = 12;
+constexpr u32 kBuckets = 1u << kHashBits;
+constexpr u32 kWays = 4;
+constexpr u32 kNear = 8;
+constexpr u32 kMaxDist = 32768;
+constexpr u32 kHistory = 32768;
+constexpr u32 kLdsBudget = 160 * 1024;
+constexpr u32 kStageWords = 16384 + 64;  // bit buffer: a block of < 65540 bytes
+
+struct ChunkDesc {
+  u64 in_off;    // absolute input offset of the chunk
+  u64 file_off;  // chunk offset inside its file
+  u64 file_len;  // length of the chunk's file
+  u64 slot;      // byte offset of the chunk's slot
+  u32 len;       // chunk bytes
+  u32 hist;      // history bytes staged before the chunk (same file)
+  u32 file;
+  u32 last;      // last chunk of its file
+};
+
+struct FileDesc {
+  u64 in_off, in_len;     // input range
+  u64 out_off, capacity;  // padded output slot
+  u32 first_chunk, chunks;
+};
+
+struct ChunkResult {
+  u32 extent;   // compressed bytes of the chunk
+  u32 status;   // 0 or kCompressionOverflow
+  u64 adler_s;  // sum of bytes mod 65521
+  u64 adler_b;  // sum of (file_len - i) * byte over the chunk, mod 65521
+};
+
+struct HuffScratch {
+  u32 key[320];
+  u16 list[320];
+  u16 sorted[320];
+  u32 weight[640];
+  u16 parent[640];
+  u16 depth_count[320];
+};
+
+// Encoder LDS; the window follows it in dynamic shared memory.
+struct EncShared {
+  union {
+    u32 table[kBuckets * kWays];  // parse: position + 1 per way, 0 = empty
+    u32 stage[kStageWords];       // emit: the block's bits
+    HuffScratch huff;             // code-length construction
+  } u;
+  u32 ml[kStep];
+  u32 freq_ll[288];
+  u32 freq_d[32];
+  u32 freq_cl[20];
+  u8 len_ll[288];
+  u8 len_d[32];
+  u8 len_cl[20];
+  u16 code_ll[288];
+  u16 code_d[32];
+  u16 code_cl[20];
+  u16 rle[320];  // code-length RLE: symbol | extra << 5
+  u32 scan[kWaves];
+  u32 nrle, hlit, hdist, hclen, mode, extent, hdr_bits, extra_bits, ntok, status;
+  u64 red_s[kWaves], red_l[kWaves];
+};
+
+constexpr u32 kSharedBytes = (sizeof(EncShared) + 15) & ~u32(15);
+
+// Largest history that fits the LDS budget next to a chunk of `chunk` bytes.
+constexpr u32 history_limit(u32 chunk) {
+  return kLdsBudget - kSharedBytes - chunk - 32 < kHistory ? kLdsBudget - kSharedBytes - chunk - 32
+                                                           : kHistory;
 }
-hipError_t run_deflate_batch(hipStream_t, Scratch&, const u8*, u64, const BatchFile*, u32, u8*, u64,
-                             u32, u32*) {
-  return hipErrorNotSupported;
+static_assert(kSharedBytes + 65535 + 32 < kLdsBudget, "encoder LDS layout exceeds the budget");
+
+__device__ __forceinline__ u32 win_u32(const u32* win, u32 q) {
+  return __builtin_amdgcn_alignbyte(win[(q >> 2) + 1], win[q >> 2], q & 3);
 }
+
+__device__ __forceinline__ u32 win_byte(const u32* win, u32 q) {
+  return (win[q >> 2] >> (8 * (q & 3))) & 0xff;
+}
+
+__device__ __forceinline__ u32 hash4(u32 v) { return (v * 2654435761u) >> (32 - kHashBits); }
+
+// Length of the common prefix of window positions a < b, at most maxlen.
+__device__ __forceinline__ u32 match_len(const u32* win, u32 a, u32 b, u32 maxlen) {
+  u32 m = 0;
+  while (m < maxlen) {
+    const u32 x = win_u32(win, a + m) ^ win_u32(win, b + m);
+    if (x) return min(maxlen, m + (__builtin_ctz(x) >> 3));
+    m += 4;
+  }
+  return maxlen;
+}
+
+__device__ __forceinline__ u64 lanemask_lt() {
+  const u32 lane = lane_id();
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// RFC 1951 length code (257..285) and extra bits for a match length 3..258.
+__device__ __forceinline__ void length_code(u32 len, u32& sym, u32& nbits, u32& extra) {
+  if (len == 258) { sym = 285; nbits = 0; extra = 0; return; }
+  if (len < 11) { sym = 254 + len; nbits = 0; extra = 0; return; }
+  const u32 l = len - 3;
+  const u32 k = 31 - __builtin_clz(l);  // 3..7
+  sym = 257 + 4 * (k - 1) + ((l >> (k - 2)) & 3);
+  nbits = k - 2;
+  extra = l & ((1u << (k - 2)) - 1);
+}
+
+// Distance code (0..29) and extra bits for a distance 1..32768.
+__device__ __forceinline__ void dist_code(u32 d, u32& sym, u32& nbits, u32& extra) {
+  if (d <= 4) { sym = d - 1; nbits = 0; extra = 0; return; }
+  const u32 x = d - 1;
+  const u32 k = 31 - __builtin_clz(x);  // 2..14
+  sym = 2 * k + ((x >> (k - 1)) & 1);
+  nbits = k - 1;
+  extra = x & ((1u << (k - 1)) - 1);
+}
+
+__device__ __forceinline__ u32 fixed_len(u32 s) {
+  return s < 144 ? 8u : s < 256 ? 9u : s < 280 ? 7u : 8u;
+}
+
+// Code lengths for `n` symbols from frequencies, at most `limit` bits; called
+// by all 64 lanes of one wave.  At least two codes are always assigned
+// (zero-frequency symbols of lowest index get weight 1), so every code is
+// complete, as zlib's trees are.  Leaves are ranked by (weight, symbol) in
+// parallel; lane 0 runs the two-queue merge for optimal depths, folds depths
+// above the limit back with the JPEG count adjustment (ITU T.81 K.3, which
+// keeps the Kraft sum at 1) and gives the shortest lengths to the heaviest
+// symbols.
+__device__ void huffman_lengths(EncShared& sh, const u32* freq, u32 n, u32 limit, u8* len) {
+  HuffScratch& hs = sh.u.huff;
+  const u32 lane = lane_id();
+  u32 m = 0;
+  for (u32 base = 0; base < n; base += 64) {
+    const u32 s = base + lane;
+    const bool used = s < n && freq[s] != 0;
+    if (s < n) len[s] = 0;
+    const u64 bal = __ballot(used);
+    if (used) hs.list[m + __popcll(bal & lanemask_lt())] = u16(s);
+    m += __popcll(bal);
+  }
+  if (m < 2) {
+    for (u32 s = 0; m < 2 && s < n; ++s)
+      if (!freq[s]) {
+        if (!lane) hs.list[m] = u16(s);
+        ++m;
+      }
+  }
+  wave_sync();
+  for (u32 i = lane; i < m; i += 64) {
+    const u32 s = hs.list[i];
+    hs.key[i] = ((freq[s] ? freq[s] : 1u) << 9) | s;
+  }
+  wave_sync();
+  for (u32 i = lane; i < m; i += 64) {
+    const u32 k = hs.key[i];
+    u32 r = 0;
+    for (u32 j = 0; j < m; ++j) r += hs.key[j] < k;
+    hs.sorted[r] = u16(k & 511);
+  }
+  wave_sync();
+  if (!lane) {
+    for (u32 i = 0; i < m; ++i) {
+      const u32 s = hs.sorted[i];
+      hs.weight[i] = freq[s] ? freq[s] : 1u;
+    }
+    // Two-queue merge: nodes 0..m-1 are the sorted leaves, m.. internal.
+    u32 leaf = 0, inner = m, next = m;
+    for (u32 k = 0; k + 1 < m; ++k) {
+      u32 pick[2];
+      for (u32 t = 0; t < 2; ++t) {
+        if (leaf < m && (inner >= next || hs.weight[leaf] <= hs.weight[inner])) pick[t] = leaf++;
+        else pick[t] = inner++;
+      }
+      hs.weight[next] = hs.weight[pick[0]] + hs.weight[pick[1]];
+      hs.parent[pick[0]] = u16(next);
+      hs.parent[pick[1]] = u16(next);
+      ++next;
+    }
+    // Depths top down (a parent is created after its children).
+    const u32 root = next - 1;
+    for (u32 i = 0; i < 320; ++i) hs.depth_count[i] = 0;
+    hs.weight[root] = 0;
+    for (u32 v = root; v-- > m;) hs.weight[v] = hs.weight[hs.parent[v]] + 1;
+    u32 maxdepth = 0;
+    for (u32 i = 0; i < m; ++i) {
+      const u32 dep = hs.weight[hs.parent[i]] + 1;
+      ++hs.depth_count[dep];
+      if (dep > maxdepth) maxdepth = dep;
+    }
+    for (u32 i = maxdepth; i > limit; --i) {
+      while (hs.depth_count[i] > 0) {
+        u32 j = i - 2;
+        while (hs.depth_count[j] == 0) --j;
+        hs.depth_count[i] -= 2;
+        hs.depth_count[i - 1] += 1;
+        hs.depth_count[j + 1] += 2;
+        hs.depth_count[j] -= 1;
+      }
+    }
+    u32 l = 1, left = hs.depth_count[1];
+    for (u32 i = m; i-- > 0;) {
+      while (!left) left = hs.depth_count[++l];
+      len[hs.sorted[i]] = u8(l);
+      --left;
+    }
+  }
+  wave_sync();
+}
+
+// Canonical codes (bit-reversed for LSB-first output) from lengths; one lane.
+__device__ void canonical_codes(const u8* len, u32 n, u16* code) {
+  u32 count[16], next[16];
+  for (u32 i = 0; i < 16; ++i) count[i] = 0;
+  for (u32 s = 0; s < n; ++s) ++count[len[s]];
+  count[0] = 0;
+  u32 c = 0;
+  for (u32 b = 1; b < 16; ++b) {
+    c = (c + count[b - 1]) << 1;
+    next[b] = c;
+  }
+  for (u32 s = 0; s < n; ++s)
+    if (len[s]) code[s] = u16(bit_reverse(next[len[s]]++, len[s]));
+}
+
+// Code-length RLE of the literal/length and distance lengths; one lane.
+__device__ void rle_lengths(EncShared& sh) {
+  const u32 total = sh.hlit + sh.hdist;
+  u32 nr = 0, i = 0;
+  for (u32 s = 0; s < 20; ++s) sh.freq_cl[s] = 0;
+  auto at = [&](u32 k) -> u32 { return k < sh.hlit ? sh.len_ll[k] : sh.len_d[k - sh.hlit]; };
+  while (i < total) {
+    const u32 v = at(i);
+    u32 run = 1;
+    while (i + run < total && at(i + run) == v) ++run;
+    if (!v) {
+      u32 r = run;
+      while (r >= 11) {
+        const u32 t = r < 138 ? r : 138;
+        sh.rle[nr++] = u16(18 | ((t - 11) << 5));
+        ++sh.freq_cl[18];
+        r -= t;
+      }
+      if (r >= 3) {
+        sh.rle[nr++] = u16(17 | ((r - 3) << 5));
+        ++sh.freq_cl[17];
+        r = 0;
+      }
+      while (r--) {
+        sh.rle[nr++] = 0;
+        ++sh.freq_cl[0];
+      }
+    } else {
+      sh.rle[nr++] = u16(v);
+      ++sh.freq_cl[v];
+      u32 r = run - 1;
+      while (r >= 3) {
+        const u32 t = r < 6 ? r : 6;
+        sh.rle[nr++] = u16(16 | ((t - 3) << 5));
+        ++sh.freq_cl[16];
+        r -= t;
+      }
+      while (r--) {
+        sh.rle[nr++] = u16(v);
+        ++sh.freq_cl[v];
+      }
+    }
+    i += run;
+  }
+  sh.nrle = nr;
+}
+
+// Serial LSB-first writer into the LDS bit buffer (header and block tail);
+// ORs into words that the caller has cleared.
+struct StageWriter {
+  u32* words;
+  u32 pos;
+  __device__ __forceinline__ void put(u32 v, u32 n) {
+    if (!n) return;
+    const u32 w = pos >> 5, s = pos & 31;
+    const u64 x = u64(v) << s;
+    if (w < kStageWords) words[w] |= u32(x);
+    if (s + n > 32 && w + 1 < kStageWords) words[w + 1] |= u32(x >> 32);
+    pos += n;
+  }
+};
+
+__device__ __forceinline__ void or_bits(u32* words, u32 pos, u64 v) {
+  const u32 w = pos >> 5, s = pos & 31;
+  const u64 lo = v << s;
+  const u32 hi = s ? u32(v >> (64 - s)) : 0u;
+  if (u32(lo) && w < kStageWords) atomicOr(&words[w], u32(lo));
+  if (u32(lo >> 32) && w + 1 < kStageWords) atomicOr(&words[w + 1], u32(lo >> 32));
+  if (hi && w + 2 < kStageWords) atomicOr(&words[w + 2], hi);
+}
+
+// Block-wide exclusive scan of one u32 per thread; returns the prefix and
+// writes the total.  Contains barriers: every thread must call it.
+__device__ __forceinline__ u32 block_scan(EncShared& sh, u32 v, u32& total) {
+  const u32 lane = lane_id(), wave = threadIdx.x >> 6;
+  u32 x = v;
+  for (u32 off = 1; off < 64; off <<= 1) {
+    const u32 y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) sh.scan[wave] = x;
+  __syncthreads();
+  u32 before = 0;
+  total = 0;
+  for (u32 w = 0; w < kWaves; ++w) {
+    const u32 s = sh.scan[w];
+    if (w < wave) before += s;
+    total += s;
+  }
+  __syncthreads();
+  return before + x - v;
+}
+
+}  // namespace
+
+// Single-stream chunk and file descriptors.
+__global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 capacity,
+                               ChunkDesc* descs, FileDesc* file) {
+  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
+  const u64 stride = u64(gridDim.x) * blockDim.x;
+  const u64 slot_bytes = (u64(chunk) + 16 + 15) & ~u64(15);
+  for (u64 c = tid; c < chunks; c += stride) {
+    ChunkDesc d;
+    d.in_off = c * chunk;
+    d.file_off = d.in_off;
+    d.file_len = n;
+    d.len = u32(min<u64>(chunk, n - min<u64>(n, d.in_off)));
+    d.hist = u32(min<u64>(hist_max, d.in_off));
+    d.file = 0;
+    d.last = c + 1 == chunks;
+    d.slot = c * slot_bytes;
+    descs[c] = d;
+  }
+  if (!tid) {
+    file->in_off = 0;
+    file->in_len = n;
+    file->out_off = 0;
+    file->capacity = capacity;
+    file->first_chunk = 0;
+    file->chunks = chunks;
+  }
+}
+
+// One workgroup per chunk (grid-stride).  Dynamic LDS: EncShared + window.
+__global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDesc* descs,
+                                                     u32 chunks, u32 slot_bytes, u32* tokens,
+                                                     u8* slots, ChunkResult* results) {
+  extern __shared__ __align__(16) u8 dyn[];
+  EncShared& sh = *reinterpret_cast<EncShared*>(dyn);
+  u32* win = reinterpret_cast<u32*>(dyn + kSharedBytes);
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const ChunkDesc d = descs[c];
+    const u32 hist = d.hist, end = d.hist + d.len;
+
+    // ---- stage the window as aligned dwords; Adler partials of the chunk ----
+    {
+      const uintptr_t addr = reinterpret_cast<uintptr_t>(in + d.in_off - hist);
+      const u32 a = u32(addr & 3);
+      const u32* g = reinterpret_cast<const u32*>(addr - a);
+      const u32 nw = (end + 3) / 4;
+      u64 s = 0, l = 0;
+      for (u32 k = t; k < nw; k += kThreads) {
+        // Source dword k holds window byte 4k; dword k+1 is read only when it
+        // holds a window byte, so no dword outside the input is touched.
+        const u32 lo = g[k];
+        const u32 hi = (a && 4 * (k + 1) < a + end) ? g[k + 1] : 0u;
+        u32 v = a ? __builtin_amdgcn_alignbyte(hi, lo, a) : lo;
+        if (4 * k + 4 > end) v &= (1u << (8 * (end - 4 * k))) - 1;
+        win[k] = v;
+        if (4 * k + 4 > hist) {
+          for (u32 i = 0; i < 4; ++i) {
+            const u32 q = 4 * k + i;
+            const u32 b = (v >> (8 * i)) & 0xff;
+            if (q >= hist && q < end) {
+              s += b;
+              l += u64(q - hist) * b;
+            }
+          }
+        }
+      }
+      for (u32 k = nw + t; k < nw + 4; k += kThreads) win[k] = 0;
+      for (u32 off = 32; off; off >>= 1) {
+        s += __shfl_down(s, off, 64);
+        l += __shfl_down(l, off, 64);
+      }
+      if (!lane) {
+        sh.red_s[wave] = s;
+        sh.red_l[wave] = l;
+      }
+    }
+    for (u32 i = t; i < kBuckets * kWays; i += kThreads) sh.u.table[i] = 0;
+    for (u32 i = t; i < 288; i += kThreads) sh.freq_ll[i] = 0;
+    if (t < 32) sh.freq_d[t] = 0;
+    if (!t) sh.extra_bits = 0;
+    __syncthreads();
+
+    // ---- history positions enter the table ----
+    u32 stepno = 0;
+    for (u32 base = 0; base < hist; base += kStep, ++stepno) {
+      const u32 q = base + t;
+      if (q < hist && q + 4 <= end)
+        atomicMax(&sh.u.table[hash4(win_u32(win, q)) * kWays + (stepno & (kWays - 1))], q + 1);
+    }
+    __syncthreads();
+
+    // ---- parse ----
+    u32* tok = tokens + d.in_off;
+    u32 ntok = 0, extra = 0;
+    for (u32 p = hist; p < end;) {
+      const u32 q = p + t;
+      const bool hashable = q + 4 <= end;
+      const u32 v = hashable ? win_u32(win, q) : 0u;
+      const u32 h = hashable ? hash4(v) : kBuckets + t;  // unique stand-in: never a bucket
+      u32 near = 0;
+      for (u32 k = kNear; k >= 1; --k) {
+        const u32 hk = __shfl_up(h, k, 64);
+        if (lane >= k && hk == h) near = k;
+      }
+      u32 best_len = 0, best_dist = 0;
+      if (hashable) {
+        const u32 maxlen = min(258u, end - q);
+        const uint4 e = *reinterpret_cast<const uint4*>(&sh.u.table[h * kWays]);
+        const u32 ent[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+        for (u32 k = 0; k < kWays; ++k) {
+          if (!ent[k]) continue;
+          const u32 cand = ent[k] - 1;
+          if (cand >= q || q - cand > kMaxDist) continue;
+          const u32 m = match_len(win, cand, q, maxlen);
+          if (m > best_len || (m == best_len && q - cand < best_dist)) {
+            best_len = m;
+            best_dist = q - cand;
+          }
+        }
+        if (near) {
+          const u32 m = match_len(win, q - near, q, maxlen);
+          if (m > best_len || (m == best_len && near < best_dist)) {
+            best_len = m;
+            best_dist = near;
+          }
+        }
+      }
+      sh.ml[t] = best_len >= 3 ? best_len : 0u;
+      __syncthreads();
+
+      // Lazy rule and the greedy walk, computed identically by every wave.
+      u32 Lr[kWaves];
+      u64 mask[kWaves];
+#pragma unroll
+      for (u32 r = 0; r < kWaves; ++r) {
+        const u32 j = r * 64 + lane;
+        const u32 cur_ml = sh.ml[j];
+        const u32 next_ml = j + 1 < kStep ? sh.ml[j + 1] : 0u;
+        Lr[r] = (cur_ml && next_ml <= cur_ml) ? cur_ml : 0u;
+        mask[r] = __ballot(Lr[r] != 0);
+      }
+      const u32 lim = min(kStep, end - p);
+      u64 starts[kWaves] = {};
+      u32 cur = 0;
+      while (cur < lim) {
+        u32 nxt = lim;
+        for (u32 r = cur >> 6; r < kWaves; ++r) {
+          u64 mm = mask[r];
+          if (r == (cur >> 6)) mm &= ~0ull << (cur & 63);
+          if (mm) {
+            nxt = r * 64 + __builtin_ctzll(mm);
+            break;
+          }
+        }
+        if (nxt > lim) nxt = lim;
+        // Literals at [cur, nxt).
+        for (u32 r = cur >> 6; r < kWaves && r * 64 < nxt; ++r) {
+          const u32 lo = max(cur, r * 64) - r * 64, hi = min(nxt, r * 64 + 64) - r * 64;
+          const u64 bits = (hi == 64 ? ~0ull : ((1ull << hi) - 1)) & ~((1ull << lo) - 1);
+          starts[r] |= bits;
+        }
+        if (nxt >= lim) {
+          cur = nxt;
+          break;
+        }
+        const u32 r = nxt >> 6;
+        starts[r] |= 1ull << (nxt & 63);
+        const u32 sel = r == 0 ? Lr[0] : r == 1 ? Lr[1] : r == 2 ? Lr[2] : Lr[3];
+        cur = nxt + __builtin_amdgcn_readlane(sel, nxt & 63);
+      }
+
+      // Tokens of this thread's position.
+      u32 before = 0, step_tokens = 0;
+#pragma unroll
+      for (u32 r = 0; r < kWaves; ++r) {
+        const u32 cnt = __popcll(starts[r]);
+        if (r < wave) before += cnt;
+        step_tokens += cnt;
+      }
+      const u64 mine = wave == 0 ? starts[0] : wave == 1 ? starts[1] : wave == 2 ? starts[2] : starts[3];
+      if ((mine >> lane) & 1) {
+        const u32 idx = ntok + before + __popcll(mine & lanemask_lt());
+        const u32 L = wave == 0 ? Lr[0] : wave == 1 ? Lr[1] : wave == 2 ? Lr[2] : Lr[3];
+        if (L) {
+          u32 ls, lb, lx, ds, db, dx;
+          length_code(L, ls, lb, lx);
+          dist_code(best_dist, ds, db, dx);
+          atomicAdd(&sh.freq_ll[ls], 1u);
+          atomicAdd(&sh.freq_d[ds], 1u);
+          extra += lb + db;
+          tok[idx] = 0x80000000u | ((L - 3) << 16) | (best_dist - 1);
+        } else {
+          const u32 lit = hashable ? (v & 0xff) : win_byte(win, q);
+          atomicAdd(&sh.freq_ll[lit], 1u);
+          tok[idx] = lit;
+        }
+      }
+      ntok += step_tokens;
+      if (hashable) atomicMax(&sh.u.table[h * kWays + (stepno & (kWays - 1))], q + 1);
+      ++stepno;
+      p += cur;
+      __syncthreads();
+    }
+    if (extra) atomicAdd(&sh.extra_bits, extra);
+    if (!t) {
+      sh.ntok = ntok;
+      sh.freq_ll[256] += 1;  // end of block
+    }
+    __syncthreads();
+
+    // ---- code lengths, costs, block type (wave 0) ----
+    if (wave == 0) {
+      huffman_lengths(sh, sh.freq_ll, 286, 15, sh.len_ll);
+      huffman_lengths(sh, sh.freq_d, 30, 15, sh.len_d);
+      if (!lane) {
+        u32 hl = 286, hd = 30;
+        while (hl > 257 && !sh.len_ll[hl - 1]) --hl;
+        while (hd > 1 && !sh.len_d[hd - 1]) --hd;
+        sh.hlit = hl;
+        sh.hdist = hd;
+        rle_lengths(sh);
+      }
+      wave_sync();
+      huffman_lengths(sh, sh.freq_cl, 19, 7, sh.len_cl);
+      u32 dyn_bits = 0, fix_bits = 0, hdr = 0;
+      for (u32 sy = lane; sy < 286; sy += 64) {
+        dyn_bits += sh.freq_ll[sy] * sh.len_ll[sy];
+        fix_bits += sh.freq_ll[sy] * fixed_len(sy);
+      }
+      if (lane < 30) {
+        dyn_bits += sh.freq_d[lane] * sh.len_d[lane];
+        fix_bits += sh.freq_d[lane] * 5;
+      }
+      for (u32 i = lane; i < sh.nrle; i += 64) {
+        const u32 sy = sh.rle[i] & 31;
+        hdr += sh.len_cl[sy] + (sy == 16 ? 2 : sy == 17 ? 3 : sy == 18 ? 7 : 0);
+      }
+      for (u32 off = 32; off; off >>= 1) {
+        dyn_bits += __shfl_down(dyn_bits, off, 64);
+        fix_bits += __shfl_down(fix_bits, off, 64);
+        hdr += __shfl_down(hdr, off, 64);
+      }
+      if (!lane) {
+        u32 hc = 19;
+        while (hc > 4 && !sh.len_cl[cl_order(hc - 1)]) --hc;
+        sh.hclen = hc;
+        hdr += 3 + 14 + 3 * hc;
+        const u64 dyn_total = u64(hdr) + dyn_bits + sh.extra_bits;
+        const u64 fix_total = 3ull + fix_bits + sh.extra_bits;
+        auto extent = [&](u64 bits) -> u64 {
+          return d.last ? (bits + 7) / 8 : (bits + 3 + 7) / 8 + 4;
+        };
+        const u64 e_stored = u64(d.len) + 5, e_fixed = extent(fix_total), e_dyn = extent(dyn_total);
+        // Ties keep stored before fixed before dynamic (the reference's order, E:312-356).
+        u32 mode = 0;
+        u64 best = e_stored;
+        if (e_fixed < best) { mode = 1; best = e_fixed; }
+        if (e_dyn < best) { mode = 2; best = e_dyn; }
+        sh.mode = mode;
+        sh.extent = u32(best);
+        sh.hdr_bits = mode == 2 ? hdr : 3u;
+        sh.status = 0;
+        if (mode == 1) {
+          for (u32 i = 0; i < 288; ++i) sh.len_ll[i] = u8(fixed_len(i));
+          for (u32 i = 0; i < 30; ++i) sh.len_d[i] = 5;
+        }
+        if (mode) {
+          canonical_codes(sh.len_ll, mode == 1 ? 288 : 286, sh.code_ll);
+          canonical_codes(sh.len_d, 30, sh.code_d);
+          if (mode == 2) canonical_codes(sh.len_cl, 19, sh.code_cl);
+        }
+        const u64 S = (sh.red_s[0] + sh.red_s[1] + sh.red_s[2] + sh.red_s[3]) % kAdlerMod;
+        const u64 L = (sh.red_l[0] + sh.red_l[1] + sh.red_l[2] + sh.red_l[3]) % kAdlerMod;
+        results[c].adler_s = S;
+        results[c].adler_b =
+            (((d.file_len - d.file_off) % kAdlerMod) * S + kAdlerMod - L) % kAdlerMod;
+      }
+    }
+    __syncthreads();
+
+    // ---- emission ----
+    const u32 mode = sh.mode;
+    u8* slot = slots + d.slot;
+    if (mode == 0) {
+      if (!t) {
+        slot[0] = u8(d.last ? 1 : 0);
+        slot[1] = u8(d.len & 0xff);
+        slot[2] = u8(d.len >> 8);
+        slot[3] = u8(~d.len & 0xff);
+        slot[4] = u8((~d.len >> 8) & 0xff);
+      }
+      for (u32 i = t; i < d.len; i += kThreads) slot[5 + i] = u8(win_byte(win, hist + i));
+      if (!t) {
+        results[c].extent = sh.extent;
+        results[c].status = 0;
+      }
+    } else {
+      const u32 words = (sh.extent + 3) / 4 + 1;
+      for (u32 i = t; i < words && i < kStageWords; i += kThreads) sh.u.stage[i] = 0;
+      __syncthreads();
+      if (!t) {
+        StageWriter out = {sh.u.stage, 0};
+        out.put(d.last ? 1u : 0u, 1);
+        out.put(mode == 1 ? 1u : 2u, 2);
+        if (mode == 2) {
+          out.put(sh.hlit - 257, 5);
+          out.put(sh.hdist - 1, 5);
+          out.put(sh.hclen - 4, 4);
+          for (u32 i = 0; i < sh.hclen; ++i) out.put(sh.len_cl[cl_order(i)], 3);
+          for (u32 i = 0; i < sh.nrle; ++i) {
+            const u32 sy = sh.rle[i] & 31, x = sh.rle[i] >> 5;
+            out.put(sh.code_cl[sy], sh.len_cl[sy]);
+            if (sy == 16) out.put(x, 2);
+            else if (sy == 17) out.put(x, 3);
+            else if (sy == 18) out.put(x, 7);
+          }
+        }
+        if (out.pos != sh.hdr_bits) sh.status = kCompressionOverflow;
+      }
+      __syncthreads();
+      u32 pos = sh.hdr_bits;
+      const u32 ntokens = sh.ntok;
+      for (u32 base = 0; base < ntokens; base += kThreads) {
+        const u32 i = base + t;
+        u64 bits = 0;
+        u32 nbits = 0;
+        if (i < ntokens) {
+          const u32 tk = tok[i];
+          if (!(tk >> 31)) {
+            bits = sh.code_ll[tk];
+            nbits = sh.len_ll[tk];
+          } else {
+            const u32 ml = ((tk >> 16) & 0xff) + 3, md = (tk & 0xffff) + 1;
+            u32 ls, lb, lx, ds, db, dx;
+            length_code(ml, ls, lb, lx);
+            dist_code(md, ds, db, dx);
+            bits = sh.code_ll[ls];
+            nbits = sh.len_ll[ls];
+            bits |= u64(lx) << nbits;
+            nbits += lb;
+            bits |= u64(sh.code_d[ds]) << nbits;
+            nbits += sh.len_d[ds];
+            bits |= u64(dx) << nbits;
+            nbits += db;
+          }
+        }
+        u32 total;
+        const u32 off = block_scan(sh, nbits, total);
+        if (nbits) or_bits(sh.u.stage, pos + off, bits);
+        pos += total;
+      }
+      __syncthreads();
+      if (!t) {
+        StageWriter out = {sh.u.stage, pos};
+        out.put(sh.code_ll[256], sh.len_ll[256]);
+        if (!d.last) {
+          out.put(0, 3);
+          if (out.pos & 7) out.pos += 8 - (out.pos & 7);
+          out.put(0, 16);
+          out.put(0xffff, 16);
+        }
+        const u32 bytes = (out.pos + 7) / 8;
+        if (bytes != sh.extent) sh.status = kCompressionOverflow;
+        results[c].extent = sh.extent;
+      }
+      __syncthreads();
+      const u32 copy_words = min((sh.extent + 3) / 4, slot_bytes / 4);
+      u32* slot32 = reinterpret_cast<u32*>(slot);
+      for (u32 i = t; i < copy_words; i += kThreads) slot32[i] = sh.u.stage[i];
+      if (!t) results[c].status = sh.status;
+    }
+    __syncthreads();
+  }
+}
+
+// One workgroup: exclusive scan of chunk extents and Adler partial sums.
+__global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 chunks, u64* sums) {
+  __shared__ u64 pe[1024], ps[1024], pb[1024];
+  const u32 t = threadIdx.x;
+  const u64 per = (u64(chunks) + 1023) / 1024;
+  const u64 lo = min<u64>(chunks, t * per), hi = min<u64>(chunks, lo + per);
+  u64 e = 0, s = 0, b = 0;
+  for (u64 i = lo; i < hi; ++i) {
+    e += results[i].extent;
+    s += results[i].adler_s;
+    b += results[i].adler_b;
+  }
+  pe[t] = e;
+  ps[t] = s;
+  pb[t] = b;
+  __syncthreads();
+  for (u32 off = 1; off < 1024; off <<= 1) {
+    const u64 xe = t >= off ? pe[t - off] : 0, xs = t >= off ? ps[t - off] : 0,
+              xb = t >= off ? pb[t - off] : 0;
+    __syncthreads();
+    pe[t] += xe;
+    ps[t] += xs;
+    pb[t] += xb;
+    __syncthreads();
+  }
+  u64 re = pe[t] - e, rs = ps[t] - s, rb = pb[t] - b;
+  for (u64 i = lo; i < hi; ++i) {
+    sums[3 * i] = re;
+    sums[3 * i + 1] = rs;
+    sums[3 * i + 2] = rb;
+    re += results[i].extent;
+    rs += results[i].adler_s;
+    rb += results[i].adler_b;
+  }
+  if (t == 1023) {
+    sums[3 * u64(chunks)] = re;
+    sums[3 * u64(chunks) + 1] = rs;
+    sums[3 * u64(chunks) + 2] = rb;
+  }
+}
+
+// Per file: status, wrapper and metadata [length, status].
+__global__ void e_wrap(const FileDesc* files, u32 count, const ChunkResult* results,
+                       const u64* sums, u8* out, u32* meta, u32* file_ok) {
+  const u32 tid = blockIdx.x * blockDim.x + threadIdx.x;
+  for (u32 fi = tid; fi < count; fi += gridDim.x * blockDim.x) {
+    const FileDesc f = files[fi];
+    u32 status = 0;
+    for (u32 k = 0; k < f.chunks; ++k)
+      if (results[f.first_chunk + k].status) status = kCompressionOverflow;
+    const u64 a0 = f.first_chunk, a1 = f.first_chunk + f.chunks;
+    const u64 body = sums[3 * a1] - sums[3 * a0];
+    const u64 total = body + 6;
+    if (total > f.capacity) status = kCompressionOverflow;
+    file_ok[fi] = status ? 0u : 1u;
+    if (status) {
+      meta[2 * u64(fi)] = 0;
+      meta[2 * u64(fi) + 1] = status;
+      continue;
+    }
+    const u64 S = (sums[3 * a1 + 1] - sums[3 * a0 + 1]) % kAdlerMod;
+    const u64 B = (sums[3 * a1 + 2] - sums[3 * a0 + 2] + f.in_len) % kAdlerMod;
+    const u32 adler = u32((B << 16) | ((S + 1) % kAdlerMod));
+    u8* o = out + f.out_off;
+    o[0] = 0x78;
+    o[1] = 0x01;
+    o[total - 4] = u8(adler >> 24);
+    o[total - 3] = u8(adler >> 16);
+    o[total - 2] = u8(adler >> 8);
+    o[total - 1] = u8(adler);
+    meta[2 * u64(fi)] = u32(total);
+    meta[2 * u64(fi) + 1] = 0;
+  }
+}
+
+// Copy chunk slots to their final places (after each file's 2-byte header).
+__global__ __launch_bounds__(256) void e_pack(const ChunkDesc* descs, const FileDesc* files,
+                                              u32 chunks, const ChunkResult* results,
+                                              const u64* sums, const u8* slots, u8* out,
+                                              const u32* file_ok) {
+  for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const ChunkDesc d = descs[c];
+    const FileDesc f = files[d.file];
+    if (!file_ok[d.file]) continue;
+    const u64 rel = sums[3 * u64(c)] - sums[3 * u64(f.first_chunk)];
+    u8* dst = out + f.out_off + 2 + rel;
+    const u8* src = slots + d.slot;
+    const u32 n = results[c].extent;
+    for (u32 i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+namespace {
+
+#define HZ_TRY(expr)                 \
+  do {                               \
+    hipError_t _e = (expr);          \
+    if (_e != hipSuccess) return _e; \
+  } while (0)
+
+u64 slot_size(u32 chunk_bytes) { return (u64(chunk_bytes) + 16 + 15) & ~u64(15); }
+
+hipError_t run_chunks(hipStream_t stream, Scratch& scratch, const u8* in, const ChunkDesc* descs,
+                      u64 chunks, const FileDesc* files, u32 file_count, u64 in_total, u8* out,
+                      u32 chunk_bytes, u32* meta) {
+  u32* tokens = nullptr;
+  u8* slots = nullptr;
+  ChunkResult* results = nullptr;
+  u64* sums = nullptr;
+  u32* file_ok = nullptr;
+  const u64 slot_bytes = slot_size(chunk_bytes);
+  HZ_TRY(scratch.alloc(&tokens, in_total ? in_total : 1));
+  HZ_TRY(scratch.alloc(&slots, chunks * slot_bytes));
+  HZ_TRY(scratch.alloc(&results, chunks));
+  HZ_TRY(scratch.alloc(&sums, 3 * (chunks + 1)));
+  HZ_TRY(scratch.alloc(&file_ok, file_count));
+  const u32 lds = kSharedBytes + history_limit(chunk_bytes) + chunk_bytes + 32;
+  HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_encode),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  const u32 grid = u32(chunks < 65536 ? chunks : 65536);
+  HZ_LAUNCH(e_encode, dim3(grid), dim3(kThreads), lds, stream, in, descs, u32(chunks),
+            u32(slot_bytes), tokens, slots, results);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, results, u32(chunks), sums);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, files, file_count,
+            results, sums, out, meta, file_ok);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(e_pack, dim3(u32(chunks < 65536 ? chunks : 65536)), dim3(256), 0, stream, descs,
+            files, u32(chunks), results, sums, slots, out, file_ok);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
+                       u64 capacity, u32 chunk_bytes, u32* meta) {
+  const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
+  ChunkDesc* descs = nullptr;
+  FileDesc* file = nullptr;
+  HZ_TRY(scratch.alloc(&descs, chunks));
+  HZ_TRY(scratch.alloc(&file, 1));
+  HZ_LAUNCH(e_single_descs, dim3(u32(std::min<u64>(1024, (chunks + 255) / 256))), dim3(256), 0,
+            stream, in_size, chunk_bytes, u32(chunks), history_limit(chunk_bytes), capacity, descs,
+            file);
+  HZ_TRY(hipGetLastError());
+  return run_chunks(stream, scratch, in, descs, chunks, file, 1, in_size, out, chunk_bytes, meta);
+}
+
+hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_total,
+                             const BatchFile* files_host, u32 count, u8* out, u64 out_total,
+                             u32 chunk_bytes, u32* meta) {
+  (void)out_total;
+  std::vector<ChunkDesc> descs;
+  std::vector<FileDesc> files(count);
+  const u64 slot_bytes = slot_size(chunk_bytes);
+  const u32 hist_max = history_limit(chunk_bytes);
+  for (u32 f = 0; f < count; ++f) {
+    const BatchFile& b = files_host[f];
+    const u64 n = b.in_size;
+    const u64 k = n ? (n + chunk_bytes - 1) / chunk_bytes : 1;
+    files[f] = {b.in_offset, n, b.out_offset, b.out_size, u32(descs.size()), u32(k)};
+    for (u64 j = 0; j < k; ++j) {
+      ChunkDesc d;
+      d.in_off = b.in_offset + j * chunk_bytes;
+      d.file_off = j * chunk_bytes;
+      d.file_len = n;
+      d.len = u32(std::min<u64>(chunk_bytes, n - std::min<u64>(n, j * chunk_bytes)));
+      d.hist = u32(std::min<u64>(hist_max, j * chunk_bytes));
+      d.file = f;
+      d.last = j + 1 == k;
+      d.slot = descs.size() * slot_bytes;
+      descs.push_back(d);
+    }
+  }
+  ChunkDesc* ddescs = nullptr;
+  FileDesc* dfiles = nullptr;
+  HZ_TRY(scratch.alloc(&ddescs, descs.size()));
+  HZ_TRY(scratch.alloc(&dfiles, count));
+  // Pageable sources: the runtime copies them before these calls return.
+  HZ_TRY(hipMemcpyAsync(ddescs, descs.data(), descs.size() * sizeof(ChunkDesc),
+                        hipMemcpyHostToDevice, stream));
+  HZ_TRY(hipMemcpyAsync(dfiles, files.data(), count * sizeof(FileDesc), hipMemcpyHostToDevice,
+                        stream));
+  return run_chunks(stream, scratch, in, ddescs, descs.size(), dfiles, count, in_total, out,
+                    chunk_bytes, meta);
+}
+
 }  // namespace hz

@@ -29,10 +29,10 @@ void profile_record(const char* name, hipEvent_t start, hipEvent_t stop);
     const bool hz_prof_ = ::hz::profiling_enabled();                           \
     if (hz_prof_ && hipEventCreate(&hz_start_) == hipSuccess &&                \
         hipEventCreate(&hz_stop_) == hipSuccess)                               \
-      hipEventRecord(hz_start_, stream);                                       \
+      (void)hipEventRecord(hz_start_, stream);                                 \
     hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);       \
     if (hz_prof_ && hz_stop_) {                                                \
-      hipEventRecord(hz_stop_, stream);                                        \
+      (void)hipEventRecord(hz_stop_, stream);                                  \
       ::hz::profile_record(#kernel, hz_start_, hz_stop_);                      \
     }                                                                          \
   } while (0)
