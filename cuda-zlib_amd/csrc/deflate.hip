@@ -749,45 +749,40 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
   }
 }
 
-// One workgroup: exclusive scan of chunk extents and Adler partial sums.
+// One workgroup: exclusive scans of chunk extents, Adler partial sums and
+// failed-chunk counts; sums[4 * i + k] holds the prefix before chunk i.
 __global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 chunks, u64* sums) {
-  __shared__ u64 pe[1024], ps[1024], pb[1024];
+  __shared__ u64 part[4][1024];
   const u32 t = threadIdx.x;
   const u64 per = (u64(chunks) + 1023) / 1024;
   const u64 lo = min<u64>(chunks, t * per), hi = min<u64>(chunks, lo + per);
-  u64 e = 0, s = 0, b = 0;
+  u64 acc[4] = {0, 0, 0, 0};
   for (u64 i = lo; i < hi; ++i) {
-    e += results[i].extent;
-    s += results[i].adler_s;
-    b += results[i].adler_b;
+    acc[0] += results[i].extent;
+    acc[1] += results[i].adler_s;
+    acc[2] += results[i].adler_b;
+    acc[3] += results[i].status != 0;
   }
-  pe[t] = e;
-  ps[t] = s;
-  pb[t] = b;
+  for (u32 k = 0; k < 4; ++k) part[k][t] = acc[k];
   __syncthreads();
   for (u32 off = 1; off < 1024; off <<= 1) {
-    const u64 xe = t >= off ? pe[t - off] : 0, xs = t >= off ? ps[t - off] : 0,
-              xb = t >= off ? pb[t - off] : 0;
+    u64 x[4];
+    for (u32 k = 0; k < 4; ++k) x[k] = t >= off ? part[k][t - off] : 0;
     __syncthreads();
-    pe[t] += xe;
-    ps[t] += xs;
-    pb[t] += xb;
+    for (u32 k = 0; k < 4; ++k) part[k][t] += x[k];
     __syncthreads();
   }
-  u64 re = pe[t] - e, rs = ps[t] - s, rb = pb[t] - b;
+  u64 run[4];
+  for (u32 k = 0; k < 4; ++k) run[k] = part[k][t] - acc[k];
   for (u64 i = lo; i < hi; ++i) {
-    sums[3 * i] = re;
-    sums[3 * i + 1] = rs;
-    sums[3 * i + 2] = rb;
-    re += results[i].extent;
-    rs += results[i].adler_s;
-    rb += results[i].adler_b;
+    for (u32 k = 0; k < 4; ++k) sums[4 * i + k] = run[k];
+    run[0] += results[i].extent;
+    run[1] += results[i].adler_s;
+    run[2] += results[i].adler_b;
+    run[3] += results[i].status != 0;
   }
-  if (t == 1023) {
-    sums[3 * u64(chunks)] = re;
-    sums[3 * u64(chunks) + 1] = rs;
-    sums[3 * u64(chunks) + 2] = rb;
-  }
+  if (t == 1023)
+    for (u32 k = 0; k < 4; ++k) sums[4 * u64(chunks) + k] = run[k];
 }
 
 // Per file: status, wrapper and metadata [length, status].
@@ -796,11 +791,9 @@ __global__ void e_wrap(const FileDesc* files, u32 count, const ChunkResult* resu
   const u32 tid = blockIdx.x * blockDim.x + threadIdx.x;
   for (u32 fi = tid; fi < count; fi += gridDim.x * blockDim.x) {
     const FileDesc f = files[fi];
-    u32 status = 0;
-    for (u32 k = 0; k < f.chunks; ++k)
-      if (results[f.first_chunk + k].status) status = kCompressionOverflow;
     const u64 a0 = f.first_chunk, a1 = f.first_chunk + f.chunks;
-    const u64 body = sums[3 * a1] - sums[3 * a0];
+    u32 status = sums[4 * a1 + 3] != sums[4 * a0 + 3] ? kCompressionOverflow : 0u;
+    const u64 body = sums[4 * a1] - sums[4 * a0];
     const u64 total = body + 6;
     if (total > f.capacity) status = kCompressionOverflow;
     file_ok[fi] = status ? 0u : 1u;
@@ -809,8 +802,8 @@ __global__ void e_wrap(const FileDesc* files, u32 count, const ChunkResult* resu
       meta[2 * u64(fi) + 1] = status;
       continue;
     }
-    const u64 S = (sums[3 * a1 + 1] - sums[3 * a0 + 1]) % kAdlerMod;
-    const u64 B = (sums[3 * a1 + 2] - sums[3 * a0 + 2] + f.in_len) % kAdlerMod;
+    const u64 S = (sums[4 * a1 + 1] - sums[4 * a0 + 1]) % kAdlerMod;
+    const u64 B = (sums[4 * a1 + 2] - sums[4 * a0 + 2] + f.in_len) % kAdlerMod;
     const u32 adler = u32((B << 16) | ((S + 1) % kAdlerMod));
     u8* o = out + f.out_off;
     o[0] = 0x78;
@@ -833,7 +826,7 @@ __global__ __launch_bounds__(256) void e_pack(const ChunkDesc* descs, const File
     const ChunkDesc d = descs[c];
     const FileDesc f = files[d.file];
     if (!file_ok[d.file]) continue;
-    const u64 rel = sums[3 * u64(c)] - sums[3 * u64(f.first_chunk)];
+    const u64 rel = sums[4 * u64(c)] - sums[4 * u64(f.first_chunk)];
     u8* dst = out + f.out_off + 2 + rel;
     const u8* src = slots + d.slot;
     const u32 n = results[c].extent;
@@ -863,7 +856,7 @@ hipError_t run_chunks(hipStream_t stream, Scratch& scratch, const u8* in, const 
   HZ_TRY(scratch.alloc(&tokens, in_total ? in_total : 1));
   HZ_TRY(scratch.alloc(&slots, chunks * slot_bytes));
   HZ_TRY(scratch.alloc(&results, chunks));
-  HZ_TRY(scratch.alloc(&sums, 3 * (chunks + 1)));
+  HZ_TRY(scratch.alloc(&sums, 4 * (chunks + 1)));
   HZ_TRY(scratch.alloc(&file_ok, file_count));
   const u32 lds = kSharedBytes + history_limit(chunk_bytes) + chunk_bytes + 32;
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_encode),
