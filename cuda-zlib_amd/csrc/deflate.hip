@@ -1,5 +1,4 @@
-// Chunked zlib encoder: one 256-thread workgroup (4 waves) per chunk
-// (default 32 KiB).
+// Chunked zlib encoder (default 32 KiB chunks).
 //
 // Stream layout (the reference's compress path, native/codec_ffi.cu:551-612,
 // encoder E:283-418): header 78 01; every chunk is one block of the cheapest
@@ -11,24 +10,31 @@
 //
 // Unlike the reference, a chunk's LZ77 window includes up to 32 KiB of the
 // same input before it (the decoder has already produced those bytes), which
-// keeps the ratio below whole-stream zlib level 1.  Per chunk:
+// keeps the ratio below whole-stream zlib level 1.
+//
+// e_parse, one 1024-thread workgroup per chunk (the LDS holds the window and
+// the hash table, so one workgroup per CU; 16 waves hide LDS latency):
 //   stage    window (history + chunk) into LDS as aligned dwords; Adler-32
 //            partial sums of the chunk bytes
 //   history  every history position enters the hash table
-//   parse    steps of 256 positions, one per thread: 4-byte hash into 4096
-//            buckets x 4 ways, candidates = the bucket plus the nearest of the
+//   parse    steps of 1024 positions, one per thread: 4-byte hash into 4096
+//            buckets x 4 ways; candidates = the bucket plus the nearest of the
 //            8 previous positions of the same wave with an equal hash; longest
-//            match (ties: nearest); one-step lazy rule (a position yields to
-//            a longer match at the next position); a wave-uniform walk over
-//            the match mask picks the greedy token starts; tokens go to a
-//            global list, histograms by LDS atomics; the step's positions are
-//            inserted into way (step mod 4) by atomicMax, so the newest
-//            position wins independently of execution order
+//            match (ties: nearest); one-step lazy rule (a position yields to a
+//            longer match at the next position).  With f(j) = j + max(1, L_j)
+//            the greedy token starts are the orbit of 0 under f, found by
+//            pointer doubling in log2(1024) rounds: round b marks
+//            f^(2^b)(x) for every marked x and squares the jump table.
+//            Tokens go to a global list, histograms by LDS atomics; the step's
+//            positions are inserted into way (step mod 4) by atomicMax, so the
+//            newest position wins independently of execution order.
+// e_emit, one 256-thread workgroup per chunk (small LDS, several per CU):
 //   huffman  wave 0: optimal code lengths (parallel rank sort, two-queue
 //            merge), limited to 15/7 bits by the JPEG count adjustment
 //   choose   exact bit costs of stored / fixed / dynamic
-//   emit     per 256 tokens: bit lengths, block-wide exclusive scan, atomicOr
-//            into an LDS bit buffer; one coalesced copy into the chunk's slot
+//   emit     4 tokens per thread per round: bit lengths, block-wide
+//            exclusive scan, atomicOr into an LDS bit buffer; one coalesced
+//            copy into the chunk's slot
 // Then a scan of chunk extents, per-file wrapper/metadata, and packing, all on
 // device (no host synchronisation).
 #include <algorithm>
@@ -40,9 +46,10 @@
 namespace hz {
 namespace {
 
-constexpr u32 kThreads = 256;
-constexpr u32 kWaves = kThreads / 64;
-constexpr u32 kStep = kThreads;  // parse positions per step
+constexpr u32 kParseThreads = 1024;
+constexpr u32 kParseWaves = kParseThreads / 64;
+constexpr u32 kStep = kParseThreads;  // parse positions per step
+constexpr u32 kLog2Step = 10;
 constexpr u32 kHashBits = 12;
 constexpr u32 kBuckets = 1u << kHashBits;
 constexpr u32 kWays = 4;
@@ -50,7 +57,9 @@ constexpr u32 kNear = 8;
 constexpr u32 kMaxDist = 32768;
 constexpr u32 kHistory = 32768;
 constexpr u32 kLdsBudget = 160 * 1024;
-constexpr u32 kStageWords = 16384 + 64;  // bit buffer: a block of < 65540 bytes
+constexpr u32 kEmitThreads = 256;
+constexpr u32 kEmitWaves = kEmitThreads / 64;
+constexpr u32 kTokensPerThread = 4;
 
 struct ChunkDesc {
   u64 in_off;    // absolute input offset of the chunk
@@ -69,12 +78,44 @@ struct FileDesc {
   u32 first_chunk, chunks;
 };
 
+// Parse results of one chunk, consumed by e_emit.
+struct ChunkStats {
+  u32 freq_ll[288];
+  u32 freq_d[32];
+  u32 ntok;
+  u32 extra_bits;  // length and distance extra bits of all matches
+  u64 sum_s;       // sum of the chunk bytes
+  u64 sum_l;       // sum of (offset in chunk) * byte
+};
+
 struct ChunkResult {
   u32 extent;   // compressed bytes of the chunk
   u32 status;   // 0 or kCompressionOverflow
   u64 adler_s;  // sum of bytes mod 65521
   u64 adler_b;  // sum of (file_len - i) * byte over the chunk, mod 65521
 };
+
+struct ParseShared {
+  u32 table[kBuckets * kWays];  // position + 1 per way, 0 = empty
+  u16 ml[kStep];                // match length per step position (0: none)
+  u16 jump[2][kStep + 1];       // pointer-doubling tables
+  u8 mark[kStep + 4];           // token starts (orbit of 0)
+  u32 freq_ll[288];
+  u32 freq_d[32];
+  u32 wave_count[kParseWaves];
+  u32 wave_end[kParseWaves];
+  u32 extra_bits;
+  u64 red_s[kParseWaves], red_l[kParseWaves];
+};
+
+constexpr u32 kParseShared = (sizeof(ParseShared) + 15) & ~u32(15);
+
+// Largest history that fits the LDS budget next to a chunk of `chunk` bytes.
+constexpr u32 history_limit(u32 chunk) {
+  return kLdsBudget - kParseShared - chunk - 32 < kHistory ? kLdsBudget - kParseShared - chunk - 32
+                                                           : kHistory;
+}
+static_assert(kParseShared + 65535 + 32 + 16384 < kLdsBudget, "parse LDS layout exceeds the budget");
 
 struct HuffScratch {
   u32 key[320];
@@ -85,14 +126,8 @@ struct HuffScratch {
   u16 depth_count[320];
 };
 
-// Encoder LDS; the window follows it in dynamic shared memory.
-struct EncShared {
-  union {
-    u32 table[kBuckets * kWays];  // parse: position + 1 per way, 0 = empty
-    u32 stage[kStageWords];       // emit: the block's bits
-    HuffScratch huff;             // code-length construction
-  } u;
-  u32 ml[kStep];
+// e_emit LDS; the bit buffer (which first serves as HuffScratch) follows it.
+struct EmitShared {
   u32 freq_ll[288];
   u32 freq_d[32];
   u32 freq_cl[20];
@@ -103,19 +138,18 @@ struct EncShared {
   u16 code_d[32];
   u16 code_cl[20];
   u16 rle[320];  // code-length RLE: symbol | extra << 5
-  u32 scan[kWaves];
-  u32 nrle, hlit, hdist, hclen, mode, extent, hdr_bits, extra_bits, ntok, status;
-  u64 red_s[kWaves], red_l[kWaves];
+  u32 scan[kEmitWaves];
+  u32 nrle, hlit, hdist, hclen, mode, extent, hdr_bits, status;
 };
 
-constexpr u32 kSharedBytes = (sizeof(EncShared) + 15) & ~u32(15);
+constexpr u32 kEmitShared = (sizeof(EmitShared) + 15) & ~u32(15);
 
-// Largest history that fits the LDS budget next to a chunk of `chunk` bytes.
-constexpr u32 history_limit(u32 chunk) {
-  return kLdsBudget - kSharedBytes - chunk - 32 < kHistory ? kLdsBudget - kSharedBytes - chunk - 32
-                                                           : kHistory;
+// Bit buffer words for a chunk: a fixed/dynamic block is only chosen when it
+// is shorter than the stored form (len + 5 bytes).
+constexpr u32 stage_words(u32 chunk) {
+  return ((chunk + 8) / 4 + 16) * 4 > sizeof(HuffScratch) ? (chunk + 8) / 4 + 16
+                                                          : u32(sizeof(HuffScratch) / 4 + 1);
 }
-static_assert(kSharedBytes + 65535 + 32 < kLdsBudget, "encoder LDS layout exceeds the budget");
 
 __device__ __forceinline__ u32 win_u32(const u32* win, u32 q) {
   return __builtin_amdgcn_alignbyte(win[(q >> 2) + 1], win[q >> 2], q & 3);
@@ -182,8 +216,7 @@ __device__ __forceinline__ u32 fixed_len(u32 s) {
 // above the limit back with the JPEG count adjustment (ITU T.81 K.3, which
 // keeps the Kraft sum at 1) and gives the shortest lengths to the heaviest
 // symbols.
-__device__ void huffman_lengths(EncShared& sh, const u32* freq, u32 n, u32 limit, u8* len) {
-  HuffScratch& hs = sh.u.huff;
+__device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 limit, u8* len) {
   const u32 lane = lane_id();
   u32 m = 0;
   for (u32 base = 0; base < n; base += 64) {
@@ -279,7 +312,7 @@ __device__ void canonical_codes(const u8* len, u32 n, u16* code) {
 }
 
 // Code-length RLE of the literal/length and distance lengths; one lane.
-__device__ void rle_lengths(EncShared& sh) {
+__device__ void rle_lengths(EmitShared& sh) {
   const u32 total = sh.hlit + sh.hdist;
   u32 nr = 0, i = 0;
   for (u32 s = 0; s < 20; ++s) sh.freq_cl[s] = 0;
@@ -329,29 +362,30 @@ __device__ void rle_lengths(EncShared& sh) {
 // ORs into words that the caller has cleared.
 struct StageWriter {
   u32* words;
+  u32 cap;
   u32 pos;
   __device__ __forceinline__ void put(u32 v, u32 n) {
     if (!n) return;
     const u32 w = pos >> 5, s = pos & 31;
     const u64 x = u64(v) << s;
-    if (w < kStageWords) words[w] |= u32(x);
-    if (s + n > 32 && w + 1 < kStageWords) words[w + 1] |= u32(x >> 32);
+    if (w < cap) words[w] |= u32(x);
+    if (s + n > 32 && w + 1 < cap) words[w + 1] |= u32(x >> 32);
     pos += n;
   }
 };
 
-__device__ __forceinline__ void or_bits(u32* words, u32 pos, u64 v) {
+__device__ __forceinline__ void or_bits(u32* words, u32 cap, u32 pos, u64 v) {
   const u32 w = pos >> 5, s = pos & 31;
   const u64 lo = v << s;
   const u32 hi = s ? u32(v >> (64 - s)) : 0u;
-  if (u32(lo) && w < kStageWords) atomicOr(&words[w], u32(lo));
-  if (u32(lo >> 32) && w + 1 < kStageWords) atomicOr(&words[w + 1], u32(lo >> 32));
-  if (hi && w + 2 < kStageWords) atomicOr(&words[w + 2], hi);
+  if (u32(lo) && w < cap) atomicOr(&words[w], u32(lo));
+  if (u32(lo >> 32) && w + 1 < cap) atomicOr(&words[w + 1], u32(lo >> 32));
+  if (hi && w + 2 < cap) atomicOr(&words[w + 2], hi);
 }
 
-// Block-wide exclusive scan of one u32 per thread; returns the prefix and
-// writes the total.  Contains barriers: every thread must call it.
-__device__ __forceinline__ u32 block_scan(EncShared& sh, u32 v, u32& total) {
+// Block-wide exclusive scan of one u32 per thread of e_emit; returns the
+// prefix and writes the total.  Contains barriers: every thread must call it.
+__device__ __forceinline__ u32 block_scan(EmitShared& sh, u32 v, u32& total) {
   const u32 lane = lane_id(), wave = threadIdx.x >> 6;
   u32 x = v;
   for (u32 off = 1; off < 64; off <<= 1) {
@@ -362,13 +396,33 @@ __device__ __forceinline__ u32 block_scan(EncShared& sh, u32 v, u32& total) {
   __syncthreads();
   u32 before = 0;
   total = 0;
-  for (u32 w = 0; w < kWaves; ++w) {
+  for (u32 w = 0; w < kEmitWaves; ++w) {
     const u32 s = sh.scan[w];
     if (w < wave) before += s;
     total += s;
   }
   __syncthreads();
   return before + x - v;
+}
+
+// Code bits of one token (LSB first) and their count.
+__device__ __forceinline__ u32 token_bits(const EmitShared& sh, u32 tk, u64& bits) {
+  if (!(tk >> 31)) {
+    bits = sh.code_ll[tk];
+    return sh.len_ll[tk];
+  }
+  const u32 ml = ((tk >> 16) & 0xff) + 3, md = (tk & 0xffff) + 1;
+  u32 ls, lb, lx, ds, db, dx;
+  length_code(ml, ls, lb, lx);
+  dist_code(md, ds, db, dx);
+  u32 n = sh.len_ll[ls];
+  bits = sh.code_ll[ls];
+  bits |= u64(lx) << n;
+  n += lb;
+  bits |= u64(sh.code_d[ds]) << n;
+  n += sh.len_d[ds];
+  bits |= u64(dx) << n;
+  return n + db;
 }
 
 }  // namespace
@@ -401,13 +455,14 @@ __global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 c
   }
 }
 
-// One workgroup per chunk (grid-stride).  Dynamic LDS: EncShared + window.
-__global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDesc* descs,
-                                                     u32 chunks, u32 slot_bytes, u32* tokens,
-                                                     u8* slots, ChunkResult* results) {
+// LZ77 parse of one chunk per workgroup (grid-stride).  Dynamic LDS:
+// ParseShared + window.
+__global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const ChunkDesc* descs,
+                                                         u32 chunks, u32* tokens,
+                                                         ChunkStats* stats) {
   extern __shared__ __align__(16) u8 dyn[];
-  EncShared& sh = *reinterpret_cast<EncShared*>(dyn);
-  u32* win = reinterpret_cast<u32*>(dyn + kSharedBytes);
+  ParseShared& sh = *reinterpret_cast<ParseShared*>(dyn);
+  u32* win = reinterpret_cast<u32*>(dyn + kParseShared);
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
     const ChunkDesc d = descs[c];
@@ -420,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
       const u32* g = reinterpret_cast<const u32*>(addr - a);
       const u32 nw = (end + 3) / 4;
       u64 s = 0, l = 0;
-      for (u32 k = t; k < nw; k += kThreads) {
+      for (u32 k = t; k < nw; k += kParseThreads) {
         // Source dword k holds window byte 4k; dword k+1 is read only when it
         // holds a window byte, so no dword outside the input is touched.
         const u32 lo = g[k];
@@ -439,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
           }
         }
       }
-      for (u32 k = nw + t; k < nw + 4; k += kThreads) win[k] = 0;
+      for (u32 k = nw + t; k < nw + 4; k += kParseThreads) win[k] = 0;
       for (u32 off = 32; off; off >>= 1) {
         s += __shfl_down(s, off, 64);
         l += __shfl_down(l, off, 64);
@@ -449,10 +504,15 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
         sh.red_l[wave] = l;
       }
     }
-    for (u32 i = t; i < kBuckets * kWays; i += kThreads) sh.u.table[i] = 0;
-    for (u32 i = t; i < 288; i += kThreads) sh.freq_ll[i] = 0;
+    for (u32 i = t; i < kBuckets * kWays; i += kParseThreads) sh.table[i] = 0;
+    for (u32 i = t; i < 288; i += kParseThreads) sh.freq_ll[i] = 0;
     if (t < 32) sh.freq_d[t] = 0;
-    if (!t) sh.extra_bits = 0;
+    if (!t) {
+      sh.extra_bits = 0;
+      sh.jump[0][kStep] = kStep;
+      sh.jump[1][kStep] = kStep;
+      sh.mark[kStep] = 0;
+    }
     __syncthreads();
 
     // ---- history positions enter the table ----
@@ -460,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
     for (u32 base = 0; base < hist; base += kStep, ++stepno) {
       const u32 q = base + t;
       if (q < hist && q + 4 <= end)
-        atomicMax(&sh.u.table[hash4(win_u32(win, q)) * kWays + (stepno & (kWays - 1))], q + 1);
+        atomicMax(&sh.table[hash4(win_u32(win, q)) * kWays + (stepno & (kWays - 1))], q + 1);
     }
     __syncthreads();
 
@@ -480,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
       u32 best_len = 0, best_dist = 0;
       if (hashable) {
         const u32 maxlen = min(258u, end - q);
-        const uint4 e = *reinterpret_cast<const uint4*>(&sh.u.table[h * kWays]);
+        const uint4 e = *reinterpret_cast<const uint4*>(&sh.table[h * kWays]);
         const u32 ent[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
         for (u32 k = 0; k < kWays; ++k) {
@@ -501,62 +561,47 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
           }
         }
       }
-      sh.ml[t] = best_len >= 3 ? best_len : 0u;
+      sh.ml[t] = u16(best_len >= 3 ? best_len : 0u);
       __syncthreads();
 
-      // Lazy rule and the greedy walk, computed identically by every wave.
-      u32 Lr[kWaves];
-      u64 mask[kWaves];
-#pragma unroll
-      for (u32 r = 0; r < kWaves; ++r) {
-        const u32 j = r * 64 + lane;
-        const u32 cur_ml = sh.ml[j];
-        const u32 next_ml = j + 1 < kStep ? sh.ml[j + 1] : 0u;
-        Lr[r] = (cur_ml && next_ml <= cur_ml) ? cur_ml : 0u;
-        mask[r] = __ballot(Lr[r] != 0);
-      }
+      // Lazy rule; f(t) = end of a token starting at t; orbit of 0 under f.
       const u32 lim = min(kStep, end - p);
-      u64 starts[kWaves] = {};
+      const u32 cur_ml = sh.ml[t];
+      const u32 next_ml = t + 1 < kStep ? sh.ml[t + 1] : 0u;
+      const u32 L = (cur_ml && next_ml <= cur_ml) ? cur_ml : 0u;
+      const u32 f = t + (L ? L : 1u);
+      sh.jump[0][t] = u16(min(f, kStep));
+      sh.mark[t] = t == 0;
+      __syncthreads();
       u32 cur = 0;
-      while (cur < lim) {
-        u32 nxt = lim;
-        for (u32 r = cur >> 6; r < kWaves; ++r) {
-          u64 mm = mask[r];
-          if (r == (cur >> 6)) mm &= ~0ull << (cur & 63);
-          if (mm) {
-            nxt = r * 64 + __builtin_ctzll(mm);
-            break;
-          }
-        }
-        if (nxt > lim) nxt = lim;
-        // Literals at [cur, nxt).
-        for (u32 r = cur >> 6; r < kWaves && r * 64 < nxt; ++r) {
-          const u32 lo = max(cur, r * 64) - r * 64, hi = min(nxt, r * 64 + 64) - r * 64;
-          const u64 bits = (hi == 64 ? ~0ull : ((1ull << hi) - 1)) & ~((1ull << lo) - 1);
-          starts[r] |= bits;
-        }
-        if (nxt >= lim) {
-          cur = nxt;
-          break;
-        }
-        const u32 r = nxt >> 6;
-        starts[r] |= 1ull << (nxt & 63);
-        const u32 sel = r == 0 ? Lr[0] : r == 1 ? Lr[1] : r == 2 ? Lr[2] : Lr[3];
-        cur = nxt + __builtin_amdgcn_readlane(sel, nxt & 63);
+      for (u32 b = 0; b < kLog2Step; ++b) {
+        // Marks of earlier rounds are visible; a mark written in this round
+        // and seen early only adds orbit members, so the result is exact.
+        const u32 j = sh.jump[cur][t];
+        if (sh.mark[t]) sh.mark[j] = 1;
+        sh.jump[cur ^ 1][t] = sh.jump[cur][j];
+        cur ^= 1;
+        __syncthreads();
       }
-
-      // Tokens of this thread's position.
-      u32 before = 0, step_tokens = 0;
+      const bool start = t < lim && sh.mark[t];
+      const u64 bal = __ballot(start);
+      // The last start of the wave ends the furthest.
+      const u32 last_end = bal ? __shfl(f, 63 - __builtin_clzll(bal), 64) : 0u;
+      if (!lane) {
+        sh.wave_count[wave] = __popcll(bal);
+        sh.wave_end[wave] = last_end;
+      }
+      __syncthreads();
+      u32 before = 0, step_tokens = 0, adv = 0;
 #pragma unroll
-      for (u32 r = 0; r < kWaves; ++r) {
-        const u32 cnt = __popcll(starts[r]);
-        if (r < wave) before += cnt;
+      for (u32 w = 0; w < kParseWaves; ++w) {
+        const u32 cnt = sh.wave_count[w];
+        if (w < wave) before += cnt;
         step_tokens += cnt;
+        adv = max(adv, sh.wave_end[w]);
       }
-      const u64 mine = wave == 0 ? starts[0] : wave == 1 ? starts[1] : wave == 2 ? starts[2] : starts[3];
-      if ((mine >> lane) & 1) {
-        const u32 idx = ntok + before + __popcll(mine & lanemask_lt());
-        const u32 L = wave == 0 ? Lr[0] : wave == 1 ? Lr[1] : wave == 2 ? Lr[2] : Lr[3];
+      if (start) {
+        const u32 idx = ntok + before + __popcll(bal & lanemask_lt());
         if (L) {
           u32 ls, lb, lx, ds, db, dx;
           length_code(L, ls, lb, lx);
@@ -572,22 +617,54 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
         }
       }
       ntok += step_tokens;
-      if (hashable) atomicMax(&sh.u.table[h * kWays + (stepno & (kWays - 1))], q + 1);
+      if (hashable) atomicMax(&sh.table[h * kWays + (stepno & (kWays - 1))], q + 1);
       ++stepno;
-      p += cur;
+      p += adv;
       __syncthreads();
     }
     if (extra) atomicAdd(&sh.extra_bits, extra);
+    __syncthreads();
+    ChunkStats& st = stats[c];
+    for (u32 i = t; i < 288; i += kParseThreads) st.freq_ll[i] = sh.freq_ll[i] + (i == 256);
+    if (t < 32) st.freq_d[t] = sh.freq_d[t];
     if (!t) {
-      sh.ntok = ntok;
-      sh.freq_ll[256] += 1;  // end of block
+      st.ntok = ntok;
+      st.extra_bits = sh.extra_bits;
+      u64 s = 0, l = 0;
+      for (u32 w = 0; w < kParseWaves; ++w) {
+        s += sh.red_s[w];
+        l += sh.red_l[w];
+      }
+      st.sum_s = s;
+      st.sum_l = l;
     }
+    __syncthreads();
+  }
+}
+
+// Block coding and bit emission of one chunk per workgroup (grid-stride).
+// Dynamic LDS: EmitShared + bit buffer of `words` words.
+__global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const ChunkDesc* descs,
+                                                       u32 chunks, const u32* tokens,
+                                                       const ChunkStats* stats, u32 words,
+                                                       u32 slot_bytes, u8* slots,
+                                                       ChunkResult* results) {
+  extern __shared__ __align__(16) u8 dyn[];
+  EmitShared& sh = *reinterpret_cast<EmitShared*>(dyn);
+  u32* stage = reinterpret_cast<u32*>(dyn + kEmitShared);
+  HuffScratch& hs = *reinterpret_cast<HuffScratch*>(stage);
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const ChunkDesc d = descs[c];
+    const ChunkStats& st = stats[c];
+    for (u32 i = t; i < 288; i += kEmitThreads) sh.freq_ll[i] = i < 286 ? st.freq_ll[i] : 0u;
+    if (t < 32) sh.freq_d[t] = t < 30 ? st.freq_d[t] : 0u;
     __syncthreads();
 
     // ---- code lengths, costs, block type (wave 0) ----
     if (wave == 0) {
-      huffman_lengths(sh, sh.freq_ll, 286, 15, sh.len_ll);
-      huffman_lengths(sh, sh.freq_d, 30, 15, sh.len_d);
+      huffman_lengths(hs, sh.freq_ll, 286, 15, sh.len_ll);
+      huffman_lengths(hs, sh.freq_d, 30, 15, sh.len_d);
       if (!lane) {
         u32 hl = 286, hd = 30;
         while (hl > 257 && !sh.len_ll[hl - 1]) --hl;
@@ -597,7 +674,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
         rle_lengths(sh);
       }
       wave_sync();
-      huffman_lengths(sh, sh.freq_cl, 19, 7, sh.len_cl);
+      huffman_lengths(hs, sh.freq_cl, 19, 7, sh.len_cl);
       u32 dyn_bits = 0, fix_bits = 0, hdr = 0;
       for (u32 sy = lane; sy < 286; sy += 64) {
         dyn_bits += sh.freq_ll[sy] * sh.len_ll[sy];
@@ -621,8 +698,8 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
         while (hc > 4 && !sh.len_cl[cl_order(hc - 1)]) --hc;
         sh.hclen = hc;
         hdr += 3 + 14 + 3 * hc;
-        const u64 dyn_total = u64(hdr) + dyn_bits + sh.extra_bits;
-        const u64 fix_total = 3ull + fix_bits + sh.extra_bits;
+        const u64 dyn_total = u64(hdr) + dyn_bits + st.extra_bits;
+        const u64 fix_total = 3ull + fix_bits + st.extra_bits;
         auto extent = [&](u64 bits) -> u64 {
           return d.last ? (bits + 7) / 8 : (bits + 3 + 7) / 8 + 4;
         };
@@ -645,8 +722,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
           canonical_codes(sh.len_d, 30, sh.code_d);
           if (mode == 2) canonical_codes(sh.len_cl, 19, sh.code_cl);
         }
-        const u64 S = (sh.red_s[0] + sh.red_s[1] + sh.red_s[2] + sh.red_s[3]) % kAdlerMod;
-        const u64 L = (sh.red_l[0] + sh.red_l[1] + sh.red_l[2] + sh.red_l[3]) % kAdlerMod;
+        const u64 S = st.sum_s % kAdlerMod, L = st.sum_l % kAdlerMod;
         results[c].adler_s = S;
         results[c].adler_b =
             (((d.file_len - d.file_off) % kAdlerMod) * S + kAdlerMod - L) % kAdlerMod;
@@ -665,17 +741,18 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
         slot[3] = u8(~d.len & 0xff);
         slot[4] = u8((~d.len >> 8) & 0xff);
       }
-      for (u32 i = t; i < d.len; i += kThreads) slot[5 + i] = u8(win_byte(win, hist + i));
+      const u8* src = in + d.in_off;
+      for (u32 i = t; i < d.len; i += kEmitThreads) slot[5 + i] = src[i];
       if (!t) {
         results[c].extent = sh.extent;
         results[c].status = 0;
       }
     } else {
-      const u32 words = (sh.extent + 3) / 4 + 1;
-      for (u32 i = t; i < words && i < kStageWords; i += kThreads) sh.u.stage[i] = 0;
+      const u32 used = min((sh.extent + 3) / 4 + 1, words);
+      for (u32 i = t; i < used; i += kEmitThreads) stage[i] = 0;
       __syncthreads();
       if (!t) {
-        StageWriter out = {sh.u.stage, 0};
+        StageWriter out = {stage, words, 0};
         out.put(d.last ? 1u : 0u, 1);
         out.put(mode == 1 ? 1u : 2u, 2);
         if (mode == 2) {
@@ -694,40 +771,31 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
         if (out.pos != sh.hdr_bits) sh.status = kCompressionOverflow;
       }
       __syncthreads();
+      const u32* tok = tokens + d.in_off;
+      const u32 ntokens = st.ntok;
       u32 pos = sh.hdr_bits;
-      const u32 ntokens = sh.ntok;
-      for (u32 base = 0; base < ntokens; base += kThreads) {
-        const u32 i = base + t;
-        u64 bits = 0;
-        u32 nbits = 0;
-        if (i < ntokens) {
-          const u32 tk = tok[i];
-          if (!(tk >> 31)) {
-            bits = sh.code_ll[tk];
-            nbits = sh.len_ll[tk];
-          } else {
-            const u32 ml = ((tk >> 16) & 0xff) + 3, md = (tk & 0xffff) + 1;
-            u32 ls, lb, lx, ds, db, dx;
-            length_code(ml, ls, lb, lx);
-            dist_code(md, ds, db, dx);
-            bits = sh.code_ll[ls];
-            nbits = sh.len_ll[ls];
-            bits |= u64(lx) << nbits;
-            nbits += lb;
-            bits |= u64(sh.code_d[ds]) << nbits;
-            nbits += sh.len_d[ds];
-            bits |= u64(dx) << nbits;
-            nbits += db;
-          }
+      for (u32 base = 0; base < ntokens; base += kEmitThreads * kTokensPerThread) {
+        const u32 first = base + t * kTokensPerThread;
+        u64 bits[kTokensPerThread];
+        u32 nbits[kTokensPerThread];
+        u32 mine = 0;
+#pragma unroll
+        for (u32 k = 0; k < kTokensPerThread; ++k) {
+          nbits[k] = first + k < ntokens ? token_bits(sh, tok[first + k], bits[k]) : 0u;
+          mine += nbits[k];
         }
         u32 total;
-        const u32 off = block_scan(sh, nbits, total);
-        if (nbits) or_bits(sh.u.stage, pos + off, bits);
+        u32 off = pos + block_scan(sh, mine, total);
+#pragma unroll
+        for (u32 k = 0; k < kTokensPerThread; ++k) {
+          if (nbits[k]) or_bits(stage, words, off, bits[k]);
+          off += nbits[k];
+        }
         pos += total;
       }
       __syncthreads();
       if (!t) {
-        StageWriter out = {sh.u.stage, pos};
+        StageWriter out = {stage, words, pos};
         out.put(sh.code_ll[256], sh.len_ll[256]);
         if (!d.last) {
           out.put(0, 3);
@@ -742,7 +810,7 @@ __global__ __launch_bounds__(kThreads) void e_encode(const u8* in, const ChunkDe
       __syncthreads();
       const u32 copy_words = min((sh.extent + 3) / 4, slot_bytes / 4);
       u32* slot32 = reinterpret_cast<u32*>(slot);
-      for (u32 i = t; i < copy_words; i += kThreads) slot32[i] = sh.u.stage[i];
+      for (u32 i = t; i < copy_words; i += kEmitThreads) slot32[i] = stage[i];
       if (!t) results[c].status = sh.status;
     }
     __syncthreads();
@@ -849,29 +917,38 @@ hipError_t run_chunks(hipStream_t stream, Scratch& scratch, const u8* in, const 
                       u32 chunk_bytes, u32* meta) {
   u32* tokens = nullptr;
   u8* slots = nullptr;
+  ChunkStats* stats = nullptr;
   ChunkResult* results = nullptr;
   u64* sums = nullptr;
   u32* file_ok = nullptr;
   const u64 slot_bytes = slot_size(chunk_bytes);
   HZ_TRY(scratch.alloc(&tokens, in_total ? in_total : 1));
   HZ_TRY(scratch.alloc(&slots, chunks * slot_bytes));
+  HZ_TRY(scratch.alloc(&stats, chunks));
   HZ_TRY(scratch.alloc(&results, chunks));
   HZ_TRY(scratch.alloc(&sums, 4 * (chunks + 1)));
   HZ_TRY(scratch.alloc(&file_ok, file_count));
-  const u32 lds = kSharedBytes + history_limit(chunk_bytes) + chunk_bytes + 32;
-  HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_encode),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  const u32 parse_lds = kParseShared + history_limit(chunk_bytes) + chunk_bytes + 32;
+  const u32 words = stage_words(chunk_bytes);
+  const u32 emit_lds = kEmitShared + 4 * words;
+  HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_parse),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, int(parse_lds)));
+  HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_emit),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, int(emit_lds)));
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
-  HZ_LAUNCH(e_encode, dim3(grid), dim3(kThreads), lds, stream, in, descs, u32(chunks),
-            u32(slot_bytes), tokens, slots, results);
+  HZ_LAUNCH(e_parse, dim3(grid), dim3(kParseThreads), parse_lds, stream, in, descs, u32(chunks),
+            tokens, stats);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), emit_lds, stream, in, descs, u32(chunks),
+            tokens, stats, words, u32(slot_bytes), slots, results);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, results, u32(chunks), sums);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, files, file_count,
             results, sums, out, meta, file_ok);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_pack, dim3(u32(chunks < 65536 ? chunks : 65536)), dim3(256), 0, stream, descs,
-            files, u32(chunks), results, sums, slots, out, file_ok);
+  HZ_LAUNCH(e_pack, dim3(grid), dim3(256), 0, stream, descs, files, u32(chunks), results, sums,
+            slots, out, file_ok);
   return hipGetLastError();
 }
 
