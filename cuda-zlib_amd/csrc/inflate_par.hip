@@ -51,6 +51,7 @@ struct State {
   u64 adler_s, adler_w;
   u64 recs_used;     // block records handed out by describe
   u64 groups_used;   // 64-slot slice groups handed out by describe
+  u64 precount;      // entries of the dense pre-candidate array
 };
 
 struct Segment {
@@ -273,15 +274,34 @@ __device__ __forceinline__ bool stored_seed(const u8* body, u64 len, u64 byte) {
   return possible && ((body[byte + 4 + n] >> 1) & 3u) == 1;
 }
 
-// Bytes past a workgroup's range staged for header validation: the longest
-// dynamic header is 3 + 14 + 57 + 318 * 14 bits (< 566 bytes).
-constexpr u32 kDiscMargin = 640;
-constexpr u32 kDiscStageWords = (kDiscRange + kDiscMargin + 32) / 4;
-using DiscStage = StageT<kDiscStageWords>;
+// Bytes past a workgroup's range staged for the prefilter: the fields it
+// reads end 3 + 14 + 57 bits after a position of the range's last byte.
+constexpr u32 kPreMargin = 24;
+constexpr u32 kPreStageWords = (kDiscRange + kPreMargin + 32) / 4;
+using PreStage = StageT<kPreStageWords>;
+// Pre-candidate entries: bit offset, plus this flag once the header is known valid.
+constexpr u64 kValidBit = 1ull << 62;
+constexpr u64 kPosMask = kValidBit - 1;
+constexpr u32 kKindShift = 30;  // wg_count: count | kind << 30
+constexpr u32 kCountMask = (1u << kKindShift) - 1;
 
-// Candidate mask for the 64 bit offsets of bytes [b0, b0 + 8), reading the
-// workgroup's stage (headers that run past it are validated from global memory).
-__device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, const DiscStage& sg, u8* lut) {
+// Kraft sums of three 3-bit code lengths (index: l0 | l1 << 3 | l2 << 6).
+__device__ __forceinline__ void build_kraft3(u16* kraft3) {
+  for (u32 i = threadIdx.x; i < 512; i += blockDim.x) {
+    u32 k = 0;
+    for (u32 j = 0; j < 3; ++j) {
+      const u32 l = (i >> (3 * j)) & 7;
+      if (l) k += 128u >> l;
+    }
+    kraft3[i] = u16(k);
+  }
+}
+
+// Prefilter of the 64 bit offsets of bytes [b0, b0 + 8): BTYPE == 2,
+// HLIT <= 29 and a complete code-length code (Kraft sum of the HCLEN lengths
+// == 128).  Every valid dynamic header passes; about 0.1 % of random offsets
+// do.  Bit offset 0 is excluded (it is always a candidate).
+__device__ u64 prefilter_mask(u64 len, u64 b0, const PreStage& sg, const u16* kraft3) {
   if (b0 >= len) return 0;
   const u64 w0 = staged_u64(sg, b0 * 8), w1 = staged_u64(sg, b0 * 8 + 64),
             w2 = staged_u64(sg, b0 * 8 + 128);
@@ -292,30 +312,29 @@ __device__ u64 candidate_mask(const u8* body, u64 len, u64 b0, const DiscStage& 
   u64 m = ~s1 & s2 & ~(s4 & s5 & s6 & s7);  // BTYPE == 2 and HLIT <= 29
   const u64 bits_left = (len - b0) * 8;
   if (bits_left < 64) m &= (1ull << bits_left) - 1;
-  const u64 staged_end = sg.bit0 + u64(sg.count) * 32;
-  u64 valid = 0;
+  if (!b0) m &= ~1ull;
+  u64 out = 0;
   while (m) {
     const u32 k = __builtin_ctzll(m);
     m &= m - 1;
     const u64 a = funnel(w0, w1, k), b = funnel(w1, w2, k);
     const u32 nc = u32((a >> 13) & 15) + 4;
-    const u64 lens = (a >> 17) | (b << 47);
+    const u64 lens = ((a >> 17) | (b << 47)) & ((1ull << (3 * nc)) - 1);
     u32 kraft = 0;
-    for (u32 i = 0; i < nc; ++i) {
-      const u32 l = u32(lens >> (3 * i)) & 7u;
-      if (l) kraft += 128u >> l;
-    }
-    if (kraft != 128) continue;
-    const u64 start = b0 * 8 + k;
-    if (!start) continue;
-    bool ok;
-    if (start + u64(kDiscMargin - 8) * 8 <= staged_end || staged_end >= len * 8) {
-      BitIn r = staged_reader(sg, len, start + 3);
-      ok = dynamic_header_fields_valid(r, lut);
-    } else {
-      ok = dynamic_header_valid(body, len, start, lut);
-    }
-    if (ok) valid |= 1ull << k;
+#pragma unroll
+    for (u32 j = 0; j < 7; ++j) kraft += kraft3[(lens >> (9 * j)) & 511];
+    if (kraft == 128) out |= 1ull << k;
+  }
+  return out;
+}
+
+// Exact header validation of the prefiltered offsets in `pre` (global reads).
+__device__ u64 validate_mask(const u8* body, u64 len, u64 b0, u64 pre, u8* lut) {
+  u64 valid = 0;
+  while (pre) {
+    const u32 k = __builtin_ctzll(pre);
+    pre &= pre - 1;
+    if (dynamic_header_valid(body, len, b0 * 8 + k, lut)) valid |= 1ull << k;
   }
   return valid;
 }
@@ -356,49 +375,67 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
   st->adler_w = 0;
   st->recs_used = 0;
   st->groups_used = 0;
+  st->precount = 0;
 }
 
-// Pass 1: per-workgroup candidate count and (up to kDiscCap) ordered entries.
+// Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
+// validated later one per lane).  A range with more than kDiscCap of them
+// validates them itself and keeps the valid ones (kind 1), or, when even those
+// overflow, leaves them to the gather pass (kind 2).  Also counts
+// stored-endpoint seeds.
 __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State* st,
                                                   u32* wg_count, u64* wg_list) {
   __shared__ u8 luts[kDiscThreads][128];
   __shared__ u32 scan[kDiscThreads];
-  __shared__ DiscStage sg;
+  __shared__ u16 kraft3[512];
+  __shared__ PreStage sg;
   if (st->status) return;
   const u64 wg = blockIdx.x;
-  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kDiscMargin);
+  build_kraft3(kraft3);
+  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
   __syncthreads();
   const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = candidate_mask(body, len, b0, sg, luts[threadIdx.x]);
-  if (b0 == 0) mask |= 1;  // bit 0 is always a candidate
+  u64 mask = prefilter_mask(len, b0, sg, kraft3);
+  u64 flag = 0;
+  if (b0 == 0) {
+    mask |= 1;  // bit 0 is always a candidate
+    flag = 1;
+  }
   u32 seeds = 0;
   for (u32 j = 0; j < kDiscBytesPerThread; ++j)
     if (b0 + j < len && stored_seed(body, len, b0 + j)) ++seeds;
   if (seeds) atomicAdd(reinterpret_cast<unsigned long long*>(&st->seeds), seeds);
   u32 total;
-  const u32 base = block_exclusive_scan(__popcll(mask), scan, total);
-  if (!threadIdx.x) wg_count[wg] = total;
-  if (total <= kDiscCap) {
-    u32 at = base;
+  u32 base = block_exclusive_scan(__popcll(mask), scan, total);
+  u32 kind = 0;
+  if (total > kDiscCap) {
+    mask = validate_mask(body, len, b0, mask & ~flag, luts[threadIdx.x]) | flag;
+    flag = mask;
+    base = block_exclusive_scan(__popcll(mask), scan, total);
+    kind = total > kDiscCap ? 2u : 1u;
+  }
+  if (!threadIdx.x) wg_count[wg] = total | (kind << kKindShift);
+  if (kind < 2) {
     while (mask) {
       const u32 k = __builtin_ctzll(mask);
       mask &= mask - 1;
-      wg_list[wg * kDiscCap + at++] = b0 * 8 + k;
+      wg_list[wg * kDiscCap + base++] = (b0 * 8 + k) | ((flag >> k) & 1 ? kValidBit : 0);
     }
   }
 }
 
-// Pass 2: one workgroup scans the per-workgroup counts into offsets.
+// Discovery pass 2: one workgroup scans the per-range counts into offsets of
+// the dense pre-candidate array.
 __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg_count,
                                                         u64* wg_offset, u64 groups,
-                                                        u64 max_candidates) {
+                                                        u64 pre_capacity) {
   __shared__ u64 part[1024];
   if (st->status) return;
   const u32 t = threadIdx.x;
   const u64 per = (groups + 1023) / 1024;
   const u64 lo = min<u64>(groups, u64(t) * per), hi = min<u64>(groups, lo + per);
   u64 sum = 0;
-  for (u64 i = lo; i < hi; ++i) sum += wg_count[i];
+  for (u64 i = lo; i < hi; ++i) sum += wg_count[i] & kCountMask;
   part[t] = sum;
   __syncthreads();
   for (u32 off = 1; off < 1024; off <<= 1) {
@@ -410,7 +447,98 @@ __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg
   u64 run = part[t] - sum;
   for (u64 i = lo; i < hi; ++i) {
     wg_offset[i] = run;
-    run += wg_count[i];
+    run += wg_count[i] & kCountMask;
+  }
+  if (t == 1023) {
+    const u64 total = part[1023];
+    st->precount = total;
+    // Only kind-2 ranges (valid headers alone overflowing a range) can push the
+    // total past the capacity, and then the valid candidates alone exceed the
+    // candidate limit.
+    if (total > pre_capacity) st->status = kCandidateOverflow;
+  }
+}
+
+// Discovery pass 3: the per-range lists in order into the dense array; kind-2
+// ranges recompute and validate here.
+__global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len, const State* st,
+                                                         const u32* wg_count, const u64* wg_list,
+                                                         const u64* wg_offset, u64* pre) {
+  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u32 scan[kDiscThreads];
+  __shared__ u16 kraft3[512];
+  __shared__ PreStage sg;
+  if (st->status) return;
+  const u64 wg = blockIdx.x;
+  const u32 count = wg_count[wg] & kCountMask, kind = wg_count[wg] >> kKindShift;
+  const u64 off = wg_offset[wg];
+  if (kind < 2) {
+    for (u32 i = threadIdx.x; i < count; i += kDiscThreads) pre[off + i] = wg_list[wg * kDiscCap + i];
+    return;
+  }
+  build_kraft3(kraft3);
+  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
+  __syncthreads();
+  const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
+  u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3), luts[threadIdx.x]);
+  if (b0 == 0) mask |= 1;
+  u32 total;
+  u32 at = block_exclusive_scan(__popcll(mask), scan, total);
+  while (mask) {
+    const u32 k = __builtin_ctzll(mask);
+    mask &= mask - 1;
+    pre[off + at++] = (b0 * 8 + k) | kValidBit;
+  }
+}
+
+// Discovery pass 4: one lane per pre-candidate validates its header; per
+// workgroup count of valid entries.
+__global__ __launch_bounds__(256) void g_validate(const u8* body, u64 len, const State* st,
+                                                  u64* pre, u32* block_valid) {
+  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u32 count;
+  if (st->status) return;
+  const u64 n = st->precount;
+  const u64 i = u64(blockIdx.x) * kDiscThreads + threadIdx.x;
+  if (u64(blockIdx.x) * kDiscThreads >= n) return;
+  if (!threadIdx.x) count = 0;
+  __syncthreads();
+  bool valid = false;
+  if (i < n) {
+    const u64 e = pre[i];
+    valid = (e & kValidBit) || dynamic_header_valid(body, len, e & kPosMask, luts[threadIdx.x]);
+    if (valid && !(e & kValidBit)) pre[i] = e | kValidBit;
+  }
+  const u64 bal = __ballot(valid);
+  if (lane_id() == 0 && bal) atomicAdd(&count, u32(__popcll(bal)));
+  __syncthreads();
+  if (!threadIdx.x) block_valid[blockIdx.x] = count;
+}
+
+// Discovery pass 5: one workgroup scans the valid counts; the candidate limit
+// (valid headers + bit 0 + stored seeds, as the reference counts them).
+__global__ __launch_bounds__(1024) void g_valid_scan(State* st, const u32* block_valid,
+                                                     u64* block_offset, u64 max_candidates) {
+  __shared__ u64 part[1024];
+  if (st->status) return;
+  const u64 blocks = (st->precount + kDiscThreads - 1) / kDiscThreads;
+  const u32 t = threadIdx.x;
+  const u64 per = (blocks + 1023) / 1024;
+  const u64 lo = min<u64>(blocks, u64(t) * per), hi = min<u64>(blocks, lo + per);
+  u64 sum = 0;
+  for (u64 i = lo; i < hi; ++i) sum += block_valid[i];
+  part[t] = sum;
+  __syncthreads();
+  for (u32 off = 1; off < 1024; off <<= 1) {
+    const u64 x = t >= off ? part[t - off] : 0ull;
+    __syncthreads();
+    part[t] += x;
+    __syncthreads();
+  }
+  u64 run = part[t] - sum;
+  for (u64 i = lo; i < hi; ++i) {
+    block_offset[i] = run;
+    run += block_valid[i];
   }
   if (t == 1023) {
     const u64 total = part[1023];
@@ -419,34 +547,25 @@ __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg
   }
 }
 
-// Pass 3: gather local lists into the sorted candidate array; overflowing
-// workgroups recompute their masks and write directly.
-__global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len, const State* st,
-                                                         const u32* wg_count, const u64* wg_list,
-                                                         const u64* wg_offset, u64* cand) {
-  __shared__ u8 luts[kDiscThreads][128];
-  __shared__ u32 scan[kDiscThreads];
-  __shared__ DiscStage sg;
+// Discovery pass 6: valid entries in order into the candidate array.
+__global__ __launch_bounds__(256) void g_valid_scatter(const State* st, const u64* pre,
+                                                       const u64* block_offset, u64* cand,
+                                                       u64 cand_capacity) {
+  __shared__ u32 wave_count[kDiscThreads / 64];
   if (st->status) return;
-  const u64 wg = blockIdx.x;
-  const u32 count = wg_count[wg];
-  const u64 off = wg_offset[wg];
-  if (count <= kDiscCap) {
-    for (u32 i = threadIdx.x; i < count; i += kDiscThreads) cand[off + i] = wg_list[wg * kDiscCap + i];
-    return;
-  }
-  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kDiscMargin);
+  const u64 n = st->precount;
+  if (u64(blockIdx.x) * kDiscThreads >= n) return;
+  const u64 i = u64(blockIdx.x) * kDiscThreads + threadIdx.x;
+  const u64 e = i < n ? pre[i] : 0;
+  const bool valid = i < n && (e & kValidBit);
+  const u64 bal = __ballot(valid);
+  const u32 wave = threadIdx.x >> 6, lane = lane_id();
+  if (!lane) wave_count[wave] = __popcll(bal);
   __syncthreads();
-  const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = candidate_mask(body, len, b0, sg, luts[threadIdx.x]);
-  if (b0 == 0) mask |= 1;
-  u32 total;
-  u32 at = block_exclusive_scan(__popcll(mask), scan, total);
-  while (mask) {
-    const u32 k = __builtin_ctzll(mask);
-    mask &= mask - 1;
-    cand[off + at++] = b0 * 8 + k;
-  }
+  u64 at = block_offset[blockIdx.x];
+  for (u32 w = 0; w < wave; ++w) at += wave_count[w];
+  at += __popcll(bal & (lane ? (~0ull >> (64 - lane)) : 0ull));
+  if (valid && at < cand_capacity) cand[at] = e & kPosMask;
 }
 
 namespace {
@@ -1442,21 +1561,36 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
 
   // Discovery.
   const u64 groups = len ? (len + kDiscRange - 1) / kDiscRange : 1;
-  u32* wg_count = nullptr;
-  u64 *wg_list = nullptr, *wg_offset = nullptr, *cand = nullptr;
+  const u64 pre_capacity = groups * kDiscCap + u64(max_candidates) + 1;
+  const u64 pre_blocks = (pre_capacity + kDiscThreads - 1) / kDiscThreads;
+  u32 *wg_count = nullptr, *block_valid = nullptr;
+  u64 *wg_list = nullptr, *wg_offset = nullptr, *pre = nullptr, *block_offset = nullptr,
+      *cand = nullptr;
   HZ_TRY(scratch.alloc(&wg_count, groups));
   HZ_TRY(scratch.alloc(&wg_list, groups * kDiscCap));
   HZ_TRY(scratch.alloc(&wg_offset, groups));
+  HZ_TRY(scratch.alloc(&pre, pre_capacity));
+  HZ_TRY(scratch.alloc(&block_valid, pre_blocks));
+  HZ_TRY(scratch.alloc(&block_offset, pre_blocks));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
   HZ_LAUNCH(g_discover, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
-                     wg_count, wg_list);
+            wg_count, wg_list);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset,
-                     groups, u64(max_candidates));
+  HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset, groups,
+            pre_capacity);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len,
-                     st, wg_count, wg_list, wg_offset, cand);
+  HZ_LAUNCH(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
+            wg_count, wg_list, wg_offset, pre);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_validate, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, body, len, st, pre,
+            block_valid);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_valid_scan, dim3(1), dim3(1024), 0, stream, st, block_valid, block_offset,
+            u64(max_candidates));
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_valid_scatter, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, st, pre,
+            block_offset, cand, cand_capacity);
   HZ_TRY(hipGetLastError());
 
   // Describe every candidate's segment.
