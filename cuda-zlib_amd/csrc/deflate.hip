@@ -177,12 +177,6 @@ __device__ __forceinline__ u64 lanemask_lt() {
   return lane ? (~0ull >> (64 - lane)) : 0ull;
 }
 
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // RFC 1951 length code (257..285) and extra bits for a match length 3..258.
 __device__ __forceinline__ void length_code(u32 len, u32& sym, u32& nbits, u32& extra) {
   if (len == 258) { sym = 285; nbits = 0; extra = 0; return; }

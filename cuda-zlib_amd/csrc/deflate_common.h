@@ -16,6 +16,7 @@ typedef uint16_t u16;
 typedef uint32_t u32;
 typedef uint64_t u64;
 typedef int32_t i32;
+typedef int64_t i64;
 
 // ---- status contract -------------------------------------------------------
 enum Status : u32 {
@@ -133,6 +134,62 @@ struct BitIn {
   }
 };
 
+// LSB-first reader over words staged in LDS, with 32-bit positions relative to
+// word 0 (a stage holds at most a few hundred kilobits).  `limit` is the
+// relative bit position of the body end (saturated), so avail() keeps the
+// body's truncation semantics; words past `nwords` read as zero.
+struct StagedBits {
+  const u32* words;
+  u32 nwords;
+  u32 pos;
+  u32 limit;
+  u64 buf;
+  u32 cnt;
+  u32 wnext;
+
+  __device__ __forceinline__ void refill() {
+    while (cnt <= 32) {
+      const u64 v = wnext < nwords ? u64(words[wnext]) : 0ull;
+      buf |= v << cnt;
+      cnt += 32;
+      ++wnext;
+    }
+  }
+  __device__ __forceinline__ void seek(u32 p) {
+    pos = p;
+    wnext = p >> 5;
+    buf = 0;
+    cnt = 0;
+    refill();
+    const u32 skip = p & 31u;
+    buf >>= skip;
+    cnt -= skip;
+    refill();
+  }
+  __device__ __forceinline__ u32 avail() const { return pos < limit ? limit - pos : 0u; }
+  __device__ __forceinline__ u32 peek(u32 n) const {
+    return n ? u32(buf & ((1ull << n) - 1ull)) : 0u;
+  }
+  __device__ __forceinline__ void drop(u32 n) {
+    buf >>= n;
+    cnt -= n;
+    pos += n;
+    if (cnt <= 32) refill();
+  }
+  __device__ __forceinline__ bool take(u32 n, u32& v) {
+    if (n > avail()) return false;
+    v = peek(n);
+    drop(n);
+    return true;
+  }
+};
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---- canonical Huffman decode tables ---------------------------------------
 // Primary LUT entry (u32): bits 0..3 code length (0 = no short code here),
 // bits 16..31 symbol.  Codes longer than the primary width use the canonical
@@ -198,8 +255,8 @@ __device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_
 // kTruncated (bits ran out first) or kBadSymbol (no code matches within
 // `maximum` bits).  Matches the reference's LUT-plus-canonical decode exactly,
 // including its behaviour at the end of the bit range.
-template <int N, int P>
-__device__ __forceinline__ i32 huff_decode(const HuffTable<N, P>& t, BitIn& r, u32& err) {
+template <int N, int P, class Reader>
+__device__ __forceinline__ i32 huff_decode(const HuffTable<N, P>& t, Reader& r, u32& err) {
   const u32 e = t.primary[r.peek(P)];
   const u32 l = e & 15u;
   if (l) {
@@ -341,9 +398,14 @@ __device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
 // validity rules and table contents as huff_build.  `scratch` holds >= 320
 // u16 in LDS (codes, then offsets/next codes); every lane must call it and
 // every lane gets the status.
-template <int N, int P>
+template <int N, int P, bool kOneWave = false>
 __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_ok,
                                bool single_ok, u32 limit, u16* scratch, u32* status) {
+  // kOneWave: called by wave 0 of a larger workgroup (wave-level syncs only).
+  auto sync = [] {
+    if (kOneWave) wave_sync();
+    else __syncthreads();
+  };
   const u32 lane = threadIdx.x;
   u16* codes = scratch;
   u16* offs = scratch + 288;
@@ -359,7 +421,7 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
     }
   }
   if (lane < 16) t.count[lane] = u16(cnt);
-  __syncthreads();
+  sync();
   if (!lane) {
     u32 st = kOk, maximum = 0;
     if (n > u32(N)) st = kBadTree;
@@ -390,7 +452,7 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
     *status = st;
   }
   for (u32 i = lane; i < (1u << P); i += 64) t.primary[i] = 0;
-  __syncthreads();
+  sync();
   const u32 st = *status;
   if (!st && t.maximum) {
     // Symbols in (length, symbol) order and canonical codes; lane l (< 16)
@@ -413,7 +475,7 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
       running += chunk;
     }
   }
-  __syncthreads();
+  sync();
   if (!st) {
     for (u32 s = lane; s < n; s += 64) {
       const u32 l = lens[s];
@@ -422,14 +484,15 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
       for (u32 k = bit_reverse(codes[s], l); k < (1u << P); k += 1u << l) t.primary[k] = e;
     }
   }
-  __syncthreads();
+  sync();
   return st;
 }
 
 // One literal/length token after the LL symbol.  Returns kOk and sets
 // length/distance (length 0 = EOB, distance 0 = literal in `lit`), or an error.
 // Order of checks follows the reference's token decode (_decode_kernels.py:393-420).
-__device__ __forceinline__ u32 decode_token(DecodeTables& t, BitIn& r, u32 window, u32& lit,
+template <class Reader>
+__device__ __forceinline__ u32 decode_token(const DecodeTables& t, Reader& r, u32 window, u32& lit,
                                              u32& length, u32& distance) {
   u32 err = 0;
   const i32 sym = huff_decode(t.ll, r, err);

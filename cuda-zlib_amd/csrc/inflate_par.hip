@@ -620,75 +620,130 @@ __device__ u32 describe_block(BitIn& r, DecodeTables& t, u64 limit, u32& final_b
   return err;
 }
 
-constexpr u64 kSyncBits = 1024;   // window in which a slice records its token starts
-constexpr u32 kSyncWords = kSyncBits / 64;
 constexpr u32 kNoMerge = 0xffffffffu;
 
-// Per-wave LDS of the describe kernel.
-struct SpecShared {
+// ---- describe: one 256-thread workgroup per candidate ----------------------
+constexpr u32 kDescThreads = 256;
+constexpr u32 kDescWaves = kDescThreads / 64;
+constexpr u32 kVisitBits = 512;  // a slice records every token start (slices <= 512 bits)
+constexpr u32 kVisitWords = kVisitBits / 64;
+constexpr u32 kDescMinSlice = 64;  // > longest token (48 bits)
+constexpr u32 kDescMaxSlice = kVisitBits;
+static_assert(u64(kDescThreads) * kDescMaxSlice <= u64(kStageBytes) * 8, "describe stage too small");
+
+struct DescShared {
   DecodeTables tables;
   Stage stage;
-  u16 codes[320];                     // scratch of cooperative table builds
-  u64 visit[64][kSyncWords];          // token starts in [slice start, + kSyncBits)
-  u64 xpos[64], evpos[64], evend[64];
-  u32 count[64], ev[64];
-  u32 merge[64];                      // offset (from slice start) where lane j-1's
-                                      // continuation met lane j's tokens, or kNoMerge
-  u32 tail[64];                       // bytes of lane j's continuation tokens
-  u32 before[64];                     // bytes lane j produced before its merge point
-  // control written by lane 0 (d0: block data start; r0: round start)
-  u64 pos, d0, r0, hint, end, size, slice;
+  u16 codes[320];                        // scratch of cooperative table builds
+  u64 visit[kDescThreads][kVisitWords];  // token starts of each slice's own decode
+  u32 xpos[kDescThreads];                // stage-relative end of each slice decode
+  u32 evpos[kDescThreads], evend[kDescThreads];
+  u32 count[kDescThreads];               // bytes of each slice decode
+  u32 ev[kDescThreads];                  // 0 none, 1 EOB, else 0x100 | status
+  u32 merge[kDescThreads];               // offset from s_j where lane j-1's continuation met
+                                         // lane j's tokens, or kNoMerge
+  u32 tail[kDescThreads];                // bytes of lane j's continuation
+  u32 before[kDescThreads];              // bytes lane j produced before its merge point
+  u32 prefix[kDescThreads];              // inclusive prefix of per-slice bytes
+  u32 entry[kDescThreads];               // stage-relative true entry of each slice
+  u32 off[kDescThreads];                 // block output offset of each slice
+  u32 runbase[kDescThreads];             // run starts: off of lane k = runbase + prefix[k-1]
+  u64 brk[kDescWaves], evm[kDescWaves], runs[kDescWaves], serial[kDescWaves];
+  u32 wsum[kDescWaves];
+  // control written by lane 0 (block_header interface: pos, d0, end, size, type, ...)
+  u64 pos, d0, hint, end, size, round;
+  u32 slice, need;
   u32 type, final_block, status, nl, nd, go, build_status, group, lanes;
 };
 
-__device__ __forceinline__ bool visited(const SpecShared& sh, u32 lane, u64 off) {
-  return off < kSyncBits && ((sh.visit[lane][off >> 6] >> (off & 63)) & 1);
+__device__ __forceinline__ bool desc_visited(const DescShared& sh, u32 lane, u32 off) {
+  return off < kVisitBits && ((sh.visit[lane][off >> 6] >> (off & 63)) & 1);
+}
+
+__device__ __forceinline__ StagedBits stage_bits(const Stage& sg, u64 len, u32 pos) {
+  StagedBits r;
+  r.words = sg.words;
+  r.nwords = sg.count;
+  const u64 lim = len * 8 - sg.bit0;  // modular: bit0 may precede the body by < 32 bits
+  r.limit = lim > 0xffffffffull ? 0xffffffffu : u32(lim);
+  r.seek(pos);
+  return r;
 }
 
 // Token-level decode from r.pos until r.pos >= stop, an EOB or an error.
 // ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  With
-// `visit`, token starts in [win0, win0 + kSyncBits) are recorded.
-__device__ void slice_decode(const DecodeTables& t, BitIn& r, u64 stop, u64* visit, u64 win0,
-                             u64& xpos, u32& count, u32& ev, u64& evpos, u64& evend) {
-  u64 produced = 0;
+// `visit`, every token start in [win0, win0 + kVisitBits) is recorded (the bits
+// of the current 64-bit word accumulate in a register).
+__device__ void desc_slice(const DecodeTables& t, StagedBits& r, u32 stop, u64* visit, u32 win0,
+                           u32& count, u32& ev, u32& evpos, u32& evend) {
+  u32 produced = 0, cw = 0;
+  u64 bits = 0;
   ev = 0;
   if (visit)
-    for (u32 w = 0; w < kSyncWords; ++w) visit[w] = 0;
+    for (u32 w = 0; w < kVisitWords; ++w) visit[w] = 0;
   for (;;) {
-    const u64 p = r.pos;
+    const u32 p = r.pos;
     if (p >= stop) break;
     if (visit) {
-      const u64 off = p - win0;
-      if (off < kSyncBits) visit[off >> 6] |= 1ull << (off & 63);
+      const u32 off = p - win0;
+      if (off < kVisitBits) {
+        const u32 w = off >> 6;
+        if (w != cw) {
+          visit[cw] = bits;
+          bits = 0;
+          cw = w;
+        }
+        bits |= 1ull << (off & 63);
+      }
     }
     u32 lit, length, distance;
-    const u32 err = decode_token(const_cast<DecodeTables&>(t), r, 32768u, lit, length, distance);
+    const u32 err = decode_token(t, r, 32768u, lit, length, distance);
     if (err) { ev = 0x100u | err; evpos = p; break; }
     if (!length) { ev = 1; evpos = p; evend = r.pos; break; }
     produced += length;
-    if (produced >= 0xffff0000ull) { ev = 0x100u | kOutputOverflow; evpos = p; break; }
+    if (produced >= 0x40000000u) { ev = 0x100u | kOutputOverflow; evpos = p; break; }
   }
-  xpos = r.pos;
-  count = u32(produced);
+  if (visit) visit[cw] = bits;
+  count = produced;
 }
 
 // Bytes produced by decoding tokens from `from` up to token start `to`.
-__device__ u32 bytes_between(const DecodeTables& t, const Stage& sg, u64 len, u64 from, u64 to) {
-  BitIn r = staged_reader(sg, len, from);
+__device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u64 len, u32 from, u32 to) {
+  StagedBits r = stage_bits(sg, len, from);
   u32 bytes = 0;
   while (r.pos < to) {
     u32 lit, length, distance;
-    if (decode_token(const_cast<DecodeTables&>(t), r, 32768u, lit, length, distance) || !length) break;
+    if (decode_token(t, r, 32768u, lit, length, distance) || !length) break;
     bytes += length;
   }
   return bytes;
+}
+
+// First set bit at index >= from in a kDescThreads-bit mask, or kDescThreads.
+__device__ __forceinline__ u32 next_bit(const u64* mask, u32 from) {
+  for (u32 w = from >> 6; w < kDescWaves; ++w) {
+    u64 m = mask[w];
+    if (w == (from >> 6)) m &= ~0ull << (from & 63);
+    if (m) return w * 64 + __builtin_ctzll(m);
+  }
+  return kDescThreads;
+}
+
+// Last set bit at index <= at (the mask has bit 0 set).
+__device__ __forceinline__ u32 prev_bit(const u64* mask, u32 at) {
+  for (u32 w = at >> 6;; --w) {
+    u64 m = mask[w];
+    if (w == (at >> 6) && (at & 63) != 63) m &= (2ull << (at & 63)) - 1;
+    if (m) return w * 64 + 63 - __builtin_clzll(m);
+    if (!w) return 0;
+  }
 }
 
 // Reads a block header at sh.pos from the stage (lane 0): stored fields, or
 // dynamic code lengths; then the wave builds fixed/dynamic tables.  Sets
 // sh.type, sh.final_block, sh.status, sh.d0 (first token or payload bit) and,
 // for stored blocks, sh.end/sh.size.
-template <typename Shared>
+template <bool kOneWave = false, typename Shared>
 __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
   const u32 lane = threadIdx.x;
   if (!staged_covers(sh.stage, body, len, sh.pos, sh.pos + 4096)) {
@@ -730,197 +785,271 @@ __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
   }
   __syncthreads();
   if (sh.type && !sh.status) {
-    const bool fixed = sh.type == 1;
-    u32 err = huff_build_wave(sh.tables.ll, sh.tables.lens, sh.nl, false, true, 15, sh.codes,
-                              &sh.build_status);
-    if (!err)
-      err = huff_build_wave(sh.tables.dd, sh.tables.lens + sh.nl, sh.nd, !fixed, true, 15,
-                            sh.codes, &sh.build_status);
-    if (!lane) sh.status = err;
+    // The tables are built by one wave (wave 0 of a larger workgroup).
+    if (!kOneWave || lane < 64) {
+      const bool fixed = sh.type == 1;
+      u32 err = huff_build_wave<288, 10, kOneWave>(sh.tables.ll, sh.tables.lens, sh.nl, false,
+                                                   true, 15, sh.codes, &sh.build_status);
+      if (!err)
+        err = huff_build_wave<32, 8, kOneWave>(sh.tables.dd, sh.tables.lens + sh.nl, sh.nd, !fixed,
+                                               true, 15, sh.codes, &sh.build_status);
+      if (!lane) sh.status = err;
+    }
     __syncthreads();
   }
 }
 
 // Describe the tokens of the fixed/dynamic block whose tables are built and
-// whose tokens start at sh.d0.  Each round:
-//   1. the 64 lanes decode evenly spaced slices speculatively, each recording
-//      the token starts in the first kSyncBits of its slice;
+// whose tokens start at sh.d0.  Each round covers 256 slices of `slice` bits:
+//   1. every lane decodes its slice speculatively, recording its token starts;
 //   2. every lane continues past its slice end until it meets a token start
 //      of the next lane (a merge: from there the two decodings coincide);
 //   3. every lane counts the bytes it produced before its merge point;
-//   4. lane 0 chains the true slice entries from the round start, decoding
-//      serially only where a slice never merged.
+//   4. a prefix sum gives every slice's output offset.  Lane 0 starts at the
+//      round's true entry; a run of merged slices needs no further work, and
+//      lane 0 decodes serially only where a merge is missing (a "break"),
+//      until the true tokens meet the next lane's tokens.
 // Results: sh.status, sh.end (bit after the EOB), sh.size, and slice groups
 // (sh.group = kNone if capacity ran out; emission then decodes serially).
-__device__ void describe_tokens(const u8* body, u64 len, u64 limit, SpecShared& sh, State* st,
+__device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& sh, State* st,
                                 u64* slice_entry, u32* slice_off, u32* group_link,
                                 u64 group_capacity) {
-  const u32 lane = threadIdx.x;
-  u64 e = sh.d0, total = 0;
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  u64 e_abs = sh.d0, total = 0;
   bool done = false, keep = true;
-  u32 last_group = kNone, status = 0, lanes = 0, group = kNone;
+  u32 last_group = kNone, status = 0, lanes_total = 0, group = kNone;
   u64 end = 0;
-  while (true) {
-    if (!lane) {
-      // Past the hint (a false candidate inside this block): full rounds.
-      const u64 span = sh.hint > e ? sh.hint - e : 64 * kMaxSlice;
-      u64 slice = (span + 63) / 64;
-      if (slice < kMinSlice) slice = kMinSlice;
-      if (slice > kMaxSlice) slice = kMaxSlice;
-      sh.r0 = e;
-      sh.slice = slice;
+  for (;;) {
+    if (!t) {
+      // Up to the hint (the next candidate) the slices spread the span evenly.
+      const u64 span = sh.hint > e_abs ? sh.hint - e_abs : u64(kDescThreads) * kDescMaxSlice;
+      u64 slice = (span + kDescThreads - 1) / kDescThreads;
+      if (slice < kDescMinSlice) slice = kDescMinSlice;
+      if (slice > kDescMaxSlice) slice = kDescMaxSlice;
+      sh.slice = u32(slice);
       sh.go = done ? 0u : 1u;
+      sh.round = e_abs;
+      sh.need = !staged_covers(sh.stage, body, len, e_abs, e_abs + u64(kDescThreads) * slice);
     }
     __syncthreads();
     if (!sh.go) break;
-    const u64 r0 = sh.r0, slice = sh.slice;
-    if (!staged_covers(sh.stage, body, len, r0, r0 + 64 * slice)) {
-      stage_range(body, len, r0, r0 + 64 * slice, sh.stage);
+    const u64 round_abs = sh.round;
+    const u32 slice = sh.slice;
+    if (sh.need) {
+      stage_range(body, len, round_abs, round_abs + u64(kDescThreads) * slice, sh.stage);
       __syncthreads();
     }
-    const u64 s0 = r0 + u64(lane) * slice;
-    {  // 1. speculative slices
-      BitIn r = staged_reader(sh.stage, len, s0);
-      slice_decode(sh.tables, r, s0 + slice, sh.visit[lane], s0, sh.xpos[lane], sh.count[lane],
-                   sh.ev[lane], sh.evpos[lane], sh.evend[lane]);
-    }
-    __syncthreads();
-    if (lane < 63) {  // 2. continuation into the next slice
+    const u32 r0 = u32(round_abs - sh.stage.bit0);
+    const u32 s0 = r0 + t * slice;
+    {  // 1. speculative slices, then 2. continuation into the next slice
+      StagedBits r = stage_bits(sh.stage, len, s0);
+      u32 cnt, ev, evpos = 0, evend = 0;
+      desc_slice(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend);
+      sh.xpos[t] = r.pos;
+      sh.count[t] = cnt;
+      sh.ev[t] = ev;
+      sh.evpos[t] = evpos;
+      sh.evend[t] = evend;
+      __syncthreads();
       u32 merge = kNoMerge, tail = 0;
-      if (!sh.ev[lane]) {
-        const u64 s1 = s0 + slice;
-        BitIn r = staged_reader(sh.stage, len, sh.xpos[lane]);
+      if (t + 1 < kDescThreads && !ev) {
+        const u32 s1 = s0 + slice;
         for (;;) {
-          const u64 off = r.pos - s1;
-          if (off >= kSyncBits || r.pos >= s1 + slice) break;
-          if (visited(sh, lane + 1, off)) { merge = u32(off); break; }
+          const u32 off = r.pos - s1;
+          if (off >= slice) break;
+          if (desc_visited(sh, t + 1, off)) { merge = off; break; }
           u32 lit, length, distance;
           if (decode_token(sh.tables, r, 32768u, lit, length, distance) || !length) break;
           tail += length;
         }
       }
-      sh.merge[lane + 1] = merge;
-      sh.tail[lane] = tail;
+      if (t + 1 < kDescThreads) sh.merge[t + 1] = merge;
+      sh.tail[t] = tail;
+      if (!t) sh.merge[0] = kNoMerge;
     }
-    if (!lane) sh.merge[0] = kNoMerge;
     __syncthreads();
-    // 3. bytes before the merge point of each lane's own decoding
-    sh.before[lane] = sh.merge[lane] != kNoMerge ? bytes_between(sh.tables, sh.stage, len, s0, s0 + sh.merge[lane]) : 0u;
+    // 3. bytes before the merge point of each lane's own decode; per-slice
+    // bytes of a merged run (own bytes after the merge point plus the
+    // continuation when the next lane merged), their prefix sum, and the
+    // break and event masks.
+    const u32 before = sh.merge[t] != kNoMerge
+                           ? desc_bytes_between(sh.tables, sh.stage, len, s0, s0 + sh.merge[t])
+                           : 0u;
+    sh.before[t] = before;
+    u32 bsl = sh.count[t] - before;
+    if (t + 1 < kDescThreads && sh.merge[t + 1] != kNoMerge) bsl += sh.tail[t];
+    u32 x = bsl;
+    for (u32 o = 1; o < 64; o <<= 1) {
+      const u32 y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) sh.wsum[wave] = x;
+    const u64 bm = __ballot(t > 0 && sh.merge[t] == kNoMerge);
+    const u64 em = __ballot(sh.ev[t] != 0);
+    if (!lane) {
+      sh.brk[wave] = bm;
+      sh.evm[wave] = em;
+      sh.runs[wave] = 0;
+      sh.serial[wave] = 0;
+    }
     __syncthreads();
-    if (!lane) {  // 4. chain the true entries
+    for (u32 w = 0; w < wave; ++w) x += sh.wsum[w];
+    sh.prefix[t] = x;
+    __syncthreads();
+    if (!t) {  // 4. runs and breaks
+      u32 lanes = kDescThreads;
+      u32 e = r0;       // true position
+      u64 T = total;    // block bytes before e
+      u32 j = 0;        // lane whose slice contains e, synced at e
+      u32 j_entry = r0;  // true entry of slice j
+      u64 j_off = T;     // output offset of slice j's entry
+      i64 adj = 0;       // bytes lane j produced before the sync point (negated)
+      bool round_done = false;
+      while (!round_done && !done) {
+        // Run from lane j: lanes j+1 .. b-1 merged, so they are synced too.
+        sh.entry[j] = j_entry;
+        sh.off[j] = u32(j_off);
+        sh.runs[j >> 6] |= 1ull << (j & 63);
+        const u64 pj = j ? sh.prefix[j - 1] : 0u;
+        sh.runbase[j] = u32(T + u64(adj) - pj);
+        const u32 b = next_bit(sh.brk, j + 1), E = next_bit(sh.evm, j);
+        if (E < b) {
+          T += u64(sh.prefix[E] - pj) + u64(adj);
+          if (sh.ev[E] == 1) end = sh.stage.bit0 + sh.evend[E];
+          else {
+            status = sh.ev[E] & 0xffu;
+            end = sh.stage.bit0 + sh.evpos[E];
+          }
+          lanes = E + 1;
+          done = true;
+          break;
+        }
+        T += u64(sh.prefix[b - 1] - pj) + u64(adj);
+        e = sh.xpos[b - 1];
+        if (b == kDescThreads) break;
+        // Break at lane b: decode serially from the true position until it
+        // meets the tokens of a later lane.
+        u32 k = b;
+        for (;;) {
+          if (k >= kDescThreads) { round_done = true; break; }
+          const u32 sk = r0 + k * slice;
+          const u32 k_entry = e;
+          const u64 k_off = T;
+          bool synced = false;
+          StagedBits r = stage_bits(sh.stage, len, e);
+          for (;;) {
+            const u32 off = e - sk;
+            if (desc_visited(sh, k, off)) { synced = true; break; }
+            if (off >= slice) break;
+            u32 lit, length, distance;
+            const u32 err = decode_token(sh.tables, r, 32768u, lit, length, distance);
+            if (err) { status = err; end = sh.stage.bit0 + e; done = true; break; }
+            if (!length) { end = sh.stage.bit0 + r.pos; done = true; break; }
+            T += length;
+            e = r.pos;
+          }
+          if (done || !synced) {
+            // Slice k decoded serially (entirely, or up to the block end).
+            sh.entry[k] = k_entry;
+            sh.off[k] = u32(k_off);
+            sh.serial[k >> 6] |= 1ull << (k & 63);
+            if (done) { lanes = k + 1; break; }
+            ++k;
+            continue;
+          }
+          j = k;
+          j_entry = k_entry;
+          j_off = k_off;
+          // The run's per-slice bytes already exclude lane k's phase-3 prefix
+          // (non-zero when an untrue continuation merged into lane k).
+          adj = i64(sh.before[k]) - i64(desc_bytes_between(sh.tables, sh.stage, len, sk, e));
+          break;
+        }
+      }
+      if (!done && T > limit) { status = kOutputOverflow; end = sh.stage.bit0 + e; done = true; }
+      if (!done && sh.stage.bit0 + e >= len * 8) { status = kTruncated; end = sh.stage.bit0 + e; done = true; }
+      total = T;
+      e_abs = sh.stage.bit0 + e;
+      // Slice groups for this round's lanes (consecutive ids, 64 slices each).
+      const u32 ng = (lanes + 63) / 64;
       u32 g = kNone;
       if (keep) {
-        const u64 gi = atomicAdd(reinterpret_cast<unsigned long long*>(&st->groups_used), 1ull);
-        if (gi < group_capacity) {
+        const u64 gi = atomicAdd(reinterpret_cast<unsigned long long*>(&st->groups_used), u64(ng));
+        if (gi + ng <= group_capacity) {
           g = u32(gi);
-          group_link[g] = kNone;
           if (last_group == kNone) group = g;
           else group_link[last_group] = g;
-          last_group = g;
+          for (u32 i = 0; i + 1 < ng; ++i) group_link[g + i] = g + i + 1;
+          group_link[g + ng - 1] = kNone;
+          last_group = g + ng - 1;
         } else {
           keep = false;
           group = kNone;
         }
       }
-      bool via_merge = false;
-      for (u32 j = 0; j < 64 && !done; ++j) {
-        const u64 sj = r0 + u64(j) * slice;
-        u32 before = 0;
-        bool synced = j == 0;
-        if (!synced && via_merge && e == sj + sh.merge[j]) {
-          synced = true;
-          before = sh.before[j];
-        }
-        if (!synced) {
-          // Advance the true position until it meets lane j's tokens.
-          for (;;) {
-            const u64 off = e - sj;
-            if (visited(sh, j, off)) {
-              synced = true;
-              before = bytes_between(sh.tables, sh.stage, len, sj, e);
-              break;
-            }
-            if (off >= kSyncBits || e >= sj + slice) break;
-            BitIn r = staged_reader(sh.stage, len, e);
-            u32 lit, length, distance;
-            const u32 err = decode_token(sh.tables, r, 32768u, lit, length, distance);
-            if (err) { status = err; end = e; done = true; break; }
-            if (!length) { end = r.pos; done = true; break; }
-            total += length;
-            e = r.pos;
-          }
-          if (done) break;
-        }
-        if (keep) {
-          slice_entry[u64(g) * 64 + j] = e;
-          slice_off[u64(g) * 64 + j] = u32(total);
-        }
-        ++lanes;
-        u64 xpos, evpos, evend;
-        u32 count, ev;
-        if (synced) {
-          xpos = sh.xpos[j];
-          count = sh.count[j];
-          ev = sh.ev[j];
-          evpos = sh.evpos[j];
-          evend = sh.evend[j];
-        } else {
-          // Lane j never met the true tokens in its window: decode its slice.
-          BitIn r = staged_reader(sh.stage, len, e);
-          slice_decode(sh.tables, r, sj + slice, nullptr, 0, xpos, count, ev, evpos, evend);
-          before = 0;
-        }
-        total += count - before;
-        if (ev == 1) { end = evend; done = true; break; }
-        if (ev) { status = ev & 0xffu; end = evpos; done = true; break; }
-        e = xpos;
-        via_merge = false;
-        if (synced && j < 63 && sh.merge[j + 1] != kNoMerge) {
-          total += sh.tail[j];
-          e = r0 + u64(j + 1) * slice + sh.merge[j + 1];
-          via_merge = true;
-        }
-        if (total > limit) { status = kOutputOverflow; end = e; done = true; break; }
-      }
-      if (!done && e >= len * 8) { status = kTruncated; end = e; done = true; }
+      lanes_total += lanes;
+      sh.group = g;
+      sh.lanes = lanes;
       sh.status = status;
       sh.end = end;
       sh.size = total;
-      sh.group = keep ? group : kNone;
-      sh.lanes = lanes;
+      sh.go = done ? 0u : 1u;
     }
     __syncthreads();
+    // Entries and offsets of the merged lanes; slice groups.
+    const u32 lanes = sh.lanes, g = sh.group;
+    if (t < lanes) {
+      u32 entry, off;
+      const bool explicit_ = ((sh.runs[wave] | sh.serial[wave]) >> lane) & 1;
+      if (explicit_) {
+        entry = sh.entry[t];
+        off = sh.off[t];
+      } else {
+        const u32 j = prev_bit(sh.runs, t);
+        entry = s0 + sh.merge[t];
+        off = sh.runbase[j] + sh.prefix[t - 1];
+      }
+      if (g != kNone) {
+        slice_entry[u64(g) * 64 + t] = sh.stage.bit0 + entry;
+        slice_off[u64(g) * 64 + t] = off;
+      }
+    }
+    done = !sh.go;
+    __syncthreads();
   }
+  if (!t) {
+    sh.group = keep ? group : kNone;
+    sh.lanes = lanes_total;
+  }
+  __syncthreads();
 }
 
 }  // namespace
 
-// One wave per candidate: describe the candidate's segment (its block and the
-// following stored/fixed blocks up to the next candidate) with wave-parallel
+// One workgroup per candidate: describe the candidate's segment (its block and
+// the following stored/fixed blocks up to the next candidate) with parallel
 // token decoding, and record per-block slices for emission.
-__global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const u64* cand, State* st,
-                                                 u64 out_size, u64* seg_end, u64* seg_size,
-                                                 u32* seg_blocks, u32* seg_next, u32* seg_flags,
-                                                 u32* seg_rec, BlockRec* recs, u64 rec_capacity,
-                                                 u64* slice_entry, u32* slice_off, u32* group_link,
-                                                 u64 group_capacity) {
-  __shared__ SpecShared sh;
+__global__ __launch_bounds__(kDescThreads) void g_describe(
+    const u8* body, u64 len, const u64* cand, State* st, u64 out_size, u64* seg_end,
+    u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags, u32* seg_rec, BlockRec* recs,
+    u64 rec_capacity, u64* slice_entry, u32* slice_off, u32* group_link, u64 group_capacity) {
+  __shared__ DescShared sh;
   if (st->status) return;
-  const u32 lane = threadIdx.x;
+  const u32 t = threadIdx.x;
   const u64 n = st->candidates;
   for (u64 c = blockIdx.x; c < n; c += gridDim.x) {
     u64 produced = 0;
     u32 blocks = 0, status = 0, final_block = 0, next = kNone, first_rec = kNone, last_rec = kNone;
     bool recs_ok = true;
-    if (!lane) {
+    if (!t) {
       sh.pos = cand[c];
       sh.stage.count = 0;
       sh.stage.bit0 = 0;
     }
     __syncthreads();
     for (;;) {
-      block_header(body, len, out_size, sh);
-      if (!lane && sh.type && !sh.status) {
+      block_header<true>(body, len, out_size, sh);
+      if (!t && sh.type && !sh.status) {
         const u64 idx = lower_bound(cand, n, sh.pos + 1);
         sh.hint = idx < n ? cand[idx] : len * 8;
         sh.group = kNone;
@@ -930,7 +1059,7 @@ __global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const 
       if (sh.type && !sh.status)
         describe_tokens(body, len, out_size, sh, st, slice_entry, slice_off, group_link,
                         group_capacity);
-      if (!lane) {
+      if (!t) {
         ++blocks;
         const u32 bstatus = sh.status;
         if (bstatus) status = bstatus;
@@ -977,7 +1106,7 @@ __global__ __launch_bounds__(64) void g_describe(const u8* body, u64 len, const 
       __syncthreads();
       if (!sh.go) break;
     }
-    if (!lane) {
+    if (!t) {
       seg_end[c] = sh.end;
       seg_size[c] = produced;
       seg_blocks[c] = blocks;
@@ -1615,7 +1744,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
   HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
   HZ_TRY(scratch.alloc(&group_link, group_capacity));
-  HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kWave), 0, stream, body, len,
+  HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kDescThreads), 0, stream, body, len,
             cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
             rec_capacity, slice_entry, slice_off, group_link, group_capacity);
   HZ_TRY(hipGetLastError());

@@ -91,3 +91,34 @@ def test_mutations_match_oracle(gpu, seed):
         want = oracle.decompress(payload, expected, *limits)
         got, status, _ = capi_decompress(payload, expected, *limits)
         assert (status, got) == (want[1], want[0]), "trial %d" % trial
+
+
+def test_fast_chain_accepts_large_dynamic_blocks(gpu):
+    """A strain stream (16 KiB dynamic blocks, ~120 kbit each) decodes through
+    the parallel chain: the serial exact walk returns immediately."""
+    import ctypes
+    import numpy as np
+    import torch
+    import workloads
+    from cuda_zlib import _native
+    raw = workloads.strain((4 << 20) // 4, 1)
+    payload = zlib.compress(raw, 6)
+    lib = _native.load()
+    dev = torch.device("cuda", 0)
+    src = torch.from_numpy(np.frombuffer(payload, np.uint8).copy()).to(dev)
+    out = torch.empty(len(raw), dtype=torch.uint8, device=dev)
+    meta = torch.zeros(2, dtype=torch.uint32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    _native.profile_collect(lib)
+    lib.HipZlibProfileEnable(1)
+    try:
+        _native.check(lib, lib.HipZlibDecompress(stream, 262144, 262144, ctypes.c_void_p(src.data_ptr()),
+                                                 len(payload), ctypes.c_void_p(out.data_ptr()),
+                                                 len(raw), ctypes.c_void_p(meta.data_ptr()), 2))
+        torch.cuda.synchronize(dev)
+    finally:
+        lib.HipZlibProfileEnable(0)
+    kernels = _native.profile_collect(lib)
+    assert int(meta.cpu().numpy()[0]) == 0
+    assert out.cpu().numpy().tobytes() == raw
+    assert kernels["g_exact_walk"][1] < 1.0, kernels["g_exact_walk"]
