@@ -515,6 +515,147 @@ __device__ __forceinline__ u32 decode_token(const DecodeTables& t, Reader& r, u3
   return kOk;
 }
 
+// ---- fast token decoding ---------------------------------------------------
+// After a table build, the primary LUT can be rewritten into a format that
+// resolves a token's class and constants with one lookup:
+//   literal/length: bits 0-3 code length (0: no code of <= P bits here),
+//     bits 4-5 kind, bits 8-15 literal byte or length extra-bit count,
+//     bits 16-31 length base;
+//   distance: bits 0-3 code length, bits 4-7 extra-bit count, bit 8 invalid
+//     symbol (30, 31), bits 16-31 distance base.
+// Codes longer than P bits and invalid prefixes take the canonical walk over
+// count/symbols, which the rewrite leaves untouched.
+enum : u32 { kKindLit = 0, kKindLen = 1, kKindEob = 2, kKindBad = 3 };
+
+__device__ __forceinline__ u32 fast_ll_entry(u32 sym, u32 l) {
+  if (sym < 256) return l | (sym << 8);
+  if (sym == 256) return l | (kKindEob << 4);
+  if (sym > 285) return l | (kKindBad << 4);
+  const u32 li = sym - 257;
+  return l | (kKindLen << 4) | (length_extra(li) << 8) | (length_base(li) << 16);
+}
+
+__device__ __forceinline__ u32 fast_d_entry(u32 sym, u32 l) {
+  if (sym > 29) return l | 0x100u;
+  return l | (dist_extra(sym) << 4) | (dist_base(sym) << 16);
+}
+
+// Rewrite a built table's primary LUT (threads `first`, `first + step`, ...).
+template <int N, int P>
+__device__ void fast_format(HuffTable<N, P>& t, bool literal_length, u32 first, u32 step) {
+  for (u32 i = first; i < (1u << P); i += step) {
+    const u32 e = t.primary[i];
+    const u32 l = e & 15u;
+    if (l) t.primary[i] = literal_length ? fast_ll_entry(e >> 16, l) : fast_d_entry(e >> 16, l);
+  }
+}
+
+// LSB-first reader over LDS words with 32-bit positions: two words in
+// registers, extraction by funnel shift.  kChecked: avail() is the distance to
+// `limit` (the body end); otherwise the caller guarantees that no consumed bit
+// lies past the body end, and avail() is unbounded.  Words are read up to
+// index (pos >> 5) + 1, which the caller keeps inside the word array.
+template <bool kChecked>
+struct WordBits {
+  const u32* words;
+  u32 w, lo, hi, off, limit;
+  __device__ __forceinline__ void seek(u32 p) {
+    w = p >> 5;
+    off = p & 31u;
+    lo = words[w];
+    hi = words[w + 1];
+  }
+  __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
+  __device__ __forceinline__ u32 bits32() const { return __builtin_amdgcn_alignbit(hi, lo, off); }
+  __device__ __forceinline__ void drop(u32 n) {  // n <= 32
+    off += n;
+    if (off >= 32) {
+      off -= 32;
+      lo = hi;
+      ++w;
+      hi = words[w + 1];
+    }
+  }
+  __device__ __forceinline__ u32 avail() const {
+    if (!kChecked) return 0xffffffffu;
+    const u32 p = pos();
+    return p < limit ? limit - p : 0u;
+  }
+};
+
+// Canonical walk over the next bits `b` (LSB first), as huff_decode does on a
+// LUT miss.  Returns the symbol and its length, or -1 with `err`.
+template <int N, int P>
+__device__ __forceinline__ i32 canon_walk(const HuffTable<N, P>& t, u32 b, u32 avail, u32& len_out,
+                                          u32& err) {
+  u32 code = 0, first = 0, index = 0;
+  for (u32 len = 1; len <= t.maximum; ++len) {
+    if (len > avail) { err = kTruncated; return -1; }
+    code |= (b >> (len - 1)) & 1u;
+    const u32 c = t.count[len];
+    if (code < first + c) {
+      len_out = len;
+      return i32(t.symbols[index + code - first]);
+    }
+    index += c;
+    first = (first + c) << 1;
+    code <<= 1;
+  }
+  err = kBadSymbol;
+  return -1;
+}
+
+// One token with fast-format tables; same results and error order as
+// decode_token over the standard format (a distance is at most 32768).
+template <class R>
+__device__ __forceinline__ u32 fast_token(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
+                                          R& r, u32& lit, u32& length, u32& distance) {
+  length = 0;
+  distance = 0;
+  u32 b = r.bits32();
+  u32 e = ll.primary[b & 1023u];
+  u32 l = e & 15u;
+  if (!l) {
+    u32 err = 0;
+    const i32 sym = canon_walk(ll, b, r.avail(), l, err);
+    if (sym < 0) return err;
+    e = fast_ll_entry(u32(sym), l);
+  }
+  if (l > r.avail()) return kTruncated;
+  r.drop(l);
+  const u32 kind = (e >> 4) & 3u;
+  if (kind == kKindLit) {
+    lit = (e >> 8) & 0xffu;
+    length = 1;
+    return kOk;
+  }
+  if (kind == kKindEob) return kOk;
+  if (kind == kKindBad) return kBadSymbol;
+  const u32 nx = (e >> 8) & 15u;
+  if (nx > r.avail()) return kTruncated;
+  b = r.bits32();
+  length = (e >> 16) + (b & ((1u << nx) - 1u));
+  r.drop(nx);
+  b = r.bits32();
+  u32 d = dd.primary[b & 255u];
+  u32 dl = d & 15u;
+  if (!dl) {
+    u32 err = 0;
+    const i32 sym = canon_walk(dd, b, r.avail(), dl, err);
+    if (sym < 0) return err;
+    d = fast_d_entry(u32(sym), dl);
+  }
+  if (dl > r.avail()) return kTruncated;
+  r.drop(dl);
+  if (d & 0x100u) return kBadSymbol;
+  const u32 dx = (d >> 4) & 15u;
+  if (dx > r.avail()) return kTruncated;
+  b = r.bits32();
+  distance = (d >> 16) + (b & ((1u << dx) - 1u));
+  r.drop(dx);
+  return kOk;
+}
+
 // zlib wrapper (RFC 1950) checks, in the reference's precedence order.
 __host__ __device__ __forceinline__ u32 check_framing(const u8* in, u64 size, u32& window,
                                                        u32& wanted) {

@@ -23,6 +23,8 @@
 // (select_chain, _decode_kernels.py:1226-1408) > emission history/window
 // (parse_block<Emit>, 683-781; EmissionStatus codec_ffi.cu:405-435) > Adler-32
 // (467-483).  Failed output is all zeros except on an Adler-32 mismatch.
+#include <algorithm>
+
 #include "deflate_common.h"
 #include "kernels.h"
 
@@ -52,6 +54,7 @@ struct State {
   u64 recs_used;     // block records handed out by describe
   u64 groups_used;   // 64-slot slice groups handed out by describe
   u64 precount;      // entries of the dense pre-candidate array
+  u64 tables_used;   // stored per-block decode tables
 };
 
 struct Segment {
@@ -77,11 +80,21 @@ struct BlockRec {
   u32 lanes;      // slices (fixed/dynamic)
   u32 group;      // first slice group
   u32 next;       // next record of the segment, or kNone
+  u32 table;      // stored fast-format tables (BlockTables), or kNone
+  u32 pad;
+};
+
+// Literal/length and distance tables of one block in the fast LUT format,
+// stored by describe for emission.
+struct BlockTables {
+  HuffTable<288, 10> ll;
+  HuffTable<32, 8> dd;
+  u32 pad[2];
 };
 
 constexpr u32 kStageBytes = 16384;                 // LDS bitstream window per wave
 constexpr u32 kStageMargin = 64;                   // bytes staged past the last slice
-constexpr u32 kStageWords = (kStageBytes + kStageMargin) / 4 + 2;
+constexpr u32 kStageWords = (kStageBytes + kStageMargin) / 4 + 4;
 constexpr u64 kMinSlice = 64;                      // bits; > longest token (48 bits)
 constexpr u64 kMaxSlice = (u64(kStageBytes) * 8) / 64;
 constexpr u32 kWindowSlots = 32;                   // token starts recorded per slice window
@@ -376,6 +389,7 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
   st->recs_used = 0;
   st->groups_used = 0;
   st->precount = 0;
+  st->tables_used = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -652,7 +666,7 @@ struct DescShared {
   u32 wsum[kDescWaves];
   // control written by lane 0 (block_header interface: pos, d0, end, size, type, ...)
   u64 pos, d0, hint, end, size, round;
-  u32 slice, need;
+  u32 slice, need, table;
   u32 type, final_block, status, nl, nd, go, build_status, group, lanes;
 };
 
@@ -660,60 +674,63 @@ __device__ __forceinline__ bool desc_visited(const DescShared& sh, u32 lane, u32
   return off < kVisitBits && ((sh.visit[lane][off >> 6] >> (off & 63)) & 1);
 }
 
-__device__ __forceinline__ StagedBits stage_bits(const Stage& sg, u64 len, u32 pos) {
-  StagedBits r;
-  r.words = sg.words;
-  r.nwords = sg.count;
+// Body end relative to the stage's word 0 (saturated).
+__device__ __forceinline__ u32 stage_limit(const Stage& sg, u64 len) {
   const u64 lim = len * 8 - sg.bit0;  // modular: bit0 may precede the body by < 32 bits
-  r.limit = lim > 0xffffffffull ? 0xffffffffu : u32(lim);
+  return lim > 0xffffffffull ? 0xffffffffu : u32(lim);
+}
+
+template <bool kChecked>
+__device__ __forceinline__ WordBits<kChecked> word_bits(const Stage& sg, u32 limit, u32 pos) {
+  WordBits<kChecked> r;
+  r.words = sg.words;
+  r.limit = limit;
   r.seek(pos);
   return r;
 }
 
-// Token-level decode from r.pos until r.pos >= stop, an EOB or an error.
-// ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  With
-// `visit`, every token start in [win0, win0 + kVisitBits) is recorded (the bits
-// of the current 64-bit word accumulate in a register).
-__device__ void desc_slice(const DecodeTables& t, StagedBits& r, u32 stop, u64* visit, u32 win0,
-                           u32& count, u32& ev, u32& evpos, u32& evend) {
+// Token-level decode from r.pos() until it reaches `stop`, an EOB or an error.
+// ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  Every token
+// start in [win0, win0 + kVisitBits) is recorded in `visit` (the bits of the
+// current 64-bit word accumulate in a register).
+template <bool kChecked>
+__device__ void desc_slice(const DecodeTables& t, WordBits<kChecked>& r, u32 stop, u64* visit,
+                           u32 win0, u32& count, u32& ev, u32& evpos, u32& evend) {
   u32 produced = 0, cw = 0;
   u64 bits = 0;
   ev = 0;
-  if (visit)
-    for (u32 w = 0; w < kVisitWords; ++w) visit[w] = 0;
+  for (u32 w = 0; w < kVisitWords; ++w) visit[w] = 0;
   for (;;) {
-    const u32 p = r.pos;
+    const u32 p = r.pos();
     if (p >= stop) break;
-    if (visit) {
-      const u32 off = p - win0;
-      if (off < kVisitBits) {
-        const u32 w = off >> 6;
-        if (w != cw) {
-          visit[cw] = bits;
-          bits = 0;
-          cw = w;
-        }
-        bits |= 1ull << (off & 63);
+    const u32 off = p - win0;
+    if (off < kVisitBits) {
+      const u32 w = off >> 6;
+      if (w != cw) {
+        visit[cw] = bits;
+        bits = 0;
+        cw = w;
       }
+      bits |= 1ull << (off & 63);
     }
     u32 lit, length, distance;
-    const u32 err = decode_token(t, r, 32768u, lit, length, distance);
+    const u32 err = fast_token(t.ll, t.dd, r, lit, length, distance);
     if (err) { ev = 0x100u | err; evpos = p; break; }
-    if (!length) { ev = 1; evpos = p; evend = r.pos; break; }
-    produced += length;
-    if (produced >= 0x40000000u) { ev = 0x100u | kOutputOverflow; evpos = p; break; }
+    if (!length) { ev = 1; evpos = p; evend = r.pos(); break; }
+    produced += length;  // <= 512 tokens of <= 258 bytes per slice
   }
-  if (visit) visit[cw] = bits;
+  visit[cw] = bits;
   count = produced;
 }
 
 // Bytes produced by decoding tokens from `from` up to token start `to`.
-__device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u64 len, u32 from, u32 to) {
-  StagedBits r = stage_bits(sg, len, from);
+template <bool kChecked>
+__device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u32 limit, u32 from, u32 to) {
+  WordBits<kChecked> r = word_bits<kChecked>(sg, limit, from);
   u32 bytes = 0;
-  while (r.pos < to) {
+  while (r.pos() < to) {
     u32 lit, length, distance;
-    if (decode_token(t, r, 32768u, lit, length, distance) || !length) break;
+    if (fast_token(t.ll, t.dd, r, lit, length, distance) || !length) break;
     bytes += length;
   }
   return bytes;
@@ -743,7 +760,7 @@ __device__ __forceinline__ u32 prev_bit(const u64* mask, u32 at) {
 // dynamic code lengths; then the wave builds fixed/dynamic tables.  Sets
 // sh.type, sh.final_block, sh.status, sh.d0 (first token or payload bit) and,
 // for stored blocks, sh.end/sh.size.
-template <bool kOneWave = false, typename Shared>
+template <bool kOneWave = false, bool kFast = false, typename Shared>
 __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
   const u32 lane = threadIdx.x;
   if (!staged_covers(sh.stage, body, len, sh.pos, sh.pos + 4096)) {
@@ -794,9 +811,211 @@ __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
         err = huff_build_wave<32, 8, kOneWave>(sh.tables.dd, sh.tables.lens + sh.nl, sh.nd, !fixed,
                                                true, 15, sh.codes, &sh.build_status);
       if (!lane) sh.status = err;
+      if (kFast && !err) {
+        wave_sync();
+        fast_format(sh.tables.ll, true, lane, 64);
+        fast_format(sh.tables.dd, false, lane, 64);
+      }
     }
     __syncthreads();
   }
+}
+
+// State of one block's description across rounds (meaningful in thread 0).
+struct DescRun {
+  u64 e_abs, total, end;
+  u32 status, lanes_total, group, last_group;
+  bool done, keep;
+};
+
+// One round of describe_tokens: 256 slices of `slice` bits from round_abs.
+template <bool kChecked>
+__device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u64* slice_entry,
+                               u32* slice_off, u32* group_link, u64 group_capacity, DescRun& run,
+                               u64 round_abs, u32 slice) {
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  const u32 blim = stage_limit(sh.stage, len);
+  const u32 r0 = u32(round_abs - sh.stage.bit0);
+  const u32 s0 = r0 + t * slice;
+  {  // 1. speculative slices, then 2. continuation into the next slice
+    WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, s0);
+    u32 cnt, ev, evpos = 0, evend = 0;
+    desc_slice<kChecked>(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend);
+    sh.xpos[t] = r.pos();
+    sh.count[t] = cnt;
+    sh.ev[t] = ev;
+    sh.evpos[t] = evpos;
+    sh.evend[t] = evend;
+    __syncthreads();
+    u32 merge = kNoMerge, tail = 0;
+    if (t + 1 < kDescThreads && !ev) {
+      const u32 s1 = s0 + slice;
+      for (;;) {
+        const u32 off = r.pos() - s1;
+        if (off >= slice) break;
+        if (desc_visited(sh, t + 1, off)) { merge = off; break; }
+        u32 lit, length, distance;
+        if (fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance) || !length) break;
+        tail += length;
+      }
+    }
+    if (t + 1 < kDescThreads) sh.merge[t + 1] = merge;
+    sh.tail[t] = tail;
+    if (!t) sh.merge[0] = kNoMerge;
+  }
+  __syncthreads();
+  // 3. bytes before the merge point of each lane's own decode; per-slice
+  // bytes of a merged run (own bytes after the merge point plus the
+  // continuation when the next lane merged), their prefix sum, and the break
+  // and event masks.
+  const u32 before = sh.merge[t] != kNoMerge
+                         ? desc_bytes_between<kChecked>(sh.tables, sh.stage, blim, s0, s0 + sh.merge[t])
+                         : 0u;
+  sh.before[t] = before;
+  u32 bsl = sh.count[t] - before;
+  if (t + 1 < kDescThreads && sh.merge[t + 1] != kNoMerge) bsl += sh.tail[t];
+  u32 x = bsl;
+  for (u32 o = 1; o < 64; o <<= 1) {
+    const u32 y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sh.wsum[wave] = x;
+  const u64 bm = __ballot(t > 0 && sh.merge[t] == kNoMerge);
+  const u64 em = __ballot(sh.ev[t] != 0);
+  if (!lane) {
+    sh.brk[wave] = bm;
+    sh.evm[wave] = em;
+    sh.runs[wave] = 0;
+    sh.serial[wave] = 0;
+  }
+  __syncthreads();
+  for (u32 w = 0; w < wave; ++w) x += sh.wsum[w];
+  sh.prefix[t] = x;
+  __syncthreads();
+  if (!t) {  // 4. runs and breaks
+    u32 lanes = kDescThreads;
+    u32 e = r0;         // true position
+    u64 T = run.total;  // block bytes before e
+    u32 j = 0;          // lane whose slice contains e, synced at e
+    u32 j_entry = r0;   // true entry of slice j
+    u64 j_off = T;      // output offset of slice j's entry
+    i64 adj = 0;        // correction of lane j's per-slice bytes for its sync point
+    bool round_done = false, done = false;
+    while (!round_done && !done) {
+      // Run from lane j: lanes j+1 .. b-1 merged, so they are synced too.
+      sh.entry[j] = j_entry;
+      sh.off[j] = u32(j_off);
+      sh.runs[j >> 6] |= 1ull << (j & 63);
+      const u64 pj = j ? sh.prefix[j - 1] : 0u;
+      sh.runbase[j] = u32(T + u64(adj) - pj);
+      const u32 b = next_bit(sh.brk, j + 1), E = next_bit(sh.evm, j);
+      if (E < b) {
+        T += u64(sh.prefix[E] - pj) + u64(adj);
+        if (sh.ev[E] == 1) run.end = sh.stage.bit0 + sh.evend[E];
+        else {
+          run.status = sh.ev[E] & 0xffu;
+          run.end = sh.stage.bit0 + sh.evpos[E];
+        }
+        lanes = E + 1;
+        done = true;
+        break;
+      }
+      T += u64(sh.prefix[b - 1] - pj) + u64(adj);
+      e = sh.xpos[b - 1];
+      if (b == kDescThreads) break;
+      // Break at lane b: decode serially from the true position until it
+      // meets the tokens of a later lane.
+      u32 k = b;
+      for (;;) {
+        if (k >= kDescThreads) { round_done = true; break; }
+        const u32 sk = r0 + k * slice;
+        const u32 k_entry = e;
+        const u64 k_off = T;
+        bool synced = false;
+        WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, e);
+        for (;;) {
+          const u32 off = e - sk;
+          if (desc_visited(sh, k, off)) { synced = true; break; }
+          if (off >= slice) break;
+          u32 lit, length, distance;
+          const u32 err = fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance);
+          if (err) { run.status = err; run.end = sh.stage.bit0 + e; done = true; break; }
+          if (!length) { run.end = sh.stage.bit0 + r.pos(); done = true; break; }
+          T += length;
+          e = r.pos();
+        }
+        if (done || !synced) {
+          // Slice k decoded serially (entirely, or up to the block end).
+          sh.entry[k] = k_entry;
+          sh.off[k] = u32(k_off);
+          sh.serial[k >> 6] |= 1ull << (k & 63);
+          if (done) { lanes = k + 1; break; }
+          ++k;
+          continue;
+        }
+        j = k;
+        j_entry = k_entry;
+        j_off = k_off;
+        // The run's per-slice bytes already exclude lane k's phase-3 prefix
+        // (non-zero when an untrue continuation merged into lane k).
+        adj = i64(sh.before[k]) - i64(desc_bytes_between<kChecked>(sh.tables, sh.stage, blim, sk, e));
+        break;
+      }
+    }
+    if (!done && T > limit) {
+      run.status = kOutputOverflow;
+      run.end = sh.stage.bit0 + e;
+      done = true;
+    }
+    if (!done && sh.stage.bit0 + e >= len * 8) {
+      run.status = kTruncated;
+      run.end = sh.stage.bit0 + e;
+      done = true;
+    }
+    run.total = T;
+    run.e_abs = sh.stage.bit0 + e;
+    run.done = done;
+    // Slice groups for this round's lanes (consecutive ids, 64 slices each).
+    const u32 ng = (lanes + 63) / 64;
+    u32 g = kNone;
+    if (run.keep) {
+      const u64 gi = atomicAdd(reinterpret_cast<unsigned long long*>(&st->groups_used), u64(ng));
+      if (gi + ng <= group_capacity) {
+        g = u32(gi);
+        if (run.last_group == kNone) run.group = g;
+        else group_link[run.last_group] = g;
+        for (u32 i = 0; i + 1 < ng; ++i) group_link[g + i] = g + i + 1;
+        group_link[g + ng - 1] = kNone;
+        run.last_group = g + ng - 1;
+      } else {
+        run.keep = false;
+        run.group = kNone;
+      }
+    }
+    run.lanes_total += lanes;
+    sh.group = g;
+    sh.lanes = lanes;
+    sh.go = done ? 0u : 1u;
+  }
+  __syncthreads();
+  // Entries and offsets of the merged lanes; slice groups.
+  const u32 lanes = sh.lanes, g = sh.group;
+  if (t < lanes) {
+    u32 entry, off;
+    if (((sh.runs[wave] | sh.serial[wave]) >> lane) & 1) {
+      entry = sh.entry[t];
+      off = sh.off[t];
+    } else {
+      const u32 j = prev_bit(sh.runs, t);
+      entry = s0 + sh.merge[t];
+      off = sh.runbase[j] + sh.prefix[t - 1];
+    }
+    if (g != kNone) {
+      slice_entry[u64(g) * 64 + t] = sh.stage.bit0 + entry;
+      slice_off[u64(g) * 64 + t] = off;
+    }
+  }
+  __syncthreads();
 }
 
 // Describe the tokens of the fixed/dynamic block whose tables are built and
@@ -809,27 +1028,36 @@ __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
 //      round's true entry; a run of merged slices needs no further work, and
 //      lane 0 decodes serially only where a merge is missing (a "break"),
 //      until the true tokens meet the next lane's tokens.
+// Rounds away from the body end decode without truncation checks.
 // Results: sh.status, sh.end (bit after the EOB), sh.size, and slice groups
 // (sh.group = kNone if capacity ran out; emission then decodes serially).
 __device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& sh, State* st,
                                 u64* slice_entry, u32* slice_off, u32* group_link,
                                 u64 group_capacity) {
-  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
-  u64 e_abs = sh.d0, total = 0;
-  bool done = false, keep = true;
-  u32 last_group = kNone, status = 0, lanes_total = 0, group = kNone;
-  u64 end = 0;
+  const u32 t = threadIdx.x;
+  DescRun run;
+  run.e_abs = sh.d0;
+  run.total = 0;
+  run.end = 0;
+  run.status = 0;
+  run.lanes_total = 0;
+  run.group = kNone;
+  run.last_group = kNone;
+  run.done = false;
+  run.keep = true;
   for (;;) {
     if (!t) {
       // Up to the hint (the next candidate) the slices spread the span evenly.
-      const u64 span = sh.hint > e_abs ? sh.hint - e_abs : u64(kDescThreads) * kDescMaxSlice;
+      const u64 span =
+          sh.hint > run.e_abs ? sh.hint - run.e_abs : u64(kDescThreads) * kDescMaxSlice;
       u64 slice = (span + kDescThreads - 1) / kDescThreads;
       if (slice < kDescMinSlice) slice = kDescMinSlice;
       if (slice > kDescMaxSlice) slice = kDescMaxSlice;
       sh.slice = u32(slice);
-      sh.go = done ? 0u : 1u;
-      sh.round = e_abs;
-      sh.need = !staged_covers(sh.stage, body, len, e_abs, e_abs + u64(kDescThreads) * slice);
+      sh.go = run.done ? 0u : 1u;
+      sh.round = run.e_abs;
+      sh.need = !staged_covers(sh.stage, body, len, run.e_abs,
+                               run.e_abs + u64(kDescThreads) * slice);
     }
     __syncthreads();
     if (!sh.go) break;
@@ -839,187 +1067,22 @@ __device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& 
       stage_range(body, len, round_abs, round_abs + u64(kDescThreads) * slice, sh.stage);
       __syncthreads();
     }
-    const u32 r0 = u32(round_abs - sh.stage.bit0);
-    const u32 s0 = r0 + t * slice;
-    {  // 1. speculative slices, then 2. continuation into the next slice
-      StagedBits r = stage_bits(sh.stage, len, s0);
-      u32 cnt, ev, evpos = 0, evend = 0;
-      desc_slice(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend);
-      sh.xpos[t] = r.pos;
-      sh.count[t] = cnt;
-      sh.ev[t] = ev;
-      sh.evpos[t] = evpos;
-      sh.evend[t] = evend;
-      __syncthreads();
-      u32 merge = kNoMerge, tail = 0;
-      if (t + 1 < kDescThreads && !ev) {
-        const u32 s1 = s0 + slice;
-        for (;;) {
-          const u32 off = r.pos - s1;
-          if (off >= slice) break;
-          if (desc_visited(sh, t + 1, off)) { merge = off; break; }
-          u32 lit, length, distance;
-          if (decode_token(sh.tables, r, 32768u, lit, length, distance) || !length) break;
-          tail += length;
-        }
-      }
-      if (t + 1 < kDescThreads) sh.merge[t + 1] = merge;
-      sh.tail[t] = tail;
-      if (!t) sh.merge[0] = kNoMerge;
-    }
-    __syncthreads();
-    // 3. bytes before the merge point of each lane's own decode; per-slice
-    // bytes of a merged run (own bytes after the merge point plus the
-    // continuation when the next lane merged), their prefix sum, and the
-    // break and event masks.
-    const u32 before = sh.merge[t] != kNoMerge
-                           ? desc_bytes_between(sh.tables, sh.stage, len, s0, s0 + sh.merge[t])
-                           : 0u;
-    sh.before[t] = before;
-    u32 bsl = sh.count[t] - before;
-    if (t + 1 < kDescThreads && sh.merge[t + 1] != kNoMerge) bsl += sh.tail[t];
-    u32 x = bsl;
-    for (u32 o = 1; o < 64; o <<= 1) {
-      const u32 y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    if (lane == 63) sh.wsum[wave] = x;
-    const u64 bm = __ballot(t > 0 && sh.merge[t] == kNoMerge);
-    const u64 em = __ballot(sh.ev[t] != 0);
-    if (!lane) {
-      sh.brk[wave] = bm;
-      sh.evm[wave] = em;
-      sh.runs[wave] = 0;
-      sh.serial[wave] = 0;
-    }
-    __syncthreads();
-    for (u32 w = 0; w < wave; ++w) x += sh.wsum[w];
-    sh.prefix[t] = x;
-    __syncthreads();
-    if (!t) {  // 4. runs and breaks
-      u32 lanes = kDescThreads;
-      u32 e = r0;       // true position
-      u64 T = total;    // block bytes before e
-      u32 j = 0;        // lane whose slice contains e, synced at e
-      u32 j_entry = r0;  // true entry of slice j
-      u64 j_off = T;     // output offset of slice j's entry
-      i64 adj = 0;       // bytes lane j produced before the sync point (negated)
-      bool round_done = false;
-      while (!round_done && !done) {
-        // Run from lane j: lanes j+1 .. b-1 merged, so they are synced too.
-        sh.entry[j] = j_entry;
-        sh.off[j] = u32(j_off);
-        sh.runs[j >> 6] |= 1ull << (j & 63);
-        const u64 pj = j ? sh.prefix[j - 1] : 0u;
-        sh.runbase[j] = u32(T + u64(adj) - pj);
-        const u32 b = next_bit(sh.brk, j + 1), E = next_bit(sh.evm, j);
-        if (E < b) {
-          T += u64(sh.prefix[E] - pj) + u64(adj);
-          if (sh.ev[E] == 1) end = sh.stage.bit0 + sh.evend[E];
-          else {
-            status = sh.ev[E] & 0xffu;
-            end = sh.stage.bit0 + sh.evpos[E];
-          }
-          lanes = E + 1;
-          done = true;
-          break;
-        }
-        T += u64(sh.prefix[b - 1] - pj) + u64(adj);
-        e = sh.xpos[b - 1];
-        if (b == kDescThreads) break;
-        // Break at lane b: decode serially from the true position until it
-        // meets the tokens of a later lane.
-        u32 k = b;
-        for (;;) {
-          if (k >= kDescThreads) { round_done = true; break; }
-          const u32 sk = r0 + k * slice;
-          const u32 k_entry = e;
-          const u64 k_off = T;
-          bool synced = false;
-          StagedBits r = stage_bits(sh.stage, len, e);
-          for (;;) {
-            const u32 off = e - sk;
-            if (desc_visited(sh, k, off)) { synced = true; break; }
-            if (off >= slice) break;
-            u32 lit, length, distance;
-            const u32 err = decode_token(sh.tables, r, 32768u, lit, length, distance);
-            if (err) { status = err; end = sh.stage.bit0 + e; done = true; break; }
-            if (!length) { end = sh.stage.bit0 + r.pos; done = true; break; }
-            T += length;
-            e = r.pos;
-          }
-          if (done || !synced) {
-            // Slice k decoded serially (entirely, or up to the block end).
-            sh.entry[k] = k_entry;
-            sh.off[k] = u32(k_off);
-            sh.serial[k >> 6] |= 1ull << (k & 63);
-            if (done) { lanes = k + 1; break; }
-            ++k;
-            continue;
-          }
-          j = k;
-          j_entry = k_entry;
-          j_off = k_off;
-          // The run's per-slice bytes already exclude lane k's phase-3 prefix
-          // (non-zero when an untrue continuation merged into lane k).
-          adj = i64(sh.before[k]) - i64(desc_bytes_between(sh.tables, sh.stage, len, sk, e));
-          break;
-        }
-      }
-      if (!done && T > limit) { status = kOutputOverflow; end = sh.stage.bit0 + e; done = true; }
-      if (!done && sh.stage.bit0 + e >= len * 8) { status = kTruncated; end = sh.stage.bit0 + e; done = true; }
-      total = T;
-      e_abs = sh.stage.bit0 + e;
-      // Slice groups for this round's lanes (consecutive ids, 64 slices each).
-      const u32 ng = (lanes + 63) / 64;
-      u32 g = kNone;
-      if (keep) {
-        const u64 gi = atomicAdd(reinterpret_cast<unsigned long long*>(&st->groups_used), u64(ng));
-        if (gi + ng <= group_capacity) {
-          g = u32(gi);
-          if (last_group == kNone) group = g;
-          else group_link[last_group] = g;
-          for (u32 i = 0; i + 1 < ng; ++i) group_link[g + i] = g + i + 1;
-          group_link[g + ng - 1] = kNone;
-          last_group = g + ng - 1;
-        } else {
-          keep = false;
-          group = kNone;
-        }
-      }
-      lanes_total += lanes;
-      sh.group = g;
-      sh.lanes = lanes;
-      sh.status = status;
-      sh.end = end;
-      sh.size = total;
-      sh.go = done ? 0u : 1u;
-    }
-    __syncthreads();
-    // Entries and offsets of the merged lanes; slice groups.
-    const u32 lanes = sh.lanes, g = sh.group;
-    if (t < lanes) {
-      u32 entry, off;
-      const bool explicit_ = ((sh.runs[wave] | sh.serial[wave]) >> lane) & 1;
-      if (explicit_) {
-        entry = sh.entry[t];
-        off = sh.off[t];
-      } else {
-        const u32 j = prev_bit(sh.runs, t);
-        entry = s0 + sh.merge[t];
-        off = sh.runbase[j] + sh.prefix[t - 1];
-      }
-      if (g != kNone) {
-        slice_entry[u64(g) * 64 + t] = sh.stage.bit0 + entry;
-        slice_off[u64(g) * 64 + t] = off;
-      }
-    }
-    done = !sh.go;
-    __syncthreads();
+    // Unchecked decoding needs every bit a round can read (its slices, one
+    // slice of continuation and a token of overshoot) before the body end.
+    const bool near_end = round_abs + u64(kDescThreads + 1) * slice + 64 > len * 8;
+    if (near_end)
+      describe_round<true>(len, limit, sh, st, slice_entry, slice_off, group_link,
+                           group_capacity, run, round_abs, slice);
+    else
+      describe_round<false>(len, limit, sh, st, slice_entry, slice_off, group_link,
+                            group_capacity, run, round_abs, slice);
   }
   if (!t) {
-    sh.group = keep ? group : kNone;
-    sh.lanes = lanes_total;
+    sh.status = run.status;
+    sh.end = run.end;
+    sh.size = run.total;
+    sh.group = run.keep ? run.group : kNone;
+    sh.lanes = run.lanes_total;
   }
   __syncthreads();
 }
@@ -1032,7 +1095,8 @@ __device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& 
 __global__ __launch_bounds__(kDescThreads) void g_describe(
     const u8* body, u64 len, const u64* cand, State* st, u64 out_size, u64* seg_end,
     u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags, u32* seg_rec, BlockRec* recs,
-    u64 rec_capacity, u64* slice_entry, u32* slice_off, u32* group_link, u64 group_capacity) {
+    u64 rec_capacity, u64* slice_entry, u32* slice_off, u32* group_link, u64 group_capacity,
+    BlockTables* tables, u64 table_capacity) {
   __shared__ DescShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -1048,14 +1112,25 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
     }
     __syncthreads();
     for (;;) {
-      block_header<true>(body, len, out_size, sh);
+      block_header<true, true>(body, len, out_size, sh);
       if (!t && sh.type && !sh.status) {
         const u64 idx = lower_bound(cand, n, sh.pos + 1);
         sh.hint = idx < n ? cand[idx] : len * 8;
         sh.group = kNone;
         sh.lanes = 0;
+        const u64 ti = atomicAdd(reinterpret_cast<unsigned long long*>(&st->tables_used), 1ull);
+        sh.table = ti < table_capacity ? u32(ti) : kNone;
       }
       __syncthreads();
+      if (sh.type && !sh.status && sh.table != kNone) {
+        // The block's tables for emission (raw words of both HuffTables).
+        const u32* src_ll = reinterpret_cast<const u32*>(&sh.tables.ll);
+        const u32* src_dd = reinterpret_cast<const u32*>(&sh.tables.dd);
+        u32* dst_ll = reinterpret_cast<u32*>(&tables[sh.table].ll);
+        u32* dst_dd = reinterpret_cast<u32*>(&tables[sh.table].dd);
+        for (u32 i = t; i < sizeof(HuffTable<288, 10>) / 4; i += kDescThreads) dst_ll[i] = src_ll[i];
+        for (u32 i = t; i < sizeof(HuffTable<32, 8>) / 4; i += kDescThreads) dst_dd[i] = src_dd[i];
+      }
       if (sh.type && !sh.status)
         describe_tokens(body, len, out_size, sh, st, slice_entry, slice_off, group_link,
                         group_capacity);
@@ -1079,6 +1154,8 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
               rec.lanes = sh.type ? sh.lanes : 0;
               rec.group = sh.type ? sh.group : kNone;
               rec.next = kNone;
+              rec.table = sh.type ? sh.table : kNone;
+              rec.pad = 0;
               recs[ri] = rec;
               if (last_rec == kNone) first_rec = u32(ri);
               else recs[last_rec].next = u32(ri);
@@ -1426,14 +1503,17 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
 }
 
 namespace {
-constexpr u32 kPushSlots = 16;
+constexpr u32 kPushSlots = 8;
+constexpr u32 kEmitThreads = kDescThreads;
 
 struct LaneEmitShared {
   DecodeTables tables;
   Stage stage;
   u16 codes[320];
-  u32 push[64][kPushSlots];
+  u32 push[kEmitThreads][kPushSlots];
   BlockRec rec;
+  u64 first, chunk_end;
+  u32 count, next_g, need;
   // block_header interface
   u64 pos, d0, end, size;
   u32 type, final_block, status, nl, nd, build_status;
@@ -1458,20 +1538,63 @@ __device__ __forceinline__ void flush_unresolved(u32* buf, u32& n, u32* list, u6
     if (at + i < capacity) list[at + i] = buf[i];
   n = 0;
 }
+
+// Decode one slice [entry, stop) into out[dst0 ..], within the block's output
+// [.., block_end).  Returns 0 or an error.
+template <bool kChecked>
+__device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64 dst0,
+                          u64 block_end, u32 window, u8* out, u32* roots, u32* unres, u32* list,
+                          u64* list_count, u64 list_capacity) {
+  WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, entry);
+  u64 dst = dst0;
+  bool any_unres = false;
+  u32 pushed = 0, err = 0;
+  u32* push = sh.push[threadIdx.x];
+  while (r.pos() < stop) {
+    u32 lit, length, distance;
+    if (fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance)) { err = kExtent; break; }
+    if (!length) break;
+    if (length > block_end - dst) { err = kExtent; break; }
+    if (!distance) {
+      out[dst++] = u8(lit);
+      continue;
+    }
+    if (distance > window || distance > dst) { err = kBadDistance; break; }
+    for (u32 j = 0; j < length; ++j) {
+      const u64 d = dst + j, src = d - distance;
+      if (src < dst0) {
+        roots[d] = u32(src);
+        bit_set(unres, d);
+        push_unresolved(push, pushed, u32(d), list, list_count, list_capacity);
+        any_unres = true;
+      } else if (any_unres && bit_get(unres, src)) {
+        roots[d] = roots[src];
+        bit_set(unres, d);
+        push_unresolved(push, pushed, u32(d), list, list_count, list_capacity);
+      } else {
+        out[d] = out[src];
+      }
+    }
+    dst += length;
+  }
+  flush_unresolved(push, pushed, list, list_count, list_capacity);
+  return err;
+}
 }  // namespace
 
-// One wave per accepted segment with block records: stored blocks are copied
-// by the wave; fixed/dynamic blocks decode their described slices in parallel,
-// one slice per lane, writing output in place.  A byte copied from before its
-// slice's output start is queued as unresolved (root = source position).
-__global__ __launch_bounds__(64) void g_emit_lanes(const u8* body, u64 len, State* st,
-                                                   const Segment* acc, const BlockRec* recs,
-                                                   const u64* slice_entry, const u32* slice_off,
-                                                   const u32* group_link, u8* out, u32* roots,
-                                                   u32* unres, u32* list, u64 list_capacity) {
+// One 256-thread workgroup per accepted segment with block records: stored
+// blocks are copied by the workgroup; fixed/dynamic blocks decode their
+// described slices in parallel, one slice per thread, with the tables that
+// describe stored (or rebuilt from the header), writing output in place.  A
+// byte copied from before its slice's output start is queued as unresolved
+// (root = source position).
+__global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
+    const u8* body, u64 len, State* st, const Segment* acc, const BlockRec* recs,
+    const u64* slice_entry, const u32* slice_off, const u32* group_link,
+    const BlockTables* tables, u8* out, u32* roots, u32* unres, u32* list, u64 list_capacity) {
   __shared__ LaneEmitShared sh;
   if (st->status) return;
-  const u32 lane = threadIdx.x;
+  const u32 t = threadIdx.x;
   const u64 segments = st->accepted;
   const u32 window = st->window;
   u64* list_count = &st->unresolved[0];
@@ -1481,13 +1604,13 @@ __global__ __launch_bounds__(64) void g_emit_lanes(const u8* body, u64 len, Stat
     u32 ri = seg.rec_first;
     u64 block_out = seg.prefix;
     u32 error = 0;
-    if (!lane) {
+    if (!t) {
       sh.stage.count = 0;
       sh.stage.bit0 = 0;
     }
     __syncthreads();
     while (ri != kNone) {
-      if (!lane) {
+      if (!t) {
         sh.rec = recs[ri];
         sh.pos = sh.rec.start;
       }
@@ -1495,63 +1618,60 @@ __global__ __launch_bounds__(64) void g_emit_lanes(const u8* body, u64 len, Stat
       const BlockRec rec = sh.rec;
       if (rec.type == 0) {
         const u64 src = rec.data >> 3;
-        for (u64 j = lane; j < rec.size; j += 64) out[block_out + j] = body[src + j];
+        for (u64 j = t; j < rec.size; j += kEmitThreads) out[block_out + j] = body[src + j];
       } else {
-        block_header(body, len, ~0ull, sh);
-        if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
+        if (rec.table != kNone) {
+          const u32* src_ll = reinterpret_cast<const u32*>(&tables[rec.table].ll);
+          const u32* src_dd = reinterpret_cast<const u32*>(&tables[rec.table].dd);
+          u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
+          u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
+          for (u32 i = t; i < sizeof(HuffTable<288, 10>) / 4; i += kEmitThreads) dst_ll[i] = src_ll[i];
+          for (u32 i = t; i < sizeof(HuffTable<32, 8>) / 4; i += kEmitThreads) dst_dd[i] = src_dd[i];
+          __syncthreads();
+        } else {
+          block_header<true, true>(body, len, ~0ull, sh);
+          if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
+        }
         u32 g = rec.group;
         u32 done = 0;
         while (g != kNone && done < rec.lanes) {
-          const u32 count = rec.lanes - done < 64 ? rec.lanes - done : 64u;
-          const u32 next_g = group_link[g];
-          const u64 first = slice_entry[u64(g) * 64];
-          const u64 group_end =
-              next_g != kNone && count == 64 && done + 64 < rec.lanes ? slice_entry[u64(next_g) * 64]
+          // One describe round: up to 256 slices in consecutive groups.
+          if (!t) {
+            const u32 count = rec.lanes - done < kEmitThreads ? rec.lanes - done : kEmitThreads;
+            const u32 ng = (count + 63) / 64;
+            const u32 next_g = group_link[g + ng - 1];
+            sh.count = count;
+            sh.next_g = next_g;
+            sh.first = slice_entry[u64(g) * 64];
+            sh.chunk_end = next_g != kNone && done + count < rec.lanes ? slice_entry[u64(next_g) * 64]
                                                                       : rec.end;
-          if (!staged_covers(sh.stage, body, len, first, group_end)) {
-            __syncthreads();
-            stage_range(body, len, first, group_end, sh.stage);
+            sh.need = !staged_covers(sh.stage, body, len, sh.first, sh.chunk_end);
           }
           __syncthreads();
+          const u32 count = sh.count;
+          if (sh.need) {
+            stage_range(body, len, sh.first, sh.chunk_end, sh.stage);
+            __syncthreads();
+          }
           u32 lerr = 0;
-          if (lane < count) {
-            const u64 entry = slice_entry[u64(g) * 64 + lane];
-            const u64 stop = lane + 1 < count ? slice_entry[u64(g) * 64 + lane + 1] : group_end;
-            const u64 dst0 = block_out + slice_off[u64(g) * 64 + lane];
-            const u64 block_end = block_out + rec.size;
-            BitIn r = staged_reader(sh.stage, len, entry);
-            u64 dst = dst0;
-            bool any_unres = false;
-            u32 pushed = 0;
-            while (r.pos < stop) {
-              u32 lit, length, distance;
-              if (decode_token(sh.tables, r, 32768u, lit, length, distance)) { lerr = kExtent; break; }
-              if (!length) break;
-              if (length > block_end - dst) { lerr = kExtent; break; }
-              if (!distance) { out[dst++] = u8(lit); continue; }
-              if (distance > window || distance > dst) { lerr = kBadDistance; break; }
-              for (u32 j = 0; j < length; ++j) {
-                const u64 d = dst + j, src = d - distance;
-                if (src < dst0) {
-                  roots[d] = u32(src);
-                  bit_set(unres, d);
-                  push_unresolved(sh.push[lane], pushed, u32(d), list, list_count, list_capacity);
-                  any_unres = true;
-                } else if (any_unres && bit_get(unres, src)) {
-                  roots[d] = roots[src];
-                  bit_set(unres, d);
-                  push_unresolved(sh.push[lane], pushed, u32(d), list, list_count, list_capacity);
-                } else {
-                  out[d] = out[src];
-                }
-              }
-              dst += length;
-            }
-            flush_unresolved(sh.push[lane], pushed, list, list_count, list_capacity);
+          if (t < count) {
+            const u64 entry = slice_entry[u64(g) * 64 + t];
+            const u64 stop = t + 1 < count ? slice_entry[u64(g) * 64 + t + 1] : sh.chunk_end;
+            const u64 dst0 = block_out + slice_off[u64(g) * 64 + t];
+            const u32 blim = stage_limit(sh.stage, len);
+            const u32 e_rel = u32(entry - sh.stage.bit0), s_rel = u32(stop - sh.stage.bit0);
+            // Unchecked decoding when the slice and a token of overshoot lie
+            // before the body end.
+            if (stop + 64 <= len * 8)
+              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
+                                       roots, unres, list, list_count, list_capacity);
+            else
+              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
+                                      roots, unres, list, list_count, list_capacity);
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
           done += count;
-          g = next_g;
+          g = sh.next_g;
           __syncthreads();
         }
       }
@@ -1559,7 +1679,7 @@ __global__ __launch_bounds__(64) void g_emit_lanes(const u8* body, u64 len, Stat
       ri = rec.next;
       __syncthreads();
     }
-    if (!lane && error) atomicMax(&st->emit_status, error);
+    if (!t && error) atomicMax(&st->emit_status, error);
     __syncthreads();
   }
 }
@@ -1741,12 +1861,16 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   u64* slice_entry = nullptr;
   u32 *slice_off = nullptr, *group_link = nullptr;
   HZ_TRY(scratch.alloc(&recs, rec_capacity));
+  const u64 table_capacity = std::min<u64>(rec_capacity, len / 8192 + 1024);
+  BlockTables* tables = nullptr;
+  HZ_TRY(scratch.alloc(&tables, table_capacity));
   HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
   HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
   HZ_TRY(scratch.alloc(&group_link, group_capacity));
   HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kDescThreads), 0, stream, body, len,
             cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
-            rec_capacity, slice_entry, slice_off, group_link, group_capacity);
+            rec_capacity, slice_entry, slice_off, group_link, group_capacity, tables,
+            table_capacity);
   HZ_TRY(hipGetLastError());
 
   // Chain selection, then the exact walk if the fast chain declined.
@@ -1770,9 +1894,9 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&list1, list_capacity));
   HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
   HZ_TRY(launch_fill(stream, bits1, 0, words * 4));
-  HZ_LAUNCH(g_emit_lanes, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
-            st, acc, recs, slice_entry, slice_off, group_link, out, roots, bits0, list0,
-            list_capacity);
+  HZ_LAUNCH(g_emit_lanes, dim3(clamp_grid(max_blocks, 4096)), dim3(kEmitThreads), 0, stream, body,
+            len, st, acc, recs, slice_entry, slice_off, group_link, tables, out, roots, bits0,
+            list0, list_capacity);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_emit_serial, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
             st, acc, out, roots, bits0, list0, list_capacity);
