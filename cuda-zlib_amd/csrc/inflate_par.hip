@@ -25,6 +25,8 @@
 // (467-483).  Failed output is all zeros except on an Adler-32 mismatch.
 #include <algorithm>
 
+#include <hip/hip_cooperative_groups.h>
+
 #include "deflate_common.h"
 #include "kernels.h"
 
@@ -1684,45 +1686,59 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   }
 }
 
-// One pointer-jumping round over the unresolved list `round & 1`.
+// Pointer jumping over the unresolved list, all rounds in one cooperative
+// launch: round r reads list (r & 1) with count counts[r] and appends the
+// still-unresolved positions to the other list, counted in counts[r + 1]
+// (zero-filled before the launch).  A position whose root is resolved takes
+// its byte; otherwise it adopts its root's root, halving every chain per
+// round.  The rounds stop once a list is empty; positions left after
+// max_rounds are counted in st->unresolved[1] (status 20 in g_finish).
 __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
-                                                 u32* bits1, u32* list0, u32* list1, u32 round,
-                                                 u64 capacity) {
-  if (st->status || st->emit_status) return;
-  const u32 cur = round & 1, nxt = cur ^ 1;
-  const u64 count = min<u64>(st->unresolved[cur], capacity);
-  if (!count) return;
-  const u32* bits = cur ? bits1 : bits0;
-  u32* next_bits = cur ? bits0 : bits1;
-  const u32* list = cur ? list1 : list0;
-  u32* next_list = cur ? list0 : list1;
+                                                 u32* bits1, u32* list0, u32* list1, u64* counts,
+                                                 u32 max_rounds, u64 capacity) {
+  cooperative_groups::grid_group grid = cooperative_groups::this_grid();
+  if (st->status || st->emit_status) return;  // uniform: nothing writes these here
   const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
   const u64 stride = u64(gridDim.x) * blockDim.x;
-  const u64 rounds_total = (count + stride - 1) / stride;
-  for (u64 it = 0; it < rounds_total; ++it) {
-    const u64 i = tid + it * stride;
-    bool keep = false;
-    u32 u = 0;
-    if (i < count) {
-      u = list[i];
-      const u32 r = roots[u];
-      const bool r_unres = (__hip_atomic_load(bits + (r >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> (r & 31)) & 1u;
-      if (!r_unres) {
-        out[u] = out[r];
-        atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
-      } else {
-        roots[u] = roots[r];
-        atomicOr(next_bits + (u >> 5), 1u << (u & 31));
-        keep = true;
+  u32 round = 0;
+  for (; round < max_rounds; ++round) {
+    // Counts were written by atomics of other workgroups before the grid barrier.
+    const u64 n_list = round ? __hip_atomic_load(&counts[round], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : __hip_atomic_load(&st->unresolved[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const u64 count = min<u64>(n_list, capacity);
+    if (!count) break;
+    const u32 cur = round & 1;
+    const u32* bits = cur ? bits1 : bits0;
+    u32* next_bits = cur ? bits0 : bits1;
+    const u32* list = cur ? list1 : list0;
+    u32* next_list = cur ? list0 : list1;
+    const u64 iters = (count + stride - 1) / stride;
+    for (u64 it = 0; it < iters; ++it) {
+      const u64 i = tid + it * stride;
+      bool keep = false;
+      u32 u = 0;
+      if (i < count) {
+        u = list[i];
+        const u32 r = roots[u];
+        const bool r_unres = (__hip_atomic_load(bits + (r >> 5), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT) >> (r & 31)) & 1u;
+        if (!r_unres) {
+          out[u] = out[r];
+          atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
+        } else {
+          roots[u] = roots[r];
+          atomicOr(next_bits + (u >> 5), 1u << (u & 31));
+          keep = true;
+        }
       }
+      append_unresolved(keep, u, next_list, &counts[round + 1], capacity);
     }
-    append_unresolved(keep, u, next_list, &st->unresolved[nxt], capacity);
+    grid.sync();
   }
-}
-
-// Resets the next round's list length before round `round` runs.
-__global__ __launch_bounds__(1) void g_resolve_reset(State* st, u32 round) {
-  st->unresolved[(round & 1) ^ 1] = 0;
+  if (!tid)
+    st->unresolved[1] = round < max_rounds ? 0
+                                           : __hip_atomic_load(&counts[max_rounds], __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Adler-32 partial sums over 4096-byte tiles, accumulated into the state.
@@ -1768,7 +1784,7 @@ __global__ __launch_bounds__(1) void g_finish(State* st, u64 n, u32 rounds, u32*
   u32 status = st->status;
   if (!status) status = st->emit_status;
   // References still unresolved after every pointer-jumping round.
-  if (!status && st->unresolved[rounds & 1]) status = kReferenceDepth;
+  if (!status && st->unresolved[1]) status = kReferenceDepth;
   if (!status) {
     const u32 a = u32((st->adler_s + 1) % kAdlerMod);
     const u32 b = u32((st->adler_w + n) % kAdlerMod);
@@ -1796,6 +1812,29 @@ u32 clamp_grid(u64 want, u32 cap) { return u32(want < 1 ? 1 : (want > cap ? cap 
     hipError_t _e = (expr);                   \
     if (_e != hipSuccess) return _e;          \
   } while (0)
+}  // namespace
+
+namespace {
+// Co-resident workgroups of g_resolve on the current device (cached).
+hipError_t resolve_grid_size(u32* grid) {
+  static int cached[64];
+  int dev = 0;
+  HZ_TRY(hipGetDevice(&dev));
+  if (dev >= 0 && dev < 64 && cached[dev]) {
+    *grid = u32(cached[dev]);
+    return hipSuccess;
+  }
+  int per_cu = 0, cus = 0;
+  HZ_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(g_resolve),
+                                                      256, 0));
+  HZ_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  int n = per_cu * cus;
+  if (n > 1024) n = 1024;
+  if (n < 1) n = 1;
+  if (dev >= 0 && dev < 64) cached[dev] = n;
+  *grid = u32(n);
+  return hipSuccess;
+}
 }  // namespace
 
 hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
@@ -1906,12 +1945,24 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   // bounded by the number of slices plus segments.
   u32 rounds = 2;
   for (u64 span = 1; span < group_capacity * 64 + u64(max_blocks); span <<= 1) ++rounds;
-  for (u32 round = 0; round < rounds; ++round) {
-    HZ_LAUNCH(g_resolve_reset, dim3(1), dim3(1), 0, stream, st, round);
-    HZ_TRY(hipGetLastError());
-    HZ_LAUNCH(g_resolve, dim3(1024), dim3(256), 0, stream, st, out, roots, bits0, bits1,
-                       list0, list1, round, list_capacity);
-    HZ_TRY(hipGetLastError());
+  u64* counts = nullptr;
+  HZ_TRY(scratch.alloc(&counts, rounds + 1));
+  HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
+  {
+    u32 resolve_grid = 0;
+    HZ_TRY(resolve_grid_size(&resolve_grid));
+    void* args[] = {&st, &out, &roots, &bits0, &bits1, &list0, &list1, &counts, &rounds,
+                    const_cast<u64*>(&list_capacity)};
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    const bool prof = profiling_enabled() && hipEventCreate(&ev0) == hipSuccess &&
+                      hipEventCreate(&ev1) == hipSuccess;
+    if (prof) (void)hipEventRecord(ev0, stream);
+    HZ_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(g_resolve), dim3(resolve_grid),
+                                      dim3(256), args, 0, stream));
+    if (prof) {
+      (void)hipEventRecord(ev1, stream);
+      profile_record("g_resolve", ev0, ev1);
+    }
   }
   HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 4095) / 4096, 8192)), dim3(256), 0, stream,
                      st, out, out_size);
