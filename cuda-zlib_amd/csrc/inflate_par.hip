@@ -559,6 +559,7 @@ __global__ __launch_bounds__(1024) void g_valid_scan(State* st, const u32* block
   if (t == 1023) {
     const u64 total = part[1023];
     st->candidates = total;
+    st->tables_used = total;  // table slots 0 .. total-1 belong to the candidates
     if (total + st->seeds > max_candidates) st->status = kCandidateOverflow;
   }
 }
@@ -1091,6 +1092,76 @@ __device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& 
 
 }  // namespace
 
+namespace {
+constexpr u32 kHeaderBytes = 640;  // > longest dynamic header (< 566 bytes)
+constexpr u32 kHeaderWords = kHeaderBytes / 4 + 4;
+
+struct HeaderShared {
+  DecodeTables tables;
+  StageT<kHeaderWords> stage;
+  u16 codes[320];
+  u64 d0;
+  u32 status, fin, nl, nd, build_status;
+};
+}  // namespace
+
+// One wave per candidate (below the table capacity): parse its dynamic
+// header, build the literal/length and distance tables in the fast format
+// into the candidate's table slot, and record the first token bit and flags
+// (hdr_info: status | BFINAL << 8 | BTYPE << 9).
+__global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const State* st,
+                                                const u64* cand, BlockTables* tables,
+                                                u64 table_capacity, u64* hdr_d0, u32* hdr_info) {
+  __shared__ HeaderShared sh;
+  if (st->status) return;
+  const u32 lane = threadIdx.x;
+  const u64 n = min<u64>(st->candidates, table_capacity);
+  for (u64 c = blockIdx.x; c < n; c += gridDim.x) {
+    const u64 pos = cand[c];
+    stage_range(body, len, pos, pos + 8, sh.stage, kHeaderBytes);
+    __syncthreads();
+    if (!lane) {
+      BitIn r = staged_reader(sh.stage, len, pos);
+      u32 fin = 0, type = 0, err = 0, nl = 0, nd = 0;
+      if (!r.take(1, fin) || !r.take(2, type)) err = kTruncated;
+      else if (type != 2) err = kBadTree;  // candidates are dynamic headers
+      else err = parse_dynamic_lengths(sh.tables, r, nl, nd);
+      sh.status = err;
+      sh.fin = fin;
+      sh.nl = nl;
+      sh.nd = nd;
+      sh.d0 = r.pos;
+    }
+    __syncthreads();
+    u32 err = sh.status;
+    if (!err) {
+      err = huff_build_wave(sh.tables.ll, sh.tables.lens, sh.nl, false, true, 15, sh.codes,
+                            &sh.build_status);
+      if (!err)
+        err = huff_build_wave(sh.tables.dd, sh.tables.lens + sh.nl, sh.nd, true, true, 15,
+                              sh.codes, &sh.build_status);
+      if (!err) {
+        fast_format(sh.tables.ll, true, lane, 64);
+        fast_format(sh.tables.dd, false, lane, 64);
+      }
+      __syncthreads();
+      if (!err) {
+        const u32* src_ll = reinterpret_cast<const u32*>(&sh.tables.ll);
+        const u32* src_dd = reinterpret_cast<const u32*>(&sh.tables.dd);
+        u32* dst_ll = reinterpret_cast<u32*>(&tables[c].ll);
+        u32* dst_dd = reinterpret_cast<u32*>(&tables[c].dd);
+        for (u32 i = lane; i < sizeof(HuffTable<288, 10>) / 4; i += 64) dst_ll[i] = src_ll[i];
+        for (u32 i = lane; i < sizeof(HuffTable<32, 8>) / 4; i += 64) dst_dd[i] = src_dd[i];
+      }
+    }
+    if (!lane) {
+      hdr_d0[c] = sh.d0;
+      hdr_info[c] = err | (sh.fin << 8) | (2u << 9);
+    }
+    __syncthreads();
+  }
+}
+
 // One workgroup per candidate: describe the candidate's segment (its block and
 // the following stored/fixed blocks up to the next candidate) with parallel
 // token decoding, and record per-block slices for emission.
@@ -1098,7 +1169,7 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
     const u8* body, u64 len, const u64* cand, State* st, u64 out_size, u64* seg_end,
     u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags, u32* seg_rec, BlockRec* recs,
     u64 rec_capacity, u64* slice_entry, u32* slice_off, u32* group_link, u64 group_capacity,
-    BlockTables* tables, u64 table_capacity) {
+    BlockTables* tables, u64 table_capacity, const u64* hdr_d0, const u32* hdr_info) {
   __shared__ DescShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -1113,18 +1184,42 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
       sh.stage.bit0 = 0;
     }
     __syncthreads();
+    bool first = true;
     for (;;) {
-      block_header<true, true>(body, len, out_size, sh);
+      // The candidate's own header was parsed by g_headers (tables in slot c).
+      const bool pre = first && c < table_capacity;
+      if (pre) {
+        if (!t) {
+          const u32 info = hdr_info[c];
+          sh.status = info & 0xffu;
+          sh.final_block = (info >> 8) & 1u;
+          sh.type = (info >> 9) & 3u;
+          sh.d0 = hdr_d0[c];
+        }
+        const u32* src_ll = reinterpret_cast<const u32*>(&tables[c].ll);
+        const u32* src_dd = reinterpret_cast<const u32*>(&tables[c].dd);
+        u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
+        u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
+        for (u32 i = t; i < sizeof(HuffTable<288, 10>) / 4; i += kDescThreads) dst_ll[i] = src_ll[i];
+        for (u32 i = t; i < sizeof(HuffTable<32, 8>) / 4; i += kDescThreads) dst_dd[i] = src_dd[i];
+        __syncthreads();
+      } else {
+        block_header<true, true>(body, len, out_size, sh);
+      }
+      first = false;
       if (!t && sh.type && !sh.status) {
         const u64 idx = lower_bound(cand, n, sh.pos + 1);
         sh.hint = idx < n ? cand[idx] : len * 8;
         sh.group = kNone;
         sh.lanes = 0;
-        const u64 ti = atomicAdd(reinterpret_cast<unsigned long long*>(&st->tables_used), 1ull);
-        sh.table = ti < table_capacity ? u32(ti) : kNone;
+        if (pre) sh.table = u32(c);
+        else {
+          const u64 ti = atomicAdd(reinterpret_cast<unsigned long long*>(&st->tables_used), 1ull);
+          sh.table = ti < table_capacity ? u32(ti) : kNone;
+        }
       }
       __syncthreads();
-      if (sh.type && !sh.status && sh.table != kNone) {
+      if (!pre && sh.type && !sh.status && sh.table != kNone) {
         // The block's tables for emission (raw words of both HuffTables).
         const u32* src_ll = reinterpret_cast<const u32*>(&sh.tables.ll);
         const u32* src_dd = reinterpret_cast<const u32*>(&sh.tables.dd);
@@ -1902,14 +1997,21 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&recs, rec_capacity));
   const u64 table_capacity = std::min<u64>(rec_capacity, len / 8192 + 1024);
   BlockTables* tables = nullptr;
+  u64* hdr_d0 = nullptr;
+  u32* hdr_info = nullptr;
   HZ_TRY(scratch.alloc(&tables, table_capacity));
+  HZ_TRY(scratch.alloc(&hdr_d0, table_capacity));
+  HZ_TRY(scratch.alloc(&hdr_info, table_capacity));
+  HZ_LAUNCH(g_headers, dim3(clamp_grid(table_capacity, 8192)), dim3(kWave), 0, stream, body, len, st,
+            cand, tables, table_capacity, hdr_d0, hdr_info);
+  HZ_TRY(hipGetLastError());
   HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
   HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
   HZ_TRY(scratch.alloc(&group_link, group_capacity));
   HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kDescThreads), 0, stream, body, len,
             cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
             rec_capacity, slice_entry, slice_off, group_link, group_capacity, tables,
-            table_capacity);
+            table_capacity, hdr_d0, hdr_info);
   HZ_TRY(hipGetLastError());
 
   // Chain selection, then the exact walk if the fast chain declined.
