@@ -25,8 +25,6 @@
 // (467-483).  Failed output is all zeros except on an Adler-32 mismatch.
 #include <algorithm>
 
-#include <hip/hip_cooperative_groups.h>
-
 #include "deflate_common.h"
 #include "kernels.h"
 
@@ -189,8 +187,10 @@ __device__ __forceinline__ u64 funnel(u64 lo, u64 hi, u32 k) {
 
 // Exact validity of a dynamic header whose BTYPE bits were already checked:
 // the same outcome as building all three tables (huff_build rules), computed
-// with Kraft sums instead of tables.  `lut` is 128 bytes of thread-private LDS.
-__device__ __forceinline__ bool dynamic_header_fields_valid(BitIn& r, u8* lut) {
+// with Kraft sums instead of tables.  `lut` is a thread's 128-entry LDS table
+// with entries `stride` bytes apart (interleaved across threads, so the
+// threads of a wave hit different banks).
+__device__ __forceinline__ bool dynamic_header_fields_valid(BitIn& r, u8* lut, u32 stride) {
   u32 hlit, hdist, hclen;
   if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return false;
   const u32 nl = hlit + 257, nd = hdist + 1, nc = hclen + 4;
@@ -219,13 +219,13 @@ __device__ __forceinline__ bool dynamic_header_fields_valid(BitIn& r, u8* lut) {
     if (!l) continue;
     const u32 c = u32(next >> (8 * l)) & 0xff;
     next += 1ull << (8 * l);
-    for (u32 k = bit_reverse(c, l); k < 128; k += 1u << l) lut[k] = u8(s | (l << 5));
+    for (u32 k = bit_reverse(c, l); k < 128; k += 1u << l) lut[k * stride] = u8(s | (l << 5));
   }
   u32 ll_kraft = 0, ll_nnz = 0, d_kraft = 0, d_nnz = 0, eob = 0, prev = 0;
   u32 i = 0;
   const u32 total = nl + nd;
   while (i < total) {
-    const u32 e = lut[r.peek(7)];
+    const u32 e = lut[r.peek(7) * stride];
     const u32 l = e >> 5, sym = e & 31;
     if (u64(l) > r.avail()) return false;
     r.drop(l);
@@ -256,6 +256,8 @@ __device__ __forceinline__ bool dynamic_header_fields_valid(BitIn& r, u8* lut) {
       d_kraft += in_d << (15 - value);
       d_nnz += in_d;
       if (i <= 256 && 256 < i + repeat) eob = 1;
+      // Kraft sums only grow: an oversubscribed code can never become valid.
+      if (ll_kraft > (1u << 15) || d_kraft > (1u << 15)) return false;
     }
     prev = value;
     i += repeat;
@@ -268,10 +270,10 @@ __device__ __forceinline__ bool dynamic_header_fields_valid(BitIn& r, u8* lut) {
 
 // Exact validity of the dynamic header at `start` (BTYPE already checked),
 // reading global memory.
-__device__ bool dynamic_header_valid(const u8* body, u64 len, u64 start, u8* lut) {
+__device__ bool dynamic_header_valid(const u8* body, u64 len, u64 start, u8* lut, u32 stride) {
   BitIn r;
   r.init(body, len, start + 3);
-  return dynamic_header_fields_valid(r, lut);
+  return dynamic_header_fields_valid(r, lut, stride);
 }
 
 // Stored-block endpoint seed at `byte` (counted like the reference's discovery,
@@ -344,12 +346,12 @@ __device__ u64 prefilter_mask(u64 len, u64 b0, const PreStage& sg, const u16* kr
 }
 
 // Exact header validation of the prefiltered offsets in `pre` (global reads).
-__device__ u64 validate_mask(const u8* body, u64 len, u64 b0, u64 pre, u8* lut) {
+__device__ u64 validate_mask(const u8* body, u64 len, u64 b0, u64 pre, u8* lut, u32 stride) {
   u64 valid = 0;
   while (pre) {
     const u32 k = __builtin_ctzll(pre);
     pre &= pre - 1;
-    if (dynamic_header_valid(body, len, b0 * 8 + k, lut)) valid |= 1ull << k;
+    if (dynamic_header_valid(body, len, b0 * 8 + k, lut, stride)) valid |= 1ull << k;
   }
   return valid;
 }
@@ -401,7 +403,7 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
 // stored-endpoint seeds.
 __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State* st,
                                                   u32* wg_count, u64* wg_list) {
-  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u8 luts[128][kDiscThreads];
   __shared__ u32 scan[kDiscThreads];
   __shared__ u16 kraft3[512];
   __shared__ PreStage sg;
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
   u32 base = block_exclusive_scan(__popcll(mask), scan, total);
   u32 kind = 0;
   if (total > kDiscCap) {
-    mask = validate_mask(body, len, b0, mask & ~flag, luts[threadIdx.x]) | flag;
+    mask = validate_mask(body, len, b0, mask & ~flag, &luts[0][threadIdx.x], kDiscThreads) | flag;
     flag = mask;
     base = block_exclusive_scan(__popcll(mask), scan, total);
     kind = total > kDiscCap ? 2u : 1u;
@@ -480,7 +482,7 @@ __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg
 __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len, const State* st,
                                                          const u32* wg_count, const u64* wg_list,
                                                          const u64* wg_offset, u64* pre) {
-  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u8 luts[128][kDiscThreads];
   __shared__ u32 scan[kDiscThreads];
   __shared__ u16 kraft3[512];
   __shared__ PreStage sg;
@@ -496,7 +498,7 @@ __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len
   stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
   __syncthreads();
   const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3), luts[threadIdx.x]);
+  u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3), &luts[0][threadIdx.x], kDiscThreads);
   if (b0 == 0) mask |= 1;
   u32 total;
   u32 at = block_exclusive_scan(__popcll(mask), scan, total);
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len
 // workgroup count of valid entries.
 __global__ __launch_bounds__(256) void g_validate(const u8* body, u64 len, const State* st,
                                                   u64* pre, u32* block_valid) {
-  __shared__ u8 luts[kDiscThreads][128];
+  __shared__ u8 luts[128][kDiscThreads];
   __shared__ u32 count;
   if (st->status) return;
   const u64 n = st->precount;
@@ -522,7 +524,7 @@ __global__ __launch_bounds__(256) void g_validate(const u8* body, u64 len, const
   bool valid = false;
   if (i < n) {
     const u64 e = pre[i];
-    valid = (e & kValidBit) || dynamic_header_valid(body, len, e & kPosMask, luts[threadIdx.x]);
+    valid = (e & kValidBit) || dynamic_header_valid(body, len, e & kPosMask, &luts[0][threadIdx.x], kDiscThreads);
     if (valid && !(e & kValidBit)) pre[i] = e | kValidBit;
   }
   const u64 bal = __ballot(valid);
@@ -1406,7 +1408,7 @@ __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, Stat
     if (type == 3) { status = kReservedBlock; break; }
     u64 limit = out_size - output;
     if (next == 0 || type == 2) {
-      if (next && !dynamic_header_valid(body, len, next, sh.lut)) { status = kUndiscovered; break; }
+      if (next && !dynamic_header_valid(body, len, next, sh.lut, 1)) { status = kUndiscovered; break; }
       limit = out_size;
     }
     BitIn r;
@@ -1781,97 +1783,99 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   }
 }
 
-// Pointer jumping over the unresolved list, all rounds in one cooperative
-// launch: round r reads list (r & 1) with count counts[r] and appends the
+// One pointer-jumping round over the unresolved list: round r reads list
+// (r & 1) with count counts[r] (round 0: the emitted list) and appends the
 // still-unresolved positions to the other list, counted in counts[r + 1]
-// (zero-filled before the launch).  A position whose root is resolved takes
-// its byte; otherwise it adopts its root's root, halving every chain per
-// round.  The rounds stop once a list is empty; positions left after
-// max_rounds are counted in st->unresolved[1] (status 20 in g_finish).
+// (zero-filled before the first round).  A position whose root is resolved
+// takes its byte; otherwise it adopts its root's root, halving every chain
+// per round.  The last round leaves its leftover count in st->unresolved[1]
+// (status 20 in g_finish).
 __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
                                                  u32* bits1, u32* list0, u32* list1, u64* counts,
-                                                 u32 max_rounds, u64 capacity) {
-  cooperative_groups::grid_group grid = cooperative_groups::this_grid();
-  if (st->status || st->emit_status) return;  // uniform: nothing writes these here
+                                                 u32 round, u32 max_rounds, u64 capacity) {
+  if (st->status || st->emit_status) return;
   const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
+  const u64 n_list = round ? counts[round] : st->unresolved[0];
+  const u64 count = min<u64>(n_list, capacity);
+  if (!count) return;
+  const u32 cur = round & 1;
+  const u32* bits = cur ? bits1 : bits0;
+  u32* next_bits = cur ? bits0 : bits1;
+  const u32* list = cur ? list1 : list0;
+  u32* next_list = cur ? list0 : list1;
+  u64* next_count = round + 1 == max_rounds ? &st->unresolved[1] : &counts[round + 1];
   const u64 stride = u64(gridDim.x) * blockDim.x;
-  u32 round = 0;
-  for (; round < max_rounds; ++round) {
-    // Counts were written by atomics of other workgroups before the grid barrier.
-    const u64 n_list = round ? __hip_atomic_load(&counts[round], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                             : __hip_atomic_load(&st->unresolved[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const u64 count = min<u64>(n_list, capacity);
-    if (!count) break;
-    const u32 cur = round & 1;
-    const u32* bits = cur ? bits1 : bits0;
-    u32* next_bits = cur ? bits0 : bits1;
-    const u32* list = cur ? list1 : list0;
-    u32* next_list = cur ? list0 : list1;
-    const u64 iters = (count + stride - 1) / stride;
-    for (u64 it = 0; it < iters; ++it) {
-      const u64 i = tid + it * stride;
-      bool keep = false;
-      u32 u = 0;
-      if (i < count) {
-        u = list[i];
-        const u32 r = roots[u];
-        const bool r_unres = (__hip_atomic_load(bits + (r >> 5), __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT) >> (r & 31)) & 1u;
-        if (!r_unres) {
-          out[u] = out[r];
-          atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
-        } else {
-          roots[u] = roots[r];
-          atomicOr(next_bits + (u >> 5), 1u << (u & 31));
-          keep = true;
-        }
+  const u64 iters = (count + stride - 1) / stride;
+  for (u64 it = 0; it < iters; ++it) {
+    const u64 i = tid + it * stride;
+    bool keep = false;
+    u32 u = 0;
+    if (i < count) {
+      u = list[i];
+      const u32 r = roots[u];
+      const bool r_unres = (__hip_atomic_load(bits + (r >> 5), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) >> (r & 31)) & 1u;
+      if (!r_unres) {
+        out[u] = out[r];
+        atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
+      } else {
+        roots[u] = roots[r];
+        atomicOr(next_bits + (u >> 5), 1u << (u & 31));
+        keep = true;
       }
-      append_unresolved(keep, u, next_list, &counts[round + 1], capacity);
     }
-    grid.sync();
+    append_unresolved(keep, u, next_list, next_count, capacity);
   }
-  if (!tid)
-    st->unresolved[1] = round < max_rounds ? 0
-                                           : __hip_atomic_load(&counts[max_rounds], __ATOMIC_RELAXED,
-                                                               __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Adler-32 partial sums over 4096-byte tiles, accumulated into the state.
+// Adler-32 partial sums, accumulated into the state: every thread takes
+// 16-byte chunks (byte sums and position-weighted sums by dot products), so
+// the output is read once with 16-byte loads.  For a chunk at offset a,
+// sum over it of (n - i) x_i = (n - a) S - L with L = sum of (i - a) x_i.
 __global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n) {
-  __shared__ u64 rs[256], rw[256];
+  __shared__ u64 red[3][256];
   if (st->status || st->emit_status) return;
-  const u64 tiles = (n + 4095) / 4096;
-  u64 acc_s = 0, acc_w = 0;
-  for (u64 tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const u64 a = tile * 4096;
-    u32 s = 0, l = 0;
-    for (u32 j = threadIdx.x; j < 4096 && a + j < n; j += 256) {
-      const u32 v = out[a + j];
-      s += v;
-      l += j * v;
+  const u64 tid = u64(blockIdx.x) * 256 + threadIdx.x, stride = u64(gridDim.x) * 256;
+  u64 s = 0, w = 0, l = 0;
+  const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  const u64 chunks = aligned ? n / 16 : 0;
+  const uint4* v = reinterpret_cast<const uint4*>(out);
+  for (u64 c = tid; c < chunks; c += stride) {
+    const uint4 q = v[c];
+    const u32 words[4] = {q.x, q.y, q.z, q.w};
+    u32 cs = 0, cl = 0;
+#pragma unroll
+    for (u32 k = 0; k < 4; ++k) {
+      const u32 ws = __builtin_amdgcn_udot4(words[k], 0x01010101u, 0u, false);
+      cs += ws;
+      cl += __builtin_amdgcn_udot4(words[k], 0x03020100u, 0u, false) + 4 * k * ws;
     }
-    rs[threadIdx.x] = s;
-    rw[threadIdx.x] = l;
-    __syncthreads();
-    for (u32 off = 128; off; off >>= 1) {
-      if (threadIdx.x < off) {
-        rs[threadIdx.x] += rs[threadIdx.x + off];
-        rw[threadIdx.x] += rw[threadIdx.x + off];
-      }
-      __syncthreads();
-    }
-    if (!threadIdx.x) {
-      const u64 S = rs[0] % kAdlerMod, L = rw[0] % kAdlerMod;
-      // sum over tile of (n - i) x_i = (n - a) S - L
-      const u64 w = (((n - a) % kAdlerMod) * S + kAdlerMod - L) % kAdlerMod;
-      acc_s += S;
-      acc_w += w;
-    }
+    const u32 x = u32((n - c * 16) % kAdlerMod);
+    s += cs;
+    w += u64(x) * cs;
+    l += cl;
+  }
+  for (u64 i = chunks * 16 + tid; i < n; i += stride) {
+    const u32 b = out[i];
+    s += b;
+    w += u64((n - i) % kAdlerMod) * b;
+  }
+  red[0][threadIdx.x] = s;
+  red[1][threadIdx.x] = w;
+  red[2][threadIdx.x] = l;
+  __syncthreads();
+  for (u32 off = 128; off; off >>= 1) {
+    if (threadIdx.x < off)
+      for (u32 k = 0; k < 3; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + off];
     __syncthreads();
   }
-  if (!threadIdx.x && (acc_s || acc_w)) {
-    atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_s), acc_s % kAdlerMod);
-    atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_w), acc_w % kAdlerMod);
+  if (!threadIdx.x) {
+    const u64 S = red[0][0] % kAdlerMod;
+    const u64 W = (red[1][0] % kAdlerMod + kAdlerMod - red[2][0] % kAdlerMod) % kAdlerMod;
+    if (S || W) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_s), S);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_w), W);
+    }
   }
 }
 
@@ -1907,29 +1911,6 @@ u32 clamp_grid(u64 want, u32 cap) { return u32(want < 1 ? 1 : (want > cap ? cap 
     hipError_t _e = (expr);                   \
     if (_e != hipSuccess) return _e;          \
   } while (0)
-}  // namespace
-
-namespace {
-// Co-resident workgroups of g_resolve on the current device (cached).
-hipError_t resolve_grid_size(u32* grid) {
-  static int cached[64];
-  int dev = 0;
-  HZ_TRY(hipGetDevice(&dev));
-  if (dev >= 0 && dev < 64 && cached[dev]) {
-    *grid = u32(cached[dev]);
-    return hipSuccess;
-  }
-  int per_cu = 0, cus = 0;
-  HZ_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(g_resolve),
-                                                      256, 0));
-  HZ_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  int n = per_cu * cus;
-  if (n > 1024) n = 1024;
-  if (n < 1) n = 1;
-  if (dev >= 0 && dev < 64) cached[dev] = n;
-  *grid = u32(n);
-  return hipSuccess;
-}
 }  // namespace
 
 hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
@@ -2050,24 +2031,13 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   u64* counts = nullptr;
   HZ_TRY(scratch.alloc(&counts, rounds + 1));
   HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
-  {
-    u32 resolve_grid = 0;
-    HZ_TRY(resolve_grid_size(&resolve_grid));
-    void* args[] = {&st, &out, &roots, &bits0, &bits1, &list0, &list1, &counts, &rounds,
-                    const_cast<u64*>(&list_capacity)};
-    hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    const bool prof = profiling_enabled() && hipEventCreate(&ev0) == hipSuccess &&
-                      hipEventCreate(&ev1) == hipSuccess;
-    if (prof) (void)hipEventRecord(ev0, stream);
-    HZ_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(g_resolve), dim3(resolve_grid),
-                                      dim3(256), args, 0, stream));
-    if (prof) {
-      (void)hipEventRecord(ev1, stream);
-      profile_record("g_resolve", ev0, ev1);
-    }
+  for (u32 round = 0; round < rounds; ++round) {
+    HZ_LAUNCH(g_resolve, dim3(1024), dim3(256), 0, stream, st, out, roots, bits0, bits1, list0,
+              list1, counts, round, rounds, list_capacity);
+    HZ_TRY(hipGetLastError());
   }
-  HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 4095) / 4096, 8192)), dim3(256), 0, stream,
-                     st, out, out_size);
+  HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048)),
+            dim3(256), 0, stream, st, out, out_size);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, rounds, meta);
   HZ_TRY(hipGetLastError());
