@@ -646,27 +646,39 @@ constexpr u32 kDescThreads = 256;
 constexpr u32 kDescWaves = kDescThreads / 64;
 constexpr u32 kVisitBits = 512;  // a slice records every token start (slices <= 512 bits)
 constexpr u32 kVisitWords = kVisitBits / 64;
-constexpr u32 kDescMinSlice = 64;  // > longest token (48 bits)
+constexpr u32 kDescMinSlice = 192;  // > longest token (48 bits); short slices rarely resynchronize
 constexpr u32 kDescMaxSlice = kVisitBits;
 static_assert(u64(kDescThreads) * kDescMaxSlice <= u64(kStageBytes) * 8, "describe stage too small");
 
 struct DescShared {
   DecodeTables tables;
   Stage stage;
-  u16 codes[320];                        // scratch of cooperative table builds
-  u64 visit[kDescThreads][kVisitWords];  // token starts of each slice's own decode
+  union {
+    u16 codes[320];                        // scratch of cooperative table builds (headers only)
+    u64 visit[kDescThreads][kVisitWords];  // token starts of each slice's own decode
+  };
   u32 xpos[kDescThreads];                // stage-relative end of each slice decode
   u32 evpos[kDescThreads], evend[kDescThreads];
   u32 count[kDescThreads];               // bytes of each slice decode
-  u32 ev[kDescThreads];                  // 0 none, 1 EOB, else 0x100 | status
+  u16 ev[kDescThreads];                  // 0 none, 1 EOB, else 0x100 | status
   u32 merge[kDescThreads];               // offset from s_j where lane j-1's continuation met
                                          // lane j's tokens, or kNoMerge
-  u32 tail[kDescThreads];                // bytes of lane j's continuation
-  u32 before[kDescThreads];              // bytes lane j produced before its merge point
-  u32 prefix[kDescThreads];              // inclusive prefix of per-slice bytes
-  u32 entry[kDescThreads];               // stage-relative true entry of each slice
-  u32 off[kDescThreads];                 // block output offset of each slice
-  u32 runbase[kDescThreads];             // run starts: off of lane k = runbase + prefix[k-1]
+  u32 merge2[kDescThreads];              // offset from s_j where lane j-2's continuation met
+                                         // lane j's tokens after crossing slice j-1 (bits 0-8;
+                                         // bits 9-31: lane j's bytes before it), or kNoMerge
+  u32 tail[kDescThreads];                // bytes of lane j's continuation up to its merge
+  union {
+    // Phases 1-3: bytes lane j produced before the first token start of
+    // visit word w >= 1 (at most 32 * 7 tokens of <= 258 bytes: fits 16 bits).
+    u16 ck[kDescThreads][kVisitWords];
+    struct {
+      u32 before[kDescThreads];   // bytes lane j produced before its merge point
+      u32 prefix[kDescThreads];   // inclusive prefix of per-slice bytes
+      u32 entry[kDescThreads];    // stage-relative true entry of each slice
+      u32 off[kDescThreads];      // block output offset of each slice
+      u32 runbase[kDescThreads];  // run starts: off of lane k = runbase + prefix[k-1]
+    };
+  };
   u64 brk[kDescWaves], evm[kDescWaves], runs[kDescWaves], serial[kDescWaves];
   u32 wsum[kDescWaves];
   // control written by lane 0 (block_header interface: pos, d0, end, size, type, ...)
@@ -697,10 +709,11 @@ __device__ __forceinline__ WordBits<kChecked> word_bits(const Stage& sg, u32 lim
 // Token-level decode from r.pos() until it reaches `stop`, an EOB or an error.
 // ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  Every token
 // start in [win0, win0 + kVisitBits) is recorded in `visit` (the bits of the
-// current 64-bit word accumulate in a register).
+// current 64-bit word accumulate in a register), and ck[w] holds the bytes
+// produced before the first token start in visit word w >= 1.
 template <bool kChecked>
 __device__ void desc_slice(const DecodeTables& t, WordBits<kChecked>& r, u32 stop, u64* visit,
-                           u32 win0, u32& count, u32& ev, u32& evpos, u32& evend) {
+                           u32 win0, u32& count, u32& ev, u32& evpos, u32& evend, u16* ck) {
   u32 produced = 0, cw = 0;
   u64 bits = 0;
   ev = 0;
@@ -715,6 +728,7 @@ __device__ void desc_slice(const DecodeTables& t, WordBits<kChecked>& r, u32 sto
         visit[cw] = bits;
         bits = 0;
         cw = w;
+        ck[w] = u16(produced);
       }
       bits |= 1ull << (off & 63);
     }
@@ -739,6 +753,18 @@ __device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u32 li
     bytes += length;
   }
   return bytes;
+}
+
+// Bytes lane `lane` produced from its slice start s0 up to its token start
+// s0 + m: the checkpoint of m's visit word plus the few tokens from that
+// word's first token start.
+template <bool kChecked>
+__device__ __forceinline__ u32 desc_bytes_before(const DescShared& sh, u32 lane, u32 limit, u32 s0,
+                                                 u32 m) {
+  const u32 w = m >> 6;
+  const u32 base = w ? u32(sh.ck[lane][w]) : 0u;
+  const u32 first = (w << 6) + u32(__builtin_ctzll(sh.visit[lane][w]));
+  return base + desc_bytes_between<kChecked>(sh.tables, sh.stage, limit, s0 + first, s0 + m);
 }
 
 // First set bit at index >= from in a kDescThreads-bit mask, or kDescThreads.
@@ -842,40 +868,62 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
   const u32 blim = stage_limit(sh.stage, len);
   const u32 r0 = u32(round_abs - sh.stage.bit0);
   const u32 s0 = r0 + t * slice;
-  {  // 1. speculative slices, then 2. continuation into the next slice
+  {  // 1. speculative slices, then 2. continuation into the next slice (and,
+     // when it meets none of that slice's tokens, into the one after)
     WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, s0);
     u32 cnt, ev, evpos = 0, evend = 0;
-    desc_slice<kChecked>(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend);
+    desc_slice<kChecked>(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend, sh.ck[t]);
     sh.xpos[t] = r.pos();
     sh.count[t] = cnt;
-    sh.ev[t] = ev;
+    sh.ev[t] = u16(ev);
     sh.evpos[t] = evpos;
     sh.evend[t] = evend;
     __syncthreads();
-    u32 merge = kNoMerge, tail = 0;
+    u32 merge = kNoMerge, merge2 = kNoMerge, tail = 0;
     if (t + 1 < kDescThreads && !ev) {
-      const u32 s1 = s0 + slice;
+      u32 k = t + 1, sk = s0 + slice;
       for (;;) {
-        const u32 off = r.pos() - s1;
-        if (off >= slice) break;
-        if (desc_visited(sh, t + 1, off)) { merge = off; break; }
+        const u32 off = r.pos() - sk;
+        if (off >= slice) {
+          if (k == t + 1 && k + 1 < kDescThreads) {
+            ++k;
+            sk += slice;
+            continue;
+          }
+          break;
+        }
+        if (desc_visited(sh, k, off)) {
+          if (k == t + 1) merge = off;
+          else merge2 = off;
+          break;
+        }
         u32 lit, length, distance;
         if (fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance) || !length) break;
         tail += length;
       }
     }
     if (t + 1 < kDescThreads) sh.merge[t + 1] = merge;
+    if (t + 2 < kDescThreads) sh.merge2[t + 2] = merge2;
     sh.tail[t] = tail;
     if (!t) sh.merge[0] = kNoMerge;
+    if (t < 2) sh.merge2[t] = kNoMerge;
   }
   __syncthreads();
-  // 3. bytes before the merge point of each lane's own decode; per-slice
+  // 3. bytes before the merge point(s) of each lane's own decode; per-slice
   // bytes of a merged run (own bytes after the merge point plus the
   // continuation when the next lane merged), their prefix sum, and the break
   // and event masks.
-  const u32 before = sh.merge[t] != kNoMerge
-                         ? desc_bytes_between<kChecked>(sh.tables, sh.stage, blim, s0, s0 + sh.merge[t])
-                         : 0u;
+  const u32 m1 = sh.merge[t], m2 = sh.merge2[t];
+  u32 before = 0;
+#pragma nounroll
+  for (u32 pass = 0; pass < 2; ++pass) {  // one call site keeps register use down
+    const u32 m = pass ? m2 : m1;
+    if (m == kNoMerge) continue;
+    const u32 v = desc_bytes_before<kChecked>(sh, t, blim, s0, m);
+    if (pass) sh.merge2[t] = m2 | (v << 9);
+    else before = v;
+  }
+  __syncthreads();  // the checkpoints share storage with the arrays below
   sh.before[t] = before;
   u32 bsl = sh.count[t] - before;
   if (t + 1 < kDescThreads && sh.merge[t + 1] != kNoMerge) bsl += sh.tail[t];
@@ -928,6 +976,21 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
       T += u64(sh.prefix[b - 1] - pj) + u64(adj);
       e = sh.xpos[b - 1];
       if (b == kDescThreads) break;
+      const u32 m2 = b + 1 < kDescThreads ? sh.merge2[b + 1] : kNoMerge;
+      if (m2 != kNoMerge) {
+        // Break at lane b, bridged by lane b-1's continuation: slice b starts
+        // at the true position, and the run resumes at lane b+1's merge point.
+        sh.entry[b] = e;
+        sh.off[b] = u32(T);
+        sh.serial[b >> 6] |= 1ull << (b & 63);
+        T += sh.tail[b - 1];
+        j = b + 1;
+        j_entry = r0 + j * slice + (m2 & 511u);
+        j_off = T;
+        adj = i64(sh.before[j]) - i64(m2 >> 9);
+        e = j_entry;
+        continue;
+      }
       // Break at lane b: decode serially from the true position until it
       // meets the tokens of a later lane.
       u32 k = b;
@@ -1055,7 +1118,10 @@ __device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& 
       // Up to the hint (the next candidate) the slices spread the span evenly.
       const u64 span =
           sh.hint > run.e_abs ? sh.hint - run.e_abs : u64(kDescThreads) * kDescMaxSlice;
-      u64 slice = (span + kDescThreads - 1) / kDescThreads;
+      // Rounds of equal slices, as few as the visit window allows.
+      const u64 per_round = u64(kDescThreads) * kDescMaxSlice;
+      const u64 rounds = (span + per_round - 1) / per_round;
+      u64 slice = (span + kDescThreads * rounds - 1) / (kDescThreads * rounds);
       if (slice < kDescMinSlice) slice = kDescMinSlice;
       if (slice > kDescMaxSlice) slice = kDescMaxSlice;
       sh.slice = u32(slice);
