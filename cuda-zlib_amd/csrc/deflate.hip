@@ -172,11 +172,6 @@ __device__ __forceinline__ u32 match_len(const u32* win, u32 a, u32 b, u32 maxle
   return maxlen;
 }
 
-__device__ __forceinline__ u64 lanemask_lt() {
-  const u32 lane = lane_id();
-  return lane ? (~0ull >> (64 - lane)) : 0ull;
-}
-
 // RFC 1951 length code (257..285) and extra bits for a match length 3..258.
 __device__ __forceinline__ void length_code(u32 len, u32& sym, u32& nbits, u32& extra) {
   if (len == 258) { sym = 285; nbits = 0; extra = 0; return; }

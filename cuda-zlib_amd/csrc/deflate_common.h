@@ -656,6 +656,83 @@ __device__ __forceinline__ u32 fast_token(const HuffTable<288, 10>& ll, const Hu
   return kOk;
 }
 
+// LSB-first reader over LDS words holding four words (128 bits) in
+// registers: the next token's lookups need only the first two (taken from
+// the old four), and the last two are reloaded on every advance for the
+// token after, so the load latency overlaps the next token's table
+// lookups.  advance(n) takes n <= 64.
+// Words are read up to index (pos >> 5) + 3, which the caller keeps inside
+// the word array; bits past the body end are never consumed when kChecked.
+template <bool kChecked>
+struct Win4 {
+  const u32* words;
+  u32 w, off, x0, x1, x2, x3, limit;
+  __device__ __forceinline__ void seek(u32 p) {
+    w = p >> 5;
+    off = p & 31u;
+    x0 = words[w];
+    x1 = words[w + 1];
+    x2 = words[w + 2];
+    x3 = words[w + 3];
+  }
+  __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
+  __device__ __forceinline__ u32 bits32() const { return __builtin_amdgcn_alignbit(x1, x0, off); }
+  __device__ __forceinline__ u64 bits64() const {
+    return u64(__builtin_amdgcn_alignbit(x1, x0, off)) |
+           (u64(__builtin_amdgcn_alignbit(x2, x1, off)) << 32);
+  }
+  __device__ __forceinline__ u32 avail() const {
+    if (!kChecked) return 0xffffffffu;
+    const u32 p = pos();
+    return p < limit ? limit - p : 0u;
+  }
+  __device__ __forceinline__ void advance(u32 n) {
+    const u32 o = off + n;
+    const u32 adv = o >> 5;  // 0, 1 or 2
+    off = o & 31u;
+    w += adv;
+    u32 c0 = x0, c1 = x1, c2 = x2, c3 = x3;
+    // Opaque register values: keeps the compiler from turning the selects
+    // below into a load through a selected pointer (into private memory).
+    asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+    x0 = adv >= 2 ? c2 : adv ? c1 : c0;
+    x1 = adv >= 2 ? c3 : adv ? c2 : c1;
+    x2 = words[w + 2];  // first used by the next advance
+    x3 = words[w + 3];
+  }
+};
+
+// One literal or match with fast-format tables when both codes hit their
+// primary LUTs: every class is resolved with selects rather than branches
+// (the distance lookup is made for literals too and ignored).  Returns false,
+// leaving the reader where it was, for anything else (a longer code, an end
+// of block, an invalid symbol, or bits too close to the limit): the caller
+// then decodes that token with fast_token.  The token takes n <= 41 bits.
+template <bool kChecked>
+__device__ __forceinline__ bool quick_token(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
+                                            Win4<kChecked>& r, u32& length, u32& lit_or_dist) {
+  const u64 b = r.bits64();
+  const u32 b32 = u32(b);
+  const u32 e = ll.primary[b32 & 1023u];
+  const u32 l = e & 15u;
+  const u32 kind = (e >> 4) & 3u;
+  const u32 is_len = kind == kKindLen ? ~0u : 0u;  // masks, not branches
+  const u32 nx = (e >> 8) & 15u & is_len;
+  const u32 s = l + nx;  // <= 20
+  const u32 d = dd.primary[(b32 >> s) & 255u];
+  const u32 dl = d & 15u, dx = (d >> 4) & 15u;
+  const u32 n = l + ((nx + dl + dx) & is_len);
+  const u32 dist_ok = (dl != 0) & ((d >> 8) ^ 1u);
+  bool ok = ((l != 0) & (kind <= kKindLen) & (~is_len | dist_ok) & 1u) != 0;
+  if (kChecked) ok = ok && n <= r.avail();
+  const u32 match_len = (e >> 16) + ((b32 >> l) & ((1u << nx) - 1u));
+  length = (match_len & is_len) | (1u & ~is_len);
+  const u32 dist = (d >> 16) + u32((b >> (s + dl)) & ((1u << dx) - 1u));
+  lit_or_dist = (dist & is_len) | ((e >> 8) & 0xffu & ~is_len);
+  r.advance(ok ? n : 0u);
+  return ok;
+}
+
 // zlib wrapper (RFC 1950) checks, in the reference's precedence order.
 __host__ __device__ __forceinline__ u32 check_framing(const u8* in, u64 size, u32& window,
                                                        u32& wanted) {
@@ -673,5 +750,11 @@ __host__ __device__ __forceinline__ u32 check_framing(const u8* in, u64 size, u3
 }
 
 __device__ __forceinline__ u32 lane_id() { return __lane_id(); }
+
+// Lanes below this one in the wave.
+__device__ __forceinline__ u64 lanemask_lt() {
+  const u32 lane = lane_id();
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
 
 }  // namespace hz

@@ -55,6 +55,7 @@ struct State {
   u64 groups_used;   // 64-slot slice groups handed out by describe
   u64 precount;      // entries of the dense pre-candidate array
   u64 tables_used;   // stored per-block decode tables
+  u64 long_count;    // pre-candidates whose header walk left the per-lane window
 };
 
 struct Segment {
@@ -98,6 +99,8 @@ constexpr u32 kStageWords = (kStageBytes + kStageMargin) / 4 + 4;
 constexpr u64 kMinSlice = 64;                      // bits; > longest token (48 bits)
 constexpr u64 kMaxSlice = (u64(kStageBytes) * 8) / 64;
 constexpr u32 kWindowSlots = 32;                   // token starts recorded per slice window
+constexpr u32 kHeaderBytes = 640;  // > longest dynamic header (< 566 bytes)
+constexpr u32 kHeaderWords = kHeaderBytes / 4 + 4;
 
 // LDS copy of a bitstream range: words[] are consecutive aligned dwords of
 // the input; body bit `bit0` is the first bit of words[0] (mod 2^64).
@@ -394,6 +397,7 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
   st->groups_used = 0;
   st->precount = 0;
   st->tables_used = 0;
+  st->long_count = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -509,25 +513,275 @@ __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len
   }
 }
 
-// Discovery pass 4: one lane per pre-candidate validates its header; per
-// workgroup count of valid entries.
-__global__ __launch_bounds__(256) void g_validate(const u8* body, u64 len, const State* st,
-                                                  u64* pre, u32* block_valid) {
-  __shared__ u8 luts[128][kDiscThreads];
+namespace {
+
+// Discovery pass 4 works on one wave per workgroup: every lane validates
+// pre-candidates of the wave's range one after another, taking the next
+// unvalidated entry whenever it finishes (every kValRound symbols), so a
+// long header walk does not idle the other lanes.  A lane's header bits
+// are copied into its LDS window and its code-length symbols are decoded
+// arithmetically from the canonical code (no per-candidate table); a walk
+// that would leave the window goes to the long list, validated by pass 4b.
+constexpr u32 kValPerWave = 128;                    // pre-candidates per wave
+constexpr u32 kValRound = 16;                       // symbols between refills
+constexpr u32 kValWindowWords = 32;                 // LDS window per lane (dwords)
+constexpr u32 kValUsableBits = (kValWindowWords - 3) * 32;  // a read touches words pos/32 .. +2
+
+struct ValShared {
+  u32 win[kValWindowWords][64];  // header bits of each lane's candidate
+};
+
+// Header walk of one lane (RFC 1951 3.2.7): the same accept/reject rules as
+// dynamic_header_fields_valid, over the lane's window.
+struct ValWalk {
+  u32 x0, x1, x2;    // window words w, w+1, w+2 (x2 loaded for the next advance)
+  u32 w, off;        // window position
+  u32 limit;         // window-relative bit limit
+  bool body_end;     // limit is the body end (else leaving the window defers)
+  u32 nl, total, i, prev, eob, ll_kraft, d_kraft, ll_nnz, d_nnz;
+  // Canonical code-length code (val_start): la[0..2] hold the left-justified
+  // 7-bit starts of the codes of lengths 2..7 as 16-bit fields; lp and bp the
+  // starts and the sorted rank of the first symbol of each length l (8-bit
+  // fields at 8 * l); slo/shi the symbols sorted by (length, symbol), 5 bits
+  // each (ranks 0-11 and 12-18).
+  u32 la0, la1, la2;
+  u64 lp, bp, slo, shi;
+  // Code-length symbol and its length at the next bits `b` (the code is
+  // complete, so every 7-bit pattern starts a code).
+  __device__ __forceinline__ u32 symbol(u32 b, u32& l) const {
+    const u32 rv = __builtin_bitreverse32(b) >> 25;  // code bits MSB first
+    const u32 r = (rv | (rv << 16)) | 0x80008000u;   // bit 15 of each field: rv >= start
+    l = 1 + __builtin_popcount((r - la0) & 0x80008000u) + __builtin_popcount((r - la1) & 0x80008000u) +
+        __builtin_popcount((r - la2) & 0x80008000u);
+    const u32 start = u32(lp >> (8 * l)) & 0xffu;
+    const u32 rank = (u32(bp >> (8 * l)) & 0xffu) + ((rv - start) >> (7 - l));
+    return rank < 12 ? u32(slo >> (5 * rank)) & 31u : u32(shi >> (5 * (rank - 12))) & 31u;
+  }
+  __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
+  __device__ __forceinline__ u32 bits() const { return __builtin_amdgcn_alignbit(x1, x0, off); }
+  __device__ __forceinline__ void seek(const ValShared& sh, u32 lane, u32 p) {
+    w = p >> 5;
+    off = p & 31u;
+    x0 = sh.win[w][lane];
+    x1 = sh.win[w + 1][lane];
+    x2 = sh.win[w + 2][lane];
+  }
+  __device__ __forceinline__ void advance(const ValShared& sh, u32 lane, u32 n) {  // n < 32
+    const u32 o = off + n;
+    const u32 adv = o >> 5;
+    off = o & 31u;
+    w += adv;
+    u32 c1 = x1, c2 = x2;
+    asm volatile("" : "+v"(c1), "+v"(c2));
+    x0 = adv ? c1 : x0;
+    x1 = adv ? c2 : c1;
+    x2 = sh.win[min(w + 2, kValWindowWords - 1)][lane];
+  }
+};
+
+enum : u32 { kValRunning = 0, kValValid = 1, kValInvalid = 2, kValLong = 3 };
+
+
+// Load candidate `pos` (its BTYPE already known to be 2) into the lane's
+// window and parse HLIT/HDIST/HCLEN and the code-length code.  Returns
+// kValRunning or a final verdict.
+__device__ u32 val_start(const u8* body, u64 len, u64 pos, ValShared& sh, u32 lane, ValWalk& v) {
+  const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+  const uintptr_t first = (base + (pos >> 3)) & ~uintptr_t(3);
+  const uintptr_t end = base + len;  // body bytes end here
+  const u32* g = reinterpret_cast<const u32*>(first);
+  if (first + 4 * kValWindowWords <= end) {
+    u32 x[kValWindowWords];  // all loads in flight at once
+#pragma unroll
+    for (u32 j = 0; j < kValWindowWords; ++j) x[j] = g[j];
+#pragma unroll
+    for (u32 j = 0; j < kValWindowWords; ++j) sh.win[j][lane] = x[j];
+  } else {
+    for (u32 j = 0; j < kValWindowWords; ++j) {
+      const uintptr_t a = first + 4 * j;
+      u32 x = 0;
+      if (a + 4 <= end) x = g[j];
+      else
+        for (u32 b = 0; b < 4; ++b)
+          if (a + b < end) x |= u32(*reinterpret_cast<const u8*>(a + b)) << (8 * b);
+      sh.win[j][lane] = x;
+    }
+  }
+  const u32 p0 = u32((base + (pos >> 3) - first) * 8 + (pos & 7));  // window bit of `pos`
+  const u64 rel_end = u64(p0) + (len * 8 - pos);                     // window bit of the body end
+  v.body_end = rel_end <= kValUsableBits;
+  v.limit = v.body_end ? u32(rel_end) : kValUsableBits;
+  v.seek(sh, lane, p0 + 3);
+  // 14 + 57 bits of fields fit in the usable window (p0 < 32).
+  if (v.pos() + 14 > v.limit) return kValInvalid;  // only at the body end
+  const u32 f = v.bits();
+  const u32 hlit = f & 31u, hdist = (f >> 5) & 31u, hclen = (f >> 10) & 15u;
+  v.advance(sh, lane, 14);
+  v.nl = hlit + 257;
+  v.total = v.nl + hdist + 1;
+  if (v.nl > 286) return kValInvalid;
+  const u32 nc = hclen + 4;
+  if (v.pos() + 3 * nc > v.limit) return kValInvalid;
+  u64 pack = 0;
+  u32 kraft = 0;
+  for (u32 i = 0; i < nc; ++i) {
+    const u32 x = v.bits() & 7u;
+    v.advance(sh, lane, 3);
+    pack |= u64(x) << (3 * cl_order(i));
+    if (x) kraft += 128u >> x;
+  }
+  if (kraft != 128) return kValInvalid;
+  // Canonical code parameters (see ValWalk).
+  u64 cnt = 0;
+  for (u32 s = 0; s < 19; ++s) cnt += 1ull << (8 * ((pack >> (3 * s)) & 7));
+  u64 lp = 0, bp = 0;
+  u32 start = 0, rank = 0;
+  for (u32 l = 1; l < 8; ++l) {
+    lp |= u64(start) << (8 * l);
+    bp |= u64(rank) << (8 * l);
+    const u32 c = u32(cnt >> (8 * l)) & 0xffu;
+    start += c << (7 - l);
+    rank += c;
+  }
+  u64 nr = bp, slo = 0, shi = 0;
+  for (u32 s = 0; s < 19; ++s) {
+    const u32 l = (pack >> (3 * s)) & 7;
+    const u32 r = u32(nr >> (8 * l)) & 0xffu;
+    nr += l ? 1ull << (8 * l) : 0ull;
+    slo |= (l && r < 12) ? u64(s) << (5 * r) : 0ull;
+    shi |= (l && r >= 12) ? u64(s) << (5 * (r - 12)) : 0ull;
+  }
+  v.lp = lp;
+  v.bp = bp;
+  v.slo = slo;
+  v.shi = shi;
+  const auto start_of = [&](u32 l) { return u32(lp >> (8 * l)) & 0xffu; };
+  v.la0 = start_of(2) | (start_of(3) << 16);
+  v.la1 = start_of(4) | (start_of(5) << 16);
+  v.la2 = start_of(6) | (start_of(7) << 16);
+  v.i = 0;
+  v.prev = 0;
+  v.eob = 0;
+  v.ll_kraft = v.d_kraft = v.ll_nnz = v.d_nnz = 0;
+  return kValRunning;
+}
+
+// One code-length symbol of the walk.
+__device__ __forceinline__ u32 val_step(const ValShared& sh, u32 lane, ValWalk& v) {
+  const u32 b = v.bits();
+  u32 l;
+  const u32 sym = v.symbol(b, l);
+  const bool rep = sym >= 16, r16 = sym == 16, r18 = sym == 18;
+  const u32 xbits = rep ? (r16 ? 2u : r18 ? 7u : 3u) : 0u;
+  const u32 need = l + xbits;
+  if (v.pos() + need > v.limit) return v.body_end ? kValInvalid : kValLong;
+  const u32 x = (b >> l) & ((1u << xbits) - 1u);
+  v.advance(sh, lane, need);
+  // Every case computed with selects; a rejected walk ends here anyway.
+  const u32 repeat = rep ? x + (r18 ? 11u : 3u) : 1u;
+  const u32 value = r16 ? v.prev : rep ? 0u : sym;
+  const u32 i = v.i;
+  const bool nz = value != 0;
+  const u32 in_ll = i < v.nl ? min(repeat, v.nl - i) : 0u;
+  const u32 in_d = repeat - in_ll;
+  v.ll_kraft += nz ? in_ll << (15 - value) : 0u;
+  v.d_kraft += nz ? in_d << (15 - value) : 0u;
+  v.ll_nnz += nz ? in_ll : 0u;
+  v.d_nnz += nz ? in_d : 0u;
+  v.eob |= (nz && i <= 256 && 256 < i + repeat) ? 1u : 0u;
+  v.prev = value;
+  v.i = i + repeat;
+  // Kraft sums only grow: an oversubscribed code can never become valid.
+  const bool bad = (r16 && i == 0) || repeat > v.total - i || v.ll_kraft > (1u << 15) ||
+                   v.d_kraft > (1u << 15);
+  if (bad) return kValInvalid;
+  if (v.i < v.total) return kValRunning;
+  const bool ll_ok = v.ll_kraft == (1u << 15) || (v.ll_nnz == 1 && v.ll_kraft == (1u << 14));
+  const bool d_ok =
+      v.d_nnz == 0 || v.d_kraft == (1u << 15) || (v.d_nnz == 1 && v.d_kraft == (1u << 14));
+  return v.eob && ll_ok && d_ok ? kValValid : kValInvalid;
+}
+
+}  // namespace
+
+// Discovery pass 4 (one wave per workgroup; see above).  Valid entries get
+// kValidBit; deferred ones are appended to long_list.
+__global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre,
+                                                 u32* long_list) {
+  __shared__ ValShared sh;
+  if (st->status) return;
+  const u64 n = st->precount;
+  const u64 q0 = u64(blockIdx.x) * kValPerWave;
+  if (q0 >= n) return;
+  const u64 q1 = min<u64>(q0 + kValPerWave, n);
+  const u32 lane = lane_id();
+  u64 cursor = q0;  // next unassigned entry (uniform)
+  u64 ci = 0;
+  bool active = false;
+  ValWalk v;
+  for (;;) {
+    // Give every idle lane the next entry that needs a walk.
+    for (;;) {
+      const u64 idle = __ballot(!active);
+      if (!idle || cursor >= q1) break;
+      if (!active) {
+        ci = cursor + __popcll(idle & lanemask_lt());
+        if (ci < q1) {
+          const u64 e = pre[ci];
+          if (!(e & kValidBit))
+            active = val_start(body, len, e & kPosMask, sh, lane, v) == kValRunning;
+        }
+      }
+      cursor += __popcll(idle);
+    }
+    if (!__ballot(active)) break;
+    for (u32 k = 0; k < kValRound; ++k) {
+      if (active) {
+        const u32 r = val_step(sh, lane, v);
+        if (r != kValRunning) {
+          active = false;
+          if (r == kValValid) pre[ci] |= kValidBit;
+          else if (r == kValLong)
+            long_list[atomicAdd(reinterpret_cast<unsigned long long*>(&st->long_count), 1ull)] =
+                u32(ci);
+        }
+      }
+    }
+  }
+}
+
+// Discovery pass 4b: one wave per deferred entry validates its header from
+// a staged copy of the longest possible header.
+__global__ __launch_bounds__(64) void g_validate_long(const u8* body, u64 len, const State* st,
+                                                      u64* pre, const u32* long_list) {
+  __shared__ StageT<kHeaderWords> stage;
+  __shared__ u8 lut[128];
+  if (st->status) return;
+  const u64 n = st->long_count;
+  for (u64 k = blockIdx.x; k < n; k += gridDim.x) {
+    const u32 ci = long_list[k];
+    const u64 pos = pre[ci] & kPosMask;
+    stage_range(body, len, pos, pos + 8, stage, kHeaderBytes);
+    __syncthreads();
+    if (!threadIdx.x) {
+      BitIn r = staged_reader(stage, len, pos + 3);
+      if (dynamic_header_fields_valid(r, lut, 1)) pre[ci] |= kValidBit;
+    }
+    __syncthreads();
+  }
+}
+
+// Discovery pass 4c: valid entries per 256-entry block.
+__global__ __launch_bounds__(256) void g_valid_count(const State* st, const u64* pre,
+                                                     u32* block_valid) {
   __shared__ u32 count;
   if (st->status) return;
   const u64 n = st->precount;
-  const u64 i = u64(blockIdx.x) * kDiscThreads + threadIdx.x;
   if (u64(blockIdx.x) * kDiscThreads >= n) return;
   if (!threadIdx.x) count = 0;
   __syncthreads();
-  bool valid = false;
-  if (i < n) {
-    const u64 e = pre[i];
-    valid = (e & kValidBit) || dynamic_header_valid(body, len, e & kPosMask, &luts[0][threadIdx.x], kDiscThreads);
-    if (valid && !(e & kValidBit)) pre[i] = e | kValidBit;
-  }
-  const u64 bal = __ballot(valid);
+  const u64 i = u64(blockIdx.x) * kDiscThreads + threadIdx.x;
+  const u64 bal = __ballot(i < n && (pre[i] & kValidBit));
   if (lane_id() == 0 && bal) atomicAdd(&count, u32(__popcll(bal)));
   __syncthreads();
   if (!threadIdx.x) block_valid[blockIdx.x] = count;
@@ -668,8 +922,8 @@ struct DescShared {
                                          // bits 9-31: lane j's bytes before it), or kNoMerge
   u32 tail[kDescThreads];                // bytes of lane j's continuation up to its merge
   union {
-    // Phases 1-3: bytes lane j produced before the first token start of
-    // visit word w >= 1 (at most 32 * 7 tokens of <= 258 bytes: fits 16 bits).
+    // Phases 1-3: bytes lane j produced by the tokens starting in visit words
+    // 0..w (read for w <= 6: at most 32 * 7 tokens of <= 258 bytes, 16 bits).
     u16 ck[kDescThreads][kVisitWords];
     struct {
       u32 before[kDescThreads];   // bytes lane j produced before its merge point
@@ -706,13 +960,37 @@ __device__ __forceinline__ WordBits<kChecked> word_bits(const Stage& sg, u32 lim
   return r;
 }
 
+template <bool kChecked>
+__device__ __forceinline__ Win4<kChecked> win4(const Stage& sg, u32 limit, u32 pos) {
+  Win4<kChecked> r;
+  r.words = sg.words;
+  r.limit = limit;
+  r.seek(pos);
+  return r;
+}
+
+// One token with the full decoder (long codes, end of block, errors) at the
+// window's position; on success the window moves past it.
+template <bool kChecked>
+__device__ __forceinline__ u32 full_token(const DecodeTables& t, Win4<kChecked>& r, u32& length,
+                                       u32& lit, u32& distance) {
+  WordBits<kChecked> q;
+  q.words = r.words;
+  q.limit = r.limit;
+  q.seek(r.pos());
+  const u32 err = fast_token(t.ll, t.dd, q, lit, length, distance);
+  if (!err) r.seek(q.pos());
+  return err;
+}
+
 // Token-level decode from r.pos() until it reaches `stop`, an EOB or an error.
 // ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  Every token
-// start in [win0, win0 + kVisitBits) is recorded in `visit` (the bits of the
-// current 64-bit word accumulate in a register), and ck[w] holds the bytes
-// produced before the first token start in visit word w >= 1.
+// start in [win0, stop) (stop - win0 <= kVisitBits) is recorded in `visit`,
+// and ck[w] ends as the bytes produced by the tokens starting in visit words
+// 0..w.  Both are stored on every token, which is cheaper than branching on
+// word changes.
 template <bool kChecked>
-__device__ void desc_slice(const DecodeTables& t, WordBits<kChecked>& r, u32 stop, u64* visit,
+__device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u64* visit,
                            u32 win0, u32& count, u32& ev, u32& evpos, u32& evend, u16* ck) {
   u32 produced = 0, cw = 0;
   u64 bits = 0;
@@ -722,34 +1000,34 @@ __device__ void desc_slice(const DecodeTables& t, WordBits<kChecked>& r, u32 sto
     const u32 p = r.pos();
     if (p >= stop) break;
     const u32 off = p - win0;
-    if (off < kVisitBits) {
-      const u32 w = off >> 6;
-      if (w != cw) {
-        visit[cw] = bits;
-        bits = 0;
-        cw = w;
-        ck[w] = u16(produced);
-      }
-      bits |= 1ull << (off & 63);
+    const u32 w = off >> 6;
+    bits = (w == cw ? bits : 0ull) | (1ull << (off & 63));
+    cw = w;
+    visit[w] = bits;
+    u32 length, x;
+    if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
+      u32 lit, distance;
+      const u32 err = full_token<kChecked>(t, r, length, lit, distance);
+      if (err) { ev = 0x100u | err; evpos = p; break; }
+      if (!length) { ev = 1; evpos = p; evend = r.pos(); break; }
     }
-    u32 lit, length, distance;
-    const u32 err = fast_token(t.ll, t.dd, r, lit, length, distance);
-    if (err) { ev = 0x100u | err; evpos = p; break; }
-    if (!length) { ev = 1; evpos = p; evend = r.pos(); break; }
     produced += length;  // <= 512 tokens of <= 258 bytes per slice
+    ck[w] = u16(produced);  // read back for words 0..6 only: <= 224 tokens, < 2^16
   }
-  visit[cw] = bits;
   count = produced;
 }
 
 // Bytes produced by decoding tokens from `from` up to token start `to`.
 template <bool kChecked>
 __device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u32 limit, u32 from, u32 to) {
-  WordBits<kChecked> r = word_bits<kChecked>(sg, limit, from);
+  Win4<kChecked> r = win4<kChecked>(sg, limit, from);
   u32 bytes = 0;
   while (r.pos() < to) {
-    u32 lit, length, distance;
-    if (fast_token(t.ll, t.dd, r, lit, length, distance) || !length) break;
+    u32 length, x;
+    if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
+      u32 lit, distance;
+      if (full_token<kChecked>(t, r, length, lit, distance) || !length) break;
+    }
     bytes += length;
   }
   return bytes;
@@ -762,7 +1040,7 @@ template <bool kChecked>
 __device__ __forceinline__ u32 desc_bytes_before(const DescShared& sh, u32 lane, u32 limit, u32 s0,
                                                  u32 m) {
   const u32 w = m >> 6;
-  const u32 base = w ? u32(sh.ck[lane][w]) : 0u;
+  const u32 base = w ? u32(sh.ck[lane][w - 1]) : 0u;  // a token starts in every word before m
   const u32 first = (w << 6) + u32(__builtin_ctzll(sh.visit[lane][w]));
   return base + desc_bytes_between<kChecked>(sh.tables, sh.stage, limit, s0 + first, s0 + m);
 }
@@ -870,7 +1148,7 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
   const u32 s0 = r0 + t * slice;
   {  // 1. speculative slices, then 2. continuation into the next slice (and,
      // when it meets none of that slice's tokens, into the one after)
-    WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, s0);
+    Win4<kChecked> r = win4<kChecked>(sh.stage, blim, s0);
     u32 cnt, ev, evpos = 0, evend = 0;
     desc_slice<kChecked>(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend, sh.ck[t]);
     sh.xpos[t] = r.pos();
@@ -892,13 +1170,18 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
           }
           break;
         }
-        if (desc_visited(sh, k, off)) {
+        const bool seen = desc_visited(sh, k, off);
+        u32 length, x;
+        const bool quick = quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x);
+        if (seen) {
           if (k == t + 1) merge = off;
           else merge2 = off;
           break;
         }
-        u32 lit, length, distance;
-        if (fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance) || !length) break;
+        if (!quick) {
+          u32 lit, distance;
+          if (full_token<kChecked>(sh.tables, r, length, lit, distance) || !length) break;
+        }
         tail += length;
       }
     }
@@ -1161,8 +1444,6 @@ __device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& 
 }  // namespace
 
 namespace {
-constexpr u32 kHeaderBytes = 640;  // > longest dynamic header (< 566 bytes)
-constexpr u32 kHeaderWords = kHeaderBytes / 4 + 4;
 
 struct HeaderShared {
   DecodeTables tables;
@@ -1710,20 +1991,33 @@ template <bool kChecked>
 __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64 dst0,
                           u64 block_end, u32 window, u8* out, u32* roots, u32* unres, u32* list,
                           u64* list_count, u64 list_capacity) {
-  WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, entry);
+  Win4<kChecked> r;
+  r.words = sh.stage.words;
+  r.limit = blim;
+  r.seek(entry);
   u64 dst = dst0;
   bool any_unres = false;
   u32 pushed = 0, err = 0;
   u32* push = sh.push[threadIdx.x];
   while (r.pos() < stop) {
-    u32 lit, length, distance;
-    if (fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance)) { err = kExtent; break; }
-    if (!length) break;
+    u32 length, x;  // x: the literal (length 1) or the distance
+    if (!quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x)) {
+      WordBits<kChecked> q;
+      q.words = r.words;
+      q.limit = r.limit;
+      q.seek(r.pos());
+      u32 lit, distance;
+      if (fast_token(sh.tables.ll, sh.tables.dd, q, lit, length, distance)) { err = kExtent; break; }
+      if (!length) break;
+      r.seek(q.pos());
+      x = length == 1 ? lit : distance;
+    }
     if (length > block_end - dst) { err = kExtent; break; }
-    if (!distance) {
-      out[dst++] = u8(lit);
+    if (length == 1) {
+      out[dst++] = u8(x);
       continue;
     }
+    const u32 distance = x;
     if (distance > window || distance > dst) { err = kBadDistance; break; }
     for (u32 j = 0; j < length; ++j) {
       const u64 d = dst + j, src = d - distance;
@@ -2013,7 +2307,14 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
             wg_count, wg_list, wg_offset, pre);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_validate, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, body, len, st, pre,
+  u32* long_list = nullptr;
+  HZ_TRY(scratch.alloc(&long_list, pre_capacity));
+  const u64 val_waves = (pre_capacity + kValPerWave - 1) / kValPerWave;
+  HZ_LAUNCH(g_validate, dim3(u32(val_waves)), dim3(64), 0, stream, body, len, st, pre, long_list);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_validate_long, dim3(2048), dim3(64), 0, stream, body, len, st, pre, long_list);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_valid_count, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, st, pre,
             block_valid);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_valid_scan, dim3(1), dim3(1024), 0, stream, st, block_valid, block_offset,
