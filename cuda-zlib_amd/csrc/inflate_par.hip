@@ -1641,6 +1641,8 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
   }
 }
 
+constexpr u32 kChainLdsNodes = 12288;  // candidates whose exits g_chain keeps in LDS
+
 // One 1024-thread workgroup: path from candidate 0, output prefixes and
 // acceptance of the whole chain.
 __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, const u64* seg_end,
@@ -1651,28 +1653,32 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
                                                 u64 out_size, u32 max_blocks, Segment* acc) {
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
+  __shared__ u32 lexit[kChainLdsNodes];  // exit_node in LDS when the candidates fit
   __shared__ u32 last_node;
   __shared__ u32 ok;
   if (st->status) return;
   const u32 t = threadIdx.x;
   const u64 n = st->candidates;
+  const bool in_lds = n <= kChainLdsNodes;
   const u64 per = (n + 1023) / 1024;
   const u64 lo = min<u64>(n, u64(t) * per), hi = min<u64>(n, lo + per);
   // 1. exits: first node outside [lo, hi) reached from each node.
   for (u64 c = hi; c-- > lo;) {
     const u32 nx = seg_next[c];
-    exit_node[c] = (nx == kNone || nx >= hi) ? nx : exit_node[nx];
+    const u32 ex = (nx == kNone || nx >= hi) ? nx : in_lds ? lexit[nx] : exit_node[nx];
+    if (in_lds) lexit[c] = ex;
+    else exit_node[c] = ex;
   }
   entry[t] = kNone;
   __syncthreads();
-  // 2. walk ranges from node 0.
+  // 2. walk ranges from node 0 (one dependent read per range).
   if (!t) {
     u32 cur = 0;
     u32 last = 0;
     while (cur != kNone) {
       entry[per ? u32(cur / per) : 0] = cur;
       last = cur;
-      cur = exit_node[cur];
+      cur = in_lds ? lexit[cur] : exit_node[cur];
     }
     last_node = last;
   }
@@ -2143,13 +2149,19 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   }
 }
 
-// One pointer-jumping round over the unresolved list: round r reads list
-// (r & 1) with count counts[r] (round 0: the emitted list) and appends the
+constexpr u32 kResolveLinks = 32;  // chain links a position follows per round
+
+// One resolution round over the unresolved list: round r reads list (r & 1)
+// with count counts[r] (round 0: the emitted list) and appends the
 // still-unresolved positions to the other list, counted in counts[r + 1]
-// (zero-filled before the first round).  A position whose root is resolved
-// takes its byte; otherwise it adopts its root's root, halving every chain
-// per round.  The last round leaves its leftover count in st->unresolved[1]
-// (status 20 in g_finish).
+// (zero-filled before the first round).  A position follows up to
+// kResolveLinks links of its root chain through this round's snapshot (the
+// unresolved bits of the previous round, and roots: any root read is an
+// earlier byte of the same chain, so concurrent updates are harmless); at a
+// resolved byte it takes that byte, else it keeps the root reached.  Round r
+// thus covers kResolveLinks^(r+1) links.  Only bytes written by earlier
+// launches are read.  The last round leaves its leftover count in
+// st->unresolved[1] (status 20 in g_finish).
 __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
                                                  u32* bits1, u32* list0, u32* list1, u64* counts,
                                                  u32 round, u32 max_rounds, u64 capacity) {
@@ -2172,14 +2184,17 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
     u32 u = 0;
     if (i < count) {
       u = list[i];
-      const u32 r = roots[u];
-      const bool r_unres = (__hip_atomic_load(bits + (r >> 5), __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT) >> (r & 31)) & 1u;
+      u32 r = roots[u];
+      bool r_unres = (bits[r >> 5] >> (r & 31)) & 1u;
+      for (u32 k = 0; r_unres && k < kResolveLinks; ++k) {
+        r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        r_unres = (bits[r >> 5] >> (r & 31)) & 1u;
+      }
       if (!r_unres) {
         out[u] = out[r];
         atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
       } else {
-        roots[u] = roots[r];
+        __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         atomicOr(next_bits + (u >> 5), 1u << (u & 31));
         keep = true;
       }
@@ -2239,10 +2254,10 @@ __global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n) 
   }
 }
 
-__global__ __launch_bounds__(1) void g_finish(State* st, u64 n, u32 rounds, u32* meta) {
+__global__ __launch_bounds__(1) void g_finish(State* st, u64 n, u32* meta) {
   u32 status = st->status;
   if (!status) status = st->emit_status;
-  // References still unresolved after every pointer-jumping round.
+  // References still unresolved after every round.
   if (!status && st->unresolved[1]) status = kReferenceDepth;
   if (!status) {
     const u32 a = u32((st->adler_s + 1) % kAdlerMod);
@@ -2390,11 +2405,12 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_emit_serial, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
             st, acc, out, roots, bits0, list0, list_capacity);
   HZ_TRY(hipGetLastError());
-  // Pointer jumping halves every reference chain per round.  A chain hops
-  // back across slices (or serially emitted segments), so its length is
-  // bounded by the number of slices plus segments.
-  u32 rounds = 2;
-  for (u64 span = 1; span < group_capacity * 64 + u64(max_blocks); span <<= 1) ++rounds;
+  // Round r covers kResolveLinks^(r+1) links of a chain.  A chain hops back
+  // across slices (or serially emitted segments), so its length is bounded
+  // by the number of slices plus segments.
+  u32 rounds = 1;
+  for (u64 span = kResolveLinks; span < group_capacity * 64 + u64(max_blocks); span *= kResolveLinks)
+    ++rounds;
   u64* counts = nullptr;
   HZ_TRY(scratch.alloc(&counts, rounds + 1));
   HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
@@ -2406,7 +2422,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048)),
             dim3(256), 0, stream, st, out, out_size);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, rounds, meta);
+  HZ_LAUNCH(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, meta);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
                      stream, st, out, out_size);
