@@ -1654,11 +1654,20 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
   __shared__ u32 lexit[kChainLdsNodes];  // exit_node in LDS when the candidates fit
-  __shared__ u32 last_node;
+  __shared__ u32 wexit[kChainLdsNodes];  // first node outside the wave's span (LDS mode)
+  __shared__ u32 wentry[16];
+  __shared__ u32 last_node, last_wave;
   __shared__ u32 ok;
   if (st->status) return;
   const u32 t = threadIdx.x;
   const u64 n = st->candidates;
+  if (!n) {  // no candidate (bit 0 always is one): nothing to accept
+    if (!t) {
+      st->chain_ok = 0;
+      st->accepted = 0;
+    }
+    return;
+  }
   const bool in_lds = n <= kChainLdsNodes;
   const u64 per = (n + 1023) / 1024;
   const u64 lo = min<u64>(n, u64(t) * per), hi = min<u64>(n, lo + per);
@@ -1670,15 +1679,51 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
     else exit_node[c] = ex;
   }
   entry[t] = kNone;
+  if (t < 16) wentry[t] = kNone;
   __syncthreads();
-  // 2. walk ranges from node 0 (one dependent read per range).
-  if (!t) {
+  // 2. entry node of every range on the path from node 0.
+  if (in_lds) {
+    // Exits from each wave's span (64 ranges) by pointer doubling, then a
+    // walk over the 16 spans, then one walk per wave inside its span.
+    const u32 wave = t >> 6;
+    const u64 whi = min<u64>(n, (u64(wave) * 64 + 64) * per);
+    for (u64 c = lo; c < hi; ++c) wexit[c] = lexit[c];
+    __syncthreads();
+    for (u32 round = 0; round < 7; ++round) {  // 2^7 > 64 ranges per span
+      for (u64 c = lo; c < hi; ++c) {
+        const u32 y = wexit[c];
+        if (y != kNone && y < whi) wexit[c] = wexit[y];
+      }
+      __syncthreads();
+    }
+    const u32 span = u32(per) * 64;
+    if (!t) {
+      u32 cur = 0, lw = 0;
+      while (cur != kNone) {
+        lw = cur / span;
+        wentry[lw] = cur;
+        cur = wexit[cur];
+      }
+      last_wave = lw;
+    }
+    __syncthreads();
+    if ((t & 63) == 0 && wentry[wave] != kNone) {
+      u32 cur = wentry[wave], last = cur;
+      while (cur != kNone && cur < whi) {
+        entry[cur / u32(per)] = cur;
+        last = cur;
+        cur = lexit[cur];
+      }
+      if (wave == last_wave) last_node = last;
+    }
+  } else if (!t) {
+    // Walk ranges from node 0 (one dependent global read per range).
     u32 cur = 0;
     u32 last = 0;
     while (cur != kNone) {
       entry[per ? u32(cur / per) : 0] = cur;
       last = cur;
-      cur = in_lds ? lexit[cur] : exit_node[cur];
+      cur = exit_node[cur];
     }
     last_node = last;
   }
