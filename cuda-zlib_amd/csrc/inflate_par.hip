@@ -909,7 +909,8 @@ struct DescShared {
   Stage stage;
   union {
     u16 codes[320];                        // scratch of cooperative table builds (headers only)
-    u64 visit[kDescThreads][kVisitWords];  // token starts of each slice's own decode
+    u64 visit[kVisitWords][kDescThreads];  // token starts of each slice's own decode (word-major:
+                                           // lanes touch consecutive banks)
   };
   u32 xpos[kDescThreads];                // stage-relative end of each slice decode
   u32 evpos[kDescThreads], evend[kDescThreads];
@@ -924,7 +925,7 @@ struct DescShared {
   union {
     // Phases 1-3: bytes lane j produced by the tokens starting in visit words
     // 0..w (read for w <= 6: at most 32 * 7 tokens of <= 258 bytes, 16 bits).
-    u16 ck[kDescThreads][kVisitWords];
+    u16 ck[kVisitWords][kDescThreads];
     struct {
       u32 before[kDescThreads];   // bytes lane j produced before its merge point
       u32 prefix[kDescThreads];   // inclusive prefix of per-slice bytes
@@ -942,7 +943,7 @@ struct DescShared {
 };
 
 __device__ __forceinline__ bool desc_visited(const DescShared& sh, u32 lane, u32 off) {
-  return off < kVisitBits && ((sh.visit[lane][off >> 6] >> (off & 63)) & 1);
+  return off < kVisitBits && ((sh.visit[off >> 6][lane] >> (off & 63)) & 1);
 }
 
 // Body end relative to the stage's word 0 (saturated).
@@ -995,7 +996,7 @@ __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u
   u32 produced = 0, cw = 0;
   u64 bits = 0;
   ev = 0;
-  for (u32 w = 0; w < kVisitWords; ++w) visit[w] = 0;
+  for (u32 w = 0; w < kVisitWords; ++w) visit[w * kDescThreads] = 0;
   for (;;) {
     const u32 p = r.pos();
     if (p >= stop) break;
@@ -1003,7 +1004,7 @@ __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u
     const u32 w = off >> 6;
     bits = (w == cw ? bits : 0ull) | (1ull << (off & 63));
     cw = w;
-    visit[w] = bits;
+    visit[w * kDescThreads] = bits;
     u32 length, x;
     if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
       u32 lit, distance;
@@ -1012,7 +1013,7 @@ __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u
       if (!length) { ev = 1; evpos = p; evend = r.pos(); break; }
     }
     produced += length;  // <= 512 tokens of <= 258 bytes per slice
-    ck[w] = u16(produced);  // read back for words 0..6 only: <= 224 tokens, < 2^16
+    ck[w * kDescThreads] = u16(produced);  // read back for words 0..6 only: <= 224 tokens, < 2^16
   }
   count = produced;
 }
@@ -1040,8 +1041,8 @@ template <bool kChecked>
 __device__ __forceinline__ u32 desc_bytes_before(const DescShared& sh, u32 lane, u32 limit, u32 s0,
                                                  u32 m) {
   const u32 w = m >> 6;
-  const u32 base = w ? u32(sh.ck[lane][w - 1]) : 0u;  // a token starts in every word before m
-  const u32 first = (w << 6) + u32(__builtin_ctzll(sh.visit[lane][w]));
+  const u32 base = w ? u32(sh.ck[w - 1][lane]) : 0u;  // a token starts in every word before m
+  const u32 first = (w << 6) + u32(__builtin_ctzll(sh.visit[w][lane]));
   return base + desc_bytes_between<kChecked>(sh.tables, sh.stage, limit, s0 + first, s0 + m);
 }
 
@@ -1150,7 +1151,8 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
      // when it meets none of that slice's tokens, into the one after)
     Win4<kChecked> r = win4<kChecked>(sh.stage, blim, s0);
     u32 cnt, ev, evpos = 0, evend = 0;
-    desc_slice<kChecked>(sh.tables, r, s0 + slice, sh.visit[t], s0, cnt, ev, evpos, evend, sh.ck[t]);
+    desc_slice<kChecked>(sh.tables, r, s0 + slice, &sh.visit[0][t], s0, cnt, ev, evpos, evend,
+                         &sh.ck[0][t]);
     sh.xpos[t] = r.pos();
     sh.count[t] = cnt;
     sh.ev[t] = u16(ev);
@@ -2007,7 +2009,7 @@ struct LaneEmitShared {
   DecodeTables tables;
   Stage stage;
   u16 codes[320];
-  u32 push[kEmitThreads][kPushSlots];
+  u32 push[kPushSlots][kEmitThreads];  // slot-major: lanes touch consecutive banks
   BlockRec rec;
   u64 first, chunk_end;
   u32 count, next_g, need;
@@ -2016,13 +2018,14 @@ struct LaneEmitShared {
   u32 type, final_block, status, nl, nd, build_status;
 };
 
+// buf: a lane's kPushSlots staging slots, kEmitThreads entries apart.
 __device__ __forceinline__ void push_unresolved(u32* buf, u32& n, u32 pos, u32* list, u64* count,
                                                 u64 capacity) {
-  buf[n++] = pos;
+  buf[n++ * kEmitThreads] = pos;
   if (n == kPushSlots) {
     const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(count), u64(kPushSlots));
     for (u32 i = 0; i < kPushSlots; ++i)
-      if (at + i < capacity) list[at + i] = buf[i];
+      if (at + i < capacity) list[at + i] = buf[i * kEmitThreads];
     n = 0;
   }
 }
@@ -2032,7 +2035,7 @@ __device__ __forceinline__ void flush_unresolved(u32* buf, u32& n, u32* list, u6
   if (!n) return;
   const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(count), u64(n));
   for (u32 i = 0; i < n; ++i)
-    if (at + i < capacity) list[at + i] = buf[i];
+    if (at + i < capacity) list[at + i] = buf[i * kEmitThreads];
   n = 0;
 }
 
@@ -2049,7 +2052,7 @@ __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64
   u64 dst = dst0;
   bool any_unres = false;
   u32 pushed = 0, err = 0;
-  u32* push = sh.push[threadIdx.x];
+  u32* push = &sh.push[0][threadIdx.x];
   while (r.pos() < stop) {
     u32 length, x;  // x: the literal (length 1) or the distance
     if (!quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x)) {
