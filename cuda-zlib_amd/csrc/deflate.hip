@@ -117,13 +117,15 @@ constexpr u32 history_limit(u32 chunk) {
 }
 static_assert(kParseShared + 65535 + 32 + 16384 < kLdsBudget, "parse LDS layout exceeds the budget");
 
+constexpr u32 kPmItems = 640;               // items of one package-merge level (< 2 * 320)
+constexpr u32 kPmWords = kPmItems / 32;
 struct HuffScratch {
   u32 key[320];
   u16 list[320];
   u16 sorted[320];
-  u32 weight[640];
-  u16 parent[640];
-  u16 depth_count[320];
+  u32 leaf[320];                  // leaf weights in sorted order
+  u32 items[2][kPmItems];         // item weights of two consecutive levels
+  u32 leafbits[16][kPmWords];     // per level: which items are leaves
 };
 
 // e_emit LDS; the bit buffer (which first serves as HuffScratch) follows it.
@@ -146,9 +148,11 @@ constexpr u32 kEmitShared = (sizeof(EmitShared) + 15) & ~u32(15);
 
 // Bit buffer words for a chunk: a fixed/dynamic block is only chosen when it
 // is shorter than the stored form (len + 5 bytes).
+// The bit buffer also holds two HuffScratch (waves 0 and 1) before emission.
 constexpr u32 stage_words(u32 chunk) {
-  return ((chunk + 8) / 4 + 16) * 4 > sizeof(HuffScratch) ? (chunk + 8) / 4 + 16
-                                                          : u32(sizeof(HuffScratch) / 4 + 1);
+  return ((chunk + 8) / 4 + 16) * 4 > 2 * sizeof(HuffScratch)
+             ? (chunk + 8) / 4 + 16
+             : u32(2 * sizeof(HuffScratch) / 4 + 1);
 }
 
 __device__ __forceinline__ u32 win_u32(const u32* win, u32 q) {
@@ -205,6 +209,16 @@ __device__ __forceinline__ u32 fixed_len(u32 s) {
 // above the limit back with the JPEG count adjustment (ITU T.81 K.3, which
 // keeps the Kraft sum at 1) and gives the shortest lengths to the heaviest
 // symbols.
+// Optimal length-limited code lengths by package-merge (one wave; every lane
+// calls).  Leaves are ranked by (frequency, symbol) in parallel.  Level
+// `limit` holds the sorted leaves; level j merges the leaves with the
+// packages of level j + 1 (sums of its consecutive item pairs), each lane
+// merging one stretch of the output along the merge path (leaves before
+// packages of equal weight).  The first 2m - 2 items of level 1 are taken;
+// a taken package takes its two children, so the taken items of every level
+// are a prefix, and a leaf's length is the number of levels whose taken
+// prefix holds it.  Unused symbols get length 0 (at least two symbols get a
+// code).
 __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 limit, u8* len) {
   const u32 lane = lane_id();
   u32 m = 0;
@@ -234,117 +248,199 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
     u32 r = 0;
     for (u32 j = 0; j < m; ++j) r += hs.key[j] < k;
     hs.sorted[r] = u16(k & 511);
+    hs.leaf[r] = k >> 9;
   }
+  for (u32 i = lane; i < 16 * kPmWords; i += 64) (&hs.leafbits[0][0])[i] = 0;
   wave_sync();
-  if (!lane) {
-    for (u32 i = 0; i < m; ++i) {
-      const u32 s = hs.sorted[i];
-      hs.weight[i] = freq[s] ? freq[s] : 1u;
+  // Level `limit`: the leaves.
+  u32* prev = hs.items[0];
+  for (u32 i = lane; i < m; i += 64) prev[i] = hs.leaf[i];
+  for (u32 i = lane; i < m; i += 64) atomicOr(&hs.leafbits[limit][i >> 5], 1u << (i & 31));
+  u32 size = m;
+  wave_sync();
+  for (u32 j = limit - 1; j >= 1; --j) {
+    u32* next = hs.items[(limit - j) & 1];
+    const u32 np = size / 2, total = m + np;
+    // Output stretch [d0, d1) of this lane; its split point along the merge
+    // path: a leaves and d0 - a packages precede it.
+    const u32 d0 = u32(u64(total) * lane / 64), d1 = u32(u64(total) * (lane + 1) / 64);
+    u32 lo = d0 > np ? d0 - np : 0u, hi = d0 < m ? d0 : m;
+    while (lo < hi) {  // least a such that leaf a comes after package d0 - 1 - a
+      const u32 a = (lo + hi) / 2, b = d0 - 1 - a;
+      const u32 pk = prev[2 * b] + prev[2 * b + 1];
+      if (hs.leaf[a] <= pk) lo = a + 1;
+      else hi = a;
     }
-    // Two-queue merge: nodes 0..m-1 are the sorted leaves, m.. internal.
-    u32 leaf = 0, inner = m, next = m;
-    for (u32 k = 0; k + 1 < m; ++k) {
-      u32 pick[2];
-      for (u32 t = 0; t < 2; ++t) {
-        if (leaf < m && (inner >= next || hs.weight[leaf] <= hs.weight[inner])) pick[t] = leaf++;
-        else pick[t] = inner++;
-      }
-      hs.weight[next] = hs.weight[pick[0]] + hs.weight[pick[1]];
-      hs.parent[pick[0]] = u16(next);
-      hs.parent[pick[1]] = u16(next);
-      ++next;
-    }
-    // Depths top down (a parent is created after its children).
-    const u32 root = next - 1;
-    for (u32 i = 0; i < 320; ++i) hs.depth_count[i] = 0;
-    hs.weight[root] = 0;
-    for (u32 v = root; v-- > m;) hs.weight[v] = hs.weight[hs.parent[v]] + 1;
-    u32 maxdepth = 0;
-    for (u32 i = 0; i < m; ++i) {
-      const u32 dep = hs.weight[hs.parent[i]] + 1;
-      ++hs.depth_count[dep];
-      if (dep > maxdepth) maxdepth = dep;
-    }
-    for (u32 i = maxdepth; i > limit; --i) {
-      while (hs.depth_count[i] > 0) {
-        u32 j = i - 2;
-        while (hs.depth_count[j] == 0) --j;
-        hs.depth_count[i] -= 2;
-        hs.depth_count[i - 1] += 1;
-        hs.depth_count[j + 1] += 2;
-        hs.depth_count[j] -= 1;
+    u32 a = lo, b = d0 - lo;
+    for (u32 d = d0; d < d1; ++d) {
+      const u32 pk = b < np ? prev[2 * b] + prev[2 * b + 1] : 0xffffffffu;
+      if (a < m && (b >= np || hs.leaf[a] <= pk)) {
+        next[d] = hs.leaf[a++];
+        atomicOr(&hs.leafbits[j][d >> 5], 1u << (d & 31));
+      } else {
+        next[d] = pk;
+        ++b;
       }
     }
-    u32 l = 1, left = hs.depth_count[1];
-    for (u32 i = m; i-- > 0;) {
-      while (!left) left = hs.depth_count[++l];
-      len[hs.sorted[i]] = u8(l);
-      --left;
+    size = total;
+    prev = next;
+    wave_sync();
+  }
+  // Taken prefixes from level 1 down: taken_j items, of which c_j leaves.
+  u32 taken = 2 * m - 2, lens_of = 0;
+  u32 c[16];
+  for (u32 j = 1; j <= 15; ++j) c[j] = 0;
+  for (u32 j = 1; j <= limit; ++j) {
+    u32 leaves = 0;
+    for (u32 w = lane; w * 32 < taken; w += 64) {
+      u32 bits = hs.leafbits[j][w];
+      if ((w + 1) * 32 > taken) bits &= (1u << (taken & 31)) - 1u;
+      leaves += __builtin_popcount(bits);
     }
+    for (u32 off = 32; off; off >>= 1) leaves += __shfl_xor(leaves, off, 64);
+    c[j] = leaves;
+    taken = 2 * (taken - leaves);
+  }
+  (void)lens_of;
+  for (u32 i = lane; i < m; i += 64) {
+    u32 l = 0;
+    for (u32 j = 1; j <= 15; ++j) l += i < c[j] ? 1u : 0u;
+    len[hs.sorted[i]] = u8(l);
   }
   wave_sync();
 }
 
-// Canonical codes (bit-reversed for LSB-first output) from lengths; one lane.
-__device__ void canonical_codes(const u8* len, u32 n, u16* code) {
-  u32 count[16], next[16];
-  for (u32 i = 0; i < 16; ++i) count[i] = 0;
-  for (u32 s = 0; s < n; ++s) ++count[len[s]];
-  count[0] = 0;
+// Canonical codes (bit-reversed) from lengths, one wave: length counts by
+// ballots, then each symbol's rank among the earlier symbols of its length.
+__device__ void canonical_codes_wave(const u8* len, u32 n, u16* code) {
+  const u32 lane = lane_id();
+  u32 cnt[16];
+#pragma unroll
+  for (u32 l = 0; l < 16; ++l) cnt[l] = 0;
+  for (u32 base = 0; base < n; base += 64) {
+    const u32 s = base + lane;
+    const u32 l = s < n ? len[s] : 0u;
+#pragma unroll
+    for (u32 k = 1; k < 16; ++k) cnt[k] += __popcll(__ballot(l == k));
+  }
+  u32 start[16];
   u32 c = 0;
-  for (u32 b = 1; b < 16; ++b) {
-    c = (c + count[b - 1]) << 1;
-    next[b] = c;
+  start[0] = 0;
+#pragma unroll
+  for (u32 k = 1; k < 16; ++k) {
+    c = (c + (k > 1 ? cnt[k - 1] : 0u)) << 1;
+    start[k] = c;
   }
-  for (u32 s = 0; s < n; ++s)
-    if (len[s]) code[s] = u16(bit_reverse(next[len[s]]++, len[s]));
+  for (u32 base = 0; base < n; base += 64) {
+    const u32 s = base + lane;
+    const u32 l = s < n ? len[s] : 0u;
+    u32 mine = 0;
+#pragma unroll
+    for (u32 k = 1; k < 16; ++k) {
+      const u64 b = __ballot(l == k);
+      if (l == k) mine = start[k] + __popcll(b & lanemask_lt());
+      start[k] += __popcll(b);
+    }
+    if (l) code[s] = u16(bit_reverse(mine, l));
+  }
 }
 
-// Code-length RLE of the literal/length and distance lengths; one lane.
-__device__ void rle_lengths(EmitShared& sh) {
-  const u32 total = sh.hlit + sh.hdist;
-  u32 nr = 0, i = 0;
-  for (u32 s = 0; s < 20; ++s) sh.freq_cl[s] = 0;
-  auto at = [&](u32 k) -> u32 { return k < sh.hlit ? sh.len_ll[k] : sh.len_d[k - sh.hlit]; };
-  while (i < total) {
-    const u32 v = at(i);
-    u32 run = 1;
-    while (i + run < total && at(i + run) == v) ++run;
-    if (!v) {
-      u32 r = run;
-      while (r >= 11) {
-        const u32 t = r < 138 ? r : 138;
-        sh.rle[nr++] = u16(18 | ((t - 11) << 5));
-        ++sh.freq_cl[18];
-        r -= t;
-      }
-      if (r >= 3) {
-        sh.rle[nr++] = u16(17 | ((r - 3) << 5));
-        ++sh.freq_cl[17];
-        r = 0;
-      }
-      while (r--) {
-        sh.rle[nr++] = 0;
-        ++sh.freq_cl[0];
-      }
-    } else {
-      sh.rle[nr++] = u16(v);
-      ++sh.freq_cl[v];
-      u32 r = run - 1;
-      while (r >= 3) {
-        const u32 t = r < 6 ? r : 6;
-        sh.rle[nr++] = u16(16 | ((t - 3) << 5));
-        ++sh.freq_cl[16];
-        r -= t;
-      }
-      while (r--) {
-        sh.rle[nr++] = u16(v);
-        ++sh.freq_cl[v];
-      }
-    }
-    i += run;
+// One past the last nonzero length in len[0, n), at least `floor` (one wave).
+__device__ __forceinline__ u32 used_extent(const u8* len, u32 n, u32 floor) {
+  const u32 lane = lane_id();
+  u32 last = 0;
+  for (u32 base = 0; base < n; base += 64) {
+    const u32 s = base + lane;
+    const u64 b = __ballot(s < n && len[s] != 0);
+    if (b) last = base + 64 - __builtin_clzll(b);
   }
-  sh.nrle = nr;
+  return last > floor ? last : floor;
+}
+
+// The RLE symbols of a run of `run` equal lengths `v` (zlib's scheme: 18/17
+// for zeros, 16 for repeats of a nonzero length after one literal copy);
+// emit(symbol | extra << 5) for each.
+template <class F>
+__device__ __forceinline__ void rle_run(u32 v, u32 run, F&& emit) {
+  if (!v) {
+    u32 r = run;
+    while (r >= 11) {
+      const u32 t = r < 138 ? r : 138;
+      emit(18u | ((t - 11) << 5));
+      r -= t;
+    }
+    if (r >= 3) {
+      emit(17u | ((r - 3) << 5));
+      r = 0;
+    }
+    while (r--) emit(0u);
+  } else {
+    emit(v);
+    u32 r = run - 1;
+    while (r >= 3) {
+      const u32 t = r < 6 ? r : 6;
+      emit(16u | ((t - 3) << 5));
+      r -= t;
+    }
+    while (r--) emit(v);
+  }
+}
+
+// Code-length RLE of the literal/length and distance lengths, one wave: the
+// same symbols as a serial left-to-right pass.  Each lane owns the runs that
+// start at its positions; run ends come from the start ballots, outputs from
+// a scan of per-run symbol counts.
+__device__ void rle_lengths_wave(EmitShared& sh) {
+  const u32 lane = lane_id();
+  const u32 total = sh.hlit + sh.hdist;  // <= 316: five ballot words
+  auto at = [&](u32 k) -> u32 { return k < sh.hlit ? sh.len_ll[k] : sh.len_d[k - sh.hlit]; };
+  if (lane < 20) sh.freq_cl[lane] = 0;
+  u64 starts[5];
+#pragma unroll
+  for (u32 c = 0; c < 5; ++c) {
+    const u32 i = c * 64 + lane;
+    const bool st = i < total && (i == 0 || at(i) != at(i - 1));
+    starts[c] = __ballot(st);
+  }
+  // Run of each start this lane owns, and its symbol count.
+  u32 v[5], run[5], cnt[5];
+#pragma unroll
+  for (u32 c = 0; c < 5; ++c) {
+    const u32 i = c * 64 + lane;
+    v[c] = run[c] = cnt[c] = 0;
+    if ((starts[c] >> lane) & 1) {
+      u32 end = total;
+      u64 rest = lane == 63 ? 0ull : starts[c] & (~0ull << (lane + 1));
+      if (rest) end = c * 64 + __builtin_ctzll(rest);
+      else
+        for (u32 k = c + 1; k < 5; ++k)
+          if (starts[k]) { end = k * 64 + __builtin_ctzll(starts[k]); break; }
+      v[c] = at(i);
+      run[c] = end - i;
+      u32 nsym = 0;
+      rle_run(v[c], run[c], [&](u32) { ++nsym; });
+      cnt[c] = nsym;
+    }
+  }
+  wave_sync();
+  u32 carry = 0;
+#pragma unroll
+  for (u32 c = 0; c < 5; ++c) {
+    u32 x = cnt[c];
+    for (u32 off = 1; off < 64; off <<= 1) {
+      const u32 y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    u32 at_sym = carry + x - cnt[c];
+    carry += __shfl(x, 63, 64);
+    if (cnt[c])
+      rle_run(v[c], run[c], [&](u32 sym) {
+        sh.rle[at_sym++] = u16(sym);
+        atomicAdd(&sh.freq_cl[sym & 31], 1u);
+      });
+  }
+  if (!lane) sh.nrle = carry;
+  wave_sync();
 }
 
 // Serial LSB-first writer into the LDS bit buffer (header and block tail);
@@ -641,7 +737,6 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
   extern __shared__ __align__(16) u8 dyn[];
   EmitShared& sh = *reinterpret_cast<EmitShared*>(dyn);
   u32* stage = reinterpret_cast<u32*>(dyn + kEmitShared);
-  HuffScratch& hs = *reinterpret_cast<HuffScratch*>(stage);
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
     const ChunkDesc d = descs[c];
@@ -650,20 +745,18 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
     if (t < 32) sh.freq_d[t] = t < 30 ? st.freq_d[t] : 0u;
     __syncthreads();
 
-    // ---- code lengths, costs, block type (wave 0) ----
+    // ---- code lengths (waves 0 and 1), RLE, costs, block type (wave 0),
+    // canonical codes (waves 0-2) ----
+    HuffScratch* hsw = reinterpret_cast<HuffScratch*>(stage);  // one per wave
+    if (wave == 0) huffman_lengths(hsw[0], sh.freq_ll, 286, 15, sh.len_ll);
+    else if (wave == 1) huffman_lengths(hsw[1], sh.freq_d, 30, 15, sh.len_d);
+    __syncthreads();
     if (wave == 0) {
-      huffman_lengths(hs, sh.freq_ll, 286, 15, sh.len_ll);
-      huffman_lengths(hs, sh.freq_d, 30, 15, sh.len_d);
-      if (!lane) {
-        u32 hl = 286, hd = 30;
-        while (hl > 257 && !sh.len_ll[hl - 1]) --hl;
-        while (hd > 1 && !sh.len_d[hd - 1]) --hd;
-        sh.hlit = hl;
-        sh.hdist = hd;
-        rle_lengths(sh);
-      }
+      sh.hlit = used_extent(sh.len_ll, 286, 257);
+      sh.hdist = used_extent(sh.len_d, 30, 1);
       wave_sync();
-      huffman_lengths(hs, sh.freq_cl, 19, 7, sh.len_cl);
+      rle_lengths_wave(sh);
+      huffman_lengths(hsw[0], sh.freq_cl, 19, 7, sh.len_cl);
       u32 dyn_bits = 0, fix_bits = 0, hdr = 0;
       for (u32 sy = lane; sy < 286; sy += 64) {
         dyn_bits += sh.freq_ll[sy] * sh.len_ll[sy];
@@ -682,9 +775,11 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         fix_bits += __shfl_down(fix_bits, off, 64);
         hdr += __shfl_down(hdr, off, 64);
       }
+      // HCLEN: one past the last nonzero code-length length in RFC order.
+      const u64 cl_used = __ballot(lane < 19 && sh.len_cl[cl_order(lane)] != 0);
       if (!lane) {
-        u32 hc = 19;
-        while (hc > 4 && !sh.len_cl[cl_order(hc - 1)]) --hc;
+        const u32 last = cl_used ? 64 - __builtin_clzll(cl_used) : 0u;
+        const u32 hc = last > 4 ? last : 4u;
         sh.hclen = hc;
         hdr += 3 + 14 + 3 * hc;
         const u64 dyn_total = u64(hdr) + dyn_bits + st.extra_bits;
@@ -702,19 +797,24 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         sh.extent = u32(best);
         sh.hdr_bits = mode == 2 ? hdr : 3u;
         sh.status = 0;
-        if (mode == 1) {
-          for (u32 i = 0; i < 288; ++i) sh.len_ll[i] = u8(fixed_len(i));
-          for (u32 i = 0; i < 30; ++i) sh.len_d[i] = 5;
-        }
-        if (mode) {
-          canonical_codes(sh.len_ll, mode == 1 ? 288 : 286, sh.code_ll);
-          canonical_codes(sh.len_d, 30, sh.code_d);
-          if (mode == 2) canonical_codes(sh.len_cl, 19, sh.code_cl);
-        }
         const u64 S = st.sum_s % kAdlerMod, L = st.sum_l % kAdlerMod;
         results[c].adler_s = S;
         results[c].adler_b =
             (((d.file_len - d.file_off) % kAdlerMod) * S + kAdlerMod - L) % kAdlerMod;
+      }
+    }
+    __syncthreads();
+    {
+      const u32 mode = sh.mode;
+      if (mode == 1) {
+        for (u32 i = t; i < 288; i += kEmitThreads) sh.len_ll[i] = u8(fixed_len(i));
+        if (t < 30) sh.len_d[t] = 5;
+        __syncthreads();
+      }
+      if (mode) {
+        if (wave == 0) canonical_codes_wave(sh.len_ll, mode == 1 ? 288 : 286, sh.code_ll);
+        else if (wave == 1) canonical_codes_wave(sh.len_d, 30, sh.code_d);
+        else if (wave == 2 && mode == 2) canonical_codes_wave(sh.len_cl, 19, sh.code_cl);
       }
     }
     __syncthreads();
@@ -740,6 +840,10 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
       const u32 used = min((sh.extent + 3) / 4 + 1, words);
       for (u32 i = t; i < used; i += kEmitThreads) stage[i] = 0;
       __syncthreads();
+      // Header: the fixed fields by thread 0 (before the scan's barriers),
+      // then the code-length RLE symbols, two per thread, placed by a scan.
+      const u32 nrle = mode == 2 ? sh.nrle : 0u;
+      const u32 fixed_bits = mode == 2 ? 17 + 3 * sh.hclen : 3u;
       if (!t) {
         StageWriter out = {stage, words, 0};
         out.put(d.last ? 1u : 0u, 1);
@@ -749,16 +853,31 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
           out.put(sh.hdist - 1, 5);
           out.put(sh.hclen - 4, 4);
           for (u32 i = 0; i < sh.hclen; ++i) out.put(sh.len_cl[cl_order(i)], 3);
-          for (u32 i = 0; i < sh.nrle; ++i) {
-            const u32 sy = sh.rle[i] & 31, x = sh.rle[i] >> 5;
-            out.put(sh.code_cl[sy], sh.len_cl[sy]);
-            if (sy == 16) out.put(x, 2);
-            else if (sy == 17) out.put(x, 3);
-            else if (sy == 18) out.put(x, 7);
-          }
         }
-        if (out.pos != sh.hdr_bits) sh.status = kCompressionOverflow;
       }
+      u64 hb[2];
+      u32 hn[2], hmine = 0;
+#pragma unroll
+      for (u32 k = 0; k < 2; ++k) {
+        const u32 i = 2 * t + k;
+        hn[k] = 0;
+        hb[k] = 0;
+        if (i < nrle) {
+          const u32 sy = sh.rle[i] & 31, x = sh.rle[i] >> 5;
+          const u32 cl = sh.len_cl[sy];
+          hb[k] = u64(sh.code_cl[sy]) | (u64(x) << cl);
+          hn[k] = cl + (sy == 16 ? 2u : sy == 17 ? 3u : sy == 18 ? 7u : 0u);
+        }
+        hmine += hn[k];
+      }
+      u32 htotal;
+      u32 hoff = fixed_bits + block_scan(sh, hmine, htotal);
+#pragma unroll
+      for (u32 k = 0; k < 2; ++k) {
+        if (hn[k]) or_bits(stage, words, hoff, hb[k]);
+        hoff += hn[k];
+      }
+      if (!t && fixed_bits + htotal != sh.hdr_bits) sh.status = kCompressionOverflow;
       __syncthreads();
       const u32* tok = tokens + d.in_off;
       const u32 ntokens = st.ntok;
