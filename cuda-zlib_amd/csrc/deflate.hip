@@ -120,7 +120,6 @@ static_assert(kParseShared + 65535 + 32 + 16384 < kLdsBudget, "parse LDS layout 
 constexpr u32 kPmItems = 640;               // items of one package-merge level (< 2 * 320)
 constexpr u32 kPmWords = kPmItems / 32;
 struct HuffScratch {
-  u32 key[320];
   u16 list[320];
   u16 sorted[320];
   u32 leaf[320];                  // leaf weights in sorted order
@@ -210,7 +209,7 @@ __device__ __forceinline__ u32 fixed_len(u32 s) {
 // keeps the Kraft sum at 1) and gives the shortest lengths to the heaviest
 // symbols.
 // Optimal length-limited code lengths by package-merge (one wave; every lane
-// calls).  Leaves are ranked by (frequency, symbol) in parallel.  Level
+// calls).  Leaves are sorted by (frequency, symbol) with a bitonic network.  Level
 // `limit` holds the sorted leaves; level j merges the leaves with the
 // packages of level j + 1 (sums of its consecutive item pairs), each lane
 // merging one stretch of the output along the merge path (leaves before
@@ -238,17 +237,56 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
       }
   }
   wave_sync();
-  for (u32 i = lane; i < m; i += 64) {
-    const u32 s = hs.list[i];
-    hs.key[i] = ((freq[s] ? freq[s] : 1u) << 9) | s;
+  // Bitonic sort of the keys (weight << 9 | symbol) over 512 slots: slot
+  // r * 64 + lane in register r; partners within a lane swap registers,
+  // partners across lanes exchange by shuffles.
+  u32 key[8];
+#pragma unroll
+  for (u32 r = 0; r < 8; ++r) {
+    const u32 i = r * 64 + lane;
+    if (i < m) {
+      const u32 s = hs.list[i];
+      key[r] = ((freq[s] ? freq[s] : 1u) << 9) | s;
+    } else {
+      key[r] = 0xffffffffu;
+    }
   }
-  wave_sync();
-  for (u32 i = lane; i < m; i += 64) {
-    const u32 k = hs.key[i];
-    u32 r = 0;
-    for (u32 j = 0; j < m; ++j) r += hs.key[j] < k;
-    hs.sorted[r] = u16(k & 511);
-    hs.leaf[r] = k >> 9;
+#pragma clang loop unroll(full)
+  for (u32 k = 2; k <= 512; k <<= 1) {
+#pragma clang loop unroll(full)
+    for (u32 j = k >> 1; j; j >>= 1) {
+      if (j >= 64) {
+        const u32 rj = j >> 6;
+#pragma clang loop unroll(full)
+        for (u32 r = 0; r < 8; ++r) {
+          if (r & rj) continue;
+          const u32 e = r * 64 + lane;
+          const bool up = (e & k) == 0;
+          const u32 a = key[r], b = key[r | rj];
+          const bool swap = up ? a > b : a < b;
+          key[r] = swap ? b : a;
+          key[r | rj] = swap ? a : b;
+        }
+      } else {
+#pragma clang loop unroll(full)
+        for (u32 r = 0; r < 8; ++r) {
+          const u32 e = r * 64 + lane;
+          const u32 other = __shfl_xor(key[r], j, 64);
+          const bool up = (e & k) == 0, lower = (lane & j) == 0;
+          // The lower slot keeps the smaller key in an ascending run.
+          const bool take_min = up == lower;
+          key[r] = take_min ? min(key[r], other) : max(key[r], other);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (u32 r = 0; r < 8; ++r) {
+    const u32 i = r * 64 + lane;
+    if (i < m) {
+      hs.sorted[i] = u16(key[r] & 511);
+      hs.leaf[i] = key[r] >> 9;
+    }
   }
   for (u32 i = lane; i < 16 * kPmWords; i += 64) (&hs.leafbits[0][0])[i] = 0;
   wave_sync();
