@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -24,9 +25,22 @@ struct PoolEntry {
   hipMemPool_t pool;
 };
 
+// A device buffer that calls carve their scratch from, kept between calls:
+// a call takes an idle arena of its device, makes its stream wait for the
+// arena's last use, and records that use again when it ends, so reuse needs
+// no allocation and no host synchronisation.
+struct Arena {
+  int device;
+  u8* base;
+  u64 capacity;
+  hipEvent_t last_use;
+  bool busy;
+};
+
 struct PoolRegistry {
   std::mutex mutex;
   std::vector<PoolEntry> pools;
+  std::vector<std::unique_ptr<Arena>> arenas;
   u64 retention = 1ull << 30;
 };
 
@@ -94,15 +108,31 @@ class DeviceScope {
   bool switched_ = false;
 };
 
-// Stream-ordered scratch for one call; everything is freed (stream-ordered)
-// when the call ends, so results stay valid for later work on the stream.
+constexpr u64 kArenaGranule = 64ull << 20;
+
+// Stream-ordered scratch for one call, carved from an arena of the device
+// (taken on the first allocation).  Requests the arena cannot hold come from
+// the pool and are freed (stream-ordered) when the call ends; the arena is
+// then grown to the call's total for later calls, within the retention
+// budget.  Results stay valid for later work on the stream.
 class Workspace final : public Scratch {
  public:
-  Workspace(hipStream_t stream, hipMemPool_t pool) : stream_(stream), pool_(pool) {}
+  Workspace(hipStream_t stream, hipMemPool_t pool, int device)
+      : stream_(stream), pool_(pool), device_(device) {}
   hipError_t alloc_bytes(void** p, u64 bytes) override {
     *p = nullptr;
     if (!bytes) bytes = 1;
     bytes = (bytes + 255) & ~u64(255);
+    if (!acquired_) {
+      hipError_t err = acquire();
+      if (err != hipSuccess) return err;
+    }
+    total_ += bytes;
+    if (arena_ && used_ + bytes <= arena_->capacity) {
+      *p = arena_->base + used_;
+      used_ += bytes;
+      return hipSuccess;
+    }
     hipError_t err = hipMallocFromPoolAsync(p, bytes, pool_, stream_);
     if (err != hipSuccess) return err;
     allocations_.push_back(*p);
@@ -110,18 +140,68 @@ class Workspace final : public Scratch {
   }
   hipError_t release() {
     hipError_t first = hipSuccess;
-    for (void* p : allocations_) {
-      hipError_t err = hipFreeAsync(p, stream_);
-      if (first == hipSuccess) first = err;
-    }
+    auto keep = [&](hipError_t err) { if (first == hipSuccess) first = err; };
+    for (void* p : allocations_) keep(hipFreeAsync(p, stream_));
     allocations_.clear();
+    if (!acquired_) return first;
+    acquired_ = false;
+    PoolRegistry& reg = registry();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    const u64 want = (total_ + kArenaGranule - 1) / kArenaGranule * kArenaGranule;
+    if (!arena_ && want <= reg.retention) {
+      auto a = std::make_unique<Arena>();
+      a->device = device_;
+      a->base = nullptr;
+      a->capacity = 0;
+      a->busy = true;
+      keep(hipEventCreateWithFlags(&a->last_use, hipEventDisableTiming));
+      if (first != hipSuccess) return first;
+      arena_ = a.get();
+      reg.arenas.push_back(std::move(a));
+    }
+    if (arena_ && total_ > arena_->capacity) {
+      // Grow for later calls: the old buffer is freed after this call's work.
+      if (arena_->base) keep(hipFreeAsync(arena_->base, stream_));
+      arena_->base = nullptr;
+      arena_->capacity = 0;
+      if (want <= reg.retention) {
+        void* base = nullptr;
+        hipError_t err = hipMallocFromPoolAsync(&base, want, pool_, stream_);
+        keep(err);
+        if (err == hipSuccess) {
+          arena_->base = static_cast<u8*>(base);
+          arena_->capacity = want;
+        }
+      }
+    }
+    if (arena_) {
+      keep(hipEventRecord(arena_->last_use, stream_));
+      arena_->busy = false;
+    }
     return first;
   }
   ~Workspace() override { release(); }
 
  private:
+  hipError_t acquire() {
+    acquired_ = true;
+    PoolRegistry& reg = registry();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    for (auto& a : reg.arenas)
+      if (a->device == device_ && !a->busy) {
+        a->busy = true;
+        arena_ = a.get();
+        return hipStreamWaitEvent(stream_, arena_->last_use, 0);
+      }
+    return hipSuccess;
+  }
+
   hipStream_t stream_;
   hipMemPool_t pool_;
+  int device_;
+  Arena* arena_ = nullptr;
+  bool acquired_ = false;
+  u64 used_ = 0, total_ = 0;
   std::vector<void*> allocations_;
 };
 
@@ -139,7 +219,7 @@ int execute(hipStream_t stream, Body&& body) {
     hipMemPool_t pool = nullptr;
     err = get_pool(scope.device(), &pool);
     if (err != hipSuccess) return int(err);
-    Workspace ws(stream, pool);
+    Workspace ws(stream, pool, scope.device());
     err = body(ws);
     hipError_t rel = ws.release();
     return int(err != hipSuccess ? err : rel);
@@ -315,6 +395,20 @@ extern "C" int HipZlibWorkspacePoolStats(int device, uint64_t* stats) {
 extern "C" int HipZlibTrimWorkspacePool(int device) {
   hipMemPool_t pool;
   if (!find_pool(device, &pool)) return 0;
+  {
+    // Idle arenas go back to the pool once their last use has finished.
+    PoolRegistry& reg = registry();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    for (auto it = reg.arenas.begin(); it != reg.arenas.end();) {
+      Arena& a = **it;
+      if (a.device != device || a.busy) { ++it; continue; }
+      hipError_t err = hipEventSynchronize(a.last_use);
+      if (err == hipSuccess && a.base) err = hipFreeAsync(a.base, nullptr);
+      if (err == hipSuccess) err = hipEventDestroy(a.last_use);
+      if (err != hipSuccess) return int(err);
+      it = reg.arenas.erase(it);
+    }
+  }
   return int(hipMemPoolTrimTo(pool, 0));
 }
 

@@ -2,21 +2,27 @@
 //
 // Pipeline (all on one stream, no host synchronisation):
 //   frame      framing checks, declared window, wanted Adler-32
-//   discover   every bit offset: cheap bit-parallel prefilter, exact dynamic
-//              header validation; ordered compaction (per-workgroup lists,
-//              scan, gather) gives a sorted candidate list without a sort
-//   describe   one wave per candidate: parse its segment (the candidate's
-//              block plus following stored/fixed blocks up to the next
-//              candidate) -> end bit, output size, block count, status
+//   discover   every bit offset: bit-parallel prefilter (BTYPE, HLIT, a
+//              complete code-length code); ordered compaction (per-workgroup
+//              lists, scan, gather) into a dense sorted array; exact header
+//              validation with lanes refilled from the array (long headers
+//              to a wave-per-header pass); valid offsets in order
+//   headers    one wave per candidate: parse its header, build and store its
+//              decode tables
+//   describe   one 256-lane workgroup per candidate: speculative slices of
+//              its blocks decoded in parallel, merged where decodings meet,
+//              give every slice's true entry and output offset, the segment
+//              end, size and status (up to the next candidate)
 //   chain      one workgroup: path from bit 0 through the segment graph,
 //              output prefixes; any anomaly defers to the exact walk
 //   exact      serial walk with the reference's status precedence (runs only
 //              when the fast chain did not accept the stream)
-//   emit       one wave per accepted segment writes output bytes in place;
-//              bytes copied from earlier segments become (position, root)
-//              entries of an unresolved list
-//   resolve    pointer-jumping rounds over the unresolved list
-//   adler      tiled Adler-32 partials, then the final status
+//   emit       one 256-lane workgroup per accepted segment decodes its slices
+//              in parallel, writing output in place; a byte copied from
+//              before its slice's start is marked unresolved with its root
+//   resolve    rounds over the unresolved bitmask, each following up to 32
+//              root links per byte
+//   adler      vectorised Adler-32 partials, then the final status
 //
 // Status semantics restate the reference's general route: framing
 // (native/codec_ffi.cu:304-329) > candidate overflow (344-360) > exact chain
@@ -49,7 +55,7 @@ struct State {
   u64 accepted;      // number of accepted segments
   u32 emit_status;
   u32 pad;
-  u64 unresolved[2]; // ping-pong list lengths for resolve rounds
+  u64 unresolved[2]; // unresolved bytes after emission / after the last resolve round
   u64 adler_s, adler_w;
   u64 recs_used;     // block records handed out by describe
   u64 groups_used;   // 64-slot slice groups handed out by describe
@@ -1876,29 +1882,13 @@ __device__ __forceinline__ bool copy_byte(u8* out, u32* roots, u32* unres, u64 s
   return false;
 }
 
-// Wave-aggregated append of positions to the unresolved list.
-__device__ __forceinline__ void append_unresolved(bool flag, u64 pos, u32* list, u64* count,
-                                                  u64 capacity) {
-  const u64 ballot = __ballot(flag);
-  if (!ballot) return;
-  const u32 lane = threadIdx.x & 63;
-  const u32 leader = __builtin_ctzll(ballot);
-  u64 base = 0;
-  if (lane == leader) base = atomicAdd(reinterpret_cast<unsigned long long*>(count), __popcll(ballot));
-  base = __shfl(base, leader, 64);
-  if (flag) {
-    const u64 at = base + __popcll(ballot & ((1ull << lane) - 1));
-    if (at < capacity) list[at] = u32(pos);
-  }
-}
-
 }  // namespace
 
 // One wave per accepted segment: lane 0 parses, the wave copies stored
 // payloads and long matches.  Output positions are absolute.
 __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, State* st,
                                                     const Segment* acc, u8* out, u32* roots,
-                                                    u32* unres, u32* list, u64 list_capacity) {
+                                                    u32* unres) {
   __shared__ EmitShared sh;
   if (st->status) return;
   const u32 lane = threadIdx.x;
@@ -1969,10 +1959,8 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
           }
           for (u32 j = 0; j < length; ++j) {
             const u64 src = dst - distance + (j % distance);
-            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src)) {
-              const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), 1ull);
-              if (at < list_capacity) list[at] = u32(dst + j);
-            }
+            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src))
+              atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), 1ull);
           }
           produced += length;
         }
@@ -1989,7 +1977,9 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
           const u64 j = j0 + lane;
           bool queued = false;
           if (j < length) queued = copy_byte(out, roots, unres, seg.prefix, begin + j, begin - d + (j % d));
-          append_unresolved(queued, begin + j, list, &st->unresolved[0], list_capacity);
+          const u64 bal = __ballot(queued);
+          if (!lane && bal)
+            atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), u64(__popcll(bal)));
         }
       } else {
         for (u64 j = lane; j < length; j += kWave) out[begin + j] = body[sh.src + j];
@@ -2002,14 +1992,12 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
 }
 
 namespace {
-constexpr u32 kPushSlots = 8;
 constexpr u32 kEmitThreads = kDescThreads;
 
 struct LaneEmitShared {
   DecodeTables tables;
   Stage stage;
   u16 codes[320];
-  u32 push[kPushSlots][kEmitThreads];  // slot-major: lanes touch consecutive banks
   BlockRec rec;
   u64 first, chunk_end;
   u32 count, next_g, need;
@@ -2018,41 +2006,18 @@ struct LaneEmitShared {
   u32 type, final_block, status, nl, nd, build_status;
 };
 
-// buf: a lane's kPushSlots staging slots, kEmitThreads entries apart.
-__device__ __forceinline__ void push_unresolved(u32* buf, u32& n, u32 pos, u32* list, u64* count,
-                                                u64 capacity) {
-  buf[n++ * kEmitThreads] = pos;
-  if (n == kPushSlots) {
-    const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(count), u64(kPushSlots));
-    for (u32 i = 0; i < kPushSlots; ++i)
-      if (at + i < capacity) list[at + i] = buf[i * kEmitThreads];
-    n = 0;
-  }
-}
-
-__device__ __forceinline__ void flush_unresolved(u32* buf, u32& n, u32* list, u64* count,
-                                                 u64 capacity) {
-  if (!n) return;
-  const u64 at = atomicAdd(reinterpret_cast<unsigned long long*>(count), u64(n));
-  for (u32 i = 0; i < n; ++i)
-    if (at + i < capacity) list[at + i] = buf[i * kEmitThreads];
-  n = 0;
-}
-
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
 // [.., block_end).  Returns 0 or an error.
 template <bool kChecked>
 __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64 dst0,
-                          u64 block_end, u32 window, u8* out, u32* roots, u32* unres, u32* list,
-                          u64* list_count, u64 list_capacity) {
+                          u64 block_end, u32 window, u8* out, u32* roots, u32* unres,
+                          u64* unres_count) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
   r.limit = blim;
   r.seek(entry);
   u64 dst = dst0;
-  bool any_unres = false;
-  u32 pushed = 0, err = 0;
-  u32* push = &sh.push[0][threadIdx.x];
+  u32 nunres = 0, err = 0;  // unresolved bytes of this slice
   while (r.pos() < stop) {
     u32 length, x;  // x: the literal (length 1) or the distance
     if (!quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x)) {
@@ -2078,19 +2043,18 @@ __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64
       if (src < dst0) {
         roots[d] = u32(src);
         bit_set(unres, d);
-        push_unresolved(push, pushed, u32(d), list, list_count, list_capacity);
-        any_unres = true;
-      } else if (any_unres && bit_get(unres, src)) {
+        ++nunres;
+      } else if (nunres && bit_get(unres, src)) {
         roots[d] = roots[src];
         bit_set(unres, d);
-        push_unresolved(push, pushed, u32(d), list, list_count, list_capacity);
+        ++nunres;
       } else {
         out[d] = out[src];
       }
     }
     dst += length;
   }
-  flush_unresolved(push, pushed, list, list_count, list_capacity);
+  if (nunres) atomicAdd(reinterpret_cast<unsigned long long*>(unres_count), u64(nunres));
   return err;
 }
 }  // namespace
@@ -2104,13 +2068,13 @@ __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64
 __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
     const u8* body, u64 len, State* st, const Segment* acc, const BlockRec* recs,
     const u64* slice_entry, const u32* slice_off, const u32* group_link,
-    const BlockTables* tables, u8* out, u32* roots, u32* unres, u32* list, u64 list_capacity) {
+    const BlockTables* tables, u8* out, u32* roots, u32* unres) {
   __shared__ LaneEmitShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
   const u64 segments = st->accepted;
   const u32 window = st->window;
-  u64* list_count = &st->unresolved[0];
+  u64* unres_count = &st->unresolved[0];
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
     if (seg.rec_first == kNone) continue;
@@ -2177,10 +2141,10 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
             // before the body end.
             if (stop + 64 <= len * 8)
               lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                       roots, unres, list, list_count, list_capacity);
+                                       roots, unres, unres_count);
             else
               lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                      roots, unres, list, list_count, list_capacity);
+                                      roots, unres, unres_count);
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
           done += count;
@@ -2199,39 +2163,34 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
 
 constexpr u32 kResolveLinks = 32;  // chain links a position follows per round
 
-// One resolution round over the unresolved list: round r reads list (r & 1)
-// with count counts[r] (round 0: the emitted list) and appends the
-// still-unresolved positions to the other list, counted in counts[r + 1]
-// (zero-filled before the first round).  A position follows up to
-// kResolveLinks links of its root chain through this round's snapshot (the
-// unresolved bits of the previous round, and roots: any root read is an
-// earlier byte of the same chain, so concurrent updates are harmless); at a
-// resolved byte it takes that byte, else it keeps the root reached.  Round r
-// thus covers kResolveLinks^(r+1) links.  Only bytes written by earlier
-// launches are read.  The last round leaves its leftover count in
-// st->unresolved[1] (status 20 in g_finish).
+// One resolution round: round r scans the unresolved bits of buffer (r & 1)
+// (round 0: the bits set by emission; counts[r] unresolved positions,
+// zero-filled before the first round) and writes every word of the other
+// buffer with the positions still unresolved, counted in counts[r + 1].  A
+// position follows up to kResolveLinks links of its root chain through this
+// round's snapshot (roots: any root read is an earlier byte of the same
+// chain, so concurrent updates are harmless); at a resolved byte it takes
+// that byte, else it keeps the root reached.  Round r thus covers
+// kResolveLinks^(r+1) links.  Only bytes written by earlier launches are
+// read.  The last round leaves its count in st->unresolved[1] (status 20 in
+// g_finish).
 __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
-                                                 u32* bits1, u32* list0, u32* list1, u64* counts,
-                                                 u32 round, u32 max_rounds, u64 capacity) {
+                                                 u32* bits1, u64* counts, u32 round,
+                                                 u32 max_rounds, u64 words) {
   if (st->status || st->emit_status) return;
-  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
-  const u64 n_list = round ? counts[round] : st->unresolved[0];
-  const u64 count = min<u64>(n_list, capacity);
-  if (!count) return;
-  const u32 cur = round & 1;
-  const u32* bits = cur ? bits1 : bits0;
-  u32* next_bits = cur ? bits0 : bits1;
-  const u32* list = cur ? list1 : list0;
-  u32* next_list = cur ? list0 : list1;
+  const u64 n_in = round ? counts[round] : st->unresolved[0];
+  if (!n_in) return;
+  const u32* bits = round & 1 ? bits1 : bits0;
+  u32* next_bits = round & 1 ? bits0 : bits1;
   u64* next_count = round + 1 == max_rounds ? &st->unresolved[1] : &counts[round + 1];
   const u64 stride = u64(gridDim.x) * blockDim.x;
-  const u64 iters = (count + stride - 1) / stride;
-  for (u64 it = 0; it < iters; ++it) {
-    const u64 i = tid + it * stride;
-    bool keep = false;
-    u32 u = 0;
-    if (i < count) {
-      u = list[i];
+  u32 kept = 0;
+  for (u64 w = u64(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
+    u32 m = bits[w], keep = 0;
+    while (m) {
+      const u32 b = u32(__builtin_ctz(m));
+      m &= m - 1;
+      const u32 u = u32(w * 32 + b);
       u32 r = roots[u];
       bool r_unres = (bits[r >> 5] >> (r & 31)) & 1u;
       for (u32 k = 0; r_unres && k < kResolveLinks; ++k) {
@@ -2240,15 +2199,16 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
       }
       if (!r_unres) {
         out[u] = out[r];
-        atomicAnd(next_bits + (u >> 5), ~(1u << (u & 31)));
       } else {
         __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        atomicOr(next_bits + (u >> 5), 1u << (u & 31));
-        keep = true;
+        keep |= 1u << b;
       }
     }
-    append_unresolved(keep, u, next_list, next_count, capacity);
+    next_bits[w] = keep;
+    kept += __builtin_popcount(keep);
   }
+  for (u32 off = 32; off; off >>= 1) kept += __shfl_xor(kept, off, 64);
+  if (lane_id() == 0 && kept) atomicAdd(reinterpret_cast<unsigned long long*>(next_count), u64(kept));
 }
 
 // Adler-32 partial sums, accumulated into the state: every thread takes
@@ -2437,21 +2397,16 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
 
   // Emission and cross-segment resolution.
   const u64 words = (out_size + 31) / 32 + 1;
-  u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr, *list0 = nullptr, *list1 = nullptr;
-  const u64 list_capacity = out_size ? out_size : 1;
-  HZ_TRY(scratch.alloc(&roots, list_capacity));
+  u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr;
+  HZ_TRY(scratch.alloc(&roots, out_size ? out_size : 1));
   HZ_TRY(scratch.alloc(&bits0, words));
   HZ_TRY(scratch.alloc(&bits1, words));
-  HZ_TRY(scratch.alloc(&list0, list_capacity));
-  HZ_TRY(scratch.alloc(&list1, list_capacity));
   HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
-  HZ_TRY(launch_fill(stream, bits1, 0, words * 4));
   HZ_LAUNCH(g_emit_lanes, dim3(clamp_grid(max_blocks, 4096)), dim3(kEmitThreads), 0, stream, body,
-            len, st, acc, recs, slice_entry, slice_off, group_link, tables, out, roots, bits0,
-            list0, list_capacity);
+            len, st, acc, recs, slice_entry, slice_off, group_link, tables, out, roots, bits0);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_emit_serial, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
-            st, acc, out, roots, bits0, list0, list_capacity);
+            st, acc, out, roots, bits0);
   HZ_TRY(hipGetLastError());
   // Round r covers kResolveLinks^(r+1) links of a chain.  A chain hops back
   // across slices (or serially emitted segments), so its length is bounded
@@ -2463,8 +2418,8 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&counts, rounds + 1));
   HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
   for (u32 round = 0; round < rounds; ++round) {
-    HZ_LAUNCH(g_resolve, dim3(1024), dim3(256), 0, stream, st, out, roots, bits0, bits1, list0,
-              list1, counts, round, rounds, list_capacity);
+    HZ_LAUNCH(g_resolve, dim3(u32(clamp_grid((words + 255) / 256, 2048))), dim3(256), 0, stream,
+              st, out, roots, bits0, bits1, counts, round, rounds, words);
     HZ_TRY(hipGetLastError());
   }
   HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048)),
