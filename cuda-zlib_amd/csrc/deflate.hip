@@ -22,15 +22,18 @@
 //            8 previous positions of the same wave with an equal hash; longest
 //            match (ties: nearest); one-step lazy rule (a position yields to a
 //            longer match at the next position).  With f(j) = j + max(1, L_j)
-//            the greedy token starts are the orbit of 0 under f, found by
-//            pointer doubling in log2(1024) rounds: round b marks
-//            f^(2^b)(x) for every marked x and squares the jump table.
+//            the greedy token starts are the orbit of 0 under f: every wave
+//            finds the first orbit point past itself from each of its
+//            positions (pointer doubling by shuffles), one thread chains the
+//            16 waves' entries, and each wave marks its orbit from its entry.
 //            Tokens go to a global list, histograms by LDS atomics; the step's
 //            positions are inserted into way (step mod 4) by atomicMax, so the
 //            newest position wins independently of execution order.
 // e_emit, one 256-thread workgroup per chunk (small LDS, several per CU):
-//   huffman  wave 0: optimal code lengths (parallel rank sort, two-queue
-//            merge), limited to 15/7 bits by the JPEG count adjustment
+//   huffman  waves 0 and 1: optimal code lengths limited to 15/7 bits
+//            (leaves sorted by a bitonic network, package-merge with each
+//            level merged along merge paths); wave-parallel code-length
+//            RLE and canonical codes
 //   choose   exact bit costs of stored / fixed / dynamic
 //   emit     4 tokens per thread per round: bit lengths, block-wide
 //            exclusive scan, atomicOr into an LDS bit buffer; one coalesced
@@ -98,12 +101,13 @@ struct ChunkResult {
 struct ParseShared {
   u32 table[kBuckets * kWays];  // position + 1 per way, 0 = empty
   u16 ml[kStep];                // match length per step position (0: none)
-  u16 jump[2][kStep + 1];       // pointer-doubling tables
+  u16 exitv[kStep];             // first orbit point past the position's wave
+  u16 went[kParseWaves];        // orbit entry of each wave (0xffff: none)
   u8 mark[kStep + 4];           // token starts (orbit of 0)
   u32 freq_ll[288];
   u32 freq_d[32];
   u32 wave_count[kParseWaves];
-  u32 wave_end[kParseWaves];
+  u32 adv;                      // step advance: first orbit point at or past the step's end
   u32 extra_bits;
   u64 red_s[kParseWaves], red_l[kParseWaves];
 };
@@ -630,12 +634,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
     for (u32 i = t; i < kBuckets * kWays; i += kParseThreads) sh.table[i] = 0;
     for (u32 i = t; i < 288; i += kParseThreads) sh.freq_ll[i] = 0;
     if (t < 32) sh.freq_d[t] = 0;
-    if (!t) {
-      sh.extra_bits = 0;
-      sh.jump[0][kStep] = kStep;
-      sh.jump[1][kStep] = kStep;
-      sh.mark[kStep] = 0;
-    }
+    if (!t) sh.extra_bits = 0;
     __syncthreads();
 
     // ---- history positions enter the table ----
@@ -662,66 +661,85 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       }
       u32 best_len = 0, best_dist = 0;
       if (hashable) {
-        const u32 maxlen = min(258u, end - q);
+        const u32 maxlen = min(258u, end - q);  // >= 4
         const uint4 e = *reinterpret_cast<const uint4*>(&sh.table[h * kWays]);
         const u32 ent[4] = {e.x, e.y, e.z, e.w};
+        // Candidates by distance (0: none): the ways, then the near position.
+        u32 dist[kWays + 1];
 #pragma unroll
         for (u32 k = 0; k < kWays; ++k) {
-          if (!ent[k]) continue;
           const u32 cand = ent[k] - 1;
-          if (cand >= q || q - cand > kMaxDist) continue;
-          const u32 m = match_len(win, cand, q, maxlen);
-          if (m > best_len || (m == best_len && q - cand < best_dist)) {
-            best_len = m;
-            best_dist = q - cand;
-          }
+          dist[k] = ent[k] && cand < q && q - cand <= kMaxDist ? q - cand : 0u;
         }
-        if (near) {
-          const u32 m = match_len(win, q - near, q, maxlen);
-          if (m > best_len || (m == best_len && near < best_dist)) {
+        dist[kWays] = near;
+        // The first dword decides most candidates: fewer than three equal
+        // bytes is no match, three is a match of 3; only four equal bytes
+        // continue the comparison.
+#pragma unroll
+        for (u32 k = 0; k <= kWays; ++k) {
+          if (!dist[k]) continue;
+          const u32 x = win_u32(win, q - dist[k]) ^ v;
+          if (x & 0xffffffu) continue;
+          const u32 m = x ? 3u : 4u + match_len(win, q - dist[k] + 4, q + 4, maxlen - 4);
+          if (m > best_len || (m == best_len && dist[k] < best_dist)) {
             best_len = m;
-            best_dist = near;
+            best_dist = dist[k];
           }
         }
       }
       sh.ml[t] = u16(best_len >= 3 ? best_len : 0u);
       __syncthreads();
 
-      // Lazy rule; f(t) = end of a token starting at t; orbit of 0 under f.
+      // Lazy rule; f(t) = end of a token starting at t.
       const u32 lim = min(kStep, end - p);
       const u32 cur_ml = sh.ml[t];
       const u32 next_ml = t + 1 < kStep ? sh.ml[t + 1] : 0u;
       const u32 L = (cur_ml && next_ml <= cur_ml) ? cur_ml : 0u;
       const u32 f = t + (L ? L : 1u);
-      sh.jump[0][t] = u16(min(f, kStep));
-      sh.mark[t] = t == 0;
+      // Token starts = orbit of 0 under f.  Each wave finds, for each of its
+      // 64 positions, the first orbit point past the wave (pointer doubling
+      // by shuffles; J[k] = f^(2^k) while inside the wave); one thread
+      // chains the waves' entries; each wave then marks its orbit from its
+      // entry (round k pushes marks 2^k hops).
+      const u32 w0 = wave * 64, wend = w0 + 64;
+      u32 J[6];
+      u32 x = f;
+#pragma unroll
+      for (u32 k = 0; k < 6; ++k) {
+        J[k] = x;
+        const u32 y = __shfl(x, int((x - w0) & 63), 64);
+        x = x < wend ? y : x;
+      }
+      sh.exitv[t] = u16(x);
       __syncthreads();
-      u32 cur = 0;
-      for (u32 b = 0; b < kLog2Step; ++b) {
-        // Marks of earlier rounds are visible; a mark written in this round
-        // and seen early only adds orbit members, so the result is exact.
-        const u32 j = sh.jump[cur][t];
-        if (sh.mark[t]) sh.mark[j] = 1;
-        sh.jump[cur ^ 1][t] = sh.jump[cur][j];
-        cur ^= 1;
-        __syncthreads();
+      if (!t) {
+        for (u32 w = 0; w < kParseWaves; ++w) sh.went[w] = 0xffffu;
+        u32 e = 0;
+        while (e < lim) {
+          sh.went[e >> 6] = u16(e);
+          e = sh.exitv[e];
+        }
+        sh.adv = e;
+      }
+      __syncthreads();
+      sh.mark[t] = t == sh.went[wave];
+      wave_sync();
+#pragma unroll
+      for (u32 k = 0; k < 6; ++k) {
+        if (sh.mark[t] && J[k] < wend) sh.mark[J[k]] = 1;
+        wave_sync();
       }
       const bool start = t < lim && sh.mark[t];
       const u64 bal = __ballot(start);
-      // The last start of the wave ends the furthest.
-      const u32 last_end = bal ? __shfl(f, 63 - __builtin_clzll(bal), 64) : 0u;
-      if (!lane) {
-        sh.wave_count[wave] = __popcll(bal);
-        sh.wave_end[wave] = last_end;
-      }
+      if (!lane) sh.wave_count[wave] = __popcll(bal);
       __syncthreads();
-      u32 before = 0, step_tokens = 0, adv = 0;
+      const u32 adv = sh.adv;
+      u32 before = 0, step_tokens = 0;
 #pragma unroll
       for (u32 w = 0; w < kParseWaves; ++w) {
         const u32 cnt = sh.wave_count[w];
         if (w < wave) before += cnt;
         step_tokens += cnt;
-        adv = max(adv, sh.wave_end[w]);
       }
       if (start) {
         const u32 idx = ntok + before + __popcll(bal & lanemask_lt());
