@@ -611,14 +611,17 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         if (4 * k + 4 > end) v &= (1u << (8 * (end - 4 * k))) - 1;
         win[k] = v;
         if (4 * k + 4 > hist) {
-          for (u32 i = 0; i < 4; ++i) {
-            const u32 q = 4 * k + i;
-            const u32 b = (v >> (8 * i)) & 0xff;
-            if (q >= hist && q < end) {
-              s += b;
-              l += u64(q - hist) * b;
-            }
-          }
+          // Chunk bytes of this dword (v is zero past the end): byte sum and
+          // position-weighted sum by dot products.
+          const u32 lo_q = 4 * k;
+          const u32 mask = lo_q >= hist ? ~0u : ~0u << (8 * (hist - lo_q));
+          const u32 b = v & mask;
+          const u32 sum = __builtin_amdgcn_udot4(b, 0x01010101u, 0u, false);
+          const u32 wsum = __builtin_amdgcn_udot4(b, 0x03020100u, 0u, false);
+          s += sum;
+          // (lo_q - hist) may be negative here: bytes before hist are masked
+          // out, so the sum over the dword's chunk bytes stays exact mod 2^64.
+          l += u64(i64(lo_q) - i64(hist)) * sum + wsum;
         }
       }
       for (u32 k = nw + t; k < nw + 4; k += kParseThreads) win[k] = 0;
