@@ -520,7 +520,7 @@ __device__ __forceinline__ u32 block_scan(EmitShared& sh, u32 v, u32& total) {
     if (lane >= off) x += y;
   }
   if (lane == 63) sh.scan[wave] = x;
-  __syncthreads();
+  lds_barrier();
   u32 before = 0;
   total = 0;
   for (u32 w = 0; w < kEmitWaves; ++w) {
@@ -528,7 +528,7 @@ __device__ __forceinline__ u32 block_scan(EmitShared& sh, u32 v, u32& total) {
     if (w < wave) before += s;
     total += s;
   }
-  __syncthreads();
+  lds_barrier();
   return before + x - v;
 }
 
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
     for (u32 i = t; i < 288; i += kParseThreads) sh.freq_ll[i] = 0;
     if (t < 32) sh.freq_d[t] = 0;
     if (!t) sh.extra_bits = 0;
-    __syncthreads();
+    lds_barrier();
 
     // ---- history positions enter the table ----
     u32 stepno = 0;
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       if (q < hist && q + 4 <= end)
         atomicMax(&sh.table[hash4(win_u32(win, q)) * kWays + (stepno & (kWays - 1))], q + 1);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- parse ----
     u32* tok = tokens + d.in_off;
@@ -691,7 +691,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         }
       }
       sh.ml[t] = u16(best_len >= 3 ? best_len : 0u);
-      __syncthreads();
+      lds_barrier();
 
       // Lazy rule; f(t) = end of a token starting at t.
       const u32 lim = min(kStep, end - p);
@@ -714,7 +714,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         x = x < wend ? y : x;
       }
       sh.exitv[t] = u16(x);
-      __syncthreads();
+      lds_barrier();
       if (!t) {
         for (u32 w = 0; w < kParseWaves; ++w) sh.went[w] = 0xffffu;
         u32 e = 0;
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         }
         sh.adv = e;
       }
-      __syncthreads();
+      lds_barrier();
       sh.mark[t] = t == sh.went[wave];
       wave_sync();
 #pragma unroll
@@ -735,7 +735,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       const bool start = t < lim && sh.mark[t];
       const u64 bal = __ballot(start);
       if (!lane) sh.wave_count[wave] = __popcll(bal);
-      __syncthreads();
+      lds_barrier();
       const u32 adv = sh.adv;
       u32 before = 0, step_tokens = 0;
 #pragma unroll
@@ -764,10 +764,10 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       if (hashable) atomicMax(&sh.table[h * kWays + (stepno & (kWays - 1))], q + 1);
       ++stepno;
       p += adv;
-      __syncthreads();
+      lds_barrier();
     }
     if (extra) atomicAdd(&sh.extra_bits, extra);
-    __syncthreads();
+    lds_barrier();
     ChunkStats& st = stats[c];
     for (u32 i = t; i < 288; i += kParseThreads) st.freq_ll[i] = sh.freq_ll[i] + (i == 256);
     if (t < 32) st.freq_d[t] = sh.freq_d[t];
@@ -782,7 +782,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       st.sum_s = s;
       st.sum_l = l;
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -802,14 +802,14 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
     const ChunkStats& st = stats[c];
     for (u32 i = t; i < 288; i += kEmitThreads) sh.freq_ll[i] = i < 286 ? st.freq_ll[i] : 0u;
     if (t < 32) sh.freq_d[t] = t < 30 ? st.freq_d[t] : 0u;
-    __syncthreads();
+    lds_barrier();
 
     // ---- code lengths (waves 0 and 1), RLE, costs, block type (wave 0),
     // canonical codes (waves 0-2) ----
     HuffScratch* hsw = reinterpret_cast<HuffScratch*>(stage);  // one per wave
     if (wave == 0) huffman_lengths(hsw[0], sh.freq_ll, 286, 15, sh.len_ll);
     else if (wave == 1) huffman_lengths(hsw[1], sh.freq_d, 30, 15, sh.len_d);
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
       sh.hlit = used_extent(sh.len_ll, 286, 257);
       sh.hdist = used_extent(sh.len_d, 30, 1);
@@ -862,13 +862,13 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
             (((d.file_len - d.file_off) % kAdlerMod) * S + kAdlerMod - L) % kAdlerMod;
       }
     }
-    __syncthreads();
+    lds_barrier();
     {
       const u32 mode = sh.mode;
       if (mode == 1) {
         for (u32 i = t; i < 288; i += kEmitThreads) sh.len_ll[i] = u8(fixed_len(i));
         if (t < 30) sh.len_d[t] = 5;
-        __syncthreads();
+        lds_barrier();
       }
       if (mode) {
         if (wave == 0) canonical_codes_wave(sh.len_ll, mode == 1 ? 288 : 286, sh.code_ll);
@@ -876,7 +876,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         else if (wave == 2 && mode == 2) canonical_codes_wave(sh.len_cl, 19, sh.code_cl);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- emission ----
     const u32 mode = sh.mode;
@@ -898,7 +898,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
     } else {
       const u32 used = min((sh.extent + 3) / 4 + 1, words);
       for (u32 i = t; i < used; i += kEmitThreads) stage[i] = 0;
-      __syncthreads();
+      lds_barrier();
       // Header: the fixed fields by thread 0 (before the scan's barriers),
       // then the code-length RLE symbols, two per thread, placed by a scan.
       const u32 nrle = mode == 2 ? sh.nrle : 0u;
@@ -937,7 +937,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         hoff += hn[k];
       }
       if (!t && fixed_bits + htotal != sh.hdr_bits) sh.status = kCompressionOverflow;
-      __syncthreads();
+      lds_barrier();
       const u32* tok = tokens + d.in_off;
       const u32 ntokens = st.ntok;
       u32 pos = sh.hdr_bits;
@@ -960,7 +960,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         }
         pos += total;
       }
-      __syncthreads();
+      lds_barrier();
       if (!t) {
         StageWriter out = {stage, words, pos};
         out.put(sh.code_ll[256], sh.len_ll[256]);
@@ -974,13 +974,13 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         if (bytes != sh.extent) sh.status = kCompressionOverflow;
         results[c].extent = sh.extent;
       }
-      __syncthreads();
+      lds_barrier();
       const u32 copy_words = min((sh.extent + 3) / 4, slot_bytes / 4);
       u32* slot32 = reinterpret_cast<u32*>(slot);
       for (u32 i = t; i < copy_words; i += kEmitThreads) slot32[i] = stage[i];
       if (!t) results[c].status = sh.status;
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 

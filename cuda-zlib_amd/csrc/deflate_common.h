@@ -184,6 +184,16 @@ struct StagedBits {
   }
 };
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global store of the wave; kernels whose threads never
+// exchange data through global memory within the launch (their stores are
+// read by later launches) use this instead and keep stores in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();

@@ -56,7 +56,6 @@ struct State {
   u32 emit_status;
   u32 pad;
   u64 unresolved[2]; // unresolved bytes after emission / after the last resolve round
-  u64 adler_s, adler_w;
   u64 recs_used;     // block records handed out by describe
   u64 groups_used;   // 64-slot slice groups handed out by describe
   u64 precount;      // entries of the dense pre-candidate array
@@ -382,6 +381,65 @@ __device__ __forceinline__ u32 block_exclusive_scan(u32 v, u32* sh, u32& total) 
   return excl;
 }
 
+// Exclusive scan of `count` u32 values (each masked by `mask`) into u64
+// offsets by one 1024-thread workgroup; returns the total.  Tiles of
+// kScanPer values per thread are staged in LDS with coalesced loads (padded
+// so that the per-thread reads of consecutive values hit distinct banks),
+// summed per thread, scanned by wave shuffles and combined over the 16 waves.
+constexpr u32 kScanThreads = 1024;
+constexpr u32 kScanPer = 8;
+constexpr u32 kScanTile = kScanThreads * kScanPer;
+struct ScanShared {
+  u32 v[kScanTile + kScanTile / kScanPer];
+  u32 wave[kScanThreads / 64];
+};
+__device__ __forceinline__ u32 scan_slot(u32 e) { return e + e / kScanPer; }
+
+__device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, ScanShared& sh) {
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  u64 carry = 0;
+  for (u64 base = 0; base < count; base += kScanTile) {
+    const u32 m = u32(min<u64>(count - base, kScanTile));
+    u32 x[kScanPer];
+#pragma unroll
+    for (u32 k = 0; k < kScanPer; ++k) {
+      const u32 e = k * kScanThreads + t;
+      x[k] = e < m ? in[base + e] & mask : 0u;
+    }
+#pragma unroll
+    for (u32 k = 0; k < kScanPer; ++k) sh.v[scan_slot(k * kScanThreads + t)] = x[k];
+    __syncthreads();
+    u32 mine = 0;
+#pragma unroll
+    for (u32 k = 0; k < kScanPer; ++k) mine += sh.v[scan_slot(t * kScanPer + k)];
+    u32 incl = mine;
+#pragma unroll
+    for (u32 off = 1; off < 64; off <<= 1) {
+      const u32 y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    if (lane == 63) sh.wave[wave] = incl;
+    __syncthreads();
+    u64 run = carry, tile_total = 0;
+#pragma unroll
+    for (u32 w = 0; w < kScanThreads / 64; ++w) {
+      const u32 c = sh.wave[w];
+      if (w < wave) run += c;
+      tile_total += c;
+    }
+    run += incl - mine;
+#pragma unroll
+    for (u32 k = 0; k < kScanPer; ++k) {
+      const u32 e = t * kScanPer + k;
+      if (e < m) out[base + e] = run;
+      run += sh.v[scan_slot(e)];
+    }
+    carry += tile_total;
+    __syncthreads();  // the next tile reuses sh
+  }
+  return carry;
+}
+
 }  // namespace
 
 __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* st) {
@@ -397,8 +455,6 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
   st->emit_status = 0;
   st->unresolved[0] = 0;
   st->unresolved[1] = 0;
-  st->adler_s = 0;
-  st->adler_w = 0;
   st->recs_used = 0;
   st->groups_used = 0;
   st->precount = 0;
@@ -457,28 +513,10 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
 __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg_count,
                                                         u64* wg_offset, u64 groups,
                                                         u64 pre_capacity) {
-  __shared__ u64 part[1024];
+  __shared__ ScanShared sh;
   if (st->status) return;
-  const u32 t = threadIdx.x;
-  const u64 per = (groups + 1023) / 1024;
-  const u64 lo = min<u64>(groups, u64(t) * per), hi = min<u64>(groups, lo + per);
-  u64 sum = 0;
-  for (u64 i = lo; i < hi; ++i) sum += wg_count[i] & kCountMask;
-  part[t] = sum;
-  __syncthreads();
-  for (u32 off = 1; off < 1024; off <<= 1) {
-    const u64 x = t >= off ? part[t - off] : 0ull;
-    __syncthreads();
-    part[t] += x;
-    __syncthreads();
-  }
-  u64 run = part[t] - sum;
-  for (u64 i = lo; i < hi; ++i) {
-    wg_offset[i] = run;
-    run += wg_count[i] & kCountMask;
-  }
-  if (t == 1023) {
-    const u64 total = part[1023];
+  const u64 total = wg_exclusive_scan(wg_count, kCountMask, groups, wg_offset, sh);
+  if (threadIdx.x == 0) {
     st->precount = total;
     // Only kind-2 ranges (valid headers alone overflowing a range) can push the
     // total past the capacity, and then the valid candidates alone exceed the
@@ -797,29 +835,11 @@ __global__ __launch_bounds__(256) void g_valid_count(const State* st, const u64*
 // (valid headers + bit 0 + stored seeds, as the reference counts them).
 __global__ __launch_bounds__(1024) void g_valid_scan(State* st, const u32* block_valid,
                                                      u64* block_offset, u64 max_candidates) {
-  __shared__ u64 part[1024];
+  __shared__ ScanShared sh;
   if (st->status) return;
   const u64 blocks = (st->precount + kDiscThreads - 1) / kDiscThreads;
-  const u32 t = threadIdx.x;
-  const u64 per = (blocks + 1023) / 1024;
-  const u64 lo = min<u64>(blocks, u64(t) * per), hi = min<u64>(blocks, lo + per);
-  u64 sum = 0;
-  for (u64 i = lo; i < hi; ++i) sum += block_valid[i];
-  part[t] = sum;
-  __syncthreads();
-  for (u32 off = 1; off < 1024; off <<= 1) {
-    const u64 x = t >= off ? part[t - off] : 0ull;
-    __syncthreads();
-    part[t] += x;
-    __syncthreads();
-  }
-  u64 run = part[t] - sum;
-  for (u64 i = lo; i < hi; ++i) {
-    block_offset[i] = run;
-    run += block_valid[i];
-  }
-  if (t == 1023) {
-    const u64 total = part[1023];
+  const u64 total = wg_exclusive_scan(block_valid, ~0u, blocks, block_offset, sh);
+  if (threadIdx.x == 0) {
     st->candidates = total;
     st->tables_used = total;  // table slots 0 .. total-1 belong to the candidates
     if (total + st->seeds > max_candidates) st->status = kCandidateOverflow;
@@ -2007,11 +2027,12 @@ struct LaneEmitShared {
 };
 
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
-// [.., block_end).  Returns 0 or an error.
+// [.., block_end); adds the slice's unresolved bytes to `unres_total`.
+// Returns 0 or an error.
 template <bool kChecked>
 __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64 dst0,
                           u64 block_end, u32 window, u8* out, u32* roots, u32* unres,
-                          u64* unres_count) {
+                          u64& unres_total) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
   r.limit = blim;
@@ -2054,7 +2075,7 @@ __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64
     }
     dst += length;
   }
-  if (nunres) atomicAdd(reinterpret_cast<unsigned long long*>(unres_count), u64(nunres));
+  unres_total += nunres;
   return err;
 }
 }  // namespace
@@ -2074,7 +2095,7 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   const u32 t = threadIdx.x;
   const u64 segments = st->accepted;
   const u32 window = st->window;
-  u64* unres_count = &st->unresolved[0];
+  u64 unres_total = 0;  // this thread's unresolved bytes, counted once per wave at the end
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
     if (seg.rec_first == kNone) continue;
@@ -2141,10 +2162,10 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
             // before the body end.
             if (stop + 64 <= len * 8)
               lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                       roots, unres, unres_count);
+                                       roots, unres, unres_total);
             else
               lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                      roots, unres, unres_count);
+                                      roots, unres, unres_total);
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
           done += count;
@@ -2159,6 +2180,9 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
     if (!t && error) atomicMax(&st->emit_status, error);
     __syncthreads();
   }
+  for (u32 off = 32; off; off >>= 1) unres_total += __shfl_down(unres_total, off, 64);
+  if (lane_id() == 0 && unres_total)
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), unres_total);
 }
 
 constexpr u32 kResolveLinks = 32;  // chain links a position follows per round
@@ -2212,19 +2236,21 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
 }
 
 // Adler-32 partial sums, accumulated into the state: every thread takes
-// 16-byte chunks (byte sums and position-weighted sums by dot products), so
-// the output is read once with 16-byte loads.  For a chunk at offset a,
-// sum over it of (n - i) x_i = (n - a) S - L with L = sum of (i - a) x_i.
-__global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n) {
-  __shared__ u64 red[3][256];
+// 16-byte chunks (byte sums and position-weighted sums by dot products), four
+// loads in flight at a time, so the output is read once with 16-byte loads.
+// For a chunk at offset a, sum over it of (n - i) x_i = (n - a) S - L with
+// L = sum of (i - a) x_i; the weighted sum is reduced mod 65521 whenever it
+// reaches 2^62, so it never wraps.
+__global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n, u64* parts) {
+  __shared__ u64 red[2][4];
   if (st->status || st->emit_status) return;
-  const u64 tid = u64(blockIdx.x) * 256 + threadIdx.x, stride = u64(gridDim.x) * 256;
-  u64 s = 0, w = 0, l = 0;
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  const u64 tid = u64(blockIdx.x) * 256 + t, stride = u64(gridDim.x) * 256;
+  u64 s = 0, w = 0;
   const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
   const u64 chunks = aligned ? n / 16 : 0;
   const uint4* v = reinterpret_cast<const uint4*>(out);
-  for (u64 c = tid; c < chunks; c += stride) {
-    const uint4 q = v[c];
+  auto add_chunk = [&](const uint4& q, u64 c) {
     const u32 words[4] = {q.x, q.y, q.z, q.w};
     u32 cs = 0, cl = 0;
 #pragma unroll
@@ -2233,48 +2259,79 @@ __global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n) 
       cs += ws;
       cl += __builtin_amdgcn_udot4(words[k], 0x03020100u, 0u, false) + 4 * k * ws;
     }
-    const u32 x = u32((n - c * 16) % kAdlerMod);
     s += cs;
-    w += u64(x) * cs;
-    l += cl;
+    w += (n - c * 16) * cs - cl;
+    if (w >> 62) w %= kAdlerMod;
+  };
+  constexpr u32 kInFlight = 4;
+  u64 c = tid;
+  for (; c + (kInFlight - 1) * stride < chunks; c += kInFlight * stride) {
+    uint4 q[kInFlight];
+#pragma unroll
+    for (u32 k = 0; k < kInFlight; ++k) q[k] = v[c + k * stride];
+#pragma unroll
+    for (u32 k = 0; k < kInFlight; ++k) add_chunk(q[k], c + k * stride);
   }
+  for (; c < chunks; c += stride) add_chunk(v[c], c);
   for (u64 i = chunks * 16 + tid; i < n; i += stride) {
     const u32 b = out[i];
     s += b;
-    w += u64((n - i) % kAdlerMod) * b;
+    w += (n - i) * b;
+    if (w >> 62) w %= kAdlerMod;
   }
-  red[0][threadIdx.x] = s;
-  red[1][threadIdx.x] = w;
-  red[2][threadIdx.x] = l;
+  s %= kAdlerMod;
+  w %= kAdlerMod;
+  for (u32 off = 32; off; off >>= 1) {
+    s += __shfl_down(s, off, 64);
+    w += __shfl_down(w, off, 64);
+  }
+  if (!lane) {
+    red[0][wave] = s;
+    red[1][wave] = w;
+  }
   __syncthreads();
-  for (u32 off = 128; off; off >>= 1) {
-    if (threadIdx.x < off)
-      for (u32 k = 0; k < 3; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + off];
-    __syncthreads();
-  }
-  if (!threadIdx.x) {
-    const u64 S = red[0][0] % kAdlerMod;
-    const u64 W = (red[1][0] % kAdlerMod + kAdlerMod - red[2][0] % kAdlerMod) % kAdlerMod;
-    if (S || W) {
-      atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_s), S);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&st->adler_w), W);
-    }
+  // One partial pair per workgroup (g_finish adds them): same-address
+  // atomics from every workgroup would serialise.
+  if (!t) {
+    parts[2 * blockIdx.x] = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) % kAdlerMod;
+    parts[2 * blockIdx.x + 1] = (red[1][0] + red[1][1] + red[1][2] + red[1][3]) % kAdlerMod;
   }
 }
 
-__global__ __launch_bounds__(1) void g_finish(State* st, u64 n, u32* meta) {
+// Final status: the Adler-32 partials of g_adler's `nparts` workgroups are
+// summed by one 256-thread workgroup and compared with the trailer.
+__global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, const u64* parts,
+                                                u32 nparts) {
+  __shared__ u64 red[2][4];
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   u32 status = st->status;
   if (!status) status = st->emit_status;
   // References still unresolved after every round.
   if (!status && st->unresolved[1]) status = kReferenceDepth;
-  if (!status) {
-    const u32 a = u32((st->adler_s + 1) % kAdlerMod);
-    const u32 b = u32((st->adler_w + n) % kAdlerMod);
+  if (!status) {  // uniform: g_adler ran and wrote every partial
+    u64 s = 0, w = 0;
+    for (u32 i = t; i < nparts; i += 256) {
+      s += parts[2 * i];
+      w += parts[2 * i + 1];
+    }
+    for (u32 off = 32; off; off >>= 1) {
+      s += __shfl_down(s, off, 64);
+      w += __shfl_down(w, off, 64);
+    }
+    if (!lane) {
+      red[0][wave] = s;
+      red[1][wave] = w;
+    }
+    __syncthreads();
+    const u32 a = u32((red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1) % kAdlerMod);
+    const u32 b = u32((red[1][0] + red[1][1] + red[1][2] + red[1][3] + n % kAdlerMod) % kAdlerMod);
     if (((b << 16) | a) != st->wanted) status = kAdlerMismatch;
   }
-  st->status = status;
-  meta[0] = status;
-  meta[1] = 0;
+  if (!t) {
+    st->status = status;
+    meta[0] = status;
+    meta[1] = 0;
+  }
 }
 
 // Zero the output unless the stream decoded (status 0) or only its checksum failed.
@@ -2422,10 +2479,13 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
               st, out, roots, bits0, bits1, counts, round, rounds, words);
     HZ_TRY(hipGetLastError());
   }
-  HZ_LAUNCH(g_adler, dim3(clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048)),
-            dim3(256), 0, stream, st, out, out_size);
+  const u32 adler_groups = clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048);
+  u64* adler_parts = nullptr;
+  HZ_TRY(scratch.alloc(&adler_parts, 2 * u64(adler_groups)));
+  HZ_LAUNCH(g_adler, dim3(adler_groups), dim3(256), 0, stream, st, out, out_size, adler_parts);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_finish, dim3(1), dim3(1), 0, stream, st, out_size, meta);
+  HZ_LAUNCH(g_finish, dim3(1), dim3(256), 0, stream, st, out_size, meta, adler_parts,
+            adler_groups);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
                      stream, st, out, out_size);
