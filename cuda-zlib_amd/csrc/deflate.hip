@@ -657,10 +657,17 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       const bool hashable = q + 4 <= end;
       const u32 v = hashable ? win_u32(win, q) : 0u;
       const u32 h = hashable ? hash4(v) : kBuckets + t;  // unique stand-in: never a bucket
+      // Nearest earlier position of the wave with the same hash (1..kNear
+      // back): the hash shifted up the wave one lane at a time (DPP
+      // wave_shr:1; lane 0 receives ~0u, which matches no hash).
       u32 near = 0;
-      for (u32 k = kNear; k >= 1; --k) {
-        const u32 hk = __shfl_up(h, k, 64);
-        if (lane >= k && hk == h) near = k;
+      {
+        u32 hk = h;
+#pragma unroll
+        for (u32 k = 1; k <= kNear; ++k) {
+          hk = u32(__builtin_amdgcn_update_dpp(-1, int(hk), 0x138, 0xf, 0xf, false));
+          if (!near && hk == h) near = k;
+        }
       }
       u32 best_len = 0, best_dist = 0;
       if (hashable) {
@@ -677,12 +684,15 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         dist[kWays] = near;
         // The first dword decides most candidates: fewer than three equal
         // bytes is no match, three is a match of 3; only four equal bytes
-        // continue the comparison.
+        // continue the comparison.  All first dwords are read at once (an
+        // absent candidate reads the position itself).
+        u32 x0[kWays + 1];
+#pragma unroll
+        for (u32 k = 0; k <= kWays; ++k) x0[k] = win_u32(win, q - dist[k]) ^ v;
 #pragma unroll
         for (u32 k = 0; k <= kWays; ++k) {
-          if (!dist[k]) continue;
-          const u32 x = win_u32(win, q - dist[k]) ^ v;
-          if (x & 0xffffffu) continue;
+          const u32 x = x0[k];
+          if (!dist[k] || (x & 0xffffffu)) continue;
           const u32 m = x ? 3u : 4u + match_len(win, q - dist[k] + 4, q + 4, maxlen - 4);
           if (m > best_len || (m == best_len && dist[k] < best_dist)) {
             best_len = m;
@@ -715,14 +725,23 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       }
       sh.exitv[t] = u16(x);
       lds_barrier();
-      if (!t) {
-        for (u32 w = 0; w < kParseWaves; ++w) sh.went[w] = 0xffffu;
-        u32 e = 0;
-        while (e < lim) {
-          sh.went[e >> 6] = u16(e);
-          e = sh.exitv[e];
+      if (wave == 0) {
+        // The chain of wave entries, by wave 0 from registers: lane l holds
+        // the exits of position l of every wave; each hop leaves its wave,
+        // so wave w is entered at most once, at iteration w.
+        u32 ex[kParseWaves];
+#pragma unroll
+        for (u32 w = 0; w < kParseWaves; ++w) ex[w] = sh.exitv[w * 64 + lane];
+        u32 e = 0, went = 0xffffu;  // e is uniform; lane w keeps wave w's entry
+#pragma unroll
+        for (u32 w = 0; w < kParseWaves; ++w) {
+          if (e < lim && (e >> 6) == w) {
+            went = lane == w ? e : went;
+            e = u32(__builtin_amdgcn_readlane(int(ex[w]), int(e & 63)));
+          }
         }
-        sh.adv = e;
+        if (lane < kParseWaves) sh.went[lane] = u16(went);
+        if (!lane) sh.adv = e;
       }
       lds_barrier();
       sh.mark[t] = t == sh.went[wave];
