@@ -1478,14 +1478,16 @@ struct HeaderShared {
   StageT<kHeaderWords> stage;
   u16 codes[320];
   u64 d0;
-  u32 status, fin, nl, nd, build_status;
+  u32 status, type, fin, nl, nd, build_status;
 };
 }  // namespace
 
 // One wave per candidate (below the table capacity): parse its dynamic
 // header, build the literal/length and distance tables in the fast format
 // into the candidate's table slot, and record the first token bit and flags
-// (hdr_info: status | BFINAL << 8 | BTYPE << 9).
+// (hdr_info: status | BFINAL << 8 | BTYPE << 9).  Bit 0 is a candidate
+// whatever its block type: a stored or fixed block there is only recorded
+// (BTYPE != 2, no tables) and g_describe parses it itself.
 __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const State* st,
                                                 const u64* cand, BlockTables* tables,
                                                 u64 table_capacity, u64* hdr_d0, u32* hdr_info) {
@@ -1501,9 +1503,9 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
       BitIn r = staged_reader(sh.stage, len, pos);
       u32 fin = 0, type = 0, err = 0, nl = 0, nd = 0;
       if (!r.take(1, fin) || !r.take(2, type)) err = kTruncated;
-      else if (type != 2) err = kBadTree;  // candidates are dynamic headers
-      else err = parse_dynamic_lengths(sh.tables, r, nl, nd);
+      else if (type == 2) err = parse_dynamic_lengths(sh.tables, r, nl, nd);
       sh.status = err;
+      sh.type = type;
       sh.fin = fin;
       sh.nl = nl;
       sh.nd = nd;
@@ -1511,7 +1513,7 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
     }
     __syncthreads();
     u32 err = sh.status;
-    if (!err) {
+    if (!err && sh.type == 2) {
       err = huff_build_wave(sh.tables.ll, sh.tables.lens, sh.nl, false, true, 15, sh.codes,
                             &sh.build_status);
       if (!err)
@@ -1533,7 +1535,7 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
     }
     if (!lane) {
       hdr_d0[c] = sh.d0;
-      hdr_info[c] = err | (sh.fin << 8) | (2u << 9);
+      hdr_info[c] = err | (sh.fin << 8) | (sh.type << 9);
     }
     __syncthreads();
   }
@@ -1563,8 +1565,9 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
     __syncthreads();
     bool first = true;
     for (;;) {
-      // The candidate's own header was parsed by g_headers (tables in slot c).
-      const bool pre = first && c < table_capacity;
+      // The candidate's own dynamic header was parsed by g_headers (tables
+      // in slot c); any other block type at bit 0 is parsed here.
+      const bool pre = first && c < table_capacity && ((hdr_info[c] >> 9) & 3u) == 2;
       if (pre) {
         if (!t) {
           const u32 info = hdr_info[c];
