@@ -920,6 +920,8 @@ __device__ u32 describe_block(BitIn& r, DecodeTables& t, u64 limit, u32& final_b
 }
 
 constexpr u32 kNoMerge = 0xffffffffu;
+constexpr u32 kDescEvents = 4;           // events a slice decode records (it stops at the last)
+constexpr u16 kNoEvent = 0xffffu;
 
 // ---- describe: one 256-thread workgroup per candidate ----------------------
 constexpr u32 kDescThreads = 256;
@@ -939,9 +941,15 @@ struct DescShared {
                                            // lanes touch consecutive banks)
   };
   u32 xpos[kDescThreads];                // stage-relative end of each slice decode
-  u32 evpos[kDescThreads], evend[kDescThreads];
   u32 count[kDescThreads];               // bytes of each slice decode
-  u16 ev[kDescThreads];                  // 0 none, 1 EOB, else 0x100 | status
+  // Events (an EOB or an undecodable token) met by each slice decode, as
+  // offsets from the slice start; the decode steps over them (past the EOB,
+  // or one bit) and stops at the kDescEvents-th.  Only an event on the true
+  // token path ends the block.
+  u8 evn[kDescThreads];                  // events recorded
+  u16 evp[kDescEvents][kDescThreads];
+  u16 evq[kDescThreads];                 // lane 0 and merged lanes: first event at or after
+                                         // the entry, or kNoEvent
   u32 merge[kDescThreads];               // offset from s_j where lane j-1's continuation met
                                          // lane j's tokens, or kNoMerge
   u32 merge2[kDescThreads];              // offset from s_j where lane j-2's continuation met
@@ -967,6 +975,10 @@ struct DescShared {
   u32 slice, need, table;
   u32 type, final_block, status, nl, nd, go, build_status, group, lanes;
 };
+// Three describe workgroups share a CU at this size; at 53 768 bytes only
+// two did (measured on MI355X: the describe pass took 27 % longer), so the
+// layout stays within 26 * 2 KiB.
+static_assert(sizeof(DescShared) <= 26 * 2048, "describe LDS no longer fits three workgroups per CU");
 
 __device__ __forceinline__ bool desc_visited(const DescShared& sh, u32 lane, u32 off) {
   return off < kVisitBits && ((sh.visit[off >> 6][lane] >> (off & 63)) & 1);
@@ -1010,18 +1022,19 @@ __device__ __forceinline__ u32 full_token(const DecodeTables& t, Win4<kChecked>&
   return err;
 }
 
-// Token-level decode from r.pos() until it reaches `stop`, an EOB or an error.
-// ev: 0 none, 1 EOB (evend = bit after it), else 0x100 | status.  Every token
-// start in [win0, stop) (stop - win0 <= kVisitBits) is recorded in `visit`,
-// and ck[w] ends as the bytes produced by the tokens starting in visit words
-// 0..w.  Both are stored on every token, which is cheaper than branching on
-// word changes.
+// Token-level decode from r.pos() until it reaches `stop`.  An event (an EOB
+// or an undecodable token) is recorded in evp (offset from win0) and stepped
+// over: past the EOB, or by one bit for an error; the decode stops at the
+// kDescEvents-th event.  Every token start in [win0, stop)
+// (stop - win0 <= kVisitBits) is recorded in `visit`, and ck[w] ends as the
+// bytes produced by the tokens starting in visit words 0..w.  Both are stored
+// on every token, which is cheaper than branching on word changes.
 template <bool kChecked>
 __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u64* visit,
-                           u32 win0, u32& count, u32& ev, u32& evpos, u32& evend, u16* ck) {
+                           u32 win0, u32& count, u32& nev, u16* evp, u16* ck) {
   u32 produced = 0, cw = 0;
   u64 bits = 0;
-  ev = 0;
+  nev = 0;
   for (u32 w = 0; w < kVisitWords; ++w) visit[w * kDescThreads] = 0;
   for (;;) {
     const u32 p = r.pos();
@@ -1035,11 +1048,15 @@ __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u
     if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
       u32 lit, distance;
       const u32 err = full_token<kChecked>(t, r, length, lit, distance);
-      if (err) { ev = 0x100u | err; evpos = p; break; }
-      if (!length) { ev = 1; evpos = p; evend = r.pos(); break; }
+      if (err || !length) {
+        evp[nev * kDescThreads] = u16(off);
+        if (++nev == kDescEvents) break;
+        if (err) r.seek(p + 1);
+        length = 0;
+      }
     }
     produced += length;  // <= 512 tokens of <= 258 bytes per slice
-    ck[w * kDescThreads] = u16(produced);  // read back for words 0..6 only: <= 224 tokens, < 2^16
+    ck[w * kDescThreads] = u16(produced);  // read back for words 0..6 only: < 2^16
   }
   count = produced;
 }
@@ -1050,10 +1067,14 @@ __device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u32 li
   Win4<kChecked> r = win4<kChecked>(sg, limit, from);
   u32 bytes = 0;
   while (r.pos() < to) {
+    const u32 p = r.pos();
     u32 length, x;
     if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
       u32 lit, distance;
-      if (full_token<kChecked>(t, r, length, lit, distance) || !length) break;
+      // Events are stepped over as desc_slice does.
+      const u32 err = full_token<kChecked>(t, r, length, lit, distance);
+      if (err) r.seek(p + 1);
+      if (err || !length) length = 0;
     }
     bytes += length;
   }
@@ -1176,17 +1197,16 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
   {  // 1. speculative slices, then 2. continuation into the next slice (and,
      // when it meets none of that slice's tokens, into the one after)
     Win4<kChecked> r = win4<kChecked>(sh.stage, blim, s0);
-    u32 cnt, ev, evpos = 0, evend = 0;
-    desc_slice<kChecked>(sh.tables, r, s0 + slice, &sh.visit[0][t], s0, cnt, ev, evpos, evend,
+    u32 cnt, nev;
+    desc_slice<kChecked>(sh.tables, r, s0 + slice, &sh.visit[0][t], s0, cnt, nev, &sh.evp[0][t],
                          &sh.ck[0][t]);
     sh.xpos[t] = r.pos();
     sh.count[t] = cnt;
-    sh.ev[t] = u16(ev);
-    sh.evpos[t] = evpos;
-    sh.evend[t] = evend;
+    sh.evn[t] = u8(nev);
     __syncthreads();
     u32 merge = kNoMerge, merge2 = kNoMerge, tail = 0;
-    if (t + 1 < kDescThreads && !ev) {
+    // A decode stopped at its last event did not reach its slice end.
+    if (t + 1 < kDescThreads && nev < kDescEvents) {
       u32 k = t + 1, sk = s0 + slice;
       for (;;) {
         const u32 off = r.pos() - sk;
@@ -1225,19 +1245,33 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
   // continuation when the next lane merged), their prefix sum, and the break
   // and event masks.
   const u32 m1 = sh.merge[t], m2 = sh.merge2[t];
-  u32 before = 0;
+  // The first event at or after the entry of lane 0 (the slice start) or of
+  // a merged lane (its merge point) lies on the true path and ends the block.
+  u32 q = kNoEvent;
+  if (t == 0 || m1 != kNoMerge) {
+    const u32 from = t == 0 ? 0u : m1;
+    const u32 n = sh.evn[t];
+    for (u32 i = n; i-- > 0;) {
+      const u32 o = sh.evp[i][t];
+      q = o >= from ? o : q;
+    }
+  }
+  sh.evq[t] = u16(q);
+  u32 before = 0, at_event = 0;
 #pragma nounroll
-  for (u32 pass = 0; pass < 2; ++pass) {  // one call site keeps register use down
-    const u32 m = pass ? m2 : m1;
+  for (u32 pass = 0; pass < 3; ++pass) {  // one call site keeps register use down
+    const u32 m = pass == 0 ? m1 : pass == 1 ? m2 : (q == kNoEvent ? kNoMerge : q);
     if (m == kNoMerge) continue;
     const u32 v = desc_bytes_before<kChecked>(sh, t, blim, s0, m);
-    if (pass) sh.merge2[t] = m2 | (v << 9);
-    else before = v;
+    if (pass == 0) before = v;
+    else if (pass == 1) sh.merge2[t] = m2 | (v << 9);
+    else at_event = v;
   }
   __syncthreads();  // the checkpoints share storage with the arrays below
   sh.before[t] = before;
   u32 bsl = sh.count[t] - before;
-  if (t + 1 < kDescThreads && sh.merge[t + 1] != kNoMerge) bsl += sh.tail[t];
+  if (q != kNoEvent) bsl = at_event - before;
+  else if (t + 1 < kDescThreads && sh.merge[t + 1] != kNoMerge) bsl += sh.tail[t];
   u32 x = bsl;
   for (u32 o = 1; o < 64; o <<= 1) {
     const u32 y = __shfl_up(x, o, 64);
@@ -1245,7 +1279,7 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
   }
   if (lane == 63) sh.wsum[wave] = x;
   const u64 bm = __ballot(t > 0 && sh.merge[t] == kNoMerge);
-  const u64 em = __ballot(sh.ev[t] != 0);
+  const u64 em = __ballot(q != kNoEvent);
   if (!lane) {
     sh.brk[wave] = bm;
     sh.evm[wave] = em;
@@ -1257,34 +1291,47 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
   sh.prefix[t] = x;
   __syncthreads();
   if (!t) {  // 4. runs and breaks
+    u32 event_at = kNoMerge;  // stage position of the true event that ends the block
     u32 lanes = kDescThreads;
     u32 e = r0;         // true position
     u64 T = run.total;  // block bytes before e
-    u32 j = 0;          // lane whose slice contains e, synced at e
+    u32 j = 0;          // run start: lane j's own decode is true from e on
     u32 j_entry = r0;   // true entry of slice j
     u64 j_off = T;      // output offset of slice j's entry
-    i64 adj = 0;        // correction of lane j's per-slice bytes for its sync point
+    u32 j_bytes = 0;    // bytes lane j's decode produced before e
     bool round_done = false, done = false;
     while (!round_done && !done) {
-      // Run from lane j: lanes j+1 .. b-1 merged, so they are synced too.
+      const u32 sj = r0 + j * slice;
       sh.entry[j] = j_entry;
       sh.off[j] = u32(j_off);
       sh.runs[j >> 6] |= 1ull << (j & 63);
-      const u64 pj = j ? sh.prefix[j - 1] : 0u;
-      sh.runbase[j] = u32(T + u64(adj) - pj);
-      const u32 b = next_bit(sh.brk, j + 1), E = next_bit(sh.evm, j);
+      // Lane j's first event at or after e is on the true path.
+      u32 qj = kNoEvent;
+      for (u32 i = sh.evn[j]; i-- > 0;) {
+        const u32 o = sh.evp[i][j];
+        qj = sj + o >= e ? o : qj;
+      }
+      if (qj != kNoEvent) {
+        T += desc_bytes_between<kChecked>(sh.tables, sh.stage, blim, sj, sj + qj) - j_bytes;
+        event_at = sj + qj;
+        lanes = j + 1;
+        done = true;
+        break;
+      }
+      // Lane j from e to its slice end, plus its continuation when lane j+1
+      // merged; merged lanes after it add their per-slice bytes.
+      const u32 bj = sh.count[j] - j_bytes +
+                     (j + 1 < kDescThreads && sh.merge[j + 1] != kNoMerge ? sh.tail[j] : 0u);
+      sh.runbase[j] = u32(T + bj - sh.prefix[j]);
+      const u32 b = next_bit(sh.brk, j + 1), E = next_bit(sh.evm, j + 1);
       if (E < b) {
-        T += u64(sh.prefix[E] - pj) + u64(adj);
-        if (sh.ev[E] == 1) run.end = sh.stage.bit0 + sh.evend[E];
-        else {
-          run.status = sh.ev[E] & 0xffu;
-          run.end = sh.stage.bit0 + sh.evpos[E];
-        }
+        T += bj + (sh.prefix[E] - sh.prefix[j]);
+        event_at = r0 + E * slice + sh.evq[E];
         lanes = E + 1;
         done = true;
         break;
       }
-      T += u64(sh.prefix[b - 1] - pj) + u64(adj);
+      T += bj + (sh.prefix[b - 1] - sh.prefix[j]);
       e = sh.xpos[b - 1];
       if (b == kDescThreads) break;
       const u32 m2 = b + 1 < kDescThreads ? sh.merge2[b + 1] : kNoMerge;
@@ -1298,7 +1345,7 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
         j = b + 1;
         j_entry = r0 + j * slice + (m2 & 511u);
         j_off = T;
-        adj = i64(sh.before[j]) - i64(m2 >> 9);
+        j_bytes = m2 >> 9;
         e = j_entry;
         continue;
       }
@@ -1332,14 +1379,21 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
           ++k;
           continue;
         }
+        // Lane k's own decode is true from e: a run starts there.
         j = k;
         j_entry = k_entry;
         j_off = k_off;
-        // The run's per-slice bytes already exclude lane k's phase-3 prefix
-        // (non-zero when an untrue continuation merged into lane k).
-        adj = i64(sh.before[k]) - i64(desc_bytes_between<kChecked>(sh.tables, sh.stage, blim, sk, e));
+        j_bytes = desc_bytes_between<kChecked>(sh.tables, sh.stage, blim, sk, e);
         break;
       }
+    }
+    if (event_at != kNoMerge) {
+      // An EOB (the block's end) or an undecodable token (its status).
+      WordBits<kChecked> r = word_bits<kChecked>(sh.stage, blim, event_at);
+      u32 lit, length, distance;
+      const u32 err = fast_token(sh.tables.ll, sh.tables.dd, r, lit, length, distance);
+      if (err) run.status = err;
+      run.end = sh.stage.bit0 + (err ? event_at : r.pos());
     }
     if (!done && T > limit) {
       run.status = kOutputOverflow;
@@ -1410,7 +1464,7 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
 // Rounds away from the body end decode without truncation checks.
 // Results: sh.status, sh.end (bit after the EOB), sh.size, and slice groups
 // (sh.group = kNone if capacity ran out; emission then decodes serially).
-__device__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& sh, State* st,
+__device__ __forceinline__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& sh, State* st,
                                 u64* slice_entry, u32* slice_off, u32* group_link,
                                 u64 group_capacity) {
   const u32 t = threadIdx.x;
