@@ -303,6 +303,7 @@ __device__ __forceinline__ bool stored_seed(const u8* body, u64 len, u64 byte) {
 // reads end 3 + 14 + 57 bits after a position of the range's last byte.
 constexpr u32 kPreMargin = 24;
 constexpr u32 kPreStageWords = (kDiscRange + kPreMargin + 32) / 4;
+constexpr u32 kSurvivorCap = 1024;  // prefilter survivors a wave checks per pass
 using PreStage = StageT<kPreStageWords>;
 // Pre-candidate entries: bit offset, plus this flag once the header is known valid.
 constexpr u64 kValidBit = 1ull << 62;
@@ -365,20 +366,26 @@ __device__ u64 validate_mask(const u8* body, u64 len, u64 b0, u64 pre, u8* lut, 
 }
 
 __device__ __forceinline__ u32 block_exclusive_scan(u32 v, u32* sh, u32& total) {
-  // 256-thread exclusive scan through LDS.
-  const u32 t = threadIdx.x;
-  sh[t] = v;
-  __syncthreads();
-  for (u32 off = 1; off < kDiscThreads; off <<= 1) {
-    const u32 x = t >= off ? sh[t - off] : 0u;
-    __syncthreads();
-    sh[t] += x;
-    __syncthreads();
+  // 256-thread exclusive scan: wave shuffles, then the four wave totals.
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  u32 incl = v;
+#pragma unroll
+  for (u32 off = 1; off < 64; off <<= 1) {
+    const u32 y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
   }
-  total = sh[kDiscThreads - 1];
-  const u32 excl = sh[t] - v;
+  if (lane == 63) sh[wave] = incl;
   __syncthreads();
-  return excl;
+  u32 before = 0;
+  total = 0;
+#pragma unroll
+  for (u32 w = 0; w < kDiscThreads / 64; ++w) {
+    const u32 c = sh[w];
+    before += w < wave ? c : 0u;
+    total += c;
+  }
+  __syncthreads();  // sh is reused by the next scan
+  return before + incl - v;
 }
 
 // Exclusive scan of `count` u32 values (each masked by `mask`) into u64
@@ -466,46 +473,129 @@ __global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* s
 // validated later one per lane).  A range with more than kDiscCap of them
 // validates them itself and keeps the valid ones (kind 1), or, when even those
 // overflow, leaves them to the gather pass (kind 2).  Also counts
-// stored-endpoint seeds.
+// stored-endpoint seeds.  Workgroups take ranges grid-stride.
 __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State* st,
-                                                  u32* wg_count, u64* wg_list) {
-  __shared__ u8 luts[128][kDiscThreads];
+                                                  u32* wg_count, u64* wg_list, u64 groups) {
+  // The prefilter's lists are dead once its result is read, before any
+  // validation uses the tables.
+  __shared__ union {
+    u8 luts[128][kDiscThreads];
+    struct {
+      u16 surv[kDiscThreads / 64][kSurvivorCap];  // per wave: offsets left to check
+      u32 pass[kDiscRange * 8 / 32];              // prefilter result, one bit per offset
+    };
+  } lds;
   __shared__ u32 scan[kDiscThreads];
   __shared__ u16 kraft3[512];
   __shared__ PreStage sg;
+  auto& luts = lds.luts;
+  auto& surv = lds.surv;
+  auto& pass = lds.pass;
   if (st->status) return;
-  const u64 wg = blockIdx.x;
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   build_kraft3(kraft3);
-  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
-  __syncthreads();
-  const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = prefilter_mask(len, b0, sg, kraft3);
-  u64 flag = 0;
-  if (b0 == 0) {
-    mask |= 1;  // bit 0 is always a candidate
-    flag = 1;
-  }
   u32 seeds = 0;
-  for (u32 j = 0; j < kDiscBytesPerThread; ++j)
-    if (b0 + j < len && stored_seed(body, len, b0 + j)) ++seeds;
-  if (seeds) atomicAdd(reinterpret_cast<unsigned long long*>(&st->seeds), seeds);
-  u32 total;
-  u32 base = block_exclusive_scan(__popcll(mask), scan, total);
-  u32 kind = 0;
-  if (total > kDiscCap) {
-    mask = validate_mask(body, len, b0, mask & ~flag, &luts[0][threadIdx.x], kDiscThreads) | flag;
-    flag = mask;
-    base = block_exclusive_scan(__popcll(mask), scan, total);
-    kind = total > kDiscCap ? 2u : 1u;
-  }
-  if (!threadIdx.x) wg_count[wg] = total | (kind << kKindShift);
-  if (kind < 2) {
-    while (mask) {
-      const u32 k = __builtin_ctzll(mask);
-      mask &= mask - 1;
-      wg_list[wg * kDiscCap + base++] = (b0 * 8 + k) | ((flag >> k) & 1 ? kValidBit : 0);
+  for (u64 wg = blockIdx.x; wg < groups; wg += gridDim.x) {
+    stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
+    for (u32 i = t; i < kDiscRange * 8 / 32; i += kDiscThreads) pass[i] = 0;
+    __syncthreads();
+    // Words past the staged ones read as zero, as body bits past the end do.
+    for (u32 i = sg.count + t; i < kPreStageWords; i += kDiscThreads) sg.words[i] = 0;
+    __syncthreads();
+    const u64 b0 = wg * kDiscRange + u64(t) * kDiscBytesPerThread;
+    // The range starts at stage byte `a` (the stage begins at the aligned word
+    // holding it); this thread's 64 offsets start at stage word 2t.
+    const u32 a = u32((reinterpret_cast<uintptr_t>(body) + wg * kDiscRange) & 3);
+    const u32 x0 = sg.words[2 * t], x1 = sg.words[2 * t + 1], x2 = sg.words[2 * t + 2],
+              x3 = sg.words[2 * t + 3], x4 = sg.words[2 * t + 4];
+    const u64 w0 = u64(__builtin_amdgcn_alignbyte(x1, x0, a)) |
+                   (u64(__builtin_amdgcn_alignbyte(x2, x1, a)) << 32);
+    const u64 w1 = u64(__builtin_amdgcn_alignbyte(x3, x2, a)) |
+                   (u64(__builtin_amdgcn_alignbyte(x4, x3, a)) << 32);
+    u64 m = 0;
+    if (b0 < len) {
+      // Bit k of s_j is stream bit (8*b0 + k + j): BTYPE == 2 and HLIT <= 29.
+      const u64 s1 = funnel(w0, w1, 1), s2 = funnel(w0, w1, 2);
+      const u64 s4 = funnel(w0, w1, 4), s5 = funnel(w0, w1, 5);
+      const u64 s6 = funnel(w0, w1, 6), s7 = funnel(w0, w1, 7);
+      m = ~s1 & s2 & ~(s4 & s5 & s6 & s7);
+      const u64 bits_left = (len - b0) * 8;
+      if (bits_left < 64) m &= (1ull << bits_left) - 1;
+      if (!b0) m &= ~1ull;
     }
+    // Stored-endpoint seeds: LEN/NLEN complement in the staged bytes first.
+  #pragma unroll
+    for (u32 j = 0; j < kDiscBytesPerThread; ++j) {
+      const u32 x = u32(funnel(w0, w1, 8 * j));
+      if (((x ^ (x >> 16)) & 0xffffu) == 0xffffu && b0 + j < len && stored_seed(body, len, b0 + j))
+        ++seeds;
+    }
+    // Complete code-length code (Kraft sum of the HCLEN lengths == 128) for
+    // the survivors, compacted per wave so that every lane checks one.
+    const u32 wave_bit0 = wave * 64 * 64;  // first offset of the wave's span (range-relative)
+    for (;;) {
+      const u32 cnt = __popcll(m);
+      u32 incl = cnt;
+  #pragma unroll
+      for (u32 off = 1; off < 64; off <<= 1) {
+        const u32 y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      const u32 total = __shfl(incl, 63, 64), excl = incl - cnt;
+      if (!total) break;
+      const u32 take = excl >= kSurvivorCap ? 0u : min(cnt, kSurvivorCap - excl);
+      for (u32 k = 0; k < take; ++k) {
+        const u32 bit = __builtin_ctzll(m);
+        m &= m - 1;
+        surv[wave][excl + k] = u16(lane * 64 + bit);
+      }
+      wave_sync();
+      const u32 n = min(total, kSurvivorCap);
+      for (u32 i = lane; i < n; i += 64) {
+        const u32 o = wave_bit0 + surv[wave][i];
+        const u32 P = 8 * a + o, wi = P >> 5, sh = P & 31;
+        const u32 y0 = sg.words[wi], y1 = sg.words[wi + 1], y2 = sg.words[wi + 2],
+                  y3 = sg.words[wi + 3];
+        const u32 A = __builtin_amdgcn_alignbit(y1, y0, sh);
+        const u32 B = __builtin_amdgcn_alignbit(y2, y1, sh);
+        const u32 C = __builtin_amdgcn_alignbit(y3, y2, sh);
+        const u32 nc = ((A >> 13) & 15u) + 4;
+        const u64 lens =
+            (u64(A >> 17) | (u64(B) << 15) | (u64(C) << 47)) & ((1ull << (3 * nc)) - 1);
+        u32 kraft = 0;
+  #pragma unroll
+        for (u32 j = 0; j < 7; ++j) kraft += kraft3[(lens >> (9 * j)) & 511];
+        if (kraft == 128) atomicOr(&pass[o >> 5], 1u << (o & 31));
+      }
+      wave_sync();  // the list is refilled next
+    }
+    __syncthreads();
+    u64 mask = u64(pass[2 * t]) | (u64(pass[2 * t + 1]) << 32);
+    u64 flag = 0;
+    if (b0 == 0) {
+      mask |= 1;  // bit 0 is always a candidate
+      flag = 1;
+    }
+    u32 total;
+    u32 base = block_exclusive_scan(__popcll(mask), scan, total);
+    u32 kind = 0;
+    if (total > kDiscCap) {
+      mask = validate_mask(body, len, b0, mask & ~flag, &luts[0][threadIdx.x], kDiscThreads) | flag;
+      flag = mask;
+      base = block_exclusive_scan(__popcll(mask), scan, total);
+      kind = total > kDiscCap ? 2u : 1u;
+    }
+    if (!threadIdx.x) wg_count[wg] = total | (kind << kKindShift);
+    if (kind < 2) {
+      while (mask) {
+        const u32 k = __builtin_ctzll(mask);
+        mask &= mask - 1;
+        wg_list[wg * kDiscCap + base++] = (b0 * 8 + k) | ((flag >> k) & 1 ? kValidBit : 0);
+      }
+    }
+    __syncthreads();  // the next range reuses the stage and the lists
   }
+  if (seeds) atomicAdd(reinterpret_cast<unsigned long long*>(&st->seeds), seeds);
 }
 
 // Discovery pass 2: one workgroup scans the per-range counts into offsets of
@@ -1464,9 +1554,10 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
 // Rounds away from the body end decode without truncation checks.
 // Results: sh.status, sh.end (bit after the EOB), sh.size, and slice groups
 // (sh.group = kNone if capacity ran out; emission then decodes serially).
-__device__ __forceinline__ void describe_tokens(const u8* body, u64 len, u64 limit, DescShared& sh, State* st,
-                                u64* slice_entry, u32* slice_off, u32* group_link,
-                                u64 group_capacity) {
+__device__ __forceinline__ void describe_tokens(const u8* body, u64 len, u64 limit,
+                                                DescShared& sh, State* st, u64* slice_entry,
+                                                u32* slice_off, u32* group_link,
+                                                u64 group_capacity) {
   const u32 t = threadIdx.x;
   DescRun run;
   run.e_abs = sh.d0;
@@ -2435,8 +2526,8 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&block_offset, pre_blocks));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
-  HZ_LAUNCH(g_discover, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
-            wg_count, wg_list);
+  HZ_LAUNCH(g_discover, dim3(clamp_grid(groups, 4096)), dim3(kDiscThreads), 0, stream, body,
+            len, st, wg_count, wg_list, groups);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset, groups,
             pre_capacity);
