@@ -2355,31 +2355,45 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
   const u32* bits = round & 1 ? bits1 : bits0;
   u32* next_bits = round & 1 ? bits0 : bits1;
   u64* next_count = round + 1 == max_rounds ? &st->unresolved[1] : &counts[round + 1];
-  const u64 stride = u64(gridDim.x) * blockDim.x;
+  const u32 lane = lane_id();
+  const u64 waves = u64(gridDim.x) * (blockDim.x / 64);
   u32 kept = 0;
-  for (u64 w = u64(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
-    u32 m = bits[w], keep = 0;
-    while (m) {
-      const u32 b = u32(__builtin_ctz(m));
-      m &= m - 1;
-      const u32 u = u32(w * 32 + b);
-      u32 r = roots[u];
-      bool r_unres = (bits[r >> 5] >> (r & 31)) & 1u;
-      for (u32 k = 0; r_unres && k < kResolveLinks; ++k) {
-        r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        r_unres = (bits[r >> 5] >> (r & 31)) & 1u;
+  // A wave reads 64 bitmap words, then takes the non-empty ones two at a
+  // time: lane l follows the root chain of bit (l & 31) of the first (l < 32)
+  // or second word, so 64 chains advance together.
+  for (u64 g = u64(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6); g * 64 < words;
+       g += waves) {
+    const u64 w = g * 64 + lane;
+    const u32 m = w < words ? bits[w] : 0u;
+    if (!m && w < words) next_bits[w] = 0;
+    u64 nz = __ballot(m != 0);
+    while (nz) {
+      const u32 i0 = u32(__builtin_ctzll(nz));
+      nz &= nz - 1;
+      const u32 i1 = nz ? u32(__builtin_ctzll(nz)) : 64u;
+      if (nz) nz &= nz - 1;
+      const u32 idx = lane < 32 ? i0 : i1;
+      const u32 mw = __shfl(m, int(idx & 63), 64);
+      const u32 b = lane & 31;
+      const bool mine = idx < 64 && ((mw >> b) & 1u);
+      bool unres = false;
+      if (mine) {
+        const u32 u = u32((g * 64 + idx) * 32 + b);
+        u32 r = roots[u];
+        unres = (bits[r >> 5] >> (r & 31)) & 1u;
+        for (u32 k = 0; unres && k < kResolveLinks; ++k) {
+          r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          unres = (bits[r >> 5] >> (r & 31)) & 1u;
+        }
+        if (!unres) out[u] = out[r];
+        else __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      if (!r_unres) {
-        out[u] = out[r];
-      } else {
-        __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        keep |= 1u << b;
-      }
+      const u64 keep = __ballot(unres);
+      if (lane == 0) next_bits[g * 64 + i0] = u32(keep);
+      if (lane == 32 && i1 < 64) next_bits[g * 64 + i1] = u32(keep >> 32);
+      kept += lane == 0 ? u32(__popcll(keep)) : 0u;
     }
-    next_bits[w] = keep;
-    kept += __builtin_popcount(keep);
   }
-  for (u32 off = 32; off; off >>= 1) kept += __shfl_xor(kept, off, 64);
   if (lane_id() == 0 && kept) atomicAdd(reinterpret_cast<unsigned long long*>(next_count), u64(kept));
 }
 
