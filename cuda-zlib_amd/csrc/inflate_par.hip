@@ -1625,6 +1625,75 @@ struct HeaderShared {
   u64 d0;
   u32 status, type, fin, nl, nd, build_status;
 };
+
+// The code lengths of a dynamic header (g_headers, lane 0), reader after
+// BTYPE: the fields and the code-length code through `r`, then the lengths
+// with a 32-bit window over the staged words (the code-length code is
+// complete, so every 7-bit pattern is a code).  Returns false, with nothing
+// decided, when a read could pass the staged words or the body end; the
+// caller then runs parse_dynamic_lengths from the same start, so the status
+// and its order are those of parse_dynamic_lengths either way.
+__device__ bool header_lengths_fast(HeaderShared& sh, u64 len, BitIn& r, u32& nl, u32& nd,
+                                    u32& err) {
+  u32 hlit, hdist, hclen;
+  if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return false;
+  nl = hlit + 257;
+  nd = hdist + 1;
+  const u32 nc = hclen + 4;
+  if (nl > 286) { err = kBadTree; return true; }
+  if (u64(3 * nc) > r.avail()) return false;
+  u64 pack = 0;
+  for (u32 i = 0; i < nc; ++i) {
+    u32 v;
+    r.take(3, v);
+    pack |= u64(v) << (3 * cl_order(i));
+  }
+  err = build_cl_table(sh.tables.cl, pack);
+  if (err) return true;
+  const u64 bit0 = sh.stage.bit0;
+  u32 p = u32(r.pos - bit0);  // stage-relative
+  // A symbol and its extra bits take at most 14 bits, read from words w, w+1.
+  const u64 staged = sh.stage.count > 1 ? u64(sh.stage.count - 1) * 32 : 0;
+  const u64 body_end = len * 8 - bit0;
+  const u32 lim = u32(min(staged, body_end));
+  const u32 total = nl + nd;
+  u32 i = 0, prev = 0;
+  u8* lens = sh.tables.lens;
+  while (i < total) {
+    if (p + 14 > lim) return false;
+    const u32 w = p >> 5;
+    const u32 b = __builtin_amdgcn_alignbit(sh.stage.words[w + 1], sh.stage.words[w], p & 31);
+    const u32 e = sh.tables.cl.primary[b & 127];
+    const u32 l = e & 15u, sym = e >> 16;
+    if (sym < 16) {
+      lens[i++] = u8(sym);
+      prev = sym;
+      p += l;
+      continue;
+    }
+    u32 repeat, value;
+    if (sym == 16) {
+      if (!i) { err = kBadRepeat; return true; }
+      repeat = 3 + ((b >> l) & 3u);
+      value = prev;
+      p += l + 2;
+    } else if (sym == 17) {
+      repeat = 3 + ((b >> l) & 7u);
+      value = 0;
+      p += l + 3;
+    } else {
+      repeat = 11 + ((b >> l) & 127u);
+      value = 0;
+      p += l + 7;
+    }
+    if (repeat > total - i) { err = kBadRepeat; return true; }
+    for (u32 j = 0; j < repeat; ++j) lens[i++] = u8(value);
+    prev = value;
+  }
+  err = lens[256] ? kOk : kBadTree;
+  r.seek(bit0 + p);
+  return true;
+}
 }  // namespace
 
 // One wave per candidate (below the table capacity): parse its dynamic
@@ -1648,7 +1717,13 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
       BitIn r = staged_reader(sh.stage, len, pos);
       u32 fin = 0, type = 0, err = 0, nl = 0, nd = 0;
       if (!r.take(1, fin) || !r.take(2, type)) err = kTruncated;
-      else if (type == 2) err = parse_dynamic_lengths(sh.tables, r, nl, nd);
+      else if (type == 2) {
+        const u64 start = r.pos;
+        if (!header_lengths_fast(sh, len, r, nl, nd, err)) {
+          r.seek(start);
+          err = parse_dynamic_lengths(sh.tables, r, nl, nd);
+        }
+      }
       sh.status = err;
       sh.type = type;
       sh.fin = fin;
