@@ -193,6 +193,27 @@ __device__ __forceinline__ u64 funnel(u64 lo, u64 hi, u32 k) {
   return k ? (lo >> k) | (hi << (64 - k)) : lo;
 }
 
+// Copy of the literal/length and distance tables, as words, by threads
+// first, first + kStep, ...: every load of a thread is issued before its
+// stores, so the copy waits for memory once.
+template <u32 kStep>
+__device__ __forceinline__ void copy_tables(u32* dll, u32* ddd, const u32* sll, const u32* sdd,
+                                            u32 first) {
+  constexpr u32 kL = sizeof(HuffTable<288, 10>) / 4, kD = sizeof(HuffTable<32, 8>) / 4;
+  constexpr u32 kRl = (kL + kStep - 1) / kStep, kRd = (kD + kStep - 1) / kStep;
+  u32 vl[kRl], vd[kRd];
+#pragma unroll
+  for (u32 k = 0; k < kRl; ++k) vl[k] = first + k * kStep < kL ? sll[first + k * kStep] : 0u;
+#pragma unroll
+  for (u32 k = 0; k < kRd; ++k) vd[k] = first + k * kStep < kD ? sdd[first + k * kStep] : 0u;
+#pragma unroll
+  for (u32 k = 0; k < kRl; ++k)
+    if (first + k * kStep < kL) dll[first + k * kStep] = vl[k];
+#pragma unroll
+  for (u32 k = 0; k < kRd; ++k)
+    if (first + k * kStep < kD) ddd[first + k * kStep] = vd[k];
+}
+
 // Exact validity of a dynamic header whose BTYPE bits were already checked:
 // the same outcome as building all three tables (huff_build rules), computed
 // with Kraft sums instead of tables.  `lut` is a thread's 128-entry LDS table
@@ -1749,8 +1770,7 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
         const u32* src_dd = reinterpret_cast<const u32*>(&sh.tables.dd);
         u32* dst_ll = reinterpret_cast<u32*>(&tables[c].ll);
         u32* dst_dd = reinterpret_cast<u32*>(&tables[c].dd);
-        for (u32 i = lane; i < sizeof(HuffTable<288, 10>) / 4; i += 64) dst_ll[i] = src_ll[i];
-        for (u32 i = lane; i < sizeof(HuffTable<32, 8>) / 4; i += 64) dst_dd[i] = src_dd[i];
+        copy_tables<64>(dst_ll, dst_dd, src_ll, src_dd, lane);
       }
     }
     if (!lane) {
@@ -1800,8 +1820,7 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
         const u32* src_dd = reinterpret_cast<const u32*>(&tables[c].dd);
         u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
         u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
-        for (u32 i = t; i < sizeof(HuffTable<288, 10>) / 4; i += kDescThreads) dst_ll[i] = src_ll[i];
-        for (u32 i = t; i < sizeof(HuffTable<32, 8>) / 4; i += kDescThreads) dst_dd[i] = src_dd[i];
+        copy_tables<kDescThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
         __syncthreads();
       } else {
         block_header<true, true>(body, len, out_size, sh);
@@ -1825,8 +1844,7 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
         const u32* src_dd = reinterpret_cast<const u32*>(&sh.tables.dd);
         u32* dst_ll = reinterpret_cast<u32*>(&tables[sh.table].ll);
         u32* dst_dd = reinterpret_cast<u32*>(&tables[sh.table].dd);
-        for (u32 i = t; i < sizeof(HuffTable<288, 10>) / 4; i += kDescThreads) dst_ll[i] = src_ll[i];
-        for (u32 i = t; i < sizeof(HuffTable<32, 8>) / 4; i += kDescThreads) dst_dd[i] = src_dd[i];
+        copy_tables<kDescThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
       }
       if (sh.type && !sh.status)
         describe_tokens(body, len, out_size, sh, st, slice_entry, slice_off, group_link,
@@ -2346,8 +2364,7 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
           const u32* src_dd = reinterpret_cast<const u32*>(&tables[rec.table].dd);
           u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
           u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
-          for (u32 i = t; i < sizeof(HuffTable<288, 10>) / 4; i += kEmitThreads) dst_ll[i] = src_ll[i];
-          for (u32 i = t; i < sizeof(HuffTable<32, 8>) / 4; i += kEmitThreads) dst_dd[i] = src_dd[i];
+          copy_tables<kEmitThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
           __syncthreads();
         } else {
           block_header<true, true>(body, len, ~0ull, sh);
