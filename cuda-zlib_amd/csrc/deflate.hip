@@ -1084,7 +1084,26 @@ __global__ __launch_bounds__(256) void e_pack(const ChunkDesc* descs, const File
     u8* dst = out + f.out_off + 2 + rel;
     const u8* src = slots + d.slot;
     const u32 n = results[c].extent;
-    for (u32 i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+    // Bytes up to the first 16-byte boundary of dst, then 16-byte stores of
+    // source dwords realigned with v_alignbyte (a slot is 16-byte aligned and
+    // has at least 16 bytes past any extent, so the fifth dword is in it),
+    // then the tail bytes.
+    const u32 head = min(n, u32((16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15));
+    const u32 blocks = (n - head) / 16;
+    for (u32 i = threadIdx.x; i < head; i += blockDim.x) dst[i] = src[i];
+    const u32* s32 = reinterpret_cast<const u32*>(src);
+    const u32 sh = head & 3;
+    for (u32 j = threadIdx.x; j < blocks; j += blockDim.x) {
+      const u32 w = (head + 16 * j) >> 2;
+      const u32 x0 = s32[w], x1 = s32[w + 1], x2 = s32[w + 2], x3 = s32[w + 3], x4 = s32[w + 4];
+      uint4 o;
+      o.x = __builtin_amdgcn_alignbyte(x1, x0, sh);
+      o.y = __builtin_amdgcn_alignbyte(x2, x1, sh);
+      o.z = __builtin_amdgcn_alignbyte(x3, x2, sh);
+      o.w = __builtin_amdgcn_alignbyte(x4, x3, sh);
+      *reinterpret_cast<uint4*>(dst + head + 16 * j) = o;
+    }
+    for (u32 i = head + 16 * blocks + threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
   }
 }
 
