@@ -2267,6 +2267,81 @@ struct LaneEmitShared {
   u32 type, final_block, status, nl, nd, build_status;
 };
 
+// Sets bits [start, start + n) of a bitmap: atomic OR on the two end words
+// (shared with neighbouring ranges), plain stores on the words between.
+__device__ __forceinline__ void bits_set_range(u32* bits, u64 start, u32 n) {
+  if (!n) return;
+  const u64 end = start + n;
+  const u64 w0 = start >> 5, w1 = (end - 1) >> 5;
+  const u32 lo = ~0u << (start & 31), hi = ~0u >> (31 - ((end - 1) & 31));
+  if (w0 == w1) {
+    atomicOr(bits + w0, lo & hi);
+    return;
+  }
+  atomicOr(bits + w0, lo);
+  for (u64 w = w0 + 1; w < w1; ++w) bits[w] = ~0u;
+  atomicOr(bits + w1, hi);
+}
+
+// out[dst + j] = out[src0 + j] for j < length where src0 + distance = dst:
+// an overlapping copy repeats the first `distance` bytes, so every byte is
+// read from [src0, dst), never from this copy's own stores.
+__device__ __forceinline__ void copy_periodic(u8* out, u64 dst, u64 src0, u32 distance,
+                                              u32 length) {
+  if (distance >= 8) {
+    u32 k = 0;  // source index of byte j, j mod distance
+    for (u32 j = 0; j < length; j += 8) {
+      u8 v[8];
+#pragma unroll
+      for (u32 i = 0; i < 8; ++i) {
+        const u32 kk = k + i >= distance ? k + i - distance : k + i;
+        v[i] = j + i < length ? out[src0 + kk] : u8(0);
+      }
+#pragma unroll
+      for (u32 i = 0; i < 8; ++i)
+        if (j + i < length) out[dst + j + i] = v[i];
+      k = k + 8 >= distance ? k + 8 - distance : k + 8;
+    }
+  } else {
+    u64 pattern = 0;
+    for (u32 i = 0; i < distance; ++i) pattern |= u64(out[src0 + i]) << (8 * i);
+    u32 k = 0;
+    for (u32 j = 0; j < length; ++j) {
+      out[dst + j] = u8(pattern >> (8 * k));
+      k = k + 1 == distance ? 0u : k + 1;
+    }
+  }
+}
+
+// dst[0, n) = src[0, n) by threads first, first + step, ...: bytes up to
+// dst's first 16-byte boundary, then 16-byte stores of source dwords
+// realigned with v_alignbyte, then the tail bytes.  Source dwords are read
+// only while they lie before src_end.
+__device__ __forceinline__ void copy_bytes(u8* dst, const u8* src, u64 n, const u8* src_end,
+                                           u32 first, u32 step) {
+  const u64 head = min<u64>(n, (16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15);
+  for (u64 i = first; i < head; i += step) dst[i] = src[i];
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src + head);
+  const u32* s32 = reinterpret_cast<const u32*>(s0 & ~uintptr_t(3));
+  const u32 sh = u32(s0 & 3);
+  // Block j reads dwords j*4 .. j*4 + 4 of s32: all of them before src_end.
+  const u64 avail_words = (reinterpret_cast<uintptr_t>(src_end) - (s0 & ~uintptr_t(3))) / 4;
+  u64 blocks = (n - head) / 16;
+  if (avail_words < 5) blocks = 0;
+  else blocks = min<u64>(blocks, (avail_words - 5) / 4 + 1);
+  for (u64 j = first; j < blocks; j += step) {
+    const u32* q = s32 + 4 * j;
+    const u32 x0 = q[0], x1 = q[1], x2 = q[2], x3 = q[3], x4 = q[4];
+    uint4 o;
+    o.x = __builtin_amdgcn_alignbyte(x1, x0, sh);
+    o.y = __builtin_amdgcn_alignbyte(x2, x1, sh);
+    o.z = __builtin_amdgcn_alignbyte(x3, x2, sh);
+    o.w = __builtin_amdgcn_alignbyte(x4, x3, sh);
+    *reinterpret_cast<uint4*>(dst + head + 16 * j) = o;
+  }
+  for (u64 i = head + 16 * blocks + first; i < n; i += step) dst[i] = src[i];
+}
+
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
 // [.., block_end); adds the slice's unresolved bytes to `unres_total`.
 // Returns 0 or an error.
@@ -2300,18 +2375,42 @@ __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64
     }
     const u32 distance = x;
     if (distance > window || distance > dst) { err = kBadDistance; break; }
-    for (u32 j = 0; j < length; ++j) {
-      const u64 d = dst + j, src = d - distance;
-      if (src < dst0) {
-        roots[d] = u32(src);
-        bit_set(unres, d);
-        ++nunres;
-      } else if (nunres && bit_get(unres, src)) {
-        roots[d] = roots[src];
-        bit_set(unres, d);
-        ++nunres;
+    const u64 src0 = dst - distance;
+    if (src0 + length <= dst0) {
+      // Every source precedes the slice: unresolved, rooted at the source.
+      for (u32 j = 0; j < length; ++j) roots[dst + j] = u32(src0 + j);
+      bits_set_range(unres, dst, length);
+      nunres += length;
+    } else if (!nunres && src0 >= dst0) {
+      // Every source is this slice's own resolved output.
+      copy_periodic(out, dst, src0, distance, length);
+    } else if (distance == 1) {
+      // A run of the byte before: resolved, or one root for the whole run.
+      const u64 p = dst - 1;
+      const bool before = p < dst0;
+      if (before || (nunres && bit_get(unres, p))) {
+        const u32 root = before ? u32(p) : roots[p];
+        for (u32 j = 0; j < length; ++j) roots[dst + j] = root;
+        bits_set_range(unres, dst, length);
+        nunres += length;
       } else {
-        out[d] = out[src];
+        const u8 v = out[p];
+        for (u32 j = 0; j < length; ++j) out[dst + j] = v;
+      }
+    } else {
+      for (u32 j = 0; j < length; ++j) {
+        const u64 d = dst + j, src = d - distance;
+        if (src < dst0) {
+          roots[d] = u32(src);
+          bit_set(unres, d);
+          ++nunres;
+        } else if (nunres && bit_get(unres, src)) {
+          roots[d] = roots[src];
+          bit_set(unres, d);
+          ++nunres;
+        } else {
+          out[d] = out[src];
+        }
       }
     }
     dst += length;
@@ -2356,8 +2455,7 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
       __syncthreads();
       const BlockRec rec = sh.rec;
       if (rec.type == 0) {
-        const u64 src = rec.data >> 3;
-        for (u64 j = t; j < rec.size; j += kEmitThreads) out[block_out + j] = body[src + j];
+        copy_bytes(out + block_out, body + (rec.data >> 3), rec.size, body + len, t, kEmitThreads);
       } else {
         if (rec.table != kNone) {
           const u32* src_ll = reinterpret_cast<const u32*>(&tables[rec.table].ll);
