@@ -109,6 +109,8 @@ class DeviceScope {
 };
 
 constexpr u64 kArenaGranule = 64ull << 20;
+// Batch files of at least this many output bytes decode by parallel slices.
+constexpr u64 kBatchWideBytes = 1024;
 
 // Stream-ordered scratch for one call, carved from an arena of the device
 // (taken on the first allocation).  Requests the arena cannot hold come from
@@ -356,8 +358,32 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
     err = hipMemcpyAsync(device_files, layout.data(), files * sizeof(BatchFile),
                          hipMemcpyHostToDevice, stream);
     if (err != hipSuccess) return err;
-    return launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
-                                metadata, encoded_rows ? encoded_metadata : nullptr);
+    const u32* encoded = encoded_rows ? encoded_metadata : nullptr;
+    // Files of at least kBatchWideBytes go to the parallel route; the rest,
+    // and any large file it hands back, to the serial one.
+    std::vector<u32> large;
+    u64 large_bits = 0;
+    for (u64 f = 0; f < files; ++f)
+      if (layout[f].out_size >= kBatchWideBytes) {
+        large.push_back(u32(f));
+        large_bits += layout[f].in_size * 8;
+      }
+    err = launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
+                               metadata, encoded, kBatchWideBytes);
+    if (err != hipSuccess || large.empty()) return err;
+    u32 *device_large = nullptr, *redo = nullptr;
+    err = ws.alloc(&device_large, large.size());
+    if (err == hipSuccess) err = ws.alloc(&redo, files);
+    if (err != hipSuccess) return err;
+    err = hipMemcpyAsync(device_large, large.data(), large.size() * sizeof(u32),
+                         hipMemcpyHostToDevice, stream);
+    if (err != hipSuccess) return err;
+    err = run_inflate_batch_wide(stream, ws, input, output, output_size, device_files,
+                                 device_large, u32(large.size()), large_bits, encoded, kMaxBlocks,
+                                 redo, metadata);
+    if (err != hipSuccess) return err;
+    return launch_inflate_batch(stream, input, output, device_files, u32(large.size()), kMaxBlocks,
+                                metadata, encoded, ~0ull, device_large, redo);
   });
 }
 

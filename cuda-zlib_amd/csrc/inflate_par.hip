@@ -2343,12 +2343,13 @@ __device__ __forceinline__ void copy_bytes(u8* dst, const u8* src, u64 n, const 
 }
 
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
-// [.., block_end); adds the slice's unresolved bytes to `unres_total`.
-// Returns 0 or an error.
-template <bool kChecked>
-__device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64 dst0,
-                          u64 block_end, u32 window, u8* out, u32* roots, u32* unres,
-                          u64& unres_total) {
+// [.., block_end) of a stream whose output starts at out[floor]; adds the
+// slice's unresolved bytes to `unres_total`.  Returns 0 or an error.  `sh`
+// holds the block's tables and the staged bits.
+template <bool kChecked, class Shared>
+__device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u64 block_end,
+                          u32 window, u8* out, u32* roots, u32* unres, u64& unres_total,
+                          u64 floor = 0) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
   r.limit = blim;
@@ -2374,7 +2375,7 @@ __device__ u32 emit_slice(LaneEmitShared& sh, u32 blim, u32 entry, u32 stop, u64
       continue;
     }
     const u32 distance = x;
-    if (distance > window || distance > dst) { err = kBadDistance; break; }
+    if (distance > window || distance > dst - floor) { err = kBadDistance; break; }
     const u64 src0 = dst - distance;
     if (src0 + length <= dst0) {
       // Every source precedes the slice: unresolved, rooted at the source.
@@ -2521,6 +2522,184 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   for (u32 off = 32; off; off >>= 1) unres_total += __shfl_down(unres_total, off, 64);
   if (lane_id() == 0 && unres_total)
     atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), unres_total);
+}
+
+// Large files of a batch: one 256-thread workgroup per file decodes its
+// blocks in turn: a stored block by a copy, a fixed or dynamic block by
+// describe's parallel slices and then one slice per thread, as g_emit_lanes
+// does.  Copies that reach before their slice are left to g_resolve over the
+// batch output.  A file whose decode meets anything unusual (any status, an
+// exhausted slice-group pool, a bad encoded row) is flagged in `redo` for
+// the serial per-file decoder, which restates the reference's statuses.
+__global__ __launch_bounds__(kDescThreads) void g_batch_wide(
+    const u8* in, u8* out, const BatchFile* files, const u32* list, u32 n, const u32* encoded,
+    u32 max_blocks, State* st, u64* slice_entry, u32* slice_off, u32* group_link,
+    u64 group_capacity, u32* roots, u32* unres, u32* redo, u32* wanted) {
+  __shared__ DescShared sh;
+  __shared__ u64 e_first, e_chunk_end;
+  __shared__ u32 e_count, e_next, e_need, bad, window;
+  const u32 t = threadIdx.x;
+  u64 unres_total = 0;
+  for (u32 i = blockIdx.x; i < n; i += gridDim.x) {
+    const u32 f = list[i];
+    const BatchFile file = files[f];
+    if (!t) {
+      u64 in_size = file.in_size;
+      u32 b = 0;
+      if (encoded) {
+        b = encoded[2 * u64(f) + 1] != 0 || encoded[2 * u64(f)] > file.in_size;
+        in_size = encoded[2 * u64(f)];
+      }
+      u32 w = 0, want = 0;
+      if (!b) b = check_framing(in + file.in_offset, in_size, w, want) != kOk;
+      bad = b;
+      window = w;
+      wanted[i] = want;
+      e_first = in_size;  // the stream length, until the block loop starts
+      sh.pos = 0;
+      sh.stage.count = 0;
+      sh.stage.bit0 = 0;
+    }
+    __syncthreads();
+    const u64 in_size = e_first;
+    const u8* body = in + file.in_offset + 2;
+    const u64 len = bad ? 0 : in_size - 6;
+    const u64 base = file.out_offset, out_size = file.out_size;
+    u64 produced = 0;
+    u32 blocks = 0;
+    __syncthreads();
+    while (!bad) {
+      block_header<true, true>(body, len, out_size - produced, sh);
+      if (sh.status || ++blocks > max_blocks) {  // uniform
+        if (!t) bad = 1;
+        break;
+      }
+      if (sh.type == 0) {
+        copy_bytes(out + base + produced, body + (sh.d0 >> 3), sh.size, body + len, t,
+                   kDescThreads);
+      } else {
+        if (!t) {
+          sh.hint = len * 8;
+          sh.group = kNone;
+          sh.lanes = 0;
+          sh.table = kNone;
+        }
+        __syncthreads();
+        describe_tokens(body, len, out_size - produced, sh, st, slice_entry, slice_off, group_link,
+                        group_capacity);
+        // A block that ends past the file's output (describe checks the
+        // limit only between rounds) is never emitted.
+        if (sh.status || sh.group == kNone || sh.size > out_size - produced) {  // uniform
+          if (!t) bad = 1;
+          break;
+        }
+        // The block's slices, one per thread, a describe round at a time.
+        const u64 block_out = base + produced, block_end = block_out + sh.size;
+        u32 g = sh.group, done = 0;
+        const u32 lanes = sh.lanes;
+        while (g != kNone && done < lanes) {
+          if (!t) {
+            const u32 count = lanes - done < kDescThreads ? lanes - done : kDescThreads;
+            const u32 ng = (count + 63) / 64;
+            const u32 next_g = group_link[g + ng - 1];
+            e_count = count;
+            e_next = next_g;
+            e_first = slice_entry[u64(g) * 64];
+            e_chunk_end = next_g != kNone && done + count < lanes ? slice_entry[u64(next_g) * 64]
+                                                                   : sh.end;
+            e_need = !staged_covers(sh.stage, body, len, e_first, e_chunk_end);
+          }
+          __syncthreads();
+          const u32 count = e_count;
+          if (e_need) {
+            stage_range(body, len, e_first, e_chunk_end, sh.stage);
+            __syncthreads();
+          }
+          if (t < count) {
+            const u64 entry = slice_entry[u64(g) * 64 + t];
+            const u64 stop = t + 1 < count ? slice_entry[u64(g) * 64 + t + 1] : e_chunk_end;
+            const u64 dst0 = block_out + slice_off[u64(g) * 64 + t];
+            const u32 blim = stage_limit(sh.stage, len);
+            const u32 e_rel = u32(entry - sh.stage.bit0), s_rel = u32(stop - sh.stage.bit0);
+            u32 lerr;
+            if (stop + 64 <= len * 8)
+              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_end, window, out, roots,
+                                       unres, unres_total, base);
+            else
+              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_end, window, out, roots,
+                                      unres, unres_total, base);
+            if (lerr) bad = 1;
+          }
+          done += count;
+          g = e_next;
+          __syncthreads();
+        }
+        if (done < lanes) bad = 1;
+      }
+      produced += sh.size;
+      if (!t) sh.pos = sh.end;
+      __syncthreads();
+      if (bad || sh.final_block) break;
+    }
+    __syncthreads();
+    if (!t) {
+      const bool ok = !bad && !sh.status && sh.final_block && produced == out_size &&
+                      (sh.end + 7) / 8 == len;
+      redo[f] = ok ? 0u : 1u;
+    }
+    __syncthreads();
+  }
+  for (u32 off = 32; off; off >>= 1) unres_total += __shfl_down(unres_total, off, 64);
+  if (lane_id() == 0 && unres_total)
+    atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), unres_total);
+}
+
+// Large batch files after resolution: Adler-32 of each decoded file against
+// its trailer; [0, 0] when it matches, else the file is flagged for the
+// serial decoder (so are all of them if a chain stayed unresolved).
+__global__ __launch_bounds__(256) void g_batch_wide_finish(const BatchFile* files, const u32* list,
+                                                           u32 n, const u8* out, const State* st,
+                                                           const u32* wanted, u32* redo,
+                                                           u32* meta) {
+  __shared__ u64 red[2][4];
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  for (u32 i = blockIdx.x; i < n; i += gridDim.x) {
+    const u32 f = list[i];
+    if (redo[f]) continue;  // uniform
+    const BatchFile file = files[f];
+    const u8* o = out + file.out_offset;
+    const u64 len = file.out_size;
+    u64 s = 0, w = 0;
+    for (u64 k = t; k < len; k += 256) {
+      const u64 v = o[k];
+      s += v;
+      w += (len - k) * v;
+      if (w >> 62) w %= kAdlerMod;
+    }
+    s %= kAdlerMod;
+    w %= kAdlerMod;
+    for (u32 off = 32; off; off >>= 1) {
+      s += __shfl_down(s, off, 64);
+      w += __shfl_down(w, off, 64);
+    }
+    if (!lane) {
+      red[0][wave] = s;
+      red[1][wave] = w;
+    }
+    __syncthreads();
+    if (!t) {
+      const u32 a = u32((red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1) % kAdlerMod);
+      const u64 w_all = red[1][0] + red[1][1] + red[1][2] + red[1][3] + len % kAdlerMod;
+      const u32 b = u32(w_all % kAdlerMod);
+      if (((b << 16) | a) == wanted[i] && !st->unresolved[1]) {
+        meta[2 * u64(f)] = 0;
+        meta[2 * u64(f) + 1] = 0;
+      } else {
+        redo[f] = 1;
+      }
+    }
+    __syncthreads();
+  }
 }
 
 constexpr u32 kResolveLinks = 32;  // chain links a position follows per round
@@ -2841,6 +3020,51 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
                      stream, st, out, out_size);
+  return hipGetLastError();
+}
+
+
+hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8* in, u8* out,
+                                  u64 out_total, const BatchFile* files, const u32* list,
+                                  u32 n, u64 in_bits, const u32* encoded, u32 max_blocks,
+                                  u32* redo, u32* meta) {
+  if (!n) return hipSuccess;
+  State* st = nullptr;
+  HZ_TRY(scratch.alloc(&st, 1));
+  HZ_TRY(launch_fill(stream, st, 0, sizeof(State)));
+  // Slice groups: at most one per 64 slices of >= kDescMinSlice bits, plus
+  // the partly filled last group of every describe round.
+  const u64 group_capacity = in_bits / (u64(kDescMinSlice) * 64) +
+                             in_bits / (u64(kDescThreads) * kDescMinSlice) + 8 * u64(n) + 64;
+  u64* slice_entry = nullptr;
+  u32 *slice_off = nullptr, *group_link = nullptr, *wanted = nullptr;
+  HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
+  HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
+  HZ_TRY(scratch.alloc(&group_link, group_capacity));
+  HZ_TRY(scratch.alloc(&wanted, u64(n) + 1));
+  const u64 words = (out_total + 31) / 32 + 1;
+  u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr;
+  HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
+  HZ_TRY(scratch.alloc(&bits0, words));
+  HZ_TRY(scratch.alloc(&bits1, words));
+  HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
+  HZ_LAUNCH(g_batch_wide, dim3(n), dim3(kDescThreads), 0, stream, in, out, files, list, n,
+            encoded, max_blocks, st, slice_entry, slice_off, group_link, group_capacity, roots,
+            bits0, redo, wanted);
+  HZ_TRY(hipGetLastError());
+  u32 rounds = 1;
+  for (u64 span = kResolveLinks; span < group_capacity * 64 + u64(max_blocks); span *= kResolveLinks)
+    ++rounds;
+  u64* counts = nullptr;
+  HZ_TRY(scratch.alloc(&counts, rounds + 1));
+  HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
+  for (u32 round = 0; round < rounds; ++round) {
+    HZ_LAUNCH(g_resolve, dim3(u32(clamp_grid((words + 255) / 256, 2048))), dim3(256), 0, stream,
+              st, out, roots, bits0, bits1, counts, round, rounds, words);
+    HZ_TRY(hipGetLastError());
+  }
+  HZ_LAUNCH(g_batch_wide_finish, dim3(n), dim3(256), 0, stream, files, list, n, out, st, wanted,
+            redo, meta);
   return hipGetLastError();
 }
 

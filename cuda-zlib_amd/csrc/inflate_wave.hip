@@ -191,12 +191,18 @@ __global__ __launch_bounds__(64) void inflate_single_kernel(const u8* in, u64 in
 // One workgroup per file.  With encoded metadata (compression's
 // [length, status] rows), a file's stream length comes from its row and a
 // failed or oversized slot is zeroed with status 22/23 (batch_decode.cuh:298-328).
+// Files of at least `skip_from` output bytes are left to the parallel
+// large-file route.  With `list`, only the listed files flagged in `redo`
+// are decoded (the large files that route handed back).
 __global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out,
                                                            const BatchFile* files, u32 count,
                                                            u32 max_blocks, u32* meta,
-                                                           const u32* encoded) {
+                                                           const u32* encoded, u64 skip_from,
+                                                           const u32* list, const u32* redo) {
   __shared__ WaveShared sh;
-  for (u32 f = blockIdx.x; f < count; f += gridDim.x) {
+  for (u32 i = blockIdx.x; i < count; i += gridDim.x) {
+    const u32 f = list ? list[i] : i;
+    if (list ? !redo[f] : files[f].out_size >= skip_from) continue;  // uniform
     const BatchFile file = files[f];
     u64 in_size = file.in_size;
     if (encoded) {
@@ -230,11 +236,12 @@ hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, 
 }
 
 hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const BatchFile* files,
-                                u32 count, u32 max_blocks, u32* meta, const u32* encoded) {
+                                u32 count, u32 max_blocks, u32* meta, const u32* encoded,
+                                u64 skip_from, const u32* list, const u32* redo) {
   if (!count) return hipSuccess;
   const u32 grid = count < 65536u ? count : 65536u;
   HZ_LAUNCH(inflate_batch_kernel, dim3(grid), dim3(kWave), 0, stream, in, out, files, count,
-                     max_blocks, meta, encoded);
+                     max_blocks, meta, encoded, skip_from, list, redo);
   return hipGetLastError();
 }
 

@@ -44,8 +44,12 @@ hipError_t launch_set_meta_rows(hipStream_t stream, u32* meta, u64 rows, u32 fir
 // inflate_wave.hip: serial-route decode (one wave per stream).
 hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
                                  u64 out_size, u32 max_blocks, u32* meta);
+// Files of at least skip_from output bytes are skipped; with `list`, only the
+// listed files whose `redo` flag is set are decoded.
 hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const BatchFile* files,
-                                u32 count, u32 max_blocks, u32* meta, const u32* encoded);
+                                u32 count, u32 max_blocks, u32* meta, const u32* encoded,
+                                u64 skip_from = ~0ull, const u32* list = nullptr,
+                                const u32* redo = nullptr);
 
 // Scratch allocation interface used by multi-kernel routes.
 struct Scratch {
@@ -61,6 +65,14 @@ struct Scratch {
 hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
                                u8* out, u64 out_size, u32 max_candidates, u32 max_blocks,
                                u32* meta);
+// Batch files listed in `list` (device) decoded by parallel slices, one
+// workgroup per file; a file that does not decode cleanly gets redo[f] = 1
+// and is left for the serial decoder, the others get [0, 0] in meta.
+// in_bits: total input bits of the listed files (sizes the slice pool).
+hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8* in, u8* out,
+                                  u64 out_total, const BatchFile* files, const u32* list,
+                                  u32 n, u64 in_bits, const u32* encoded, u32 max_blocks,
+                                  u32* redo, u32* meta);
 
 // deflate.hip: chunked encode of one stream / a batch of streams.
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,

@@ -1,0 +1,117 @@
+"""Batch decode parity: every file against the oracle's serial inflate.
+
+Batch files of at least 1 KiB of output decode by parallel slices, one
+workgroup per file; a file that does not decode cleanly there is handed to the
+serial per-file decoder.  Either way each file's [status, 0] row and output
+(decoded prefix then zeros on failure, the reference's DecodeOneFile,
+native/batch_decode.cuh:123-296) must equal the oracle's serial inflate.
+"""
+
+import random
+import zlib
+
+import numpy as np
+import pytest
+
+import workloads
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _files(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        size = int(rng.choice([0, 300, 1024, 5000, 40000, 70000, 150000]))
+        kind = i % 3
+        if kind == 0:
+            raw = workloads.text_like(size, rng)
+        elif kind == 1:
+            raw = rng.normal(0.0, 1.0, (size + 3) // 4).astype("<f4").tobytes()[:size]
+        else:
+            raw = bytes(rng.integers(0, 256, size, dtype=np.uint8))
+        level = int(rng.choice([1, 6, 9]))
+        out.append((raw, zlib.compress(raw, level)))
+    return out
+
+
+def _mutate(payload, rng):
+    data = bytearray(payload)
+    kind = rng.randrange(5)
+    if kind == 0 and len(data) > 8:  # flip a bit in the body
+        i = rng.randrange(2, len(data) - 4)
+        data[i] ^= 1 << rng.randrange(8)
+    elif kind == 1 and len(data) > 12:  # truncate
+        del data[rng.randrange(6, len(data) - 1):]
+    elif kind == 2:  # wrong checksum
+        data[-1] ^= 0x5A
+    elif kind == 3 and len(data) > 8:  # overwrite a run of body bytes
+        i = rng.randrange(2, len(data) - 4)
+        for j in range(i, min(i + 16, len(data) - 4)):
+            data[j] = rng.randrange(256)
+    return bytes(data)
+
+
+def _check(streams, expected):
+    import torch
+    from cuda_zlib import decompress_zlib_batch_checked
+    out, meta = decompress_zlib_batch_checked(b"".join(streams), [len(s) for s in streams],
+                                              expected, 0)
+    torch.cuda.synchronize()
+    host = out.cpu().numpy().tobytes()
+    rows = meta.cpu().numpy()
+    at = 0
+    for i, (stream, n) in enumerate(zip(streams, expected)):
+        want, want_status = oracle.inflate_serial(stream, n)
+        assert int(rows[i, 1]) == 0
+        assert int(rows[i, 0]) == want_status, "file %d: status %d, oracle %d" % (
+            i, int(rows[i, 0]), want_status)
+        assert host[at:at + n] == want, "file %d output differs" % i
+        at += n
+
+
+def test_valid_files_match_the_serial_oracle(gpu):
+    files = _files(11, 48)
+    _check([p for _, p in files], [len(r) for r, _ in files])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_corrupted_files_match_the_serial_oracle(gpu, seed):
+    rng = random.Random(seed)
+    files = _files(100 + seed, 40)
+    streams, expected = [], []
+    for raw, payload in files:
+        if rng.random() < 0.6:
+            payload = _mutate(payload, rng)
+        n = len(raw)
+        if rng.random() < 0.1:
+            n += rng.choice([-1, 1]) if n else 1
+        streams.append(payload)
+        expected.append(n)
+    _check(streams, expected)
+
+
+def test_encoded_rows_route_large_files_like_small_ones(gpu):
+    """Bad [length, status] rows give 22 / 23 and zeroed outputs, large files too."""
+    import torch
+    from cuda_zlib import compress_zlib_batch_padded, decompress_zlib_batch_checked
+    rng = np.random.default_rng(5)
+    raws = [workloads.text_like(int(n), rng) for n in (200, 3000, 20000, 70000, 500, 9000)]
+    sizes = [len(r) for r in raws]
+    enc, meta = compress_zlib_batch_padded(b"".join(raws), sizes, 0)
+    caps = [n + 5 * max(1, -(-n // 32768)) + 6 for n in sizes]
+    rows = meta.clone()
+    rows[1, 1] = 1            # a failed compression row
+    rows[2, 0] = caps[2] + 1  # a stream longer than its slot
+    rows[5, 1] = 22
+    out, dmeta = decompress_zlib_batch_checked(enc, caps, sizes, 0, encoded_metadata=rows)
+    torch.cuda.synchronize()
+    status = dmeta.cpu().numpy()[:, 0].tolist()
+    assert status == [0, 22, 23, 0, 0, 22]
+    host = out.cpu().numpy().tobytes()
+    at = 0
+    for i, raw in enumerate(raws):
+        got = host[at:at + len(raw)]
+        assert got == (raw if status[i] == 0 else bytes(len(raw)))
+        at += len(raw)
