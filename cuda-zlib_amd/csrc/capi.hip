@@ -110,7 +110,7 @@ class DeviceScope {
 
 constexpr u64 kArenaGranule = 64ull << 20;
 // Batch files of at least this many output bytes decode by parallel slices.
-constexpr u64 kBatchWideBytes = 1024;
+constexpr u64 kBatchWideBytes = 256;
 
 // Stream-ordered scratch for one call, carved from an arena of the device
 // (taken on the first allocation).  Requests the arena cannot hold come from

@@ -1,6 +1,6 @@
 """Batch decode parity: every file against the oracle's serial inflate.
 
-Batch files of at least 1 KiB of output decode by parallel slices, one
+Batch files of at least 256 B of output decode by parallel slices, one
 workgroup per file; a file that does not decode cleanly there is handed to the
 serial per-file decoder.  Either way each file's [status, 0] row and output
 (decoded prefix then zeros on failure, the reference's DecodeOneFile,
