@@ -51,12 +51,14 @@ namespace {
 
 constexpr u32 kParseThreads = 1024;
 constexpr u32 kParseWaves = kParseThreads / 64;
+static_assert(kParseWaves <= 16, "the wave-count scan covers one 16-lane DPP row");
 constexpr u32 kStep = kParseThreads;  // parse positions per step
 constexpr u32 kLog2Step = 10;
 constexpr u32 kHashBits = 12;
 constexpr u32 kBuckets = 1u << kHashBits;
 constexpr u32 kWays = 4;
-constexpr u32 kNear = 8;
+constexpr u32 kNear = 4;
+constexpr u32 kWalkMatches = 4;  // waves with at most this many match lanes walk their orbit
 constexpr u32 kMaxDist = 32768;
 constexpr u32 kHistory = 32768;
 constexpr u32 kLdsBudget = 160 * 1024;
@@ -103,7 +105,7 @@ struct ParseShared {
   u16 ml[kStep];                // match length per step position (0: none)
   u16 exitv[kStep];             // first orbit point past the position's wave
   u16 went[kParseWaves];        // orbit entry of each wave (0xffff: none)
-  u8 mark[kStep + 4];           // token starts (orbit of 0)
+  u8 mark[kStep];               // token starts of waves that mark by doubling
   u32 freq_ll[288];
   u32 freq_d[32];
   u32 wave_count[kParseWaves];
@@ -169,12 +171,31 @@ __device__ __forceinline__ u32 win_byte(const u32* win, u32 q) {
 __device__ __forceinline__ u32 hash4(u32 v) { return (v * 2654435761u) >> (32 - kHashBits); }
 
 // Length of the common prefix of window positions a < b, at most maxlen.
+// One dword first (most candidates end there), then sixteen bytes a round
+// (five dwords of each side in flight); bytes read past the window's end are
+// ignored by the clamp to maxlen (the LDS allocation holds 32 bytes past the
+// largest window).
 __device__ __forceinline__ u32 match_len(const u32* win, u32 a, u32 b, u32 maxlen) {
-  u32 m = 0;
-  while (m < maxlen) {
-    const u32 x = win_u32(win, a + m) ^ win_u32(win, b + m);
-    if (x) return min(maxlen, m + (__builtin_ctz(x) >> 3));
-    m += 4;
+  {
+    const u32 x = win_u32(win, a) ^ win_u32(win, b);
+    if (x) return min(maxlen, __builtin_ctz(x) >> 3);
+  }
+  const u32 sa = a & 3, sb = b & 3;
+  const u32* pa = win + (a >> 2) + 1;
+  const u32* pb = win + (b >> 2) + 1;
+  for (u32 m = 4; m < maxlen; m += 16, pa += 4, pb += 4) {
+    u32 da[5], db[5];
+#pragma unroll
+    for (u32 k = 0; k < 5; ++k) {
+      da[k] = pa[k];
+      db[k] = pb[k];
+    }
+#pragma unroll
+    for (u32 k = 0; k < 4; ++k) {
+      const u32 x = __builtin_amdgcn_alignbyte(da[k + 1], da[k], sa) ^
+                    __builtin_amdgcn_alignbyte(db[k + 1], db[k], sb);
+      if (x) return min(maxlen, m + 4 * k + (__builtin_ctz(x) >> 3));
+    }
   }
   return maxlen;
 }
@@ -329,10 +350,14 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
     wave_sync();
   }
   // Taken prefixes from level 1 down: taken_j items, of which c_j leaves.
-  u32 taken = 2 * m - 2, lens_of = 0;
+  // (Levels are unrolled so that c[] stays in registers.)
+  u32 taken = 2 * m - 2;
   u32 c[16];
-  for (u32 j = 1; j <= 15; ++j) c[j] = 0;
-  for (u32 j = 1; j <= limit; ++j) {
+#pragma unroll
+  for (u32 j = 0; j < 16; ++j) c[j] = 0;
+#pragma unroll
+  for (u32 j = 1; j <= 15; ++j) {
+    if (j > limit) break;
     u32 leaves = 0;
     for (u32 w = lane; w * 32 < taken; w += 64) {
       u32 bits = hs.leafbits[j][w];
@@ -343,9 +368,9 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
     c[j] = leaves;
     taken = 2 * (taken - leaves);
   }
-  (void)lens_of;
   for (u32 i = lane; i < m; i += 64) {
     u32 l = 0;
+#pragma unroll
     for (u32 j = 1; j <= 15; ++j) l += i < c[j] ? 1u : 0u;
     len[hs.sorted[i]] = u8(l);
   }
@@ -711,9 +736,8 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       const u32 f = t + (L ? L : 1u);
       // Token starts = orbit of 0 under f.  Each wave finds, for each of its
       // 64 positions, the first orbit point past the wave (pointer doubling
-      // by shuffles; J[k] = f^(2^k) while inside the wave); one thread
-      // chains the waves' entries; each wave then marks its orbit from its
-      // entry (round k pushes marks 2^k hops).
+      // by shuffles; J[k] = f^(2^k) while inside the wave); wave 0 chains the
+      // waves' entries; each wave then finds its orbit from its entry.
       const u32 w0 = wave * 64, wend = w0 + 64;
       u32 J[6];
       u32 x = f;
@@ -744,24 +768,54 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         if (!lane) sh.adv = e;
       }
       lds_barrier();
-      sh.mark[t] = t == sh.went[wave];
-      wave_sync();
-#pragma unroll
-      for (u32 k = 0; k < 6; ++k) {
-        if (sh.mark[t] && J[k] < wend) sh.mark[J[k]] = 1;
+      // The wave's orbit from its entry.  With few match lanes it is walked
+      // over them (a literal's successor is the next lane): every lane from
+      // the current point up to the next match lane starts a token, and the
+      // walk resumes past that match, in scalar registers.  Otherwise marks
+      // are pushed from the entry, 2^k hops in round k.
+      u64 starts = 0;
+      const u64 matches = __ballot(L != 0);
+      const u32 entry = u32(__builtin_amdgcn_readfirstlane(int(sh.went[wave])));
+      if (__popcll(matches) > kWalkMatches) {
+        sh.mark[t] = t == entry;
         wave_sync();
+#pragma unroll
+        for (u32 k = 0; k < 6; ++k) {
+          if (sh.mark[t] && J[k] < wend) sh.mark[J[k]] = 1;
+          wave_sync();
+        }
+        starts = __ballot(sh.mark[t]);
+      } else {
+        u32 e = entry == 0xffffu ? 64u : entry - w0;
+        while (e < 64) {
+          const u64 from = ~0ull << e;
+          const u64 m = matches & from;
+          if (!m) {
+            starts |= from;
+            break;
+          }
+          const u32 s = u32(__builtin_ctzll(m));
+          starts |= from & (~0ull >> (63 - s));
+          e = s + u32(__builtin_amdgcn_readlane(int(L), int(s)));
+        }
       }
-      const bool start = t < lim && sh.mark[t];
+      const bool start = t < lim && ((starts >> lane) & 1);
       const u64 bal = __ballot(start);
       if (!lane) sh.wave_count[wave] = __popcll(bal);
       lds_barrier();
       const u32 adv = sh.adv;
-      u32 before = 0, step_tokens = 0;
-#pragma unroll
-      for (u32 w = 0; w < kParseWaves; ++w) {
-        const u32 cnt = sh.wave_count[w];
-        if (w < wave) before += cnt;
-        step_tokens += cnt;
+      // Tokens of the earlier waves and of the step: an inclusive scan of the
+      // wave counts over lanes 0-15 (DPP row shifts stay inside one row).
+      u32 before, step_tokens;
+      {
+        u32 inc = lane < kParseWaves ? sh.wave_count[lane] : 0u;
+        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x111, 0xf, 0xf, false));
+        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x112, 0xf, 0xf, false));
+        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x114, 0xf, 0xf, false));
+        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x118, 0xf, 0xf, false));
+        const u32 w = u32(__builtin_amdgcn_readfirstlane(int(wave)));
+        before = w ? u32(__builtin_amdgcn_readlane(int(inc), int(w - 1))) : 0u;
+        step_tokens = u32(__builtin_amdgcn_readlane(int(inc), int(kParseWaves - 1)));
       }
       if (start) {
         const u32 idx = ntok + before + __popcll(bal & lanemask_lt());
