@@ -727,6 +727,8 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       }
       sh.ml[t] = u16(best_len >= 3 ? best_len : 0u);
       lds_barrier();
+      // Every lookup of the step is done: its positions enter the table.
+      if (hashable) atomicMax(&sh.table[h * kWays + (stepno & (kWays - 1))], q + 1);
 
       // Lazy rule; f(t) = end of a token starting at t.
       const u32 lim = min(kStep, end - p);
@@ -750,9 +752,10 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       sh.exitv[t] = u16(x);
       lds_barrier();
       if (wave == 0) {
-        // The chain of wave entries, by wave 0 from registers: lane l holds
-        // the exits of position l of every wave; each hop leaves its wave,
-        // so wave w is entered at most once, at iteration w.
+        // The chain of wave entries, by wave 0 from registers (one wave only:
+        // the hops are scalar work, and the scalar unit is shared by the
+        // CU): lane l holds the exits of position l of every wave; each hop
+        // leaves its wave, so wave w is entered at most once, at iteration w.
         u32 ex[kParseWaves];
 #pragma unroll
         for (u32 w = 0; w < kParseWaves; ++w) ex[w] = sh.exitv[w * 64 + lane];
@@ -768,6 +771,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         if (!lane) sh.adv = e;
       }
       lds_barrier();
+      const u32 entry = u32(__builtin_amdgcn_readfirstlane(int(sh.went[wave])));
       // The wave's orbit from its entry.  With few match lanes it is walked
       // over them (a literal's successor is the next lane): every lane from
       // the current point up to the next match lane starts a token, and the
@@ -775,7 +779,6 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       // are pushed from the entry, 2^k hops in round k.
       u64 starts = 0;
       const u64 matches = __ballot(L != 0);
-      const u32 entry = u32(__builtin_amdgcn_readfirstlane(int(sh.went[wave])));
       if (__popcll(matches) > kWalkMatches) {
         sh.mark[t] = t == entry;
         wave_sync();
@@ -834,10 +837,13 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         }
       }
       ntok += step_tokens;
-      if (hashable) atomicMax(&sh.table[h * kWays + (stepno & (kWays - 1))], q + 1);
       ++stepno;
       p += adv;
-      lds_barrier();
+      // No barrier here: the next step writes ml before its first barrier,
+      // and exitv, went, adv, wave_count and mark after it; this step read
+      // ml, exitv, went and mark before its last barrier, and adv and
+      // wave_count before reaching the next step's first; its table entries
+      // went in before its second barrier.
     }
     if (extra) atomicAdd(&sh.extra_bits, extra);
     lds_barrier();
