@@ -17,18 +17,19 @@
 //   stage    window (history + chunk) into LDS as aligned dwords; Adler-32
 //            partial sums of the chunk bytes
 //   history  every history position enters the hash table
-//   parse    steps of 1024 positions, one per thread: 4-byte hash into 4096
-//            buckets x 4 ways; candidates = the bucket plus the nearest of the
-//            8 previous positions of the same wave with an equal hash; longest
+//   parse    steps of 1024 positions, one per thread: 4-byte hash into 16384
+//            one-way buckets; candidates = the bucket plus the nearest of the
+//            2 previous positions of the same wave with an equal hash; longest
 //            match (ties: nearest); one-step lazy rule (a position yields to a
 //            longer match at the next position).  With f(j) = j + max(1, L_j)
 //            the greedy token starts are the orbit of 0 under f: every wave
 //            finds the first orbit point past itself from each of its
-//            positions (pointer doubling by shuffles), one thread chains the
-//            16 waves' entries, and each wave marks its orbit from its entry.
+//            positions (pointer doubling by shuffles), wave 0 chains the 16
+//            waves' entries, and each wave walks its orbit from its entry over
+//            its match lanes (or marks it by doubling when matches are dense).
 //            Tokens go to a global list, histograms by LDS atomics; the step's
-//            positions are inserted into way (step mod 4) by atomicMax, so the
-//            newest position wins independently of execution order.
+//            positions enter the table by atomicMax, so the newest position
+//            wins independently of execution order.
 // e_emit, one 256-thread workgroup per chunk (small LDS, several per CU):
 //   huffman  waves 0 and 1: optimal code lengths limited to 15/7 bits
 //            (leaves sorted by a bitonic network, package-merge with each
@@ -54,10 +55,10 @@ constexpr u32 kParseWaves = kParseThreads / 64;
 static_assert(kParseWaves <= 16, "the wave-count scan covers one 16-lane DPP row");
 constexpr u32 kStep = kParseThreads;  // parse positions per step
 constexpr u32 kLog2Step = 10;
-constexpr u32 kHashBits = 12;
+constexpr u32 kHashBits = 14;
 constexpr u32 kBuckets = 1u << kHashBits;
-constexpr u32 kWays = 4;
-constexpr u32 kNear = 4;
+constexpr u32 kWays = 1;
+constexpr u32 kNear = 2;
 constexpr u32 kWalkMatches = 4;  // waves with at most this many match lanes walk their orbit
 constexpr u32 kMaxDist = 32768;
 constexpr u32 kHistory = 32768;
@@ -697,8 +698,8 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       u32 best_len = 0, best_dist = 0;
       if (hashable) {
         const u32 maxlen = min(258u, end - q);  // >= 4
-        const uint4 e = *reinterpret_cast<const uint4*>(&sh.table[h * kWays]);
-        const u32 ent[4] = {e.x, e.y, e.z, e.w};
+        static_assert(kWays == 1, "one read holds a bucket");
+        const u32 ent[kWays] = {sh.table[h]};
         // Candidates by distance (0: none): the ways, then the near position.
         u32 dist[kWays + 1];
 #pragma unroll

@@ -777,13 +777,19 @@ __device__ u32 val_start(const u8* body, u64 len, u64 pos, ValShared& sh, u32 la
   if (v.nl > 286) return kValInvalid;
   const u32 nc = hclen + 4;
   if (v.pos() + 3 * nc > v.limit) return kValInvalid;
+  // The 3 * nc <= 57 bits of code-length-code lengths, read at once from the
+  // three window words in registers, then skipped in two advances.
+  const u64 field = u64(__builtin_amdgcn_alignbit(v.x1, v.x0, v.off)) |
+                    (u64(__builtin_amdgcn_alignbit(v.x2, v.x1, v.off)) << 32);
+  v.advance(sh, lane, 3 * nc - 3 * (nc >> 1));
+  v.advance(sh, lane, 3 * (nc >> 1));
   u64 pack = 0;
   u32 kraft = 0;
-  for (u32 i = 0; i < nc; ++i) {
-    const u32 x = v.bits() & 7u;
-    v.advance(sh, lane, 3);
+#pragma unroll
+  for (u32 i = 0; i < 19; ++i) {
+    const u32 x = i < nc ? u32(field >> (3 * i)) & 7u : 0u;
     pack |= u64(x) << (3 * cl_order(i));
-    if (x) kraft += 128u >> x;
+    kraft += x ? 128u >> x : 0u;
   }
   if (kraft != 128) return kValInvalid;
   // Canonical code parameters (see ValWalk).
