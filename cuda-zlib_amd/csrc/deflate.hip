@@ -156,9 +156,10 @@ constexpr u32 kEmitShared = (sizeof(EmitShared) + 15) & ~u32(15);
 // is shorter than the stored form (len + 5 bytes).
 // The bit buffer also holds two HuffScratch (waves 0 and 1) before emission.
 constexpr u32 stage_words(u32 chunk) {
-  return ((chunk + 8) / 4 + 16) * 4 > 2 * sizeof(HuffScratch)
-             ? (chunk + 8) / 4 + 16
-             : u32(2 * sizeof(HuffScratch) / 4 + 1);
+  // A multiple of 4 words: the stage is cleared and copied out as uint4.
+  return (((chunk + 8) / 4 + 16) * 4 > 2 * sizeof(HuffScratch)
+              ? (chunk + 8) / 4 + 16 + 3
+              : u32(2 * sizeof(HuffScratch) / 4 + 1 + 3)) & ~3u;
 }
 
 __device__ __forceinline__ u32 win_u32(const u32* win, u32 q) {
@@ -976,8 +977,9 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         results[c].status = 0;
       }
     } else {
-      const u32 used = min((sh.extent + 3) / 4 + 1, words);
-      for (u32 i = t; i < used; i += kEmitThreads) stage[i] = 0;
+      const u32 used4 = min(((sh.extent + 3) / 4 + 1 + 3) / 4, words / 4);
+      for (u32 i = t; i < used4; i += kEmitThreads)
+        reinterpret_cast<uint4*>(stage)[i] = uint4{0u, 0u, 0u, 0u};
       lds_barrier();
       // Header: the fixed fields by thread 0 (before the scan's barriers),
       // then the code-length RLE symbols, two per thread, placed by a scan.
@@ -1021,14 +1023,35 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
       const u32* tok = tokens + d.in_off;
       const u32 ntokens = st.ntok;
       u32 pos = sh.hdr_bits;
-      for (u32 base = 0; base < ntokens; base += kEmitThreads * kTokensPerThread) {
+      // The tokens of the next round are loaded (one 16-byte load per
+      // thread) while the current round is coded, so the global-memory
+      // latency overlaps the scan's barriers.
+      static_assert(kTokensPerThread == 4, "one uint4 of tokens per thread and round");
+      constexpr u32 kRound = kEmitThreads * kTokensPerThread;
+      // (A batch file's chunk may start at any byte, so its token list is
+      // only 4-byte aligned: then the four tokens load one by one.)
+      const bool aligned16 = (reinterpret_cast<uintptr_t>(tok) & 15) == 0;
+      const auto load4 = [&](u32 first) -> uint4 {
+        if (aligned16 && first + 4 <= ntokens) return *reinterpret_cast<const uint4*>(tok + first);
+        uint4 r = {0u, 0u, 0u, 0u};
+        if (first < ntokens) r.x = tok[first];
+        if (first + 1 < ntokens) r.y = tok[first + 1];
+        if (first + 2 < ntokens) r.z = tok[first + 2];
+        if (first + 3 < ntokens) r.w = tok[first + 3];
+        return r;
+      };
+      uint4 next = load4(t * kTokensPerThread);
+      for (u32 base = 0; base < ntokens; base += kRound) {
         const u32 first = base + t * kTokensPerThread;
+        const uint4 cur = next;
+        next = load4(first + kRound);
+        const u32 tk[4] = {cur.x, cur.y, cur.z, cur.w};
         u64 bits[kTokensPerThread];
         u32 nbits[kTokensPerThread];
         u32 mine = 0;
 #pragma unroll
         for (u32 k = 0; k < kTokensPerThread; ++k) {
-          nbits[k] = first + k < ntokens ? token_bits(sh, tok[first + k], bits[k]) : 0u;
+          nbits[k] = first + k < ntokens ? token_bits(sh, tk[k], bits[k]) : 0u;
           mine += nbits[k];
         }
         u32 total;
@@ -1055,9 +1078,12 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         results[c].extent = sh.extent;
       }
       lds_barrier();
-      const u32 copy_words = min((sh.extent + 3) / 4, slot_bytes / 4);
-      u32* slot32 = reinterpret_cast<u32*>(slot);
-      for (u32 i = t; i < copy_words; i += kEmitThreads) slot32[i] = stage[i];
+      // Whole uint4s: the slot size and the stage size are multiples of 16
+      // bytes, and the stage is zero past the stream up to used4.
+      const u32 copy4 = min(((sh.extent + 3) / 4 + 3) / 4, min(slot_bytes / 16, words / 4));
+      uint4* slot128 = reinterpret_cast<uint4*>(slot);
+      const uint4* stage128 = reinterpret_cast<const uint4*>(stage);
+      for (u32 i = t; i < copy4; i += kEmitThreads) slot128[i] = stage128[i];
       if (!t) results[c].status = sh.status;
     }
     lds_barrier();
