@@ -629,26 +629,40 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       const u32* g = reinterpret_cast<const u32*>(addr - a);
       const u32 nw = (end + 3) / 4;
       u64 s = 0, l = 0;
-      for (u32 k = t; k < nw; k += kParseThreads) {
-        // Source dword k holds window byte 4k; dword k+1 is read only when it
-        // holds a window byte, so no dword outside the input is touched.
-        const u32 lo = g[k];
-        const u32 hi = (a && 4 * (k + 1) < a + end) ? g[k + 1] : 0u;
-        u32 v = a ? __builtin_amdgcn_alignbyte(hi, lo, a) : lo;
-        if (4 * k + 4 > end) v &= (1u << (8 * (end - 4 * k))) - 1;
-        win[k] = v;
-        if (4 * k + 4 > hist) {
-          // Chunk bytes of this dword (v is zero past the end): byte sum and
-          // position-weighted sum by dot products.
-          const u32 lo_q = 4 * k;
-          const u32 mask = lo_q >= hist ? ~0u : ~0u << (8 * (hist - lo_q));
-          const u32 b = v & mask;
-          const u32 sum = __builtin_amdgcn_udot4(b, 0x01010101u, 0u, false);
-          const u32 wsum = __builtin_amdgcn_udot4(b, 0x03020100u, 0u, false);
-          s += sum;
-          // (lo_q - hist) may be negative here: bytes before hist are masked
-          // out, so the sum over the dword's chunk bytes stays exact mod 2^64.
-          l += u64(i64(lo_q) - i64(hist)) * sum + wsum;
+      // A thread's dwords are loaded kStageBatch at a time, all loads in
+      // flight before the first is used (one memory latency per batch).
+      constexpr u32 kStageBatch = 16;
+      for (u32 k0 = t; k0 < nw; k0 += kStageBatch * kParseThreads) {
+        u32 lo[kStageBatch], hi[kStageBatch];
+#pragma unroll
+        for (u32 j = 0; j < kStageBatch; ++j) {
+          // Source dword k holds window byte 4k; dword k+1 is read only when
+          // it holds a window byte, so no dword outside the input is touched.
+          const u32 k = k0 + j * kParseThreads;
+          lo[j] = k < nw ? g[k] : 0u;
+          hi[j] = (k < nw && a && 4 * (k + 1) < a + end) ? g[k + 1] : 0u;
+        }
+#pragma unroll
+        for (u32 j = 0; j < kStageBatch; ++j) {
+          const u32 k = k0 + j * kParseThreads;
+          if (k >= nw) break;
+          u32 v = a ? __builtin_amdgcn_alignbyte(hi[j], lo[j], a) : lo[j];
+          if (4 * k + 4 > end) v &= (1u << (8 * (end - 4 * k))) - 1;
+          win[k] = v;
+          if (4 * k + 4 > hist) {
+            // Chunk bytes of this dword (v is zero past the end): byte sum
+            // and position-weighted sum by dot products.
+            const u32 lo_q = 4 * k;
+            const u32 mask = lo_q >= hist ? ~0u : ~0u << (8 * (hist - lo_q));
+            const u32 b = v & mask;
+            const u32 sum = __builtin_amdgcn_udot4(b, 0x01010101u, 0u, false);
+            const u32 wsum = __builtin_amdgcn_udot4(b, 0x03020100u, 0u, false);
+            s += sum;
+            // (lo_q - hist) may be negative here: bytes before hist are
+            // masked out, so the sum over the dword's chunk bytes stays exact
+            // mod 2^64.
+            l += u64(i64(lo_q) - i64(hist)) * sum + wsum;
+          }
         }
       }
       for (u32 k = nw + t; k < nw + 4; k += kParseThreads) win[k] = 0;

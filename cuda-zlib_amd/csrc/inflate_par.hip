@@ -131,7 +131,21 @@ __device__ void stage_range(const u8* body, u64 len, u64 bit0, u64 bit1, StageT<
   u64 words = end_word > first_word ? end_word - first_word : 0;
   if (words > W) words = W;
   const u32* g = reinterpret_cast<const u32*>(first_word << 2);
-  for (u64 i = threadIdx.x; i < words; i += blockDim.x) sg.words[i] = g[i];
+  // Eight loads per thread in flight before the first store.
+  constexpr u32 kBatch = 8;
+  for (u64 i0 = threadIdx.x; i0 < words; i0 += kBatch * blockDim.x) {
+    u32 x[kBatch];
+#pragma unroll
+    for (u32 j = 0; j < kBatch; ++j) {
+      const u64 i = i0 + u64(j) * blockDim.x;
+      x[j] = i < words ? g[i] : 0u;
+    }
+#pragma unroll
+    for (u32 j = 0; j < kBatch; ++j) {
+      const u64 i = i0 + u64(j) * blockDim.x;
+      if (i < words) sg.words[i] = x[j];
+    }
+  }
   if (!threadIdx.x) {
     sg.count = u32(words);
     sg.bit0 = (first_word << 5) - (u64(base) << 3);  // body bit of word 0, mod 2^64
