@@ -334,6 +334,42 @@ __device__ __forceinline__ bool stored_seed(const u8* body, u64 len, u64 byte) {
   return possible && ((body[byte + 4 + n] >> 1) & 3u) == 1;
 }
 
+// stage_range split in two, so that a range's words can be loaded into
+// registers (kPer per thread) while the previous range is still in use, and
+// stored into the stage later.
+template <u32 W, u32 kPer>
+struct StagePrefetch {
+  u32 x[kPer];
+  u64 first_word;
+  u32 words;
+  __device__ __forceinline__ void load(const u8* body, u64 len, u64 bit0, u64 bit1, u64 margin) {
+    const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+    first_word = (base + (bit0 >> 3)) >> 2;
+    u64 last_byte = (bit1 + 7) / 8 + margin;
+    if (last_byte > len) last_byte = len;
+    const u64 end_word = (base + last_byte + 3) >> 2;  // words holding body bytes only
+    u64 n = end_word > first_word ? end_word - first_word : 0;
+    words = u32(n > W ? W : n);
+    const u32* g = reinterpret_cast<const u32*>(first_word << 2);
+#pragma unroll
+    for (u32 j = 0; j < kPer; ++j) {
+      const u32 i = threadIdx.x + j * blockDim.x;
+      x[j] = i < words ? g[i] : 0u;
+    }
+  }
+  __device__ __forceinline__ void store(StageT<W>& sg, const u8* body) const {
+#pragma unroll
+    for (u32 j = 0; j < kPer; ++j) {
+      const u32 i = threadIdx.x + j * blockDim.x;
+      if (i < words) sg.words[i] = x[j];
+    }
+    if (!threadIdx.x) {
+      sg.count = words;
+      sg.bit0 = (first_word << 5) - (u64(reinterpret_cast<uintptr_t>(body)) << 3);
+    }
+  }
+};
+
 // Bytes past a workgroup's range staged for the prefilter: the fields it
 // reads end 3 + 14 + 57 bits after a position of the range's last byte.
 constexpr u32 kPreMargin = 24;
@@ -530,13 +566,22 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   build_kraft3(kraft3);
   u32 seeds = 0;
+  // The next range's words are loaded while the current range is checked.
+  static_assert(kPreStageWords <= 3 * kDiscThreads, "three words per thread hold a range");
+  StagePrefetch<kPreStageWords, 3> next;
+  if (blockIdx.x < groups)
+    next.load(body, len, u64(blockIdx.x) * kDiscRange * 8, (u64(blockIdx.x) + 1) * kDiscRange * 8,
+              kPreMargin);
   for (u64 wg = blockIdx.x; wg < groups; wg += gridDim.x) {
-    stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
+    next.store(sg, body);
     for (u32 i = t; i < kDiscRange * 8 / 32; i += kDiscThreads) pass[i] = 0;
     __syncthreads();
     // Words past the staged ones read as zero, as body bits past the end do.
     for (u32 i = sg.count + t; i < kPreStageWords; i += kDiscThreads) sg.words[i] = 0;
     __syncthreads();
+    if (wg + gridDim.x < groups)
+      next.load(body, len, (wg + gridDim.x) * kDiscRange * 8, (wg + gridDim.x + 1) * kDiscRange * 8,
+                kPreMargin);
     const u64 b0 = wg * kDiscRange + u64(t) * kDiscBytesPerThread;
     // The range starts at stage byte `a` (the stage begins at the aligned word
     // holding it); this thread's 64 offsets start at stage word 2t.
