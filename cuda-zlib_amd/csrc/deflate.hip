@@ -682,11 +682,10 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
     lds_barrier();
 
     // ---- history positions enter the table ----
-    u32 stepno = 0;
-    for (u32 base = 0; base < hist; base += kStep, ++stepno) {
+#pragma unroll 4
+    for (u32 base = 0; base < hist; base += kStep) {
       const u32 q = base + t;
-      if (q < hist && q + 4 <= end)
-        atomicMax(&sh.table[hash4(win_u32(win, q)) * kWays + (stepno & (kWays - 1))], q + 1);
+      if (q < hist && q + 4 <= end) atomicMax(&sh.table[hash4(win_u32(win, q))], q + 1);
     }
     lds_barrier();
 
@@ -744,7 +743,7 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       sh.ml[t] = u16(best_len >= 3 ? best_len : 0u);
       lds_barrier();
       // Every lookup of the step is done: its positions enter the table.
-      if (hashable) atomicMax(&sh.table[h * kWays + (stepno & (kWays - 1))], q + 1);
+      if (hashable) atomicMax(&sh.table[h], q + 1);
 
       // Lazy rule; f(t) = end of a token starting at t.
       const u32 lim = min(kStep, end - p);
@@ -853,7 +852,6 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         }
       }
       ntok += step_tokens;
-      ++stepno;
       p += adv;
       // No barrier here: the next step writes ml before its first barrier,
       // and exitv, went, adv, wave_count and mark after it; this step read

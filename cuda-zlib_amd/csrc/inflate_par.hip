@@ -1046,8 +1046,18 @@ __global__ __launch_bounds__(256) void g_valid_scatter(const State* st, const u6
 namespace {
 
 // Lower bound of `key` in the sorted candidate array.
-__device__ u64 lower_bound(const u64* cand, u64 n, u64 key) {
-  u64 lo = 0, hi = n;
+// First index at or after `from` whose candidate is >= key, when every
+// entry before `from` is known to be below `key` (the list is sorted):
+// galloping from `from`, so an answer close to it costs one or two loads
+// instead of a full binary search of dependent loads.
+__device__ u64 lower_bound_from(const u64* cand, u64 n, u64 from, u64 key) {
+  if (from >= n || cand[from] >= key) return from;
+  u64 below = from, step = 1;  // cand[below] < key
+  while (below + step < n && cand[below + step] < key) {
+    below += step;
+    step <<= 1;
+  }
+  u64 lo = below + 1, hi = below + step < n ? below + step : n;  // answer in [lo, hi]
   while (lo < hi) {
     const u64 mid = lo + (hi - lo) / 2;
     if (cand[mid] < key) lo = mid + 1;
@@ -1861,38 +1871,42 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
   for (u64 c = blockIdx.x; c < n; c += gridDim.x) {
     u64 produced = 0;
     u32 blocks = 0, status = 0, final_block = 0, next = kNone, first_rec = kNone, last_rec = kNone;
+    // Thread 0: every candidate before this index lies at or before sh.pos
+    // (the list is sorted and sh.pos only grows).
+    u64 search_from = c + 1;
     bool recs_ok = true;
+    // The candidate's own dynamic header was parsed by g_headers (tables in
+    // slot c); any other block type at bit 0 is parsed below.  Its position,
+    // header results and tables load at once (one memory latency).
+    const u32 info0 = c < table_capacity ? hdr_info[c] : 0u;
+    const bool pre0 = c < table_capacity && ((info0 >> 9) & 3u) == 2;
     if (!t) {
       sh.pos = cand[c];
       sh.stage.count = 0;
       sh.stage.bit0 = 0;
+      if (pre0) {
+        sh.status = info0 & 0xffu;
+        sh.final_block = (info0 >> 8) & 1u;
+        sh.type = (info0 >> 9) & 3u;
+        sh.d0 = hdr_d0[c];
+      }
+    }
+    if (pre0) {
+      const u32* src_ll = reinterpret_cast<const u32*>(&tables[c].ll);
+      const u32* src_dd = reinterpret_cast<const u32*>(&tables[c].dd);
+      u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
+      u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
+      copy_tables<kDescThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
     }
     __syncthreads();
     bool first = true;
     for (;;) {
-      // The candidate's own dynamic header was parsed by g_headers (tables
-      // in slot c); any other block type at bit 0 is parsed here.
-      const bool pre = first && c < table_capacity && ((hdr_info[c] >> 9) & 3u) == 2;
-      if (pre) {
-        if (!t) {
-          const u32 info = hdr_info[c];
-          sh.status = info & 0xffu;
-          sh.final_block = (info >> 8) & 1u;
-          sh.type = (info >> 9) & 3u;
-          sh.d0 = hdr_d0[c];
-        }
-        const u32* src_ll = reinterpret_cast<const u32*>(&tables[c].ll);
-        const u32* src_dd = reinterpret_cast<const u32*>(&tables[c].dd);
-        u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
-        u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
-        copy_tables<kDescThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
-        __syncthreads();
-      } else {
-        block_header<true, true>(body, len, out_size, sh);
-      }
+      const bool pre = first && pre0;
+      if (!pre) block_header<true, true>(body, len, out_size, sh);
       first = false;
       if (!t && sh.type && !sh.status) {
-        const u64 idx = lower_bound(cand, n, sh.pos + 1);
+        const u64 idx = lower_bound_from(cand, n, search_from, sh.pos + 1);
+        search_from = idx;
         sh.hint = idx < n ? cand[idx] : len * 8;
         sh.group = kNone;
         sh.lanes = 0;
@@ -1917,6 +1931,10 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
       if (!t) {
         ++blocks;
         const u32 bstatus = sh.status;
+        // Whether the block ends on a candidate, looked up before the record
+        // is reserved so that the two memory latencies overlap.
+        const u64 end_idx = lower_bound_from(cand, n, search_from, sh.end);
+        const bool end_is_cand = end_idx < n && cand[end_idx] == sh.end;
         if (bstatus) status = bstatus;
         else {
           produced += sh.size;
@@ -1946,8 +1964,8 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
           else if (sh.final_block) final_block = 1;
           else {
             const u64 p = sh.end;
-            const u64 idx = lower_bound(cand, n, p);
-            if (idx < n && cand[idx] == p) next = u32(idx);
+            search_from = end_idx;
+            if (end_is_cand) next = u32(end_idx);
             else {
               BitIn h;
               h.init(body, len, p);
