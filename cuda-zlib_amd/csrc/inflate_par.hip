@@ -2541,43 +2541,52 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
       if (rec.type == 0) {
         copy_bytes(out + block_out, body + (rec.data >> 3), rec.size, body + len, t, kEmitThreads);
       } else {
-        if (rec.table != kNone) {
-          const u32* src_ll = reinterpret_cast<const u32*>(&tables[rec.table].ll);
-          const u32* src_dd = reinterpret_cast<const u32*>(&tables[rec.table].dd);
-          u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
-          u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
-          copy_tables<kEmitThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
-          __syncthreads();
-        } else {
+        if (rec.table == kNone) {
           block_header<true, true>(body, len, ~0ull, sh);
           if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
         }
+        bool tables_pending = rec.table != kNone;
         u32 g = rec.group;
         u32 done = 0;
         while (g != kNone && done < rec.lanes) {
-          // One describe round: up to 256 slices in consecutive groups.
+          // One describe round: up to 256 slices in consecutive groups.  The
+          // round's slice entries and offsets, and in the first round the
+          // block's tables, load together (one memory latency).
+          const u32 count = rec.lanes - done < kEmitThreads ? rec.lanes - done : kEmitThreads;
+          u64 entry = 0, stop = 0;
+          u32 off = 0;
+          if (t < count) {
+            entry = slice_entry[u64(g) * 64 + t];
+            off = slice_off[u64(g) * 64 + t];
+            if (t + 1 < count) stop = slice_entry[u64(g) * 64 + t + 1];
+          }
+          if (tables_pending) {
+            const u32* src_ll = reinterpret_cast<const u32*>(&tables[rec.table].ll);
+            const u32* src_dd = reinterpret_cast<const u32*>(&tables[rec.table].dd);
+            u32* dst_ll = reinterpret_cast<u32*>(&sh.tables.ll);
+            u32* dst_dd = reinterpret_cast<u32*>(&sh.tables.dd);
+            copy_tables<kEmitThreads>(dst_ll, dst_dd, src_ll, src_dd, t);
+            tables_pending = false;
+          }
           if (!t) {
-            const u32 count = rec.lanes - done < kEmitThreads ? rec.lanes - done : kEmitThreads;
-            const u32 ng = (count + 63) / 64;
-            const u32 next_g = group_link[g + ng - 1];
-            sh.count = count;
+            // The next round's first group and first entry only when one
+            // follows (a block of at most 256 slices has a single round).
+            const bool more = done + count < rec.lanes;
+            const u32 next_g = more ? group_link[g + (count + 63) / 64 - 1] : kNone;
             sh.next_g = next_g;
-            sh.first = slice_entry[u64(g) * 64];
-            sh.chunk_end = next_g != kNone && done + count < rec.lanes ? slice_entry[u64(next_g) * 64]
-                                                                      : rec.end;
-            sh.need = !staged_covers(sh.stage, body, len, sh.first, sh.chunk_end);
+            sh.first = entry;
+            sh.chunk_end = next_g != kNone ? slice_entry[u64(next_g) * 64] : rec.end;
+            sh.need = !staged_covers(sh.stage, body, len, entry, sh.chunk_end);
           }
           __syncthreads();
-          const u32 count = sh.count;
           if (sh.need) {
             stage_range(body, len, sh.first, sh.chunk_end, sh.stage);
             __syncthreads();
           }
           u32 lerr = 0;
           if (t < count) {
-            const u64 entry = slice_entry[u64(g) * 64 + t];
-            const u64 stop = t + 1 < count ? slice_entry[u64(g) * 64 + t + 1] : sh.chunk_end;
-            const u64 dst0 = block_out + slice_off[u64(g) * 64 + t];
+            if (t + 1 >= count) stop = sh.chunk_end;
+            const u64 dst0 = block_out + off;
             const u32 blim = stage_limit(sh.stage, len);
             const u32 e_rel = u32(entry - sh.stage.bit0), s_rel = u32(stop - sh.stage.bit0);
             // Unchecked decoding when the slice and a token of overshoot lie
