@@ -271,14 +271,18 @@ extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const ui
   if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
   return execute(stream, [&](Workspace& ws) -> hipError_t {
     if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, 0, kInvalidBounds);
-    hipError_t err = launch_fill(stream, output, 0, output_size);
-    if (err != hipSuccess) return err;
-    if (input_size > kMaxBytes || chunk_bytes < 256 || chunk_bytes > 65535)
+    // A rejected call returns a zeroed slot; an accepted one has the bytes
+    // after its stream (or the whole slot, on failure) zeroed by run_deflate.
+    auto reject = [&]() -> hipError_t {
+      hipError_t err = launch_fill(stream, output, 0, output_size);
+      if (err != hipSuccess) return err;
       return launch_set_meta(stream, metadata, 0, kInvalidBounds);
+    };
+    if (input_size > kMaxBytes || chunk_bytes < 256 || chunk_bytes > 65535) return reject();
     const u64 chunks = chunk_count(input_size, u64(chunk_bytes));
     if (2 * chunks - 1 > kMaxBlocks || input_size + chunks * 5 + 6 > kMaxBytes ||
         output_size != input_size + chunks * 5 + 6)
-      return launch_set_meta(stream, metadata, 0, kInvalidBounds);
+      return reject();
     return run_deflate(stream, ws, input, input_size, output, output_size, u32(chunk_bytes),
                        metadata);
   });

@@ -1258,6 +1258,25 @@ hipError_t run_chunks(hipStream_t stream, Scratch& scratch, const u8* in, const 
 
 }  // namespace
 
+// Zeros the single stream's slot after its stream: [meta[0], capacity), which
+// is the whole slot when compression failed (meta[0] is then 0).  The stream
+// itself is written in full by e_wrap and e_pack.
+__global__ __launch_bounds__(256) void e_zero_tail(u8* out, u64 capacity, const u32* meta) {
+  const u64 from = min<u64>(meta[0], capacity);
+  const u64 first16 = (from + 15) & ~u64(15), end16 = capacity & ~u64(15);
+  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x, stride = u64(gridDim.x) * blockDim.x;
+  // Unaligned bytes at both ends, then 16-byte stores (out is 256-byte aligned).
+  if (first16 >= end16) {
+    for (u64 i = from + tid; i < capacity; i += stride) out[i] = 0;
+    return;
+  }
+  for (u64 i = from + tid; i < first16; i += stride) out[i] = 0;
+  for (u64 i = end16 + tid; i < capacity; i += stride) out[i] = 0;
+  uint4* o = reinterpret_cast<uint4*>(out + first16);
+  const u64 n16 = (end16 - first16) / 16;
+  for (u64 i = tid; i < n16; i += stride) o[i] = uint4{0u, 0u, 0u, 0u};
+}
+
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
                        u64 capacity, u32 chunk_bytes, u32* meta) {
   const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
@@ -1269,7 +1288,10 @@ hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 i
             stream, in_size, chunk_bytes, u32(chunks), history_limit(chunk_bytes), capacity, descs,
             file);
   HZ_TRY(hipGetLastError());
-  return run_chunks(stream, scratch, in, descs, chunks, file, 1, in_size, out, chunk_bytes, meta);
+  HZ_TRY(run_chunks(stream, scratch, in, descs, chunks, file, 1, in_size, out, chunk_bytes, meta));
+  HZ_LAUNCH(e_zero_tail, dim3(u32(std::min<u64>(1024, (capacity / 16 + 255) / 256 + 1))), dim3(256),
+            0, stream, out, capacity, meta);
+  return hipGetLastError();
 }
 
 hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_total,
