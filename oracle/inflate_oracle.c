@@ -1,8 +1,8 @@
 /* CPU oracle for the zlib/DEFLATE codec -- TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the reference codec's decode semantics, used by the
- * tests, smoke() and bench.py's cpu_baseline leg as the checker.  Nothing in
- * the product links or calls this file.
+ * tests, smoke() and bench.py's cpu_baseline leg to check results against.
+ * Nothing in the product links or calls this file.
  *
  * What it restates (reference file:line, paths under src/cuda_zlib/):
  *   - zlib framing and its precedence: native/codec_ffi.cu:304-329, _codec.py:97-112

@@ -1,7 +1,7 @@
 """ctypes wrapper over the CPU oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
-module, as the checker.  The product never imports it.
+module, to check results against.  The product never imports it.
 """
 
 import ctypes
