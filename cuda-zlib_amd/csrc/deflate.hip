@@ -103,7 +103,6 @@ struct ChunkResult {
 
 struct ParseShared {
   u32 table[kBuckets * kWays];  // position + 1 per way, 0 = empty
-  u16 ml[kStep];                // match length per step position (0: none)
   u16 exitv[kStep];             // first orbit point past the position's wave
   u16 went[kParseWaves];        // orbit entry of each wave (0xffff: none)
   u8 mark[kStep];               // token starts of waves that mark by doubling
@@ -740,15 +739,13 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
           }
         }
       }
-      sh.ml[t] = u16(best_len >= 3 ? best_len : 0u);
-      lds_barrier();
-      // Every lookup of the step is done: its positions enter the table.
-      if (hashable) atomicMax(&sh.table[h], q + 1);
-
-      // Lazy rule; f(t) = end of a token starting at t.
+      // Lazy rule; f(t) = end of a token starting at t.  The next position's
+      // match length comes from the next lane (DPP wave_shl:1); a wave's last
+      // lane has no lookahead and takes its match greedily, so the step needs
+      // no barrier here.
       const u32 lim = min(kStep, end - p);
-      const u32 cur_ml = sh.ml[t];
-      const u32 next_ml = t + 1 < kStep ? sh.ml[t + 1] : 0u;
+      const u32 cur_ml = best_len >= 3 ? best_len : 0u;
+      const u32 next_ml = u32(__builtin_amdgcn_update_dpp(0, int(cur_ml), 0x130, 0xf, 0xf, false));
       const u32 L = (cur_ml && next_ml <= cur_ml) ? cur_ml : 0u;
       const u32 f = t + (L ? L : 1u);
       // Token starts = orbit of 0 under f.  Each wave finds, for each of its
@@ -766,6 +763,8 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       }
       sh.exitv[t] = u16(x);
       lds_barrier();
+      // Every lookup of the step is done: its positions enter the table.
+      if (hashable) atomicMax(&sh.table[h], q + 1);
       if (wave == 0) {
         // The chain of wave entries, by wave 0 from registers (one wave only:
         // the hops are scalar work, and the scalar unit is shared by the
@@ -853,11 +852,11 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       }
       ntok += step_tokens;
       p += adv;
-      // No barrier here: the next step writes ml before its first barrier,
-      // and exitv, went, adv, wave_count and mark after it; this step read
-      // ml, exitv, went and mark before its last barrier, and adv and
-      // wave_count before reaching the next step's first; its table entries
-      // went in before its second barrier.
+      // No barrier here: the next step writes exitv before its first
+      // barrier, and went, adv, wave_count and mark after it; this step read
+      // exitv, went and mark before its last barrier, and adv and wave_count
+      // before reaching the next step's first; its table entries went in
+      // before its second barrier, after every lookup of the step.
     }
     if (extra) atomicAdd(&sh.extra_bits, extra);
     lds_barrier();
