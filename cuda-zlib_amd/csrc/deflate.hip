@@ -108,7 +108,7 @@ struct ParseShared {
   u8 mark[kStep];               // token starts of waves that mark by doubling
   u32 freq_ll[288];
   u32 freq_d[32];
-  u32 wave_count[kParseWaves];
+  u32 wave_count[2][kParseWaves];  // token counts of the last two steps, by step parity
   u32 adv;                      // step advance: first orbit point at or past the step's end
   u32 extra_bits;
   u64 red_s[kParseWaves], red_l[kParseWaves];
@@ -691,6 +691,25 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
     // ---- parse ----
     u32* tok = tokens + d.in_off;
     u32 ntok = 0, extra = 0;
+    // A step's tokens are stored during the next step, once every wave's
+    // count is in LDS (no barrier of its own): pend_tok is this lane's token,
+    // pend_bal the wave's token lanes, pend_buf the counts' buffer.
+    u32 pend_tok = 0, pend_buf = 0, cur_buf = 0;
+    u64 pend_bal = 0;
+    bool pending = false;
+    const auto flush = [&]() {
+      // Tokens of the earlier waves and of the step: an inclusive scan of the
+      // wave counts over lanes 0-15 (DPP row shifts stay inside one row).
+      u32 inc = lane < kParseWaves ? sh.wave_count[pend_buf][lane] : 0u;
+      inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x111, 0xf, 0xf, false));
+      inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x112, 0xf, 0xf, false));
+      inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x114, 0xf, 0xf, false));
+      inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x118, 0xf, 0xf, false));
+      const u32 w = u32(__builtin_amdgcn_readfirstlane(int(wave)));
+      const u32 before = w ? u32(__builtin_amdgcn_readlane(int(inc), int(w - 1))) : 0u;
+      if ((pend_bal >> lane) & 1) tok[ntok + before + __popcll(pend_bal & lanemask_lt())] = pend_tok;
+      ntok += u32(__builtin_amdgcn_readlane(int(inc), int(kParseWaves - 1)));
+    };
     for (u32 p = hist; p < end;) {
       const u32 q = p + t;
       const bool hashable = q + 4 <= end;
@@ -765,6 +784,9 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       lds_barrier();
       // Every lookup of the step is done: its positions enter the table.
       if (hashable) atomicMax(&sh.table[h], q + 1);
+      // The previous step's tokens: waves 1-15 now, while wave 0 chains;
+      // wave 0 after the chain.
+      if (pending && wave != 0) flush();
       if (wave == 0) {
         // The chain of wave entries, by wave 0 from registers (one wave only:
         // the hops are scalar work, and the scalar unit is shared by the
@@ -785,7 +807,9 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         if (!lane) sh.adv = e;
       }
       lds_barrier();
+      if (pending && wave == 0) flush();
       const u32 entry = u32(__builtin_amdgcn_readfirstlane(int(sh.went[wave])));
+      const u32 adv = sh.adv;
       // The wave's orbit from its entry.  With few match lanes it is walked
       // over them (a literal's successor is the next lane): every lane from
       // the current point up to the next match lane starts a token, and the
@@ -818,24 +842,8 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       }
       const bool start = t < lim && ((starts >> lane) & 1);
       const u64 bal = __ballot(start);
-      if (!lane) sh.wave_count[wave] = __popcll(bal);
-      lds_barrier();
-      const u32 adv = sh.adv;
-      // Tokens of the earlier waves and of the step: an inclusive scan of the
-      // wave counts over lanes 0-15 (DPP row shifts stay inside one row).
-      u32 before, step_tokens;
-      {
-        u32 inc = lane < kParseWaves ? sh.wave_count[lane] : 0u;
-        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x111, 0xf, 0xf, false));
-        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x112, 0xf, 0xf, false));
-        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x114, 0xf, 0xf, false));
-        inc += u32(__builtin_amdgcn_update_dpp(0, int(inc), 0x118, 0xf, 0xf, false));
-        const u32 w = u32(__builtin_amdgcn_readfirstlane(int(wave)));
-        before = w ? u32(__builtin_amdgcn_readlane(int(inc), int(w - 1))) : 0u;
-        step_tokens = u32(__builtin_amdgcn_readlane(int(inc), int(kParseWaves - 1)));
-      }
+      if (!lane) sh.wave_count[cur_buf][wave] = __popcll(bal);
       if (start) {
-        const u32 idx = ntok + before + __popcll(bal & lanemask_lt());
         if (L) {
           u32 ls, lb, lx, ds, db, dx;
           length_code(L, ls, lb, lx);
@@ -843,21 +851,27 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
           atomicAdd(&sh.freq_ll[ls], 1u);
           atomicAdd(&sh.freq_d[ds], 1u);
           extra += lb + db;
-          tok[idx] = 0x80000000u | ((L - 3) << 16) | (best_dist - 1);
+          pend_tok = 0x80000000u | ((L - 3) << 16) | (best_dist - 1);
         } else {
           const u32 lit = hashable ? (v & 0xff) : win_byte(win, q);
           atomicAdd(&sh.freq_ll[lit], 1u);
-          tok[idx] = lit;
+          pend_tok = lit;
         }
       }
-      ntok += step_tokens;
+      pend_bal = bal;
+      pend_buf = cur_buf;
+      cur_buf ^= 1u;
+      pending = true;
       p += adv;
       // No barrier here: the next step writes exitv before its first
-      // barrier, and went, adv, wave_count and mark after it; this step read
-      // exitv, went and mark before its last barrier, and adv and wave_count
-      // before reaching the next step's first; its table entries went in
-      // before its second barrier, after every lookup of the step.
+      // barrier, and went, adv, mark and the other count buffer after it;
+      // this step read exitv, went and mark before its last barrier, and adv
+      // right after it; its counts are read during the next step, before
+      // that step's second barrier; its table entries went in before its
+      // last barrier, after every lookup of the step.
     }
+    lds_barrier();
+    if (pending) flush();
     if (extra) atomicAdd(&sh.extra_bits, extra);
     lds_barrier();
     ChunkStats& st = stats[c];
