@@ -2,8 +2,8 @@
 
 The encoder's contract (the reference's compress path, native/codec_ffi.cu:551-612
 and src/cuda_zlib/_codec.py:142-205) is a valid zlib stream of at most
-``n + 5 * chunks + 6`` bytes with metadata ``[encoded_length, status]``; the
-checker is CPU ``zlib.decompress`` plus the oracle's decoder.
+``n + 5 * chunks + 6`` bytes with metadata ``[encoded_length, status]``;
+streams are checked with CPU ``zlib.decompress`` and the oracle's decoder.
 """
 
 import ctypes

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the GPU decoder's checker.
+"""Pins the CPU oracle before the GPU decoder's results are checked against it.
 
 Checks: zlib.decompress / zlib.adler32 on valid streams (closed-form oracle),
 the statuses and failed outputs the reference's own tests pin, brute-force
