@@ -3001,7 +3001,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&block_offset, pre_blocks));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
-  HZ_LAUNCH(g_discover, dim3(clamp_grid(groups, 4096)), dim3(kDiscThreads), 0, stream, body,
+  HZ_LAUNCH(g_discover, dim3(clamp_grid(groups, 8192)), dim3(kDiscThreads), 0, stream, body,
             len, st, wg_count, wg_list, groups);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset, groups,
