@@ -425,21 +425,36 @@ extern "C" int HipZlibWorkspacePoolStats(int device, uint64_t* stats) {
 extern "C" int HipZlibTrimWorkspacePool(int device) {
   hipMemPool_t pool;
   if (!find_pool(device, &pool)) return 0;
+  // Idle arenas of the device leave the registry under the lock (no call can
+  // take them any more); waiting for their last use and freeing them happen
+  // after the lock is released, so calls on other streams are never held up
+  // by this wait.
+  std::vector<std::unique_ptr<Arena>> idle;
   {
-    // Idle arenas go back to the pool once their last use has finished.
     PoolRegistry& reg = registry();
     std::lock_guard<std::mutex> lock(reg.mutex);
     for (auto it = reg.arenas.begin(); it != reg.arenas.end();) {
-      Arena& a = **it;
-      if (a.device != device || a.busy) { ++it; continue; }
-      hipError_t err = hipEventSynchronize(a.last_use);
-      if (err == hipSuccess && a.base) err = hipFreeAsync(a.base, nullptr);
-      if (err == hipSuccess) err = hipEventDestroy(a.last_use);
-      if (err != hipSuccess) return int(err);
-      it = reg.arenas.erase(it);
+      if ((*it)->device == device && !(*it)->busy) {
+        idle.push_back(std::move(*it));
+        it = reg.arenas.erase(it);
+      } else {
+        ++it;
+      }
     }
   }
-  return int(hipMemPoolTrimTo(pool, 0));
+  int previous = 0;
+  hipError_t first = hipGetDevice(&previous);
+  if (first == hipSuccess && previous != device) first = hipSetDevice(device);
+  auto keep = [&](hipError_t err) { if (first == hipSuccess) first = err; };
+  for (auto& a : idle) {
+    keep(hipEventSynchronize(a->last_use));
+    // A synchronous free: the pool must hold the pages again before the trim.
+    if (a->base) keep(hipFree(a->base));
+    keep(hipEventDestroy(a->last_use));
+  }
+  if (first == hipSuccess) first = hipMemPoolTrimTo(pool, 0);
+  if (previous != device) hipSetDevice(previous);
+  return int(first);
 }
 
 namespace hz {

@@ -123,3 +123,23 @@ def test_oracle_not_imported_by_the_package():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.lower(), f
+
+
+def test_retention_can_be_set_and_read_without_a_device():
+    """Before any pool exists the controls touch no GPU: set, then read back."""
+    import subprocess
+    import sys
+    script = (
+        "import ctypes, sys; sys.path[:0] = [%r]\n"
+        "from cuda_zlib import _native\n"
+        "lib = _native._bind(ctypes.CDLL(_native.LIBRARY_PATH))\n"
+        "assert lib.HipZlibSetWorkspaceRetention(12345) == 0\n"
+        "stats = (ctypes.c_uint64 * 4)()\n"
+        "assert lib.HipZlibWorkspacePoolStats(0, stats) == 0\n"
+        "assert list(stats) == [12345, 0, 0, 0], list(stats)\n"
+        "assert lib.HipZlibTrimWorkspacePool(0) == 0\n"
+        "assert lib.HipZlibWorkspacePoolStats(0, None) == _native.INVALID_ARGUMENT\n"
+        % os.path.join(ROOT, "cuda-zlib_amd"))
+    proc = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True,
+                          timeout=120, env=dict(os.environ, HIP_VISIBLE_DEVICES=""))
+    assert proc.returncode == 0, proc.stderr
