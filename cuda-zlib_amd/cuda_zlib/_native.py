@@ -60,6 +60,14 @@ def load(path=LIBRARY_PATH):
     with _LOCK:
         if _LIBRARY is None:
             retention = workspace_retention()
+            # torch brings its own copy of the HIP runtime: load it first, so
+            # that the codec library binds to the runtime torch's tensors and
+            # streams belong to (loaded the other way round, the codec's calls
+            # find no device).
+            try:
+                import torch  # noqa: F401
+            except ImportError:
+                pass
             if not os.path.exists(path):
                 raise BackendUnavailable(
                     "native HIP codec library is not built (%s); run __graft_entry__.build()" % path)
