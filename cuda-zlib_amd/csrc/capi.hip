@@ -123,8 +123,7 @@ class Workspace final : public Scratch {
       : stream_(stream), pool_(pool), device_(device) {}
   hipError_t alloc_bytes(void** p, u64 bytes) override {
     *p = nullptr;
-    if (!bytes) bytes = 1;
-    bytes = (bytes + 255) & ~u64(255);
+    bytes = scratch_round(bytes);
     if (!acquired_) {
       hipError_t err = acquire();
       if (err != hipSuccess) return err;
@@ -286,6 +285,87 @@ extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const ui
     return run_deflate(stream, ws, input, input_size, output, output_size, u32(chunk_bytes),
                        metadata);
   });
+}
+
+// ---- compression without allocation ------------------------------------------
+// HipZlibCompressNoAlloc carves its scratch from this array instead of the
+// pool.  Every GPU the library runs on holds its own copy for the life of the
+// process; calls on one GPU share it, so calls that overlap on a GPU race.
+// Host code never passes the array's name to a kernel: it uses the device
+// address hipGetSymbolAddress returns for the current device.
+constexpr u64 kNoAllocScratchBytes = 48ull << 20;
+static __device__ __align__(256) u8 scratch[kNoAllocScratchBytes];
+
+namespace hz {
+namespace {
+
+// Device address of `scratch` on `device` (which must be current), looked up
+// once per device and kept.
+hipError_t no_alloc_scratch(int device, void** out) {
+  static std::mutex* mutex = new std::mutex;
+  static std::vector<void*>* addresses = new std::vector<void*>;
+  std::lock_guard<std::mutex> lock(*mutex);
+  if (device < 0) return hipErrorInvalidDevice;
+  if (addresses->size() <= size_t(device)) addresses->resize(size_t(device) + 1, nullptr);
+  void*& slot = (*addresses)[size_t(device)];
+  if (!slot) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return err;
+    if (!p) return hipErrorInvalidSymbol;
+    slot = p;
+  }
+  *out = slot;
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace hz
+
+extern "C" int HipZlibCompressNoAlloc(hipStream_t stream, int64_t chunk_bytes,
+                                      const uint8_t* input, uint64_t input_size, uint8_t* output,
+                                      uint64_t output_size, uint32_t* metadata,
+                                      uint64_t metadata_count) {
+  if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
+  // Calls HipZlibCompress would reject with status 23 get the same result.
+  const bool bounds = output_size <= kMaxBytes && input_size <= kMaxBytes && chunk_bytes >= 256 &&
+                      chunk_bytes <= 65535;
+  u64 chunks = 1;
+  bool accepted = bounds;
+  if (bounds) {
+    chunks = chunk_count(input_size, u64(chunk_bytes));
+    accepted = 2 * chunks - 1 <= kMaxBlocks && input_size + chunks * 5 + 6 <= kMaxBytes &&
+               output_size == input_size + chunks * 5 + 6;
+  }
+  if (accepted) {
+    const u64 need = deflate_scratch_bytes(input_size, u32(chunk_bytes));
+    if (need > kNoAllocScratchBytes) {
+      g_last_error = "HipZlibCompressNoAlloc: this input needs " + std::to_string(need) +
+                     " bytes of scratch, more than the " + std::to_string(kNoAllocScratchBytes) +
+                     " bytes the no-allocation entry point holds; use HipZlibCompress";
+      return HIP_ZLIB_INVALID_ARGUMENT;
+    }
+  }
+  try {
+    DeviceScope scope;
+    hipError_t err = scope.enter(stream);
+    if (err != hipSuccess) return int(err);
+    if (output_size > kMaxBytes) return int(launch_set_meta(stream, metadata, 0, kInvalidBounds));
+    if (!accepted) {
+      err = launch_fill(stream, output, 0, output_size);
+      if (err == hipSuccess) err = launch_set_meta(stream, metadata, 0, kInvalidBounds);
+      return int(err);
+    }
+    void* region = nullptr;
+    err = no_alloc_scratch(scope.device(), &region);
+    if (err != hipSuccess) return int(err);
+    FixedScratch fixed(region, kNoAllocScratchBytes);
+    return int(run_deflate(stream, fixed, input, input_size, output, output_size,
+                           u32(chunk_bytes), metadata));
+  } catch (...) {
+    g_last_error = "native HIP codec handler exception";
+    return HIP_ZLIB_INVALID_ARGUMENT;
+  }
 }
 
 extern "C" int HipZlibCompressBatch(hipStream_t stream, int64_t chunk_bytes,

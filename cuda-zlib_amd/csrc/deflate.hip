@@ -1229,22 +1229,35 @@ namespace {
 
 u64 slot_size(u32 chunk_bytes) { return (u64(chunk_bytes) + 16 + 15) & ~u64(15); }
 
-hipError_t run_chunks(hipStream_t stream, Scratch& scratch, const u8* in, const ChunkDesc* descs,
-                      u64 chunks, const FileDesc* files, u32 file_count, u64 in_total, u8* out,
-                      u32 chunk_bytes, u32* meta) {
+// Scratch of one encode call.  Every buffer is carved before the first
+// launch, so that a call which cannot get its scratch enqueues nothing.
+struct ChunkBuffers {
+  ChunkDesc* descs = nullptr;
+  FileDesc* files = nullptr;
   u32* tokens = nullptr;
   u8* slots = nullptr;
   ChunkStats* stats = nullptr;
   ChunkResult* results = nullptr;
   u64* sums = nullptr;
   u32* file_ok = nullptr;
+};
+
+hipError_t alloc_chunks(Scratch& scratch, u64 chunks, u32 file_count, u64 in_total,
+                        u32 chunk_bytes, ChunkBuffers& b) {
+  HZ_TRY(scratch.alloc(&b.descs, chunks));
+  HZ_TRY(scratch.alloc(&b.files, file_count));
+  HZ_TRY(scratch.alloc(&b.tokens, in_total ? in_total : 1));
+  HZ_TRY(scratch.alloc(&b.slots, chunks * slot_size(chunk_bytes)));
+  HZ_TRY(scratch.alloc(&b.stats, chunks));
+  HZ_TRY(scratch.alloc(&b.results, chunks));
+  HZ_TRY(scratch.alloc(&b.sums, 4 * (chunks + 1)));
+  HZ_TRY(scratch.alloc(&b.file_ok, file_count));
+  return hipSuccess;
+}
+
+hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u64 chunks,
+                      u32 file_count, u8* out, u32 chunk_bytes, u32* meta) {
   const u64 slot_bytes = slot_size(chunk_bytes);
-  HZ_TRY(scratch.alloc(&tokens, in_total ? in_total : 1));
-  HZ_TRY(scratch.alloc(&slots, chunks * slot_bytes));
-  HZ_TRY(scratch.alloc(&stats, chunks));
-  HZ_TRY(scratch.alloc(&results, chunks));
-  HZ_TRY(scratch.alloc(&sums, 4 * (chunks + 1)));
-  HZ_TRY(scratch.alloc(&file_ok, file_count));
   const u32 parse_lds = kParseShared + history_limit(chunk_bytes) + chunk_bytes + 32;
   const u32 words = stage_words(chunk_bytes);
   const u32 emit_lds = kEmitShared + 4 * words;
@@ -1253,19 +1266,19 @@ hipError_t run_chunks(hipStream_t stream, Scratch& scratch, const u8* in, const 
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_emit),
                              hipFuncAttributeMaxDynamicSharedMemorySize, int(emit_lds)));
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
-  HZ_LAUNCH(e_parse, dim3(grid), dim3(kParseThreads), parse_lds, stream, in, descs, u32(chunks),
-            tokens, stats);
+  HZ_LAUNCH(e_parse, dim3(grid), dim3(kParseThreads), parse_lds, stream, in, b.descs, u32(chunks),
+            b.tokens, b.stats);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), emit_lds, stream, in, descs, u32(chunks),
-            tokens, stats, words, u32(slot_bytes), slots, results);
+  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), emit_lds, stream, in, b.descs, u32(chunks),
+            b.tokens, b.stats, words, u32(slot_bytes), b.slots, b.results);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, results, u32(chunks), sums);
+  HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, b.results, u32(chunks), b.sums);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, files, file_count,
-            results, sums, out, meta, file_ok);
+  HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, b.files, file_count,
+            b.results, b.sums, out, meta, b.file_ok);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_pack, dim3(grid), dim3(256), 0, stream, descs, files, u32(chunks), results, sums,
-            slots, out, file_ok);
+  HZ_LAUNCH(e_pack, dim3(grid), dim3(256), 0, stream, b.descs, b.files, u32(chunks), b.results,
+            b.sums, b.slots, out, b.file_ok);
   return hipGetLastError();
 }
 
@@ -1293,18 +1306,31 @@ __global__ __launch_bounds__(256) void e_zero_tail(u8* out, u64 capacity, const 
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
                        u64 capacity, u32 chunk_bytes, u32* meta) {
   const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
-  ChunkDesc* descs = nullptr;
-  FileDesc* file = nullptr;
-  HZ_TRY(scratch.alloc(&descs, chunks));
-  HZ_TRY(scratch.alloc(&file, 1));
+  ChunkBuffers b;
+  HZ_TRY(alloc_chunks(scratch, chunks, 1, in_size, chunk_bytes, b));
   HZ_LAUNCH(e_single_descs, dim3(u32(std::min<u64>(1024, (chunks + 255) / 256))), dim3(256), 0,
-            stream, in_size, chunk_bytes, u32(chunks), history_limit(chunk_bytes), capacity, descs,
-            file);
+            stream, in_size, chunk_bytes, u32(chunks), history_limit(chunk_bytes), capacity, b.descs,
+            b.files);
   HZ_TRY(hipGetLastError());
-  HZ_TRY(run_chunks(stream, scratch, in, descs, chunks, file, 1, in_size, out, chunk_bytes, meta));
+  HZ_TRY(run_chunks(stream, b, in, chunks, 1, out, chunk_bytes, meta));
   HZ_LAUNCH(e_zero_tail, dim3(u32(std::min<u64>(1024, (capacity / 16 + 255) / 256 + 1))), dim3(256),
             0, stream, out, capacity, meta);
   return hipGetLastError();
+}
+
+u64 deflate_scratch_bytes(u64 in_size, u32 chunk_bytes) {
+  struct Sizing final : Scratch {
+    u64 total = 0;
+    hipError_t alloc_bytes(void** p, u64 bytes) override {
+      *p = nullptr;
+      total += scratch_round(bytes);
+      return hipSuccess;
+    }
+  } sizing;
+  const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
+  ChunkBuffers b;
+  alloc_chunks(sizing, chunks, 1, in_size, chunk_bytes, b);
+  return sizing.total;
 }
 
 hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_total,
@@ -1316,13 +1342,13 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
   const u64 slot_bytes = slot_size(chunk_bytes);
   const u32 hist_max = history_limit(chunk_bytes);
   for (u32 f = 0; f < count; ++f) {
-    const BatchFile& b = files_host[f];
-    const u64 n = b.in_size;
+    const BatchFile& bf = files_host[f];
+    const u64 n = bf.in_size;
     const u64 k = n ? (n + chunk_bytes - 1) / chunk_bytes : 1;
-    files[f] = {b.in_offset, n, b.out_offset, b.out_size, u32(descs.size()), u32(k)};
+    files[f] = {bf.in_offset, n, bf.out_offset, bf.out_size, u32(descs.size()), u32(k)};
     for (u64 j = 0; j < k; ++j) {
       ChunkDesc d;
-      d.in_off = b.in_offset + j * chunk_bytes;
+      d.in_off = bf.in_offset + j * chunk_bytes;
       d.file_off = j * chunk_bytes;
       d.file_len = n;
       d.len = u32(std::min<u64>(chunk_bytes, n - std::min<u64>(n, j * chunk_bytes)));
@@ -1333,17 +1359,14 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
       descs.push_back(d);
     }
   }
-  ChunkDesc* ddescs = nullptr;
-  FileDesc* dfiles = nullptr;
-  HZ_TRY(scratch.alloc(&ddescs, descs.size()));
-  HZ_TRY(scratch.alloc(&dfiles, count));
+  ChunkBuffers b;
+  HZ_TRY(alloc_chunks(scratch, descs.size(), count, in_total, chunk_bytes, b));
   // Pageable sources: the runtime copies them before these calls return.
-  HZ_TRY(hipMemcpyAsync(ddescs, descs.data(), descs.size() * sizeof(ChunkDesc),
+  HZ_TRY(hipMemcpyAsync(b.descs, descs.data(), descs.size() * sizeof(ChunkDesc),
                         hipMemcpyHostToDevice, stream));
-  HZ_TRY(hipMemcpyAsync(dfiles, files.data(), count * sizeof(FileDesc), hipMemcpyHostToDevice,
+  HZ_TRY(hipMemcpyAsync(b.files, files.data(), count * sizeof(FileDesc), hipMemcpyHostToDevice,
                         stream));
-  return run_chunks(stream, scratch, in, ddescs, descs.size(), dfiles, count, in_total, out,
-                    chunk_bytes, meta);
+  return run_chunks(stream, b, in, descs.size(), count, out, chunk_bytes, meta);
 }
 
 }  // namespace hz

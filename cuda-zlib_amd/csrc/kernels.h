@@ -51,6 +51,9 @@ hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const
                                 u64 skip_from = ~0ull, const u32* list = nullptr,
                                 const u32* redo = nullptr);
 
+// Every scratch buffer is a multiple of 256 bytes and 256-byte aligned.
+inline u64 scratch_round(u64 bytes) { return ((bytes ? bytes : 1) + 255) & ~u64(255); }
+
 // Scratch allocation interface used by multi-kernel routes.
 struct Scratch {
   virtual hipError_t alloc_bytes(void** p, u64 bytes) = 0;
@@ -74,7 +77,25 @@ hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8
                                   u32 n, u64 in_bits, const u32* encoded, u32 max_blocks,
                                   u32* redo, u32* meta);
 
+// Scratch carved from one caller-given device region; a request past its end
+// fails with hipErrorOutOfMemory and carves nothing.
+struct FixedScratch final : Scratch {
+  u8* base;
+  u64 capacity, used = 0;
+  FixedScratch(void* region, u64 bytes) : base(static_cast<u8*>(region)), capacity(bytes) {}
+  hipError_t alloc_bytes(void** p, u64 bytes) override {
+    *p = nullptr;
+    const u64 n = scratch_round(bytes);
+    if (n > capacity - used) return hipErrorOutOfMemory;
+    *p = base + used;
+    used += n;
+    return hipSuccess;
+  }
+};
+
 // deflate.hip: chunked encode of one stream / a batch of streams.
+// deflate_scratch_bytes: the scratch run_deflate takes for one stream.
+u64 deflate_scratch_bytes(u64 in_size, u32 chunk_bytes);
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
                        u64 capacity, u32 chunk_bytes, u32* meta);
 hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_total,

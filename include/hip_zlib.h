@@ -61,6 +61,21 @@ int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_sizes, uint6
                            uint64_t encoded_cols, uint8_t* output, uint64_t output_size,
                            uint32_t* metadata, uint64_t metadata_rows, uint64_t metadata_cols);
 
+/* HipZlibCompress without any allocation: same arguments, results and
+ * metadata, but the scratch comes from a fixed 48 MiB device array that the
+ * library holds on each GPU for the life of the process, instead of the pool.
+ * It calls no hipMalloc/hipFree or allocating routine, for callers that cannot
+ * allocate (code under HIP graph capture, allocation-free serving loops).
+ * Inputs are limited by that array: with 32 KiB chunks up to about 9.5 MiB
+ * (scratch is about 5 bytes per input byte).  A larger input returns
+ * HIP_ZLIB_INVALID_ARGUMENT, with the bytes it would need in
+ * HipZlibErrorString(-1), and enqueues nothing.  Calls on one GPU share the
+ * array: calls that overlap on a GPU (on different streams, or from different
+ * threads) race, so callers serialise them.  No counterpart in the reference. */
+int HipZlibCompressNoAlloc(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
+                           uint64_t input_size, uint8_t* output, uint64_t output_size,
+                           uint32_t* metadata, uint64_t metadata_count);
+
 /* Workspace pool controls.  Replace CudaZlibSetWorkspaceRetention,
  * CudaZlibWorkspacePoolStats and CudaZlibTrimWorkspacePool (codec_ffi.cu:1113-1142).
  * Retention may only change before the first pool is created.
