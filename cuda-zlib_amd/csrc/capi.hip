@@ -264,6 +264,59 @@ extern "C" int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int
   });
 }
 
+extern "C" int HipZlibDecompressFormat(hipStream_t stream, int32_t format,
+                                       const uint8_t* dictionary, uint64_t dictionary_size,
+                                       int64_t max_candidates, int64_t max_blocks,
+                                       const uint8_t* input, uint64_t input_size, uint8_t* output,
+                                       uint64_t output_size, uint32_t* metadata,
+                                       uint64_t metadata_count) {
+  if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
+  if (format != kFormatZlib && format != kFormatRaw && format != kFormatGzip)
+    return invalid("unknown stream format (0 zlib, 1 raw DEFLATE, 2 gzip)");
+  if (format == kFormatGzip && dictionary_size) return invalid("gzip streams take no dictionary");
+  if (dictionary_size && !dictionary) return invalid("missing preset dictionary");
+  if (dictionary_size > kMaxBytes) return invalid("preset dictionary exceeds 2**32 - 1 bytes");
+  return execute(stream, [&](Workspace& ws) -> hipError_t {
+    if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, kInvalidBounds, 0);
+    auto fail = [&](u32 status) -> hipError_t {
+      hipError_t err = launch_fill(stream, output, 0, output_size);
+      if (err != hipSuccess) return err;
+      return launch_set_meta(stream, metadata, status, 0);
+    };
+    if (input_size > kMaxBytes || max_candidates < 1 || max_candidates > kMaxCandidates ||
+        max_blocks < 1 || max_blocks > kMaxBlocks)
+      return fail(kInvalidBounds);
+    const u64 fixed = format == kFormatZlib ? 8 : format == kFormatGzip ? 18 : 0;
+    if (input_size < fixed) return fail(kTruncatedZlib);
+    const bool default_limits = max_candidates == kMaxCandidates && max_blocks == kMaxBlocks;
+    if (default_limits && output_size <= 65536 && input_size <= 131072)
+      return launch_inflate_single(stream, input, input_size, output, output_size,
+                                   u32(max_blocks), metadata, u32(format), dictionary,
+                                   dictionary_size);
+    StreamFormat fmt;
+    fmt.format = u32(format);
+    fmt.dict = dictionary;
+    fmt.dict_len = dictionary_size;
+    if (!dictionary_size)
+      return run_inflate_general(stream, ws, input, input_size, output, output_size,
+                                 u32(max_candidates), u32(max_blocks), metadata, fmt);
+    // With a dictionary the output is decoded behind its last window of
+    // bytes (the history back-references may reach), then copied out.
+    const u64 hist = std::min<u64>(dictionary_size, 32768);
+    u8* ext = nullptr;
+    hipError_t err = ws.alloc(&ext, hist + output_size);
+    if (err != hipSuccess) return err;
+    err = hipMemcpyAsync(ext, dictionary + (dictionary_size - hist), hist,
+                         hipMemcpyDeviceToDevice, stream);
+    if (err != hipSuccess) return err;
+    fmt.out_base = hist;
+    err = run_inflate_general(stream, ws, input, input_size, ext, output_size,
+                              u32(max_candidates), u32(max_blocks), metadata, fmt);
+    if (err != hipSuccess || !output_size) return err;
+    return hipMemcpyAsync(output, ext + hist, output_size, hipMemcpyDeviceToDevice, stream);
+  });
+}
+
 extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
                                uint64_t input_size, uint8_t* output, uint64_t output_size,
                                uint32_t* metadata, uint64_t metadata_count) {

@@ -42,6 +42,10 @@ enum Status : u32 {
   kAdlerMismatch = 21,
   kCompressionOverflow = 22,
   kInvalidBounds = 23,
+  // Statuses of the wrapper formats the reference does not decode (gzip,
+  // raw DEFLATE, preset dictionaries); the zlib entry points never give them.
+  kGzipCheckMismatch = 24,  // gzip CRC-32 or ISIZE differs from the output
+  kDictionaryMismatch = 25, // the preset dictionary's Adler-32 is not the DICTID
 };
 
 constexpr u64 kMaxBytes = 0xffffffffull;   // per-buffer bound (4 GiB - 1)
@@ -756,6 +760,135 @@ __host__ __device__ __forceinline__ u32 check_framing(const u8* in, u64 size, u3
   window = 1u << ((cmf >> 4) + 8);
   wanted = (u32(in[size - 4]) << 24) | (u32(in[size - 3]) << 16) | (u32(in[size - 2]) << 8) |
            u32(in[size - 1]);
+  return kOk;
+}
+
+// ---- wrapper formats -----------------------------------------------------------
+// zlib (RFC 1950), raw DEFLATE (RFC 1951 alone) and gzip (RFC 1952, one
+// member).  The drop-in zlib entry points use kFormatZlib without a
+// dictionary, whose statuses are the reference's (check_framing above).
+enum Format : u32 { kFormatZlib = 0, kFormatRaw = 1, kFormatGzip = 2 };
+enum Check : u32 { kCheckNone = 0, kCheckAdler = 1, kCheckCrc = 2 };
+
+struct Frame {
+  u64 body;      // first body byte
+  u64 body_len;  // body bytes, up to the trailer
+  u32 window;    // largest allowed back-reference distance
+  u32 check;     // trailer check (Check)
+  u32 wanted;    // expected Adler-32 or CRC-32
+  u32 isize;     // gzip: output size mod 2^32
+  u32 dict_id;   // zlib with FDICT: the DICTID
+  u32 needs_dict;
+};
+
+// CRC-32 (the gzip polynomial, reflected: bit 31 holds x^0) ---------------------
+constexpr u32 kCrcPoly = 0xEDB88320u;
+
+__host__ __device__ __forceinline__ u32 crc_byte_update(u32 c, u32 byte) {
+  c ^= byte;
+#pragma unroll
+  for (u32 k = 0; k < 8; ++k) c = (c >> 1) ^ ((c & 1u) ? kCrcPoly : 0u);
+  return c;
+}
+
+// a * b mod P over GF(2), both in the reflected representation.
+__host__ __device__ inline u32 crc_mul(u32 a, u32 b) {
+  u32 p = 0;
+  for (u32 i = 0; i < 32; ++i) {
+    if ((a >> (31 - i)) & 1u) p ^= b;
+    b = (b >> 1) ^ ((b & 1u) ? kCrcPoly : 0u);  // b * x
+  }
+  return p;
+}
+
+// x^(8n) mod P: the factor that appends n bytes after a register value.
+__host__ __device__ inline u32 crc_shift_bytes(u64 n) {
+  u32 r = 1u << 31;   // x^0
+  u32 f = 1u << 23;   // x^8
+  while (n) {
+    if (n & 1u) r = crc_mul(r, f);
+    f = crc_mul(f, f);
+    n >>= 1;
+  }
+  return r;
+}
+
+// CRC-32 of a message from `linear`, its register value computed from 0 (no
+// initial or final inversion): the initial all-ones register contributes
+// ~0 * x^(8n), and the result is inverted.
+__host__ __device__ inline u32 crc_finish(u32 linear, u64 n) {
+  return ~(crc_mul(0xffffffffu, crc_shift_bytes(n)) ^ linear);
+}
+
+// Parses the wrapper of a `size`-byte stream in `format`.  `have_dict` says
+// whether the caller supplied a preset dictionary.  Statuses follow the zlib
+// route's order: truncated wrapper 14, bad header 15, gzip magic under zlib 16,
+// a preset dictionary nobody supplied 17.
+__host__ __device__ inline u32 parse_frame(const u8* in, u64 size, u32 format, bool have_dict,
+                                           Frame& f) {
+  f.body = 0;
+  f.body_len = 0;
+  f.window = 32768;
+  f.check = kCheckNone;
+  f.wanted = 0;
+  f.isize = 0;
+  f.dict_id = 0;
+  f.needs_dict = 0;
+  if (format == kFormatRaw) {
+    f.body_len = size;
+    return kOk;
+  }
+  if (format == kFormatZlib) {
+    u32 window, wanted;
+    const u32 st = check_framing(in, size, window, wanted);
+    const bool fdict = st == kUnsupportedDictionary;
+    if (st && !(fdict && have_dict)) return st;
+    f.window = fdict ? 1u << ((in[0] >> 4) + 8) : window;
+    f.check = kCheckAdler;
+    f.wanted = (u32(in[size - 4]) << 24) | (u32(in[size - 3]) << 16) | (u32(in[size - 2]) << 8) |
+               u32(in[size - 1]);
+    f.body = 2;
+    if (fdict) {
+      if (size < 12) return kTruncatedZlib;
+      f.needs_dict = 1;
+      f.dict_id = (u32(in[2]) << 24) | (u32(in[3]) << 16) | (u32(in[4]) << 8) | u32(in[5]);
+      f.body = 6;
+    }
+    f.body_len = size - f.body - 4;
+    return kOk;
+  }
+  // gzip: ID1 ID2 CM FLG MTIME(4) XFL OS [XLEN extra] [name\0] [comment\0] [CRC16],
+  // body, CRC-32 and ISIZE (little endian).
+  if (size < 18) return kTruncatedZlib;
+  if (in[0] != 0x1f || in[1] != 0x8b || in[2] != 8 || (in[3] & 0xe0)) return kInvalidHeader;
+  const u32 flg = in[3];
+  const u64 limit = size - 8;  // the header ends before the trailer
+  u64 p = 10;
+  if (flg & 4) {
+    if (p + 2 > limit) return kTruncatedZlib;
+    p += 2 + (u64(in[p]) | (u64(in[p + 1]) << 8));
+    if (p > limit) return kTruncatedZlib;
+  }
+  for (u32 field = 8; field <= 16; field <<= 1) {  // FNAME, then FCOMMENT
+    if (!(flg & field)) continue;
+    while (p < limit && in[p]) ++p;
+    if (p >= limit) return kTruncatedZlib;
+    ++p;
+  }
+  if (flg & 2) {
+    if (p + 2 > limit) return kTruncatedZlib;
+    u32 c = 0xffffffffu;
+    for (u64 i = 0; i < p; ++i) c = crc_byte_update(c, in[i]);
+    if (((~c) & 0xffffu) != (u32(in[p]) | (u32(in[p + 1]) << 8))) return kInvalidHeader;
+    p += 2;
+  }
+  f.body = p;
+  f.body_len = limit - p;
+  f.check = kCheckCrc;
+  f.wanted = u32(in[size - 8]) | (u32(in[size - 7]) << 8) | (u32(in[size - 6]) << 16) |
+             (u32(in[size - 5]) << 24);
+  f.isize = u32(in[size - 4]) | (u32(in[size - 3]) << 8) | (u32(in[size - 2]) << 16) |
+            (u32(in[size - 1]) << 24);
   return kOk;
 }
 

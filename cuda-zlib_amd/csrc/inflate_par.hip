@@ -61,6 +61,10 @@ struct State {
   u64 precount;      // entries of the dense pre-candidate array
   u64 tables_used;   // stored per-block decode tables
   u64 long_count;    // pre-candidates whose header walk left the per-lane window
+  u64 start_bit;     // body bit of the first block (0 unless a wrapper field precedes it)
+  u64 floor;         // lowest output position a back-reference may read (history allowed: 0)
+  u32 isize;         // gzip: the trailer's ISIZE
+  u32 pad2;
 };
 
 struct Segment {
@@ -398,7 +402,22 @@ __device__ __forceinline__ void build_kraft3(u16* kraft3) {
 // HLIT <= 29 and a complete code-length code (Kraft sum of the HCLEN lengths
 // == 128).  Every valid dynamic header passes; about 0.1 % of random offsets
 // do.  Bit offset 0 is excluded (it is always a candidate).
-__device__ u64 prefilter_mask(u64 len, u64 b0, const PreStage& sg, const u16* kraft3) {
+// The offsets of a thread's 64 (body bits 8*b0 .. 8*b0+63) that may be
+// candidates: those after `s0`, the first block's bit.  `first` gets s0's own
+// bit when it lies here: it is always a candidate, whatever its block type.
+__device__ __forceinline__ u64 start_mask(u64 s0, u64 b0, u64& first) {
+  const u64 lo = b0 * 8;
+  first = 0;
+  if (s0 >= lo + 64) return 0;
+  u64 m = s0 > lo ? ~0ull << (s0 - lo) : ~0ull;
+  if (s0 >= lo) {
+    first = 1ull << (s0 - lo);
+    m &= ~first;
+  }
+  return m;
+}
+
+__device__ u64 prefilter_mask(u64 len, u64 b0, const PreStage& sg, const u16* kraft3, u64 s0) {
   if (b0 >= len) return 0;
   const u64 w0 = staged_u64(sg, b0 * 8), w1 = staged_u64(sg, b0 * 8 + 64),
             w2 = staged_u64(sg, b0 * 8 + 128);
@@ -409,7 +428,8 @@ __device__ u64 prefilter_mask(u64 len, u64 b0, const PreStage& sg, const u16* kr
   u64 m = ~s1 & s2 & ~(s4 & s5 & s6 & s7);  // BTYPE == 2 and HLIT <= 29
   const u64 bits_left = (len - b0) * 8;
   if (bits_left < 64) m &= (1ull << bits_left) - 1;
-  if (!b0) m &= ~1ull;
+  u64 first;
+  m &= start_mask(s0, b0, first);
   u64 out = 0;
   while (m) {
     const u32 k = __builtin_ctzll(m);
@@ -520,12 +540,53 @@ __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, S
 
 }  // namespace
 
-__global__ __launch_bounds__(1) void g_frame(const u8* in, u64 in_size, State* st) {
-  u32 window, wanted;
-  const u32 status = check_framing(in, in_size, window, wanted);
+// Wrapper checks and the state's initial values.  `body_off` is where the
+// host-side launches place the body (2 for zlib, 10 for gzip, 0 for raw); a
+// wrapper field between it and the first block (a zlib DICTID, gzip's
+// optional fields) becomes start_bit.  A zlib stream with FDICT checks the
+// dictionary's Adler-32 against its DICTID (the workgroup sums the bytes).
+__global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 format,
+                                               const u8* dict, u64 dict_len, u64 body_off,
+                                               u64 out_base, State* st) {
+  __shared__ Frame frame;
+  __shared__ u32 status;
+  __shared__ u64 red[2][4];
+  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  if (!t) status = parse_frame(in, in_size, format, dict_len > 0, frame);
+  __syncthreads();
+  if (!status && frame.needs_dict) {  // uniform
+    u64 s = 0, w = 0;
+    for (u64 i = t; i < dict_len; i += 256) {
+      s += dict[i];
+      w += ((dict_len - i) % kAdlerMod) * dict[i];
+    }
+    s %= kAdlerMod;
+    w %= kAdlerMod;
+    for (u32 off = 32; off; off >>= 1) {
+      s += __shfl_down(s, off, 64);
+      w += __shfl_down(w, off, 64);
+    }
+    if (!lane) {
+      red[0][wave] = s;
+      red[1][wave] = w;
+    }
+    __syncthreads();
+    if (!t) {
+      const u32 a = u32((red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1) % kAdlerMod);
+      const u32 b =
+          u32((red[1][0] + red[1][1] + red[1][2] + red[1][3] + dict_len % kAdlerMod) % kAdlerMod);
+      if (((b << 16) | a) != frame.dict_id) status = kDictionaryMismatch;
+    }
+  }
+  if (t) return;
   st->status = status;
-  st->window = window;
-  st->wanted = wanted;
+  st->window = frame.window;
+  st->wanted = frame.wanted;
+  st->isize = frame.isize;
+  st->start_bit = status ? 0 : (frame.body - body_off) * 8;
+  // The dictionary's bytes before out_base are history only for a raw stream
+  // given one or a zlib stream that asks for it (FDICT).
+  st->floor = (format == kFormatRaw || frame.needs_dict) ? 0 : out_base;
   st->chain_ok = 0;
   st->candidates = 0;
   st->seeds = 0;
@@ -563,6 +624,7 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
   auto& surv = lds.surv;
   auto& pass = lds.pass;
   if (st->status) return;
+  const u64 s0 = st->start_bit;
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   build_kraft3(kraft3);
   u32 seeds = 0;
@@ -592,7 +654,8 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
                    (u64(__builtin_amdgcn_alignbyte(x2, x1, a)) << 32);
     const u64 w1 = u64(__builtin_amdgcn_alignbyte(x3, x2, a)) |
                    (u64(__builtin_amdgcn_alignbyte(x4, x3, a)) << 32);
-    u64 m = 0;
+    u64 m = 0, first = 0;
+    const u64 allowed = start_mask(s0, b0, first);
     if (b0 < len) {
       // Bit k of s_j is stream bit (8*b0 + k + j): BTYPE == 2 and HLIT <= 29.
       const u64 s1 = funnel(w0, w1, 1), s2 = funnel(w0, w1, 2);
@@ -601,7 +664,7 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
       m = ~s1 & s2 & ~(s4 & s5 & s6 & s7);
       const u64 bits_left = (len - b0) * 8;
       if (bits_left < 64) m &= (1ull << bits_left) - 1;
-      if (!b0) m &= ~1ull;
+      m &= allowed;
     }
     // Stored-endpoint seeds: LEN/NLEN complement in the staged bytes first.
   #pragma unroll
@@ -651,17 +714,15 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
     }
     __syncthreads();
     u64 mask = u64(pass[2 * t]) | (u64(pass[2 * t + 1]) << 32);
-    u64 flag = 0;
-    if (b0 == 0) {
-      mask |= 1;  // bit 0 is always a candidate
-      flag = 1;
-    }
+    const u64 flag = first;  // the first block is always a candidate
+    mask |= first;
+    u64 valid_flag = flag;
     u32 total;
     u32 base = block_exclusive_scan(__popcll(mask), scan, total);
     u32 kind = 0;
     if (total > kDiscCap) {
       mask = validate_mask(body, len, b0, mask & ~flag, &luts[0][threadIdx.x], kDiscThreads) | flag;
-      flag = mask;
+      valid_flag = mask;
       base = block_exclusive_scan(__popcll(mask), scan, total);
       kind = total > kDiscCap ? 2u : 1u;
     }
@@ -670,7 +731,7 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
       while (mask) {
         const u32 k = __builtin_ctzll(mask);
         mask &= mask - 1;
-        wg_list[wg * kDiscCap + base++] = (b0 * 8 + k) | ((flag >> k) & 1 ? kValidBit : 0);
+        wg_list[wg * kDiscCap + base++] = (b0 * 8 + k) | ((valid_flag >> k) & 1 ? kValidBit : 0);
       }
     }
     __syncthreads();  // the next range reuses the stage and the lists
@@ -716,8 +777,12 @@ __global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len
   stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
   __syncthreads();
   const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3), &luts[0][threadIdx.x], kDiscThreads);
-  if (b0 == 0) mask |= 1;
+  const u64 s0 = st->start_bit;
+  u64 first;
+  start_mask(s0, b0, first);
+  u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3, s0),
+                           &luts[0][threadIdx.x], kDiscThreads);
+  mask |= first;
   u32 total;
   u32 at = block_exclusive_scan(__popcll(mask), scan, total);
   while (mask) {
@@ -2002,7 +2067,8 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
                                                 const u32* seg_next, const u32* seg_flags,
                                                 const u32* seg_rec,
                                                 u32* exit_node, u64 len,
-                                                u64 out_size, u32 max_blocks, Segment* acc) {
+                                                u64 out_size, u32 max_blocks, Segment* acc,
+                                                u64 out_base) {
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
   __shared__ u32 lexit[kChainLdsNodes];  // exit_node in LDS when the candidates fit
@@ -2118,7 +2184,7 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
   __syncthreads();
   if (!ok) return;
   // 4. write accepted segments in order.
-  u64 offset = psize[t] - s, index = pcount[t] - k;
+  u64 offset = out_base + psize[t] - s, index = pcount[t] - k;
   cur = entry[t];
   while (cur != kNone && cur < hi) {
     acc[index].start = cand[cur];
@@ -2144,10 +2210,12 @@ struct WalkShared {
 // the fast chain did not accept the stream.  On success it rebuilds the
 // accepted list one block per entry.
 __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, State* st,
-                                                   u64 out_size, u32 max_blocks, Segment* acc) {
+                                                   u64 out_size, u32 max_blocks, Segment* acc,
+                                                   u64 out_base) {
   __shared__ WalkShared sh;
   if (st->status || st->chain_ok || threadIdx.x) return;
-  u64 next = 0, output = 0, n = 0;
+  const u64 start = st->start_bit;
+  u64 next = start, output = 0, n = 0;
   u32 status = 0;
   for (;;) {
     if (n >= max_blocks) { status = kBlockCapacity; break; }
@@ -2157,8 +2225,11 @@ __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, Stat
     if (!h.take(1, f) || !h.take(2, type)) { status = kTruncated; break; }
     if (type == 3) { status = kReservedBlock; break; }
     u64 limit = out_size - output;
-    if (next == 0 || type == 2) {
-      if (next && !dynamic_header_valid(body, len, next, sh.lut, 1)) { status = kUndiscovered; break; }
+    if (next == start || type == 2) {
+      if (next != start && !dynamic_header_valid(body, len, next, sh.lut, 1)) {
+        status = kUndiscovered;
+        break;
+      }
       limit = out_size;
     }
     BitIn r;
@@ -2172,7 +2243,7 @@ __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, Stat
     if (size > out_size - output) { status = kOutputOverflow; break; }
     acc[n].start = next;
     acc[n].end = end;
-    acc[n].prefix = output;
+    acc[n].prefix = out_base + output;
     acc[n].size = size;
     acc[n].rec_first = kNone;
     acc[n].rec_count = 1;
@@ -2292,7 +2363,7 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
             ++produced;
             continue;
           }
-          if (distance > window || distance > dst) { error = kBadDistance; break; }
+          if (distance > window || distance > dst - st->floor) { error = kBadDistance; break; }
           if (length >= kCoopMatch) {
             sh.begin = dst;
             sh.length = length;
@@ -2519,6 +2590,7 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   const u32 t = threadIdx.x;
   const u64 segments = st->accepted;
   const u32 window = st->window;
+  const u64 floor = st->floor;
   u64 unres_total = 0;  // this thread's unresolved bytes, counted once per wave at the end
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
@@ -2593,10 +2665,10 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
             // before the body end.
             if (stop + 64 <= len * 8)
               lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                       roots, unres, unres_total);
+                                       roots, unres, unres_total, floor);
             else
               lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                      roots, unres, unres_total);
+                                      roots, unres, unres_total, floor);
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
           done += count;
@@ -2921,17 +2993,102 @@ __global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n, 
   }
 }
 
-// Final status: the Adler-32 partials of g_adler's `nparts` workgroups are
-// summed by one 256-thread workgroup and compared with the trailer.
+constexpr u32 kCrcTile = 16384;  // output bytes per CRC-32 tile (256 threads x 64)
+
+// CRC-32 registers (computed from 0, no inversions) of the 16 KiB tiles of
+// out[0..n), one workgroup per tile (grid-stride).  The last tile is read
+// right-aligned behind zero bytes: leading zeros leave a register that starts
+// at 0 unchanged, so every thread's 64-byte piece has full length and the
+// pieces join with one factor per tree level (x^(8 * 64 * 2^l)).
+__global__ __launch_bounds__(256) void g_crc_tiles(const State* st, const u8* out, u64 n,
+                                                   u64* parts, u64 tiles) {
+  __shared__ u32 table[256];
+  __shared__ u32 factor[8];
+  __shared__ u32 red[256];
+  if (st->status || st->emit_status) return;
+  const u32 t = threadIdx.x;
+  table[t] = crc_byte_update(0, t);
+  if (t < 8) factor[t] = crc_shift_bytes(u64(64) << t);
+  __syncthreads();
+  for (u64 tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const u64 begin = tile * kCrcTile;
+    const u64 m = min<u64>(kCrcTile, n - begin);
+    const u64 pad = kCrcTile - m;
+    const u64 lo = u64(t) * 64;  // this thread's piece in the padded tile
+    u32 c = 0;
+    const u8* src = out + begin + lo;
+    if (!pad && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+      const uint4* v = reinterpret_cast<const uint4*>(src);
+      uint4 q[4] = {v[0], v[1], v[2], v[3]};
+      const u32* w = reinterpret_cast<const u32*>(q);
+      for (u32 j = 0; j < 16; ++j)
+        for (u32 k = 0; k < 4; ++k) c = table[(c ^ (w[j] >> (8 * k))) & 0xffu] ^ (c >> 8);
+    } else {
+      for (u32 j = 0; j < 64; ++j) {
+        const u64 p = lo + j;
+        const u32 b = p >= pad ? out[begin + p - pad] : 0u;
+        c = table[(c ^ b) & 0xffu] ^ (c >> 8);
+      }
+    }
+    red[t] = c;
+    __syncthreads();
+    for (u32 l = 0; l < 8; ++l) {
+      const u32 w = 1u << l;
+      if ((t & (2 * w - 1)) == 0) red[t] = crc_mul(red[t], factor[l]) ^ red[t + w];
+      __syncthreads();
+    }
+    if (!t) parts[tile] = red[0];
+    __syncthreads();
+  }
+}
+
+// CRC-32 of out[0..n) from g_crc_tiles' registers, by one 256-thread
+// workgroup: each thread joins a run of tiles, then the runs join pairwise.
+// Valid in thread 0.
+__device__ u32 crc_from_tiles(const u64* parts, u64 n) {
+  __shared__ u32 reg[256];
+  __shared__ u64 len[256];
+  const u32 t = threadIdx.x;
+  const u64 tiles = (n + kCrcTile - 1) / kCrcTile;
+  const u64 per = (tiles + 255) / 256;
+  const u64 lo = min<u64>(tiles, t * per), hi = min<u64>(tiles, lo + per);
+  const u32 full = crc_shift_bytes(kCrcTile);
+  u32 c = 0;
+  u64 bytes = 0;
+  for (u64 k = lo; k < hi; ++k) {
+    const u64 m = min<u64>(kCrcTile, n - k * kCrcTile);
+    c = crc_mul(c, m == kCrcTile ? full : crc_shift_bytes(m)) ^ u32(parts[k]);
+    bytes += m;
+  }
+  reg[t] = c;
+  len[t] = bytes;
+  __syncthreads();
+  for (u32 w = 1; w < 256; w <<= 1) {
+    if ((t & (2 * w - 1)) == 0) {
+      reg[t] = crc_mul(reg[t], crc_shift_bytes(len[t + w])) ^ reg[t + w];
+      len[t] += len[t + w];
+    }
+    __syncthreads();
+  }
+  return crc_finish(reg[0], n);
+}
+
+// Final status: the trailer check over the output (`check`): Adler-32 from
+// g_adler's `nparts` workgroup partials, CRC-32 and size from g_crc_tiles'
+// tile registers, or nothing; one 256-thread workgroup.
 __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, const u64* parts,
-                                                u32 nparts) {
+                                                u32 nparts, u32 check) {
   __shared__ u64 red[2][4];
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   u32 status = st->status;
   if (!status) status = st->emit_status;
   // References still unresolved after every round.
   if (!status && st->unresolved[1]) status = kReferenceDepth;
-  if (!status) {  // uniform: g_adler ran and wrote every partial
+  if (!status && check == kCheckCrc) {  // uniform
+    const u32 got = crc_from_tiles(parts, n);
+    if (!t && (got != st->wanted || u32(n) != st->isize)) status = kGzipCheckMismatch;
+  }
+  if (!status && check == kCheckAdler) {  // uniform: g_adler ran and wrote every partial
     u64 s = 0, w = 0;
     for (u32 i = t; i < nparts; i += 256) {
       s += parts[2 * i];
@@ -2960,7 +3117,7 @@ __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, con
 // Zero the output unless the stream decoded (status 0) or only its checksum failed.
 __global__ __launch_bounds__(256) void g_zero_on_failure(const State* st, u8* out, u64 n) {
   const u32 status = st->status;
-  if (!status || status == kAdlerMismatch) return;
+  if (!status || status == kAdlerMismatch || status == kGzipCheckMismatch) return;
   const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
   const u64 stride = u64(gridDim.x) * blockDim.x;
   for (u64 i = tid; i < n; i += stride) out[i] = 0;
@@ -2978,12 +3135,22 @@ u32 clamp_grid(u64 want, u32 cap) { return u32(want < 1 ? 1 : (want > cap ? cap 
 
 hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
                                u8* out, u64 out_size, u32 max_candidates, u32 max_blocks,
-                               u32* meta) {
-  const u8* body = in + 2;
-  const u64 len = in_size - 6;
+                               u32* meta, const StreamFormat& fmt) {
+  // The body as the launches see it: after the wrapper's fixed fields and
+  // before its trailer; g_frame finds where the first block starts inside it.
+  const u64 body_off = fmt.format == kFormatGzip ? 10 : fmt.format == kFormatRaw ? 0 : 2;
+  const u64 trailer = fmt.format == kFormatGzip ? 8 : fmt.format == kFormatRaw ? 0 : 4;
+  const u8* body = in + body_off;
+  const u64 len = in_size - body_off - trailer;
+  const u32 check = fmt.format == kFormatGzip ? kCheckCrc
+                    : fmt.format == kFormatRaw ? kCheckNone : kCheckAdler;
+  // The stream's output starts `out_base` bytes into `out` (dictionary history).
+  const u64 out_base = fmt.out_base, out_total = out_base + out_size;
+  u8* stream_out = out + out_base;
   State* st = nullptr;
   HZ_TRY(scratch.alloc(&st, 1));
-  HZ_LAUNCH(g_frame, dim3(1), dim3(1), 0, stream, in, in_size, st);
+  HZ_LAUNCH(g_frame, dim3(1), dim3(256), 0, stream, in, in_size, fmt.format, fmt.dict,
+            fmt.dict_len, body_off, out_base, st);
   HZ_TRY(hipGetLastError());
 
   // Discovery.
@@ -3069,16 +3236,16 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   Segment* acc = nullptr;
   HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
   HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size, seg_blocks,
-            seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc);
+            seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc, out_base);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size, max_blocks,
-            acc);
+            acc, out_base);
   HZ_TRY(hipGetLastError());
 
   // Emission and cross-segment resolution.
-  const u64 words = (out_size + 31) / 32 + 1;
+  const u64 words = (out_total + 31) / 32 + 1;
   u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr;
-  HZ_TRY(scratch.alloc(&roots, out_size ? out_size : 1));
+  HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
   HZ_TRY(scratch.alloc(&bits0, words));
   HZ_TRY(scratch.alloc(&bits1, words));
   HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
@@ -3102,16 +3269,26 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
               st, out, roots, bits0, bits1, counts, round, rounds, words);
     HZ_TRY(hipGetLastError());
   }
-  const u32 adler_groups = clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048);
-  u64* adler_parts = nullptr;
-  HZ_TRY(scratch.alloc(&adler_parts, 2 * u64(adler_groups)));
-  HZ_LAUNCH(g_adler, dim3(adler_groups), dim3(256), 0, stream, st, out, out_size, adler_parts);
-  HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_finish, dim3(1), dim3(256), 0, stream, st, out_size, meta, adler_parts,
-            adler_groups);
+  u64* parts = nullptr;
+  u32 nparts = 0;
+  if (check == kCheckAdler) {
+    nparts = clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048);
+    HZ_TRY(scratch.alloc(&parts, 2 * u64(nparts)));
+    HZ_LAUNCH(g_adler, dim3(nparts), dim3(256), 0, stream, st, stream_out, out_size, parts);
+    HZ_TRY(hipGetLastError());
+  } else if (check == kCheckCrc) {
+    const u64 tiles = (out_size + kCrcTile - 1) / kCrcTile;
+    HZ_TRY(scratch.alloc(&parts, tiles ? tiles : 1));
+    if (tiles) {
+      HZ_LAUNCH(g_crc_tiles, dim3(clamp_grid(tiles, 4096)), dim3(256), 0, stream, st, stream_out,
+                out_size, parts, tiles);
+      HZ_TRY(hipGetLastError());
+    }
+  }
+  HZ_LAUNCH(g_finish, dim3(1), dim3(256), 0, stream, st, out_size, meta, parts, nparts, check);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
-                     stream, st, out, out_size);
+                     stream, st, stream_out, out_size);
   return hipGetLastError();
 }
 

@@ -21,6 +21,16 @@ struct WaveShared {
   u32 action;  // 0 done, 1 match copy, 2 stored copy
   u32 error;
   u64 begin, length, distance, src;
+  Frame frame;
+};
+
+// Wrapper of the stream a wave decodes: the format and, for zlib streams
+// with a preset dictionary or raw streams, the dictionary whose last bytes
+// precede the output as history.
+struct WaveFormat {
+  u32 format = kFormatZlib;
+  const u8* dict = nullptr;
+  u64 dict_len = 0;
 };
 
 // Copy a match of `length` bytes to out[begin..) from `d` bytes back.  Reads
@@ -71,9 +81,30 @@ __device__ u32 wave_adler(const u8* out, u64 n, u32 lane) {
   return (b << 16) | a;
 }
 
+// CRC-32 of out[0..n) by one wave; result valid in lane 0.  Each lane takes a
+// contiguous piece (register computed from 0), and pieces are joined by
+// shuffles: left * x^(8 |right|) + right.
+__device__ u32 wave_crc(const u8* out, u64 n, u32 lane) {
+  const u64 piece = (n + kWave - 1) / kWave;
+  const u64 lo = min<u64>(n, lane * piece), hi = min<u64>(n, lo + piece);
+  u32 c = 0;
+  for (u64 i = lo; i < hi; ++i) c = crc_byte_update(c, out[i]);
+  u64 len = hi - lo;
+  for (u32 width = 1; width < kWave; width <<= 1) {
+    const u32 right = __shfl_down(c, width, kWave);
+    const u64 right_len = __shfl_down(len, width, kWave);
+    if ((lane & (2 * width - 1)) == 0 && lane + width < kWave) {
+      c = crc_mul(c, crc_shift_bytes(right_len)) ^ right;
+      len += right_len;
+    }
+  }
+  return crc_finish(c, n);
+}
+
 // Decodes one stream with a 64-thread workgroup and writes [status, 0].
 __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_size,
-                                 u32 max_blocks, u32* meta, WaveShared& sh) {
+                                 u32 max_blocks, u32* meta, WaveShared& sh,
+                                 const WaveFormat fmt = WaveFormat()) {
   const u32 lane = threadIdx.x;
   if (in_size > kMaxBytes || out_size > kMaxBytes || !max_blocks || max_blocks > kMaxBlocks) {
     if (!lane) { meta[0] = kInvalidBounds; meta[1] = 0; }
@@ -83,15 +114,32 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
   __syncthreads();
 
   // Lane-0 private parser state.
-  u32 error = 0, final_block = 0, blocks = 0, window = 0, wanted = 0;
+  u32 error = 0, final_block = 0, blocks = 0, window = 0;
   u64 produced = 0, body_bytes = 0;
   bool need_header = true, complete = false;
   BitIn r;
   if (!lane) {
-    error = check_framing(in, in_size, window, wanted);
+    sh.error = parse_frame(in, in_size, fmt.format, fmt.dict_len > 0, sh.frame);
+    // Only a zlib stream that asks for a dictionary (FDICT) uses one.
+    if (fmt.format == kFormatZlib && !sh.frame.needs_dict) sh.frame.dict_id = 0;
+  }
+  __syncthreads();
+  // The dictionary history a back-reference may reach (within the window).
+  u64 hist = 0;
+  if (!sh.error && (fmt.format == kFormatRaw || sh.frame.needs_dict)) {
+    hist = fmt.dict_len;
+    if (sh.frame.needs_dict) {
+      const u32 id = wave_adler(fmt.dict, fmt.dict_len, lane);
+      if (!lane && id != sh.frame.dict_id) sh.error = kDictionaryMismatch;
+    }
+  }
+  __syncthreads();
+  if (!lane) {
+    error = sh.error;
+    window = sh.frame.window;
     if (!error) {
-      body_bytes = in_size - 6;
-      r.init(in + 2, body_bytes, 0);
+      body_bytes = sh.frame.body_len;
+      r.init(in + sh.frame.body, body_bytes, 0);
     }
   }
 
@@ -114,7 +162,7 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
             if (u64(n) * 8 > r.avail()) { error = kTruncated; break; }
             sh.begin = produced;
             sh.length = n;
-            sh.src = (r.pos >> 3) + 2;
+            sh.src = (r.pos >> 3) + sh.frame.body;
             produced += n;
             r.seek(r.pos + u64(n) * 8);
             complete = final_block != 0;
@@ -135,7 +183,18 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
         }
         if (length > out_size - produced) { error = kOutputOverflow; break; }
         if (!distance) { out[produced++] = u8(lit); continue; }
-        if (distance > produced) { error = kBadDistance; break; }
+        if (distance > produced + hist) { error = kBadDistance; break; }
+        if (distance > produced) {
+          // Reaches into the dictionary: byte by byte, sources in the
+          // dictionary or (for an overlapping copy) in this copy's period.
+          const i64 first = i64(produced) - i64(distance);
+          for (u32 j = 0; j < length; ++j) {
+            const i64 s = first + i64(j % distance);
+            out[produced + j] = s < 0 ? fmt.dict[i64(fmt.dict_len) + s] : out[s];
+          }
+          produced += length;
+          continue;
+        }
         if (length >= kCoopMatch) {
           sh.begin = produced;
           sh.length = length;
@@ -169,9 +228,13 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
   }
 
   u32 status = sh.error;
-  if (!status) {
+  if (!status && sh.frame.check == kCheckAdler) {
     const u32 got = wave_adler(out, out_size, lane);
-    if (!lane && got != wanted) status = kAdlerMismatch;
+    if (!lane && got != sh.frame.wanted) status = kAdlerMismatch;
+  } else if (!status && sh.frame.check == kCheckCrc) {
+    const u32 got = wave_crc(out, out_size, lane);
+    if (!lane && (got != sh.frame.wanted || u32(out_size) != sh.frame.isize))
+      status = kGzipCheckMismatch;
   }
   if (!lane) {
     meta[0] = status;
@@ -183,9 +246,14 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
 
 __global__ __launch_bounds__(64) void inflate_single_kernel(const u8* in, u64 in_size, u8* out,
                                                             u64 out_size, u32 max_blocks,
-                                                            u32* meta) {
+                                                            u32* meta, u32 format, const u8* dict,
+                                                            u64 dict_len) {
   __shared__ WaveShared sh;
-  inflate_one_wave(in, in_size, out, out_size, max_blocks, meta, sh);
+  WaveFormat fmt;
+  fmt.format = format;
+  fmt.dict = dict;
+  fmt.dict_len = dict_len;
+  inflate_one_wave(in, in_size, out, out_size, max_blocks, meta, sh, fmt);
 }
 
 // One workgroup per file.  With encoded metadata (compression's
@@ -229,9 +297,10 @@ __global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out
 }
 
 hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
-                                 u64 out_size, u32 max_blocks, u32* meta) {
+                                 u64 out_size, u32 max_blocks, u32* meta, u32 format,
+                                 const u8* dict, u64 dict_len) {
   HZ_LAUNCH(inflate_single_kernel, dim3(1), dim3(kWave), 0, stream, in, in_size, out,
-                     out_size, max_blocks, meta);
+                     out_size, max_blocks, meta, format, dict, dict_len);
   return hipGetLastError();
 }
 

@@ -42,8 +42,13 @@ hipError_t launch_set_meta(hipStream_t stream, u32* meta, u32 first, u32 second)
 hipError_t launch_set_meta_rows(hipStream_t stream, u32* meta, u64 rows, u32 first, u32 second);
 
 // inflate_wave.hip: serial-route decode (one wave per stream).
+// format: kFormatZlib / kFormatRaw / kFormatGzip; dict (dict_len bytes, device)
+// is the preset dictionary of a zlib stream with FDICT or the history of a
+// raw stream (null and 0: none).
 hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
-                                 u64 out_size, u32 max_blocks, u32* meta);
+                                 u64 out_size, u32 max_blocks, u32* meta,
+                                 u32 format = kFormatZlib, const u8* dict = nullptr,
+                                 u64 dict_len = 0);
 // Files of at least skip_from output bytes are skipped; with `list`, only the
 // listed files whose `redo` flag is set are decoded.
 hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const BatchFile* files,
@@ -64,10 +69,23 @@ struct Scratch {
   virtual ~Scratch() {}
 };
 
-// inflate_par.hip: general-route decode.
+// Wrapper of a stream for the general route: its format, the preset
+// dictionary (device; a zlib stream with FDICT checks its Adler-32), and the
+// number of history bytes that precede the stream's output in the output
+// buffer (the dictionary's last bytes, placed there by the caller).
+struct StreamFormat {
+  u32 format = kFormatZlib;
+  const u8* dict = nullptr;
+  u64 dict_len = 0;
+  u64 out_base = 0;
+};
+
+// inflate_par.hip: general-route decode.  The stream's out_size bytes go to
+// out[fmt.out_base ..]; callers guarantee in_size covers the wrapper's fixed
+// fields (zlib 8 bytes, gzip 18).
 hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size,
                                u8* out, u64 out_size, u32 max_candidates, u32 max_blocks,
-                               u32* meta);
+                               u32* meta, const StreamFormat& fmt = StreamFormat());
 // Batch files listed in `list` (device) decoded by parallel slices, one
 // workgroup per file; a file that does not decode cleanly gets redo[f] = 1
 // and is left for the serial decoder, the others get [0, 0] in meta.

@@ -9,6 +9,8 @@ from ._codec import (compress_zlib, decompress_zlib, compile_kernels,
 from ._codec import (compress_zlib_batch_padded, decompress_zlib_batch_checked,
                      compress_zlib_batch, decompress_zlib_batch,
                      compress_zlib_batch_host, decompress_zlib_batch_host)
+from ._codec import (decompress_gzip, decompress_gzip_checked, decompress_deflate_raw,
+                     decompress_deflate_raw_checked)
 from ._errors import BackendUnavailable, CodecError, UnsupportedStream
 
 __all__ = ["compress_zlib", "decompress_zlib", "compile_kernels",
@@ -17,5 +19,7 @@ __all__ = ["compress_zlib", "decompress_zlib", "compile_kernels",
            "compress_zlib_batch_padded", "decompress_zlib_batch_checked",
            "compress_zlib_batch", "decompress_zlib_batch",
            "compress_zlib_batch_host", "decompress_zlib_batch_host",
+           "decompress_gzip", "decompress_gzip_checked",
+           "decompress_deflate_raw", "decompress_deflate_raw_checked",
            "BackendUnavailable", "CodecError", "UnsupportedStream"]
 __version__ = "0.1.0"

@@ -26,6 +26,8 @@ SIGNATURES = {
     "HipZlibCompress": [_P, _I64, _P, _U64, _P, _U64, _P, _U64],
     "HipZlibCompressNoAlloc": [_P, _I64, _P, _U64, _P, _U64, _P, _U64],
     "HipZlibDecompress": [_P, _I64, _I64, _P, _U64, _P, _U64, _P, _U64],
+    "HipZlibDecompressFormat": [_P, ctypes.c_int32, _P, _U64, _I64, _I64, _P, _U64, _P, _U64, _P,
+                                _U64],
     "HipZlibCompressBatch": [_P, _I64, _I64P, _U64, _P, _U64, _P, _U64, _P, _U64, _U64],
     "HipZlibDecompressBatch": [_P, _I64P, _U64, _I64P, _U64, _P, _U64, _P, _U64, _U64, _P, _U64,
                                _P, _U64, _U64],

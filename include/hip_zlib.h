@@ -41,6 +41,25 @@ int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int64_t max_bl
                       const uint8_t* input, uint64_t input_size, uint8_t* output,
                       uint64_t output_size, uint32_t* metadata, uint64_t metadata_count);
 
+/* Decompress one stream in a wrapper format the reference does not decode:
+ * format 0 zlib, 1 raw DEFLATE (RFC 1951, no wrapper or checksum), 2 gzip
+ * (RFC 1952, one member: optional header fields, FHCRC, CRC-32 and ISIZE
+ * checked).  dictionary (device, dictionary_size bytes; null and 0 for none)
+ * is the preset dictionary of a zlib stream whose header sets FDICT (its
+ * Adler-32 must equal the DICTID) or the history of a raw stream; a zlib
+ * stream without FDICT ignores it, and gzip takes none.  Arguments, metadata
+ * [status, 0] and failure behaviour are HipZlibDecompress's, with two more
+ * statuses: 24 (gzip CRC-32 or ISIZE mismatch; output kept, as for 21) and 25
+ * (dictionary Adler-32 differs from the DICTID).  Bytes after the stream's end
+ * (such as a second gzip member) give status 12.  Format 0 without a
+ * dictionary is exactly HipZlibDecompress.  No counterpart in the reference,
+ * which rejects gzip with status 16 and dictionaries with 17
+ * (src/cuda_zlib/_codec.py:105-111). */
+int HipZlibDecompressFormat(hipStream_t stream, int32_t format, const uint8_t* dictionary,
+                            uint64_t dictionary_size, int64_t max_candidates, int64_t max_blocks,
+                            const uint8_t* input, uint64_t input_size, uint8_t* output,
+                            uint64_t output_size, uint32_t* metadata, uint64_t metadata_count);
+
 /* Compress `files` packed inputs (host array input_sizes) into consecutive
  * padded slots; metadata (files x 2 u32, device) rows are [encoded_length, status].
  * The host-side size list is copied to the device before the call returns.

@@ -112,7 +112,8 @@ def test_capacity_formula_matches_the_reference():
 
 def test_status_table_is_complete():
     from cuda_zlib import _codec
-    assert sorted(_codec._MESSAGES) == [s for s in range(24) if s != 8]
+    # 0-23 are the reference's; 24 and 25 belong to the gzip / dictionary entry points.
+    assert sorted(_codec._MESSAGES) == [s for s in range(26) if s != 8]
     assert _codec._MESSAGES[21].endswith("Adler32 mismatch")
 
 
