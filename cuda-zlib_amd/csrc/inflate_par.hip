@@ -1783,19 +1783,19 @@ struct HeaderShared {
   DecodeTables tables;
   StageT<kHeaderWords> stage;
   u16 codes[320];
+  u32 runs[320];  // code-length runs of the wave walk: first index | value << 9 | repeat << 13
   u64 d0;
   u32 status, type, fin, nl, nd, build_status;
+  u32 walk, p, lim, nruns;  // wave walk: start (stage bit), read limit, runs found
 };
 
-// The code lengths of a dynamic header (g_headers, lane 0), reader after
-// BTYPE: the fields and the code-length code through `r`, then the lengths
-// with a 32-bit window over the staged words (the code-length code is
-// complete, so every 7-bit pattern is a code).  Returns false, with nothing
-// decided, when a read could pass the staged words or the body end; the
-// caller then runs parse_dynamic_lengths from the same start, so the status
-// and its order are those of parse_dynamic_lengths either way.
-__device__ bool header_lengths_fast(HeaderShared& sh, u64 len, BitIn& r, u32& nl, u32& nd,
-                                    u32& err) {
+// Fields and code-length code of a dynamic header (g_headers, lane 0),
+// reader after BTYPE.  Returns false when a read could pass the staged words
+// or the body end (the caller then runs parse_dynamic_lengths from the same
+// start, so statuses and their order are that function's either way);
+// otherwise sets err, and with err == 0 the code-length table is built and
+// sh.p / sh.lim / nl / nd describe the walk over the lengths.
+__device__ bool header_prelude(HeaderShared& sh, u64 len, BitIn& r, u32& nl, u32& nd, u32& err) {
   u32 hlit, hdist, hclen;
   if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return false;
   nl = hlit + 257;
@@ -1812,48 +1812,71 @@ __device__ bool header_lengths_fast(HeaderShared& sh, u64 len, BitIn& r, u32& nl
   err = build_cl_table(sh.tables.cl, pack);
   if (err) return true;
   const u64 bit0 = sh.stage.bit0;
-  u32 p = u32(r.pos - bit0);  // stage-relative
+  sh.p = u32(r.pos - bit0);  // stage-relative
   // A symbol and its extra bits take at most 14 bits, read from words w, w+1.
   const u64 staged = sh.stage.count > 1 ? u64(sh.stage.count - 1) * 32 : 0;
   const u64 body_end = len * 8 - bit0;
-  const u32 lim = u32(min(staged, body_end));
-  const u32 total = nl + nd;
-  u32 i = 0, prev = 0;
-  u8* lens = sh.tables.lens;
-  while (i < total) {
-    if (p + 14 > lim) return false;
-    const u32 w = p >> 5;
-    const u32 b = __builtin_amdgcn_alignbit(sh.stage.words[w + 1], sh.stage.words[w], p & 31);
-    const u32 e = sh.tables.cl.primary[b & 127];
-    const u32 l = e & 15u, sym = e >> 16;
-    if (sym < 16) {
-      lens[i++] = u8(sym);
-      prev = sym;
-      p += l;
-      continue;
-    }
-    u32 repeat, value;
-    if (sym == 16) {
-      if (!i) { err = kBadRepeat; return true; }
-      repeat = 3 + ((b >> l) & 3u);
-      value = prev;
-      p += l + 2;
-    } else if (sym == 17) {
-      repeat = 3 + ((b >> l) & 7u);
-      value = 0;
-      p += l + 3;
-    } else {
-      repeat = 11 + ((b >> l) & 127u);
-      value = 0;
-      p += l + 7;
-    }
-    if (repeat > total - i) { err = kBadRepeat; return true; }
-    for (u32 j = 0; j < repeat; ++j) lens[i++] = u8(value);
-    prev = value;
-  }
-  err = lens[256] ? kOk : kBadTree;
-  r.seek(bit0 + p);
+  sh.lim = u32(min(staged, body_end));
   return true;
+}
+
+// The code lengths of a dynamic header by the whole wave, after
+// header_prelude.  The code-length code is complete, so every 7-bit pattern
+// starts a code: each lane decodes the symbol (and extra bits) at its own bit
+// of a 64-bit batch, and the true path hops through the batch by lane reads,
+// recording runs; lanes then fill the lengths from the runs.  Returns kOk,
+// an error status (the one parse_dynamic_lengths gives: every read on the
+// path lies before the limit), or kNone when the walk would read past it.
+__device__ u32 header_lengths_wave(HeaderShared& sh, u32 total) {
+  const u32 lane = lane_id();
+  const u32 lim = sh.lim;
+  u32 p = sh.p, i = 0, prev = 0, nruns = 0, status = kOk;
+  while (i < total && status == kOk) {
+    // This lane's symbol at bit p + lane: its advance (0: past the limit),
+    // symbol and repeat count.
+    const u32 q = p + lane;
+    u32 adv = 0, sym = 0, rep = 1;
+    if (q + 14 <= lim) {
+      const u32 w = q >> 5;
+      const u32 b = __builtin_amdgcn_alignbit(sh.stage.words[w + 1], sh.stage.words[w], q & 31);
+      const u32 e = sh.tables.cl.primary[b & 127];
+      const u32 l = e & 15u;
+      sym = e >> 16;
+      const u32 x = b >> l;
+      adv = sym < 16 ? l : sym == 16 ? l + 2 : sym == 17 ? l + 3 : l + 7;
+      rep = sym < 16 ? 1u : sym == 16 ? 3 + (x & 3u) : sym == 17 ? 3 + (x & 7u) : 11 + (x & 127u);
+      if (!l) adv = 0;
+    }
+    u32 off = 0;  // uniform: the path's position in the batch
+    while (off < 64 && i < total) {
+      const u32 a = u32(__builtin_amdgcn_readlane(int(adv), int(off)));
+      if (!a) return kNone;
+      const u32 sy = u32(__builtin_amdgcn_readlane(int(sym), int(off)));
+      const u32 r = u32(__builtin_amdgcn_readlane(int(rep), int(off)));
+      if (sy == 16 && !i) { status = kBadRepeat; break; }
+      if (r > total - i) { status = kBadRepeat; break; }
+      const u32 value = sy < 16 ? sy : sy == 16 ? prev : 0u;
+      if (!lane) sh.runs[nruns] = i | (value << 9) | (r << 13);
+      ++nruns;
+      i += r;
+      prev = value;
+      off += a;
+    }
+    p += off;
+  }
+  wave_sync();
+  if (status == kOk) {
+    for (u32 k = lane; k < nruns; k += 64) {
+      const u32 e = sh.runs[k];
+      const u32 first = e & 511u, value = (e >> 9) & 15u, r = e >> 13;
+      for (u32 j = 0; j < r; ++j) sh.tables.lens[first + j] = u8(value);
+    }
+    wave_sync();
+    if (!sh.tables.lens[256]) status = kBadTree;
+  }
+  if (!lane) sh.p = p;
+  wave_sync();
+  return status;
 }
 }  // namespace
 
@@ -1874,20 +1897,40 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
     const u64 pos = cand[c];
     stage_range(body, len, pos, pos + 8, sh.stage, kHeaderBytes);
     __syncthreads();
+    // Lane 0 reads the fields and the code-length code; the wave walks the
+    // lengths; lane 0 falls back to the serial parser when the walk cannot
+    // finish within the staged words.
+    u64 start = 0;
     if (!lane) {
       BitIn r = staged_reader(sh.stage, len, pos);
       u32 fin = 0, type = 0, err = 0, nl = 0, nd = 0;
+      sh.walk = 0;
       if (!r.take(1, fin) || !r.take(2, type)) err = kTruncated;
       else if (type == 2) {
-        const u64 start = r.pos;
-        if (!header_lengths_fast(sh, len, r, nl, nd, err)) {
-          r.seek(start);
-          err = parse_dynamic_lengths(sh.tables, r, nl, nd);
-        }
+        start = r.pos;
+        if (!header_prelude(sh, len, r, nl, nd, err)) err = kNone;
+        else if (!err) sh.walk = 1;
       }
       sh.status = err;
       sh.type = type;
       sh.fin = fin;
+      sh.nl = nl;
+      sh.nd = nd;
+      sh.d0 = r.pos;
+    }
+    __syncthreads();
+    if (sh.walk) {
+      const u32 st_walk = header_lengths_wave(sh, sh.nl + sh.nd);
+      if (!lane) {
+        sh.status = st_walk;
+        sh.d0 = sh.stage.bit0 + sh.p;
+      }
+    }
+    __syncthreads();
+    if (!lane && sh.status == kNone) {
+      BitIn r = staged_reader(sh.stage, len, start);
+      u32 nl = 0, nd = 0;
+      sh.status = parse_dynamic_lengths(sh.tables, r, nl, nd);
       sh.nl = nl;
       sh.nd = nd;
       sh.d0 = r.pos;
@@ -2281,8 +2324,10 @@ __device__ __forceinline__ void bit_set(u32* bits, u64 i) {
 // Copies one output byte from `src` to `dst` inside a segment starting at
 // `seg`; sources outside the segment or still unresolved make the byte
 // unresolved.  Returns true when the byte was queued.
+// Written bytes are added to Adler-32 sums S (s) and W (w), a byte at output
+// position p weighing end - p.
 __device__ __forceinline__ bool copy_byte(u8* out, u32* roots, u32* unres, u64 seg, u64 dst,
-                                          u64 src) {
+                                          u64 src, u64& s, u64& w, u64 end) {
   if (src < seg) {
     roots[dst] = u32(src);
     bit_set(unres, dst);
@@ -2293,8 +2338,42 @@ __device__ __forceinline__ bool copy_byte(u8* out, u32* roots, u32* unres, u64 s
     bit_set(unres, dst);
     return true;
   }
-  out[dst] = out[src];
+  const u8 v = out[src];
+  out[dst] = v;
+  s += v;
+  w += (end - dst) * v;
+  if (w >> 62) w %= kAdlerMod;
   return false;
+}
+
+// Adler-32 pairs are added (atomically) into this many slots per producing
+// kernel, so that g_finish sums a few hundred pairs whatever the grids.
+constexpr u32 kAdlerSlots = 64;
+
+// Sum of a workgroup's per-thread Adler-32 pairs, reduced mod 65521 (valid
+// in thread 0); `red` holds two u64 per wave.
+__device__ __forceinline__ void adler_block_sum(u64& s, u64& w, u64 (*red)[16]) {
+  const u32 t = threadIdx.x, waves = blockDim.x / 64;
+  s %= kAdlerMod;
+  w %= kAdlerMod;
+  for (u32 off = 32; off; off >>= 1) {
+    s += __shfl_down(s, off, 64);
+    w += __shfl_down(w, off, 64);
+  }
+  if (lane_id() == 0) {
+    red[0][t >> 6] = s;
+    red[1][t >> 6] = w;
+  }
+  __syncthreads();
+  if (!t) {
+    s = w = 0;
+    for (u32 k = 0; k < waves; ++k) {
+      s += red[0][k];
+      w += red[1][k];
+    }
+    s %= kAdlerMod;
+    w %= kAdlerMod;
+  }
 }
 
 }  // namespace
@@ -2303,12 +2382,14 @@ __device__ __forceinline__ bool copy_byte(u8* out, u32* roots, u32* unres, u64 s
 // payloads and long matches.  Output positions are absolute.
 __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, State* st,
                                                     const Segment* acc, u8* out, u32* roots,
-                                                    u32* unres) {
+                                                    u32* unres, u64 out_end, u64* parts) {
   __shared__ EmitShared sh;
+  __shared__ u64 red[2][16];
   if (st->status) return;
   const u32 lane = threadIdx.x;
   const u64 segments = st->accepted;
   const u32 window = st->window;
+  u64 as = 0, aw = 0;  // Adler-32 sums of the bytes this lane writes
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
     if (seg.rec_first != kNone) continue;
@@ -2360,6 +2441,9 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
           if (length > seg.size - produced) { error = kExtent; break; }
           if (!distance) {
             out[dst] = u8(lit);
+            as += lit;
+            aw += (out_end - dst) * lit;
+            if (aw >> 62) aw %= kAdlerMod;
             ++produced;
             continue;
           }
@@ -2374,7 +2458,7 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
           }
           for (u32 j = 0; j < length; ++j) {
             const u64 src = dst - distance + (j % distance);
-            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src))
+            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src, as, aw, out_end))
               atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), 1ull);
           }
           produced += length;
@@ -2391,31 +2475,55 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
         for (u64 j0 = 0; j0 < length; j0 += kWave) {
           const u64 j = j0 + lane;
           bool queued = false;
-          if (j < length) queued = copy_byte(out, roots, unres, seg.prefix, begin + j, begin - d + (j % d));
+          if (j < length)
+            queued = copy_byte(out, roots, unres, seg.prefix, begin + j, begin - d + (j % d), as,
+                               aw, out_end);
           const u64 bal = __ballot(queued);
           if (!lane && bal)
             atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), u64(__popcll(bal)));
         }
       } else {
-        for (u64 j = lane; j < length; j += kWave) out[begin + j] = body[sh.src + j];
+        for (u64 j = lane; j < length; j += kWave) {
+          const u8 v = body[sh.src + j];
+          out[begin + j] = v;
+          as += v;
+          aw += (out_end - begin - j) * v;
+          if (aw >> 62) aw %= kAdlerMod;
+        }
       }
       __syncthreads();
     }
     if (!lane && sh.error) atomicMax(&st->emit_status, sh.error);
     __syncthreads();
   }
+  // Most workgroups emit nothing here (segments without block records are
+  // rare): skip the reduction when no lane wrote a byte.
+  if (__ballot((as | aw) != 0) == 0) return;
+  adler_block_sum(as, aw, red);
+  if (!lane) {
+    const u32 slot = blockIdx.x % kAdlerSlots;
+    atomicAdd(reinterpret_cast<unsigned long long*>(&parts[2 * slot]), as);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&parts[2 * slot + 1]), aw);
+  }
 }
 
 namespace {
 constexpr u32 kEmitThreads = kDescThreads;
+
+// Output bytes of one round (256 slices) that g_emit_lanes stages in LDS
+// before writing them out in 16-byte stores; rounds with more output write
+// the output buffer directly.
+constexpr u32 kOutStage = 15104;
 
 struct LaneEmitShared {
   DecodeTables tables;
   Stage stage;
   u16 codes[320];
   BlockRec rec;
-  u64 first, chunk_end;
+  u64 first, chunk_end, round_lo, round_hi;
   u32 count, next_g, need;
+  u64 red[2][kEmitThreads / 64];
+  __align__(16) u8 ostage[kOutStage + 16];
   // block_header interface
   u64 pos, d0, end, size;
   u32 type, final_block, status, nl, nd, build_status;
@@ -2437,10 +2545,90 @@ __device__ __forceinline__ void bits_set_range(u32* bits, u64 start, u32 n) {
   atomicOr(bits + w1, hi);
 }
 
+// Adler-32 partial sums of output bytes as they are produced: S = sum of the
+// bytes, W = sum of (end - position) * byte, where `end` is the stream's end
+// position, so that a byte at stream position i weighs n - i.  W is reduced
+// mod 65521 before it can wrap.
+struct AdlerAcc {
+  u64 s = 0, w = 0;
+  __device__ __forceinline__ void add_byte(u32 x, u64 weight) {
+    s += x;
+    w += weight * x;
+    if (w >> 62) w %= kAdlerMod;
+  }
+  // Sixteen bytes whose first weighs `weight0` (each next one 1 less).
+  __device__ __forceinline__ void add16(const uint4& q, u64 weight0) {
+    const u32 words[4] = {q.x, q.y, q.z, q.w};
+    u32 cs = 0, cl = 0;
+#pragma unroll
+    for (u32 k = 0; k < 4; ++k) {
+      const u32 ws = __builtin_amdgcn_udot4(words[k], 0x01010101u, 0u, false);
+      cs += ws;
+      cl += __builtin_amdgcn_udot4(words[k], 0x03020100u, 0u, false) + 4 * k * ws;
+    }
+    s += cs;
+    w += weight0 * cs - cl;
+    if (w >> 62) w %= kAdlerMod;
+  }
+};
+
+// Where a slice's output bytes go.  GlobalBytes writes the output buffer (and
+// with kAdler adds every byte to the thread's Adler-32 sums); StagedBytes
+// writes a workgroup's LDS stage that holds output positions [base, ...),
+// copied out (and summed) once the round is done.  zero() fills bytes whose
+// value a later resolve round provides.
+template <bool kAdler>
+struct GlobalBytes {
+  u8* out;
+  AdlerAcc* acc;
+  u64 end;
+  __device__ __forceinline__ u8 get(u64 p) const { return out[p]; }
+  __device__ __forceinline__ void put(u64 p, u8 v) const {
+    out[p] = v;
+    if (kAdler) acc->add_byte(v, end - p);
+  }
+  __device__ __forceinline__ void zero(u64, u32) const {}
+};
+
+struct StagedBytes {
+  u8* lds;
+  u64 base;
+  __device__ __forceinline__ u8 get(u64 p) const { return lds[p - base]; }
+  __device__ __forceinline__ void put(u64 p, u8 v) const { lds[p - base] = v; }
+  __device__ __forceinline__ void zero(u64 p, u32 n) const {
+    for (u32 j = 0; j < n; ++j) lds[p - base + j] = 0;
+  }
+};
+
+// A round's output: positions [base, base + kOutStage) in the LDS stage
+// (copied out and summed when the round is done), later ones straight to
+// the output buffer (summed as they are written).
+struct RoundBytes {
+  u8* lds;
+  u64 base, split;  // split = base + stage bytes
+  u8* out;
+  AdlerAcc* acc;
+  u64 end;
+  __device__ __forceinline__ u8 get(u64 p) const { return p < split ? lds[u32(p - base)] : out[p]; }
+  __device__ __forceinline__ void put(u64 p, u8 v) const {
+    if (p < split) {
+      lds[u32(p - base)] = v;
+    } else {
+      out[p] = v;
+      acc->add_byte(v, end - p);
+    }
+  }
+  __device__ __forceinline__ void zero(u64 p, u32 n) const {
+    for (u32 j = 0; j < n; ++j)
+      if (p + j < split) lds[u32(p + j - base)] = 0;
+  }
+};
+
 // out[dst + j] = out[src0 + j] for j < length where src0 + distance = dst:
 // an overlapping copy repeats the first `distance` bytes, so every byte is
 // read from [src0, dst), never from this copy's own stores.
-__device__ __forceinline__ void copy_periodic(u8* out, u64 dst, u64 src0, u32 distance,
+template <class Sink>
+__device__ __forceinline__ void copy_periodic(const Sink& out, u64 dst, u64 src0, u32 distance,
                                               u32 length) {
   if (distance >= 8) {
     u32 k = 0;  // source index of byte j, j mod distance
@@ -2449,19 +2637,19 @@ __device__ __forceinline__ void copy_periodic(u8* out, u64 dst, u64 src0, u32 di
 #pragma unroll
       for (u32 i = 0; i < 8; ++i) {
         const u32 kk = k + i >= distance ? k + i - distance : k + i;
-        v[i] = j + i < length ? out[src0 + kk] : u8(0);
+        v[i] = j + i < length ? out.get(src0 + kk) : u8(0);
       }
 #pragma unroll
       for (u32 i = 0; i < 8; ++i)
-        if (j + i < length) out[dst + j + i] = v[i];
+        if (j + i < length) out.put(dst + j + i, v[i]);
       k = k + 8 >= distance ? k + 8 - distance : k + 8;
     }
   } else {
     u64 pattern = 0;
-    for (u32 i = 0; i < distance; ++i) pattern |= u64(out[src0 + i]) << (8 * i);
+    for (u32 i = 0; i < distance; ++i) pattern |= u64(out.get(src0 + i)) << (8 * i);
     u32 k = 0;
     for (u32 j = 0; j < length; ++j) {
-      out[dst + j] = u8(pattern >> (8 * k));
+      out.put(dst + j, u8(pattern >> (8 * k)));
       k = k + 1 == distance ? 0u : k + 1;
     }
   }
@@ -2471,10 +2659,16 @@ __device__ __forceinline__ void copy_periodic(u8* out, u64 dst, u64 src0, u32 di
 // dst's first 16-byte boundary, then 16-byte stores of source dwords
 // realigned with v_alignbyte, then the tail bytes.  Source dwords are read
 // only while they lie before src_end.
+// With `acc`, every copied byte is also added to the Adler-32 sums; the
+// destination's first byte weighs `weight0`.
 __device__ __forceinline__ void copy_bytes(u8* dst, const u8* src, u64 n, const u8* src_end,
-                                           u32 first, u32 step) {
+                                           u32 first, u32 step, AdlerAcc* acc = nullptr,
+                                           u64 weight0 = 0) {
   const u64 head = min<u64>(n, (16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15);
-  for (u64 i = first; i < head; i += step) dst[i] = src[i];
+  for (u64 i = first; i < head; i += step) {
+    dst[i] = src[i];
+    if (acc) acc->add_byte(src[i], weight0 - i);
+  }
   const uintptr_t s0 = reinterpret_cast<uintptr_t>(src + head);
   const u32* s32 = reinterpret_cast<const u32*>(s0 & ~uintptr_t(3));
   const u32 sh = u32(s0 & 3);
@@ -2492,17 +2686,21 @@ __device__ __forceinline__ void copy_bytes(u8* dst, const u8* src, u64 n, const 
     o.z = __builtin_amdgcn_alignbyte(x3, x2, sh);
     o.w = __builtin_amdgcn_alignbyte(x4, x3, sh);
     *reinterpret_cast<uint4*>(dst + head + 16 * j) = o;
+    if (acc) acc->add16(o, weight0 - head - 16 * j);
   }
-  for (u64 i = head + 16 * blocks + first; i < n; i += step) dst[i] = src[i];
+  for (u64 i = head + 16 * blocks + first; i < n; i += step) {
+    dst[i] = src[i];
+    if (acc) acc->add_byte(src[i], weight0 - i);
+  }
 }
 
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
 // [.., block_end) of a stream whose output starts at out[floor]; adds the
 // slice's unresolved bytes to `unres_total`.  Returns 0 or an error.  `sh`
 // holds the block's tables and the staged bits.
-template <bool kChecked, class Shared>
+template <bool kChecked, class Shared, class Sink>
 __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u64 block_end,
-                          u32 window, u8* out, u32* roots, u32* unres, u64& unres_total,
+                          u32 window, const Sink& out, u32* roots, u32* unres, u64& unres_total,
                           u64 floor = 0) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
@@ -2525,7 +2723,7 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
     }
     if (length > block_end - dst) { err = kExtent; break; }
     if (length == 1) {
-      out[dst++] = u8(x);
+      out.put(dst++, u8(x));
       continue;
     }
     const u32 distance = x;
@@ -2535,6 +2733,7 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
       // Every source precedes the slice: unresolved, rooted at the source.
       for (u32 j = 0; j < length; ++j) roots[dst + j] = u32(src0 + j);
       bits_set_range(unres, dst, length);
+      out.zero(dst, length);
       nunres += length;
     } else if (!nunres && src0 >= dst0) {
       // Every source is this slice's own resolved output.
@@ -2547,10 +2746,11 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
         const u32 root = before ? u32(p) : roots[p];
         for (u32 j = 0; j < length; ++j) roots[dst + j] = root;
         bits_set_range(unres, dst, length);
+        out.zero(dst, length);
         nunres += length;
       } else {
-        const u8 v = out[p];
-        for (u32 j = 0; j < length; ++j) out[dst + j] = v;
+        const u8 v = out.get(p);
+        for (u32 j = 0; j < length; ++j) out.put(dst + j, v);
       }
     } else {
       for (u32 j = 0; j < length; ++j) {
@@ -2558,13 +2758,15 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
         if (src < dst0) {
           roots[d] = u32(src);
           bit_set(unres, d);
+          out.zero(d, 1);
           ++nunres;
         } else if (nunres && bit_get(unres, src)) {
           roots[d] = roots[src];
           bit_set(unres, d);
+          out.zero(d, 1);
           ++nunres;
         } else {
-          out[d] = out[src];
+          out.put(d, out.get(src));
         }
       }
     }
@@ -2581,10 +2783,10 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
 // describe stored (or rebuilt from the header), writing output in place.  A
 // byte copied from before its slice's output start is queued as unresolved
 // (root = source position).
-__global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
+__global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4))) void g_emit_lanes(
     const u8* body, u64 len, State* st, const Segment* acc, const BlockRec* recs,
     const u64* slice_entry, const u32* slice_off, const u32* group_link,
-    const BlockTables* tables, u8* out, u32* roots, u32* unres) {
+    const BlockTables* tables, u8* out, u32* roots, u32* unres, u64 out_end, u64* parts) {
   __shared__ LaneEmitShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -2592,6 +2794,7 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   const u32 window = st->window;
   const u64 floor = st->floor;
   u64 unres_total = 0;  // this thread's unresolved bytes, counted once per wave at the end
+  AdlerAcc sums;        // Adler-32 sums of the bytes this thread writes
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
     if (seg.rec_first == kNone) continue;
@@ -2611,7 +2814,8 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
       __syncthreads();
       const BlockRec rec = sh.rec;
       if (rec.type == 0) {
-        copy_bytes(out + block_out, body + (rec.data >> 3), rec.size, body + len, t, kEmitThreads);
+        copy_bytes(out + block_out, body + (rec.data >> 3), rec.size, body + len, t, kEmitThreads,
+                   &sums, out_end - block_out);
       } else {
         if (rec.table == kNone) {
           block_header<true, true>(body, len, ~0ull, sh);
@@ -2649,28 +2853,63 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
             sh.first = entry;
             sh.chunk_end = next_g != kNone ? slice_entry[u64(next_g) * 64] : rec.end;
             sh.need = !staged_covers(sh.stage, body, len, entry, sh.chunk_end);
+            // The round's output: from its first slice to the next round's.
+            sh.round_lo = block_out + off;
+            sh.round_hi = block_out + (next_g != kNone ? slice_off[u64(next_g) * 64] : rec.size);
           }
           __syncthreads();
           if (sh.need) {
             stage_range(body, len, sh.first, sh.chunk_end, sh.stage);
             __syncthreads();
           }
+          // The round's output goes through the LDS stage, whose byte 0 is
+          // the output position `lo16` (16-byte aligned in memory), as far
+          // as the stage reaches; any rest goes straight to the output.
+          const u64 lo = sh.round_lo, hi = sh.round_hi;
+          const u64 skew = (reinterpret_cast<uintptr_t>(out) + lo) & 15u;
+          const u64 lo16 = lo - skew;
+          const u64 split = min<u64>(hi, lo16 + kOutStage);
           u32 lerr = 0;
           if (t < count) {
             if (t + 1 >= count) stop = sh.chunk_end;
             const u64 dst0 = block_out + off;
             const u32 blim = stage_limit(sh.stage, len);
             const u32 e_rel = u32(entry - sh.stage.bit0), s_rel = u32(stop - sh.stage.bit0);
+            // Writes stay inside the round: a slice that would pass its end
+            // is an extent error.
+            const u64 rend = min(block_out + rec.size, hi);
+            const RoundBytes sink{sh.ostage, lo16, split, out, &sums, out_end};
             // Unchecked decoding when the slice and a token of overshoot lie
             // before the body end.
-            if (stop + 64 <= len * 8)
-              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                       roots, unres, unres_total, floor);
+            if (dst0 < lo)
+              lerr = kExtent;  // offsets out of order: never from a consistent describe
+            else if (stop + 64 <= len * 8)
+              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
+                                       unres, unres_total, floor);
             else
-              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_out + rec.size, window, out,
-                                      roots, unres, unres_total, floor);
+              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
+                                      unres, unres_total, floor);
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
+          // The staged part in whole 16-byte lines (bytes of the neighbouring
+          // round in its first line one by one), summed on the way.
+          __syncthreads();
+          const u64 span = split - lo16;
+          for (u64 k = t; 16 * k < span; k += kEmitThreads) {
+            const u64 r0 = 16 * k, a = lo16 + r0;
+            if (r0 >= skew && r0 + 16 <= span) {
+              const uint4 q = *reinterpret_cast<const uint4*>(sh.ostage + r0);
+              *reinterpret_cast<uint4*>(out + a) = q;
+              sums.add16(q, out_end - a);
+            } else {
+              for (u32 j = 0; j < 16; ++j) {
+                if (r0 + j < skew || r0 + j >= span) continue;
+                const u8 v = sh.ostage[r0 + j];
+                out[a + j] = v;
+                sums.add_byte(v, out_end - (a + j));
+              }
+            }
+          }
           done += count;
           g = sh.next_g;
           __syncthreads();
@@ -2686,6 +2925,29 @@ __global__ __launch_bounds__(kEmitThreads) void g_emit_lanes(
   for (u32 off = 32; off; off >>= 1) unres_total += __shfl_down(unres_total, off, 64);
   if (lane_id() == 0 && unres_total)
     atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), unres_total);
+  // The workgroup's Adler-32 partial pair.
+  u64 ps = sums.s % kAdlerMod, pw = sums.w % kAdlerMod;
+  for (u32 off = 32; off; off >>= 1) {
+    ps += __shfl_down(ps, off, 64);
+    pw += __shfl_down(pw, off, 64);
+  }
+  if (lane_id() == 0) {
+    sh.red[0][t >> 6] = ps;
+    sh.red[1][t >> 6] = pw;
+  }
+  __syncthreads();
+  if (!t) {
+    u64 a = 0, b = 0;
+    for (u32 w = 0; w < kEmitThreads / 64; ++w) {
+      a += sh.red[0][w];
+      b += sh.red[1][w];
+    }
+    const u32 slot = blockIdx.x % kAdlerSlots;
+    if (a | b) {  // workgroups that wrote nothing add nothing
+      atomicAdd(reinterpret_cast<unsigned long long*>(&parts[2 * slot]), a % kAdlerMod);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&parts[2 * slot + 1]), b % kAdlerMod);
+    }
+  }
 }
 
 // Large files of a batch: one 256-thread workgroup per file decodes its
@@ -2787,10 +3049,12 @@ __global__ __launch_bounds__(kDescThreads) void g_batch_wide(
             const u32 e_rel = u32(entry - sh.stage.bit0), s_rel = u32(stop - sh.stage.bit0);
             u32 lerr;
             if (stop + 64 <= len * 8)
-              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_end, window, out, roots,
+              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_end, window,
+                                       GlobalBytes<false>{out, nullptr, 0}, roots,
                                        unres, unres_total, base);
             else
-              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_end, window, out, roots,
+              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_end, window,
+                                      GlobalBytes<false>{out, nullptr, 0}, roots,
                                       unres, unres_total, base);
             if (lerr) bad = 1;
           }
@@ -2879,12 +3143,17 @@ constexpr u32 kResolveLinks = 32;  // chain links a position follows per round
 // kResolveLinks^(r+1) links.  Only bytes written by earlier launches are
 // read.  The last round leaves its count in st->unresolved[1] (status 20 in
 // g_finish).
+// With `parts`, every resolved byte is added to this workgroup's Adler-32
+// pair parts[2b], parts[2b + 1] (a byte at position p weighs out_end - p).
 __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
                                                  u32* bits1, u64* counts, u32 round,
-                                                 u32 max_rounds, u64 words) {
+                                                 u32 max_rounds, u64 words, u64 out_end,
+                                                 u64* parts) {
+  __shared__ u64 red[2][16];
   if (st->status || st->emit_status) return;
   const u64 n_in = round ? counts[round] : st->unresolved[0];
   if (!n_in) return;
+  u64 as = 0, aw = 0;
   const u32* bits = round & 1 ? bits1 : bits0;
   u32* next_bits = round & 1 ? bits0 : bits1;
   u64* next_count = round + 1 == max_rounds ? &st->unresolved[1] : &counts[round + 1];
@@ -2918,8 +3187,15 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
           r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           unres = (bits[r >> 5] >> (r & 31)) & 1u;
         }
-        if (!unres) out[u] = out[r];
-        else __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!unres) {
+          const u8 v = out[r];
+          out[u] = v;
+          as += v;
+          aw += (out_end - u) * v;
+          if (aw >> 62) aw %= kAdlerMod;
+        } else {
+          __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       const u64 keep = __ballot(unres);
       if (lane == 0) next_bits[g * 64 + i0] = u32(keep);
@@ -2928,68 +3204,13 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
     }
   }
   if (lane_id() == 0 && kept) atomicAdd(reinterpret_cast<unsigned long long*>(next_count), u64(kept));
-}
-
-// Adler-32 partial sums, accumulated into the state: every thread takes
-// 16-byte chunks (byte sums and position-weighted sums by dot products), four
-// loads in flight at a time, so the output is read once with 16-byte loads.
-// For a chunk at offset a, sum over it of (n - i) x_i = (n - a) S - L with
-// L = sum of (i - a) x_i; the weighted sum is reduced mod 65521 whenever it
-// reaches 2^62, so it never wraps.
-__global__ __launch_bounds__(256) void g_adler(State* st, const u8* out, u64 n, u64* parts) {
-  __shared__ u64 red[2][4];
-  if (st->status || st->emit_status) return;
-  const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
-  const u64 tid = u64(blockIdx.x) * 256 + t, stride = u64(gridDim.x) * 256;
-  u64 s = 0, w = 0;
-  const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
-  const u64 chunks = aligned ? n / 16 : 0;
-  const uint4* v = reinterpret_cast<const uint4*>(out);
-  auto add_chunk = [&](const uint4& q, u64 c) {
-    const u32 words[4] = {q.x, q.y, q.z, q.w};
-    u32 cs = 0, cl = 0;
-#pragma unroll
-    for (u32 k = 0; k < 4; ++k) {
-      const u32 ws = __builtin_amdgcn_udot4(words[k], 0x01010101u, 0u, false);
-      cs += ws;
-      cl += __builtin_amdgcn_udot4(words[k], 0x03020100u, 0u, false) + 4 * k * ws;
+  if (parts) {  // uniform
+    adler_block_sum(as, aw, red);
+    if (!threadIdx.x) {
+      const u32 slot = blockIdx.x % kAdlerSlots;
+      atomicAdd(reinterpret_cast<unsigned long long*>(&parts[2 * slot]), as);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&parts[2 * slot + 1]), aw);
     }
-    s += cs;
-    w += (n - c * 16) * cs - cl;
-    if (w >> 62) w %= kAdlerMod;
-  };
-  constexpr u32 kInFlight = 4;
-  u64 c = tid;
-  for (; c + (kInFlight - 1) * stride < chunks; c += kInFlight * stride) {
-    uint4 q[kInFlight];
-#pragma unroll
-    for (u32 k = 0; k < kInFlight; ++k) q[k] = v[c + k * stride];
-#pragma unroll
-    for (u32 k = 0; k < kInFlight; ++k) add_chunk(q[k], c + k * stride);
-  }
-  for (; c < chunks; c += stride) add_chunk(v[c], c);
-  for (u64 i = chunks * 16 + tid; i < n; i += stride) {
-    const u32 b = out[i];
-    s += b;
-    w += (n - i) * b;
-    if (w >> 62) w %= kAdlerMod;
-  }
-  s %= kAdlerMod;
-  w %= kAdlerMod;
-  for (u32 off = 32; off; off >>= 1) {
-    s += __shfl_down(s, off, 64);
-    w += __shfl_down(w, off, 64);
-  }
-  if (!lane) {
-    red[0][wave] = s;
-    red[1][wave] = w;
-  }
-  __syncthreads();
-  // One partial pair per workgroup (g_finish adds them): same-address
-  // atomics from every workgroup would serialise.
-  if (!t) {
-    parts[2 * blockIdx.x] = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) % kAdlerMod;
-    parts[2 * blockIdx.x + 1] = (red[1][0] + red[1][1] + red[1][2] + red[1][3]) % kAdlerMod;
   }
 }
 
@@ -3074,8 +3295,9 @@ __device__ u32 crc_from_tiles(const u64* parts, u64 n) {
 }
 
 // Final status: the trailer check over the output (`check`): Adler-32 from
-// g_adler's `nparts` workgroup partials, CRC-32 and size from g_crc_tiles'
-// tile registers, or nothing; one 256-thread workgroup.
+// the `nparts` pairs the emitters and resolve rounds accumulated (every
+// output byte is summed once, by whichever kernel wrote it), CRC-32 and size
+// from g_crc_tiles' tile registers, or nothing; one 256-thread workgroup.
 __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, const u64* parts,
                                                 u32 nparts, u32 check) {
   __shared__ u64 red[2][4];
@@ -3088,11 +3310,11 @@ __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, con
     const u32 got = crc_from_tiles(parts, n);
     if (!t && (got != st->wanted || u32(n) != st->isize)) status = kGzipCheckMismatch;
   }
-  if (!status && check == kCheckAdler) {  // uniform: g_adler ran and wrote every partial
+  if (!status && check == kCheckAdler) {  // uniform: every emitter and round wrote its pair
     u64 s = 0, w = 0;
     for (u32 i = t; i < nparts; i += 256) {
-      s += parts[2 * i];
-      w += parts[2 * i + 1];
+      s += parts[2 * i] % kAdlerMod;
+      w += parts[2 * i + 1] % kAdlerMod;
     }
     for (u32 off = 32; off; off >>= 1) {
       s += __shfl_down(s, off, 64);
@@ -3244,39 +3466,53 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
 
   // Emission and cross-segment resolution.
   const u64 words = (out_total + 31) / 32 + 1;
-  u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr;
-  HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
-  HZ_TRY(scratch.alloc(&bits0, words));
-  HZ_TRY(scratch.alloc(&bits1, words));
-  HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
-  HZ_LAUNCH(g_emit_lanes, dim3(clamp_grid(max_blocks, 4096)), dim3(kEmitThreads), 0, stream, body,
-            len, st, acc, recs, slice_entry, slice_off, group_link, tables, out, roots, bits0);
-  HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_emit_serial, dim3(clamp_grid(max_blocks, 4096)), dim3(kWave), 0, stream, body, len,
-            st, acc, out, roots, bits0);
-  HZ_TRY(hipGetLastError());
   // Round r covers kResolveLinks^(r+1) links of a chain.  A chain hops back
   // across slices (or serially emitted segments), so its length is bounded
   // by the number of slices plus segments.
   u32 rounds = 1;
   for (u64 span = kResolveLinks; span < group_capacity * 64 + u64(max_blocks); span *= kResolveLinks)
     ++rounds;
-  u64* counts = nullptr;
-  HZ_TRY(scratch.alloc(&counts, rounds + 1));
-  HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
+  // Adler-32 partial pairs: kAdlerSlots each for the lane emitter, the
+  // serial emitter and the resolve rounds (workgroups add theirs, so they
+  // start at zero), summed by g_finish.  The pairs, the round counts and the
+  // first unresolved bitmap share one zero fill.
+  const u32 emit_grid = clamp_grid(max_blocks, 4096);
+  const u32 resolve_grid = clamp_grid((words + 255) / 256, 2048);
+  u8* zeroed = nullptr;
+  const u64 zero_u64 = 2 * u64(3 * kAdlerSlots) + rounds + 1;
+  HZ_TRY(scratch.alloc(&zeroed, 8 * zero_u64 + 4 * words));
+  u64* adler_parts = reinterpret_cast<u64*>(zeroed);
+  u64* counts = adler_parts + 2 * u64(3 * kAdlerSlots);
+  u32* bits0 = reinterpret_cast<u32*>(counts + rounds + 1);
+  u32 *roots = nullptr, *bits1 = nullptr;
+  HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
+  HZ_TRY(scratch.alloc(&bits1, words));
+  HZ_TRY(launch_fill(stream, zeroed, 0, 8 * zero_u64 + 4 * words));
+  const u64 out_end = out_total;  // a byte at position p is stream byte n - (out_end - p)
+  HZ_LAUNCH(g_emit_lanes, dim3(emit_grid), dim3(kEmitThreads), 0, stream, body, len, st, acc,
+            recs, slice_entry, slice_off, group_link, tables, out, roots, bits0, out_end,
+            adler_parts);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_emit_serial, dim3(emit_grid), dim3(kWave), 0, stream, body, len, st, acc, out,
+            roots, bits0, out_end, adler_parts + 2 * kAdlerSlots);
+  HZ_TRY(hipGetLastError());
   for (u32 round = 0; round < rounds; ++round) {
-    HZ_LAUNCH(g_resolve, dim3(u32(clamp_grid((words + 255) / 256, 2048))), dim3(256), 0, stream,
-              st, out, roots, bits0, bits1, counts, round, rounds, words);
+    HZ_LAUNCH(g_resolve, dim3(resolve_grid), dim3(256), 0, stream, st, out, roots, bits0, bits1,
+              counts, round, rounds, words, out_end, adler_parts + 4 * kAdlerSlots);
     HZ_TRY(hipGetLastError());
   }
   u64* parts = nullptr;
   u32 nparts = 0;
   if (check == kCheckAdler) {
-    nparts = clamp_grid((out_size + 16 * 256 * 8 - 1) / (16 * 256 * 8), 2048);
-    HZ_TRY(scratch.alloc(&parts, 2 * u64(nparts)));
-    HZ_LAUNCH(g_adler, dim3(nparts), dim3(256), 0, stream, st, stream_out, out_size, parts);
+    // The pairs of the emitters, then those of the resolve rounds.
+    HZ_LAUNCH(g_finish, dim3(1), dim3(256), 0, stream, st, out_size, meta, adler_parts,
+              3 * kAdlerSlots, check);
     HZ_TRY(hipGetLastError());
-  } else if (check == kCheckCrc) {
+    HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
+              stream, st, stream_out, out_size);
+    return hipGetLastError();
+  }
+  if (check == kCheckCrc) {
     const u64 tiles = (out_size + kCrcTile - 1) / kCrcTile;
     HZ_TRY(scratch.alloc(&parts, tiles ? tiles : 1));
     if (tiles) {
@@ -3329,7 +3565,7 @@ hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8
   HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
   for (u32 round = 0; round < rounds; ++round) {
     HZ_LAUNCH(g_resolve, dim3(u32(clamp_grid((words + 255) / 256, 2048))), dim3(256), 0, stream,
-              st, out, roots, bits0, bits1, counts, round, rounds, words);
+              st, out, roots, bits0, bits1, counts, round, rounds, words, 0ull, nullptr);
     HZ_TRY(hipGetLastError());
   }
   HZ_LAUNCH(g_batch_wide_finish, dim3(n), dim3(256), 0, stream, files, list, n, out, st, wanted,
