@@ -73,6 +73,36 @@ __host__ __device__ __forceinline__ u32 bit_reverse(u32 code, u32 len) {
   return __builtin_bitreverse32(code) >> (32 - len);
 }
 
+// Bytes b .. b+3 of (hi:lo) (b < 4): v_alignbyte_b32 in GPU code.
+__host__ __device__ __forceinline__ u32 funnel_bytes(u32 hi, u32 lo, u32 b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_alignbyte(hi, lo, b);
+#else
+  return u32(((u64(hi) << 32) | lo) >> (8 * (b & 3u)));
+#endif
+}
+
+// Dot product of the four bytes of x with the four bytes of w (v_dot4_u32_u8).
+__host__ __device__ __forceinline__ u32 byte_dot(u32 x, u32 w) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_udot4(x, w, 0u, false);
+#else
+  u32 d = 0;
+  for (u32 k = 0; k < 32; k += 8) d += ((x >> k) & 0xffu) * ((w >> k) & 0xffu);
+  return d;
+#endif
+}
+
+// The low 32 bits of (hi:lo) >> s for s < 32: v_alignbit_b32 in GPU code;
+// the same value by shifts in the host build of the readers (CPU bounds tests).
+__host__ __device__ __forceinline__ u32 funnel32(u32 hi, u32 lo, u32 s) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_alignbit(hi, lo, s);
+#else
+  return u32(((u64(hi) << 32) | lo) >> (s & 31u));
+#endif
+}
+
 // ---- bit input --------------------------------------------------------------
 // LSB-first reader over a byte range [data, data + bytes).  The reader loads
 // aligned dwords only, and only dwords that hold at least one byte of the
@@ -90,7 +120,7 @@ struct BitIn {
   u64 wnext;      // next dword index to load
   u64 wlimit;     // dwords holding range bytes
 
-  __device__ __forceinline__ void init(const u8* data, u64 bytes, u64 start_bit) {
+  __host__ __device__ __forceinline__ void init(const u8* data, u64 bytes, u64 start_bit) {
     const uintptr_t addr = reinterpret_cast<uintptr_t>(data);
     words = reinterpret_cast<const u32*>(addr & ~uintptr_t(3));
     base_bit = u64(addr & 3u) * 8u;
@@ -98,7 +128,7 @@ struct BitIn {
     wlimit = (u64(addr & 3u) + bytes + 3u) >> 2;
     seek(start_bit);
   }
-  __device__ __forceinline__ void refill() {
+  __host__ __device__ __forceinline__ void refill() {
     while (cnt <= 32) {
       const u64 v = wnext < wlimit ? u64(words[wnext]) : 0ull;
       buf |= v << cnt;
@@ -106,7 +136,7 @@ struct BitIn {
       ++wnext;
     }
   }
-  __device__ __forceinline__ void seek(u64 p) {
+  __host__ __device__ __forceinline__ void seek(u64 p) {
     pos = p;
     const u64 a = base_bit + p;
     wnext = a >> 5;
@@ -118,19 +148,19 @@ struct BitIn {
     cnt -= skip;
     refill();
   }
-  __device__ __forceinline__ u64 avail() const { return pos <= total ? total - pos : 0; }
+  __host__ __device__ __forceinline__ u64 avail() const { return pos <= total ? total - pos : 0; }
   // Callers guarantee n <= 32 and have checked avail() where it matters.
-  __device__ __forceinline__ u32 peek(u32 n) const {
+  __host__ __device__ __forceinline__ u32 peek(u32 n) const {
     return n ? u32(buf & ((1ull << n) - 1ull)) : 0u;
   }
-  __device__ __forceinline__ void drop(u32 n) {
+  __host__ __device__ __forceinline__ void drop(u32 n) {
     buf >>= n;
     cnt -= n;
     pos += n;
     if (cnt <= 32) refill();
   }
   // take(n): returns false (truncation) when fewer than n bits remain.
-  __device__ __forceinline__ bool take(u32 n, u32& v) {
+  __host__ __device__ __forceinline__ bool take(u32 n, u32& v) {
     if (u64(n) > avail()) return false;
     v = peek(n);
     drop(n);
@@ -151,7 +181,7 @@ struct StagedBits {
   u32 cnt;
   u32 wnext;
 
-  __device__ __forceinline__ void refill() {
+  __host__ __device__ __forceinline__ void refill() {
     while (cnt <= 32) {
       const u64 v = wnext < nwords ? u64(words[wnext]) : 0ull;
       buf |= v << cnt;
@@ -159,7 +189,7 @@ struct StagedBits {
       ++wnext;
     }
   }
-  __device__ __forceinline__ void seek(u32 p) {
+  __host__ __device__ __forceinline__ void seek(u32 p) {
     pos = p;
     wnext = p >> 5;
     buf = 0;
@@ -170,17 +200,17 @@ struct StagedBits {
     cnt -= skip;
     refill();
   }
-  __device__ __forceinline__ u32 avail() const { return pos < limit ? limit - pos : 0u; }
-  __device__ __forceinline__ u32 peek(u32 n) const {
+  __host__ __device__ __forceinline__ u32 avail() const { return pos < limit ? limit - pos : 0u; }
+  __host__ __device__ __forceinline__ u32 peek(u32 n) const {
     return n ? u32(buf & ((1ull << n) - 1ull)) : 0u;
   }
-  __device__ __forceinline__ void drop(u32 n) {
+  __host__ __device__ __forceinline__ void drop(u32 n) {
     buf >>= n;
     cnt -= n;
     pos += n;
     if (cnt <= 32) refill();
   }
-  __device__ __forceinline__ bool take(u32 n, u32& v) {
+  __host__ __device__ __forceinline__ bool take(u32 n, u32& v) {
     if (n > avail()) return false;
     v = peek(n);
     drop(n);
@@ -229,7 +259,7 @@ __host__ __device__ __forceinline__ u32 cl_order(u32 i) {
 // Returns 0 or kBadTree.  Must be called by one thread.  Semantics follow the
 // reference's Huffman::build (_decode_kernels.py:141-183).
 template <int N, int P>
-__device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_ok,
+__host__ __device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_ok,
                           bool single_ok, u32 limit) {
   for (u32 i = 0; i < 16; ++i) t.count[i] = 0;
   t.maximum = 0;
@@ -270,7 +300,7 @@ __device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bool empty_
 // `maximum` bits).  Matches the reference's LUT-plus-canonical decode exactly,
 // including its behaviour at the end of the bit range.
 template <int N, int P, class Reader>
-__device__ __forceinline__ i32 huff_decode(const HuffTable<N, P>& t, Reader& r, u32& err) {
+__host__ __device__ __forceinline__ i32 huff_decode(const HuffTable<N, P>& t, Reader& r, u32& err) {
   const u32 e = t.primary[r.peek(P)];
   const u32 l = e & 15u;
   if (l) {
@@ -305,7 +335,7 @@ struct DecodeTables {
 };
 
 // Fixed Huffman tables (RFC 1951 3.2.6).
-__device__ inline u32 build_fixed_tables(DecodeTables& t) {
+__host__ __device__ inline u32 build_fixed_tables(DecodeTables& t) {
   for (u32 i = 0; i < 288; ++i) t.lens[i] = i < 144 ? 8 : i < 256 ? 9 : i < 280 ? 7 : 8;
   u32 err = huff_build(t.ll, t.lens, 288, false, true, 15);
   if (err) return err;
@@ -316,7 +346,7 @@ __device__ inline u32 build_fixed_tables(DecodeTables& t) {
 // Code-length code table from 19 packed 3-bit lengths (symbol s at bits 3s):
 // counts and next codes live in packed registers, so no private arrays.
 // The code must be complete (RFC 1951 allows no other).  Returns 0 or kBadTree.
-__device__ inline u32 build_cl_table(HuffTable<19, 7>& t, u64 pack) {
+__host__ __device__ inline u32 build_cl_table(HuffTable<19, 7>& t, u64 pack) {
   u64 cnt = 0;  // byte l = number of symbols of length l
   for (u32 s = 0; s < 19; ++s) cnt += 1ull << (8 * ((pack >> (3 * s)) & 7));
   u32 kraft = 0, maximum = 0;
@@ -353,7 +383,7 @@ __device__ inline u32 build_cl_table(HuffTable<19, 7>& t, u64 pack) {
 // HDIST, HCLEN and the code-length code, then decodes the nl + nd lengths into
 // t.lens.  Reader positioned after BTYPE.  Error order follows the reference's
 // dynamic_tables (_decode_kernels.py:240-283).
-__device__ inline u32 parse_dynamic_lengths(DecodeTables& t, BitIn& r, u32& nl, u32& nd) {
+__host__ __device__ inline u32 parse_dynamic_lengths(DecodeTables& t, BitIn& r, u32& nl, u32& nd) {
   u32 hlit, hdist, hclen;
   if (!r.take(5, hlit) || !r.take(5, hdist) || !r.take(4, hclen)) return kTruncated;
   nl = hlit + 257;
@@ -397,7 +427,7 @@ __device__ inline u32 parse_dynamic_lengths(DecodeTables& t, BitIn& r, u32& nl, 
 }
 
 // Dynamic block header (RFC 1951 3.2.7), reader positioned after BTYPE.
-__device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
+__host__ __device__ inline u32 build_dynamic_tables(DecodeTables& t, BitIn& r) {
   u32 nl, nd;
   u32 err = parse_dynamic_lengths(t, r, nl, nd);
   if (err) return err;
@@ -506,7 +536,7 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
 // length/distance (length 0 = EOB, distance 0 = literal in `lit`), or an error.
 // Order of checks follows the reference's token decode (_decode_kernels.py:393-420).
 template <class Reader>
-__device__ __forceinline__ u32 decode_token(const DecodeTables& t, Reader& r, u32 window, u32& lit,
+__host__ __device__ __forceinline__ u32 decode_token(const DecodeTables& t, Reader& r, u32 window, u32& lit,
                                              u32& length, u32& distance) {
   u32 err = 0;
   const i32 sym = huff_decode(t.ll, r, err);
@@ -541,7 +571,7 @@ __device__ __forceinline__ u32 decode_token(const DecodeTables& t, Reader& r, u3
 // count/symbols, which the rewrite leaves untouched.
 enum : u32 { kKindLit = 0, kKindLen = 1, kKindEob = 2, kKindBad = 3 };
 
-__device__ __forceinline__ u32 fast_ll_entry(u32 sym, u32 l) {
+__host__ __device__ __forceinline__ u32 fast_ll_entry(u32 sym, u32 l) {
   if (sym < 256) return l | (sym << 8);
   if (sym == 256) return l | (kKindEob << 4);
   if (sym > 285) return l | (kKindBad << 4);
@@ -549,14 +579,14 @@ __device__ __forceinline__ u32 fast_ll_entry(u32 sym, u32 l) {
   return l | (kKindLen << 4) | (length_extra(li) << 8) | (length_base(li) << 16);
 }
 
-__device__ __forceinline__ u32 fast_d_entry(u32 sym, u32 l) {
+__host__ __device__ __forceinline__ u32 fast_d_entry(u32 sym, u32 l) {
   if (sym > 29) return l | 0x100u;
   return l | (dist_extra(sym) << 4) | (dist_base(sym) << 16);
 }
 
 // Rewrite a built table's primary LUT (threads `first`, `first + step`, ...).
 template <int N, int P>
-__device__ void fast_format(HuffTable<N, P>& t, bool literal_length, u32 first, u32 step) {
+__host__ __device__ void fast_format(HuffTable<N, P>& t, bool literal_length, u32 first, u32 step) {
   for (u32 i = first; i < (1u << P); i += step) {
     const u32 e = t.primary[i];
     const u32 l = e & 15u;
@@ -573,15 +603,15 @@ template <bool kChecked>
 struct WordBits {
   const u32* words;
   u32 w, lo, hi, off, limit;
-  __device__ __forceinline__ void seek(u32 p) {
+  __host__ __device__ __forceinline__ void seek(u32 p) {
     w = p >> 5;
     off = p & 31u;
     lo = words[w];
     hi = words[w + 1];
   }
-  __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
-  __device__ __forceinline__ u32 bits32() const { return __builtin_amdgcn_alignbit(hi, lo, off); }
-  __device__ __forceinline__ void drop(u32 n) {  // n <= 32
+  __host__ __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
+  __host__ __device__ __forceinline__ u32 bits32() const { return funnel32(hi, lo, off); }
+  __host__ __device__ __forceinline__ void drop(u32 n) {  // n <= 32
     off += n;
     if (off >= 32) {
       off -= 32;
@@ -590,7 +620,7 @@ struct WordBits {
       hi = words[w + 1];
     }
   }
-  __device__ __forceinline__ u32 avail() const {
+  __host__ __device__ __forceinline__ u32 avail() const {
     if (!kChecked) return 0xffffffffu;
     const u32 p = pos();
     return p < limit ? limit - p : 0u;
@@ -600,7 +630,7 @@ struct WordBits {
 // Canonical walk over the next bits `b` (LSB first), as huff_decode does on a
 // LUT miss.  Returns the symbol and its length, or -1 with `err`.
 template <int N, int P>
-__device__ __forceinline__ i32 canon_walk(const HuffTable<N, P>& t, u32 b, u32 avail, u32& len_out,
+__host__ __device__ __forceinline__ i32 canon_walk(const HuffTable<N, P>& t, u32 b, u32 avail, u32& len_out,
                                           u32& err) {
   u32 code = 0, first = 0, index = 0;
   for (u32 len = 1; len <= t.maximum; ++len) {
@@ -622,7 +652,7 @@ __device__ __forceinline__ i32 canon_walk(const HuffTable<N, P>& t, u32 b, u32 a
 // One token with fast-format tables; same results and error order as
 // decode_token over the standard format (a distance is at most 32768).
 template <class R>
-__device__ __forceinline__ u32 fast_token(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
+__host__ __device__ __forceinline__ u32 fast_token(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
                                           R& r, u32& lit, u32& length, u32& distance) {
   length = 0;
   distance = 0;
@@ -745,6 +775,73 @@ __device__ __forceinline__ bool quick_token(const HuffTable<288, 10>& ll, const 
   lit_or_dist = (dist & is_len) | ((e >> 8) & 0xffu & ~is_len);
   r.advance(ok ? n : 0u);
   return ok;
+}
+
+// Adler-32 partial sums of output bytes as they are produced: S = sum of the
+// bytes, W = sum of (end - position) * byte, where `end` is the stream's end
+// position, so that a byte at stream position i weighs n - i.  W is reduced
+// mod 65521 before it can wrap.
+struct AdlerAcc {
+  u64 s = 0, w = 0;
+  __host__ __device__ __forceinline__ void add_byte(u32 x, u64 weight) {
+    s += x;
+    w += weight * x;
+    if (w >> 62) w %= kAdlerMod;
+  }
+  // Sixteen bytes whose first weighs `weight0` (each next one 1 less).
+  __host__ __device__ __forceinline__ void add16(const uint4& q, u64 weight0) {
+    const u32 words[4] = {q.x, q.y, q.z, q.w};
+    u32 cs = 0, cl = 0;
+#pragma unroll
+    for (u32 k = 0; k < 4; ++k) {
+      const u32 ws = byte_dot(words[k], 0x01010101u);
+      cs += ws;
+      cl += byte_dot(words[k], 0x03020100u) + 4 * k * ws;
+    }
+    s += cs;
+    w += weight0 * cs - cl;
+    if (w >> 62) w %= kAdlerMod;
+  }
+};
+
+// dst[0, n) = src[0, n) by threads first, first + step, ...: bytes up to
+// dst's first 16-byte boundary, then 16-byte stores of source dwords
+// realigned with v_alignbyte, then the tail bytes.  Source dwords are read
+// only while they lie before src_end.
+// With `acc`, every copied byte is also added to the Adler-32 sums; the
+// destination's first byte weighs `weight0`.
+__host__ __device__ __forceinline__ void copy_bytes(u8* dst, const u8* src, u64 n, const u8* src_end,
+                                           u32 first, u32 step, AdlerAcc* acc = nullptr,
+                                           u64 weight0 = 0) {
+  const u64 align = (16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15;
+  const u64 head = n < align ? n : align;
+  for (u64 i = first; i < head; i += step) {
+    dst[i] = src[i];
+    if (acc) acc->add_byte(src[i], weight0 - i);
+  }
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src + head);
+  const u32* s32 = reinterpret_cast<const u32*>(s0 & ~uintptr_t(3));
+  const u32 sh = u32(s0 & 3);
+  // Block j reads dwords j*4 .. j*4 + 4 of s32: all of them before src_end.
+  const u64 avail_words = (reinterpret_cast<uintptr_t>(src_end) - (s0 & ~uintptr_t(3))) / 4;
+  u64 blocks = (n - head) / 16;
+  if (avail_words < 5) blocks = 0;
+  else if (blocks > (avail_words - 5) / 4 + 1) blocks = (avail_words - 5) / 4 + 1;
+  for (u64 j = first; j < blocks; j += step) {
+    const u32* q = s32 + 4 * j;
+    const u32 x0 = q[0], x1 = q[1], x2 = q[2], x3 = q[3], x4 = q[4];
+    uint4 o;
+    o.x = funnel_bytes(x1, x0, sh);
+    o.y = funnel_bytes(x2, x1, sh);
+    o.z = funnel_bytes(x3, x2, sh);
+    o.w = funnel_bytes(x4, x3, sh);
+    *reinterpret_cast<uint4*>(dst + head + 16 * j) = o;
+    if (acc) acc->add16(o, weight0 - head - 16 * j);
+  }
+  for (u64 i = head + 16 * blocks + first; i < n; i += step) {
+    dst[i] = src[i];
+    if (acc) acc->add_byte(src[i], weight0 - i);
+  }
 }
 
 // zlib wrapper (RFC 1950) checks, in the reference's precedence order.

@@ -2545,33 +2545,6 @@ __device__ __forceinline__ void bits_set_range(u32* bits, u64 start, u32 n) {
   atomicOr(bits + w1, hi);
 }
 
-// Adler-32 partial sums of output bytes as they are produced: S = sum of the
-// bytes, W = sum of (end - position) * byte, where `end` is the stream's end
-// position, so that a byte at stream position i weighs n - i.  W is reduced
-// mod 65521 before it can wrap.
-struct AdlerAcc {
-  u64 s = 0, w = 0;
-  __device__ __forceinline__ void add_byte(u32 x, u64 weight) {
-    s += x;
-    w += weight * x;
-    if (w >> 62) w %= kAdlerMod;
-  }
-  // Sixteen bytes whose first weighs `weight0` (each next one 1 less).
-  __device__ __forceinline__ void add16(const uint4& q, u64 weight0) {
-    const u32 words[4] = {q.x, q.y, q.z, q.w};
-    u32 cs = 0, cl = 0;
-#pragma unroll
-    for (u32 k = 0; k < 4; ++k) {
-      const u32 ws = __builtin_amdgcn_udot4(words[k], 0x01010101u, 0u, false);
-      cs += ws;
-      cl += __builtin_amdgcn_udot4(words[k], 0x03020100u, 0u, false) + 4 * k * ws;
-    }
-    s += cs;
-    w += weight0 * cs - cl;
-    if (w >> 62) w %= kAdlerMod;
-  }
-};
-
 // Where a slice's output bytes go.  GlobalBytes writes the output buffer (and
 // with kAdler adds every byte to the thread's Adler-32 sums); StagedBytes
 // writes a workgroup's LDS stage that holds output positions [base, ...),
@@ -2652,45 +2625,6 @@ __device__ __forceinline__ void copy_periodic(const Sink& out, u64 dst, u64 src0
       out.put(dst + j, u8(pattern >> (8 * k)));
       k = k + 1 == distance ? 0u : k + 1;
     }
-  }
-}
-
-// dst[0, n) = src[0, n) by threads first, first + step, ...: bytes up to
-// dst's first 16-byte boundary, then 16-byte stores of source dwords
-// realigned with v_alignbyte, then the tail bytes.  Source dwords are read
-// only while they lie before src_end.
-// With `acc`, every copied byte is also added to the Adler-32 sums; the
-// destination's first byte weighs `weight0`.
-__device__ __forceinline__ void copy_bytes(u8* dst, const u8* src, u64 n, const u8* src_end,
-                                           u32 first, u32 step, AdlerAcc* acc = nullptr,
-                                           u64 weight0 = 0) {
-  const u64 head = min<u64>(n, (16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15);
-  for (u64 i = first; i < head; i += step) {
-    dst[i] = src[i];
-    if (acc) acc->add_byte(src[i], weight0 - i);
-  }
-  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src + head);
-  const u32* s32 = reinterpret_cast<const u32*>(s0 & ~uintptr_t(3));
-  const u32 sh = u32(s0 & 3);
-  // Block j reads dwords j*4 .. j*4 + 4 of s32: all of them before src_end.
-  const u64 avail_words = (reinterpret_cast<uintptr_t>(src_end) - (s0 & ~uintptr_t(3))) / 4;
-  u64 blocks = (n - head) / 16;
-  if (avail_words < 5) blocks = 0;
-  else blocks = min<u64>(blocks, (avail_words - 5) / 4 + 1);
-  for (u64 j = first; j < blocks; j += step) {
-    const u32* q = s32 + 4 * j;
-    const u32 x0 = q[0], x1 = q[1], x2 = q[2], x3 = q[3], x4 = q[4];
-    uint4 o;
-    o.x = __builtin_amdgcn_alignbyte(x1, x0, sh);
-    o.y = __builtin_amdgcn_alignbyte(x2, x1, sh);
-    o.z = __builtin_amdgcn_alignbyte(x3, x2, sh);
-    o.w = __builtin_amdgcn_alignbyte(x4, x3, sh);
-    *reinterpret_cast<uint4*>(dst + head + 16 * j) = o;
-    if (acc) acc->add16(o, weight0 - head - 16 * j);
-  }
-  for (u64 i = head + 16 * blocks + first; i < n; i += step) {
-    dst[i] = src[i];
-    if (acc) acc->add_byte(src[i], weight0 - i);
   }
 }
 

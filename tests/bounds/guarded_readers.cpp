@@ -1,0 +1,260 @@
+// CPU bounds check of the codec's device readers, compiled for the host.
+//
+// The decode kernels read compressed bytes through BitIn (global memory),
+// WordBits over LDS-staged words, and copy stored payloads with copy_bytes;
+// wrappers are parsed by parse_frame.  Here the same code (deflate_common.h,
+// built with hipcc --offload-host-only) reads buffers that end exactly at a
+// PROT_NONE page, so a read past the end is a SIGSEGV instead of a silent
+// garbage value -- the check that cannot be made on the GPU without faulting
+// it.  Every truncation of every input is decoded; the statuses are printed
+// for the Python side to compare.
+//
+// Usage: guarded_readers <mode> <file>...
+//   walk   decode each zlib stream (and every truncation) with BitIn
+//   staged the same body decoded with WordBits/fast_token over guarded words
+//   copy   copy_bytes over every length/alignment pair up to 96 bytes
+//   frame  parse_frame on every truncation, in each format
+//   guard  reads one byte past a guarded buffer (must crash: checks the guard)
+#include <sys/mman.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "deflate_common.h"
+
+using namespace hz;
+
+namespace {
+
+// `n` bytes that end where an inaccessible page begins.
+struct Guarded {
+  u8* map = nullptr;
+  size_t length = 0;
+  u8* data = nullptr;
+  Guarded(const u8* src, size_t n) {
+    const size_t page = size_t(sysconf(_SC_PAGESIZE));
+    const size_t body = (n + page - 1) / page * page + page;  // a mapped page before the data too
+    length = body + page;
+    map = static_cast<u8*>(mmap(nullptr, length, PROT_READ | PROT_WRITE,
+                                MAP_PRIVATE | MAP_ANONYMOUS, -1, 0));
+    if (map == MAP_FAILED) { perror("mmap"); exit(2); }
+    if (mprotect(map + body, page, PROT_NONE)) { perror("mprotect"); exit(2); }
+    data = map + body - n;
+    if (n) memcpy(data, src, n);
+  }
+  ~Guarded() { munmap(map, length); }
+};
+
+std::vector<u8> read_file(const char* path) {
+  FILE* f = fopen(path, "rb");
+  if (!f) { perror(path); exit(2); }
+  std::vector<u8> v;
+  u8 buf[65536];
+  size_t k;
+  while ((k = fread(buf, 1, sizeof buf, f)) > 0) v.insert(v.end(), buf, buf + k);
+  fclose(f);
+  return v;
+}
+
+// Serial inflate of a raw DEFLATE body with the product's BitIn and table
+// builders; output into a guarded buffer of `limit` bytes.  Returns a status.
+u32 inflate_body(const u8* body, u64 len, u8* out, u64 limit, u64& produced) {
+  static DecodeTables t;
+  BitIn r;
+  r.init(body, len, 0);
+  produced = 0;
+  for (u32 blocks = 0; blocks < 100000; ++blocks) {
+    u32 final_block, type;
+    if (!r.take(1, final_block) || !r.take(2, type)) return kTruncated;
+    if (type == 3) return kReservedBlock;
+    if (type == 0) {
+      r.seek((r.pos + 7) & ~u64(7));
+      u32 n, comp;
+      if (!r.take(16, n) || !r.take(16, comp)) return kTruncated;
+      if ((n ^ comp) != 0xffffu) return kBadSymbol;
+      if (n > limit - produced) return kOutputOverflow;
+      if (u64(n) * 8 > r.avail()) return kTruncated;
+      copy_bytes(out + produced, body + (r.pos >> 3), n, body + len, 0, 1);
+      produced += n;
+      r.seek(r.pos + u64(n) * 8);
+    } else {
+      const u32 err = type == 1 ? build_fixed_tables(t) : build_dynamic_tables(t, r);
+      if (err) return err;
+      for (;;) {
+        u32 lit, length, distance;
+        const u32 e = decode_token(t, r, 32768u, lit, length, distance);
+        if (e) return e;
+        if (!length) break;
+        if (length > limit - produced) return kOutputOverflow;
+        if (!distance) {
+          out[produced++] = u8(lit);
+          continue;
+        }
+        if (distance > produced) return kBadDistance;
+        for (u32 j = 0; j < length; ++j, ++produced) out[produced] = out[produced - distance];
+      }
+    }
+    if (final_block) return (r.pos + 7) / 8 == len ? kOk : kExtent;
+  }
+  return kBlockCapacity;
+}
+
+// The same body through WordBits and fast_token over staged words, the way
+// the describe and emission kernels read their LDS stage: the words hold the
+// body plus a margin of zero words (what stage_range leaves past the body
+// end), and the checked reader stops at the body's last bit.
+u32 staged_body(const u8* body, u64 len, u64& produced) {
+  static DecodeTables t;
+  const u32 margin_words = 16;
+  const u64 words = (len + 3) / 4 + margin_words;
+  std::vector<u32> host(words, 0u);
+  memcpy(host.data(), body, len);
+  Guarded g(reinterpret_cast<const u8*>(host.data()), words * 4);
+  const u32* w = reinterpret_cast<const u32*>(g.data);
+  BitIn hdr;
+  hdr.init(body, len, 0);
+  produced = 0;
+  for (u32 blocks = 0; blocks < 100000; ++blocks) {
+    u32 final_block, type;
+    if (!hdr.take(1, final_block) || !hdr.take(2, type)) return kTruncated;
+    if (type == 3) return kReservedBlock;
+    if (type == 0) {
+      hdr.seek((hdr.pos + 7) & ~u64(7));
+      u32 n, comp;
+      if (!hdr.take(16, n) || !hdr.take(16, comp)) return kTruncated;
+      if ((n ^ comp) != 0xffffu) return kBadSymbol;
+      if (u64(n) * 8 > hdr.avail()) return kTruncated;
+      produced += n;
+      hdr.seek(hdr.pos + u64(n) * 8);
+    } else {
+      u32 err = type == 1 ? build_fixed_tables(t) : build_dynamic_tables(t, hdr);
+      if (err) return err;
+      fast_format(t.ll, true, 0, 1);
+      fast_format(t.dd, false, 0, 1);
+      WordBits<true> q;
+      q.words = w;
+      q.limit = u32(len * 8);
+      q.seek(u32(hdr.pos));
+      for (;;) {
+        u32 lit, length, distance;
+        err = fast_token(t.ll, t.dd, q, lit, length, distance);
+        if (err) return err;
+        if (!length) break;
+        produced += length;
+      }
+      hdr.seek(q.pos());
+    }
+    if (final_block) return (hdr.pos + 7) / 8 == len ? kOk : kExtent;
+  }
+  return kBlockCapacity;
+}
+
+int mode_walk(int argc, char** argv, bool staged) {
+  for (int i = 0; i < argc; ++i) {
+    const std::vector<u8> s = read_file(argv[i]);
+    // The output bound is what the whole stream decodes to (at most 4 MiB):
+    // the guarded output buffer ends there, so no truncation may write past it.
+    u64 bound = 4u << 20;
+    {
+      std::vector<u8> big(bound);
+      Frame f;
+      u64 produced = 0;
+      if (!parse_frame(s.data(), s.size(), kFormatZlib, false, f))
+        inflate_body(s.data() + f.body, f.body_len, big.data(), bound, produced);
+      bound = produced;
+    }
+    std::vector<u8> zeros(bound, 0);
+    Guarded out(zeros.data(), bound);
+    printf("%s", argv[i]);
+    u64 sum = 0;
+    for (u64 n = 0; n <= s.size(); ++n) {
+      Guarded in(s.data(), n);
+      Frame f;
+      u32 st = parse_frame(in.data, n, kFormatZlib, false, f);
+      u64 produced = 0;
+      if (!st) {
+        if (staged) st = staged_body(in.data + f.body, f.body_len, produced);
+        else st = inflate_body(in.data + f.body, f.body_len, out.data, bound, produced);
+      }
+      sum = sum * 31 + st;
+      if (n == s.size()) printf(" full=%u bytes=%llu", st, (unsigned long long)produced);
+    }
+    printf(" digest=%llu\n", (unsigned long long)sum);
+  }
+  return 0;
+}
+
+int mode_copy() {
+  u8 src[256], expect[256];
+  for (u32 i = 0; i < 256; ++i) src[i] = u8(i * 7 + 3);
+  u32 cases = 0;
+  for (u32 n = 0; n <= 96; ++n)
+    for (u32 sa = 0; sa < 16; ++sa)
+      for (u32 da = 0; da < 16; ++da) {
+        // Source ends at the guard; the destination buffer is guarded too.
+        Guarded s(src + sa, n);
+        std::vector<u8> zeros(n + da, 0);
+        Guarded d(zeros.data(), n + da);
+        AdlerAcc acc;
+        copy_bytes(d.data + da, s.data, n, s.data + n, 0, 1, &acc, n);
+        memcpy(expect, src + sa, n);
+        if (memcmp(d.data + da, expect, n)) {
+          printf("copy mismatch n=%u sa=%u da=%u\n", n, sa, da);
+          return 1;
+        }
+        u64 s1 = 0, w1 = 0;
+        for (u32 j = 0; j < n; ++j) {
+          s1 += expect[j];
+          w1 += u64(n - j) * expect[j];
+        }
+        if (acc.s != s1 || acc.w % kAdlerMod != w1 % kAdlerMod) {
+          printf("copy sums n=%u sa=%u da=%u\n", n, sa, da);
+          return 1;
+        }
+        ++cases;
+      }
+  printf("copy cases=%u\n", cases);
+  return 0;
+}
+
+int mode_frame(int argc, char** argv) {
+  for (int i = 0; i < argc; ++i) {
+    const std::vector<u8> s = read_file(argv[i]);
+    printf("%s", argv[i]);
+    for (u32 format = 0; format < 3; ++format) {
+      u64 sum = 0;
+      for (u64 n = 0; n <= s.size(); ++n) {
+        Guarded in(s.data(), n);
+        Frame f;
+        const u32 st = parse_frame(in.data, n, format, false, f);
+        sum = sum * 31 + st + (st ? 0 : f.body * 7 + f.body_len);
+        if (n == s.size()) printf(" f%u=%u", format, st);
+      }
+      printf(" d%u=%llu", format, (unsigned long long)sum);
+    }
+    printf("\n");
+  }
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) return 2;
+  const char* mode = argv[1];
+  if (!strcmp(mode, "walk")) return mode_walk(argc - 2, argv + 2, false);
+  if (!strcmp(mode, "staged")) return mode_walk(argc - 2, argv + 2, true);
+  if (!strcmp(mode, "copy")) return mode_copy();
+  if (!strcmp(mode, "frame")) return mode_frame(argc - 2, argv + 2);
+  if (!strcmp(mode, "guard")) {
+    const u8 byte = 1;
+    Guarded g(&byte, 1);
+    volatile const u8* p = g.data;
+    printf("%u\n", unsigned(p[1]));  // the first byte of the inaccessible page
+    return 0;
+  }
+  return 2;
+}
