@@ -372,8 +372,9 @@ class Gpu:
         return lambda: self.check(self.lib.HipZlibDecompress(
             self.handle, MAX, MAX, _ptr(src), n_in, _ptr(out), n_out, _ptr(meta), 2))
 
-    def encode_call(self, src, n, enc, capacity, meta, chunk=32768):
-        return lambda: self.check(self.lib.HipZlibCompress(
+    def encode_call(self, src, n, enc, capacity, meta, chunk=32768, independent=False):
+        entry = self.lib.HipZlibCompressIndependent if independent else self.lib.HipZlibCompress
+        return lambda: self.check(entry(
             self.handle, chunk, _ptr(src), n, _ptr(enc), capacity, _ptr(meta), 2))
 
 
@@ -402,11 +403,23 @@ def extra_configs(gpu, generated):
         stream = enc[:length].cpu().numpy().tobytes()
         assert zlib.decompress(stream) == raw, "c2 stream fails zlib"
         ms = gpu.median_ms(call)
+        # The same encode with every chunk's window confined to the chunk (the
+        # reference's encoder semantics).
+        call_ind = gpu.encode_call(src, n, enc, capacity, meta, independent=True)
+        call_ind()
+        torch.cuda.synchronize()
+        length_ind, status = (int(v) for v in meta.cpu().numpy())
+        assert status == 0, "c2 independent encode status %d" % status
+        assert zlib.decompress(enc[:length_ind].cpu().numpy().tobytes()) == raw, \
+            "c2 independent stream fails zlib"
+        ms_ind = gpu.median_ms(call_ind)
         l6 = generated.get("c2_l6", {})
         result["c2_encode_256MiB_text"] = {
             "gbs": gbs(n, ms), "ms": round(ms, 3), "hbm_fraction": round(gbs(n, ms) / HBM_PEAK_GBS, 6),
             "ratio": round(length / n, 6), "zlib_l1_ratio": round(info["zlib_l1"] / n, 6),
             "zlib_l6_ratio": round(l6["zlib_l6"] / n, 6) if "zlib_l6" in l6 else None,
+            "independent_chunks": {"gbs": gbs(n, ms_ind), "ms": round(ms_ind, 3),
+                                   "ratio": round(length_ind / n, 6)},
             "cpu_zlib_l1_single_gbs": round(n / info["zlib_l1_s"] / 1e9, 4),
             "chunk_bytes": 32768, "round_trips_through": "zlib.decompress"}
         del src, enc, raw

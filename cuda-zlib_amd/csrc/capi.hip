@@ -317,9 +317,13 @@ extern "C" int HipZlibDecompressFormat(hipStream_t stream, int32_t format,
   });
 }
 
-extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
-                               uint64_t input_size, uint8_t* output, uint64_t output_size,
-                               uint32_t* metadata, uint64_t metadata_count) {
+namespace {
+
+// HipZlibCompress and HipZlibCompressIndependent: the same checks and
+// outputs; `independent` limits every chunk's window to the chunk.
+int compress_stream(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
+                    uint64_t input_size, uint8_t* output, uint64_t output_size, uint32_t* metadata,
+                    uint64_t metadata_count, bool independent) {
   if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
   return execute(stream, [&](Workspace& ws) -> hipError_t {
     if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, 0, kInvalidBounds);
@@ -336,8 +340,25 @@ extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const ui
         output_size != input_size + chunks * 5 + 6)
       return reject();
     return run_deflate(stream, ws, input, input_size, output, output_size, u32(chunk_bytes),
-                       metadata);
+                       metadata, independent);
   });
+}
+
+}  // namespace
+
+extern "C" int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
+                               uint64_t input_size, uint8_t* output, uint64_t output_size,
+                               uint32_t* metadata, uint64_t metadata_count) {
+  return compress_stream(stream, chunk_bytes, input, input_size, output, output_size, metadata,
+                         metadata_count, false);
+}
+
+extern "C" int HipZlibCompressIndependent(hipStream_t stream, int64_t chunk_bytes,
+                                          const uint8_t* input, uint64_t input_size,
+                                          uint8_t* output, uint64_t output_size,
+                                          uint32_t* metadata, uint64_t metadata_count) {
+  return compress_stream(stream, chunk_bytes, input, input_size, output, output_size, metadata,
+                         metadata_count, true);
 }
 
 // ---- compression without allocation ------------------------------------------

@@ -10,7 +10,9 @@
 //
 // Unlike the reference, a chunk's LZ77 window includes up to 32 KiB of the
 // same input before it (the decoder has already produced those bytes), which
-// keeps the ratio below whole-stream zlib level 1.
+// keeps the ratio below whole-stream zlib level 1.  The independent mode
+// (run_deflate with `independent`) limits every window to its own chunk, as
+// the reference's per-chunk encoder does.
 //
 // e_parse, one 1024-thread workgroup per chunk (the LDS holds the window and
 // the hash table, so one workgroup per CU; 16 waves hide LDS latency):
@@ -1304,13 +1306,13 @@ __global__ __launch_bounds__(256) void e_zero_tail(u8* out, u64 capacity, const 
 }
 
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
-                       u64 capacity, u32 chunk_bytes, u32* meta) {
+                       u64 capacity, u32 chunk_bytes, u32* meta, bool independent) {
   const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
   ChunkBuffers b;
   HZ_TRY(alloc_chunks(scratch, chunks, 1, in_size, chunk_bytes, b));
   HZ_LAUNCH(e_single_descs, dim3(u32(std::min<u64>(1024, (chunks + 255) / 256))), dim3(256), 0,
-            stream, in_size, chunk_bytes, u32(chunks), history_limit(chunk_bytes), capacity, b.descs,
-            b.files);
+            stream, in_size, chunk_bytes, u32(chunks), independent ? 0u : history_limit(chunk_bytes),
+            capacity, b.descs, b.files);
   HZ_TRY(hipGetLastError());
   HZ_TRY(run_chunks(stream, b, in, chunks, 1, out, chunk_bytes, meta));
   HZ_LAUNCH(e_zero_tail, dim3(u32(std::min<u64>(1024, (capacity / 16 + 255) / 256 + 1))), dim3(256),

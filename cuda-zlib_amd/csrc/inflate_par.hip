@@ -2628,6 +2628,92 @@ __device__ __forceinline__ void copy_periodic(const Sink& out, u64 dst, u64 src0
   }
 }
 
+// One match of a slice whose output starts at dst0: bytes copied from before
+// dst0 (or from bytes of this slice still unresolved) are marked unresolved
+// with their root; the rest are copied.  `nunres` counts the slice's
+// unresolved bytes so far.
+template <class Sink>
+__device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u32 distance,
+                                           u32 length, u32* roots, u32* unres, u32& nunres) {
+  const u64 src0 = dst - distance;
+  if (src0 + length <= dst0) {
+    // Every source precedes the slice: unresolved, rooted at the source.
+    for (u32 j = 0; j < length; ++j) roots[dst + j] = u32(src0 + j);
+    bits_set_range(unres, dst, length);
+    out.zero(dst, length);
+    nunres += length;
+  } else if (!nunres && src0 >= dst0) {
+    // Every source is this slice's own resolved output.
+    copy_periodic(out, dst, src0, distance, length);
+  } else if (distance == 1) {
+    // A run of the byte before: resolved, or one root for the whole run.
+    const u64 p = dst - 1;
+    const bool before = p < dst0;
+    if (before || (nunres && bit_get(unres, p))) {
+      const u32 root = before ? u32(p) : roots[p];
+      for (u32 j = 0; j < length; ++j) roots[dst + j] = root;
+      bits_set_range(unres, dst, length);
+      out.zero(dst, length);
+      nunres += length;
+    } else {
+      const u8 v = out.get(p);
+      for (u32 j = 0; j < length; ++j) out.put(dst + j, v);
+    }
+  } else {
+    for (u32 j = 0; j < length; ++j) {
+      const u64 d = dst + j, src = d - distance;
+      if (src < dst0) {
+        roots[d] = u32(src);
+        bit_set(unres, d);
+        out.zero(d, 1);
+        ++nunres;
+      } else if (nunres && bit_get(unres, src)) {
+        roots[d] = roots[src];
+        bit_set(unres, d);
+        out.zero(d, 1);
+        ++nunres;
+      } else {
+        out.put(d, out.get(src));
+      }
+    }
+  }
+}
+
+// Matches a slice decode holds back: literals are written as they are
+// decoded, matches queue here (in order) and are copied when a lane of the
+// wave has kMatchQueue of them and when the slice ends, so that the lanes of
+// a wave copy together rather than each literal step waiting for the copies
+// of the few lanes that met a match.  A match only reads bytes before its own
+// position, which are literals (already written) or earlier matches (copied
+// first), so the output is the same as copying each match at once.
+constexpr u32 kMatchQueue = 4;
+struct MatchQueue {
+  u32 at[kMatchQueue] = {};    // output offset from the slice start
+  u32 code[kMatchQueue] = {};  // length | distance << 9
+  u32 n = 0;
+  __device__ __forceinline__ void push(u32 offset, u32 length, u32 distance) {
+#pragma unroll
+    for (u32 k = 0; k < kMatchQueue; ++k) {
+      at[k] = n == k ? offset : at[k];
+      code[k] = n == k ? (length | (distance << 9)) : code[k];
+    }
+    ++n;
+  }
+  // Copies the queued matches in order (the head, then the rest moves up).
+  template <class Sink>
+  __device__ __forceinline__ void flush(const Sink& out, u64 dst0, u32* roots, u32* unres,
+                                        u32& nunres) {
+    for (; n; --n) {
+      emit_match(out, dst0, dst0 + at[0], code[0] >> 9, code[0] & 511u, roots, unres, nunres);
+#pragma unroll
+      for (u32 k = 0; k + 1 < kMatchQueue; ++k) {
+        at[k] = at[k + 1];
+        code[k] = code[k + 1];
+      }
+    }
+  }
+};
+
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
 // [.., block_end) of a stream whose output starts at out[floor]; adds the
 // slice's unresolved bytes to `unres_total`.  Returns 0 or an error.  `sh`
@@ -2642,69 +2728,50 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
   r.seek(entry);
   u64 dst = dst0;
   u32 nunres = 0, err = 0;  // unresolved bytes of this slice
-  while (r.pos() < stop) {
-    u32 length, x;  // x: the literal (length 1) or the distance
-    if (!quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x)) {
-      WordBits<kChecked> q;
-      q.words = r.words;
-      q.limit = r.limit;
-      q.seek(r.pos());
-      u32 lit, distance;
-      if (fast_token(sh.tables.ll, sh.tables.dd, q, lit, length, distance)) { err = kExtent; break; }
-      if (!length) break;
-      r.seek(q.pos());
-      x = length == 1 ? lit : distance;
-    }
-    if (length > block_end - dst) { err = kExtent; break; }
-    if (length == 1) {
-      out.put(dst++, u8(x));
-      continue;
-    }
-    const u32 distance = x;
-    if (distance > window || distance > dst - floor) { err = kBadDistance; break; }
-    const u64 src0 = dst - distance;
-    if (src0 + length <= dst0) {
-      // Every source precedes the slice: unresolved, rooted at the source.
-      for (u32 j = 0; j < length; ++j) roots[dst + j] = u32(src0 + j);
-      bits_set_range(unres, dst, length);
-      out.zero(dst, length);
-      nunres += length;
-    } else if (!nunres && src0 >= dst0) {
-      // Every source is this slice's own resolved output.
-      copy_periodic(out, dst, src0, distance, length);
-    } else if (distance == 1) {
-      // A run of the byte before: resolved, or one root for the whole run.
-      const u64 p = dst - 1;
-      const bool before = p < dst0;
-      if (before || (nunres && bit_get(unres, p))) {
-        const u32 root = before ? u32(p) : roots[p];
-        for (u32 j = 0; j < length; ++j) roots[dst + j] = root;
-        bits_set_range(unres, dst, length);
-        out.zero(dst, length);
-        nunres += length;
-      } else {
-        const u8 v = out.get(p);
-        for (u32 j = 0; j < length; ++j) out.put(dst + j, v);
-      }
-    } else {
-      for (u32 j = 0; j < length; ++j) {
-        const u64 d = dst + j, src = d - distance;
-        if (src < dst0) {
-          roots[d] = u32(src);
-          bit_set(unres, d);
-          out.zero(d, 1);
-          ++nunres;
-        } else if (nunres && bit_get(unres, src)) {
-          roots[d] = roots[src];
-          bit_set(unres, d);
-          out.zero(d, 1);
-          ++nunres;
+  MatchQueue q;
+  bool live = true;
+  for (;;) {
+    // One copy site for queued matches: when a lane's queue is full, and
+    // once every lane of the wave has finished decoding.
+    const bool any_live = __ballot(live) != 0;
+    if (live) {
+      u32 length = 0, x = 0;  // x: the literal (length 1) or the distance
+      if (r.pos() >= stop) {
+        live = false;
+      } else if (!quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x)) {
+        WordBits<kChecked> w;
+        w.words = r.words;
+        w.limit = r.limit;
+        w.seek(r.pos());
+        u32 lit, distance;
+        if (fast_token(sh.tables.ll, sh.tables.dd, w, lit, length, distance)) {
+          err = kExtent;
+          live = false;
+        } else if (!length) {
+          live = false;
         } else {
-          out.put(d, out.get(src));
+          r.seek(w.pos());
+          x = length == 1 ? lit : distance;
+        }
+      }
+      if (live && length > block_end - dst) {
+        err = kExtent;
+        live = false;
+      }
+      if (live) {
+        if (length == 1) {
+          out.put(dst++, u8(x));
+        } else if (x > window || x > dst - floor) {
+          err = kBadDistance;
+          live = false;
+        } else {
+          q.push(u32(dst - dst0), length, x);
+          dst += length;
         }
       }
     }
-    dst += length;
+    if (!any_live || __ballot(q.n == kMatchQueue)) q.flush(out, dst0, roots, unres, nunres);
+    if (!any_live) break;
   }
   unres_total += nunres;
   return err;

@@ -114,8 +114,10 @@ struct FixedScratch final : Scratch {
 // deflate.hip: chunked encode of one stream / a batch of streams.
 // deflate_scratch_bytes: the scratch run_deflate takes for one stream.
 u64 deflate_scratch_bytes(u64 in_size, u32 chunk_bytes);
+// With `independent`, every chunk's LZ77 window is the chunk alone (no
+// history from the bytes before it).
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
-                       u64 capacity, u32 chunk_bytes, u32* meta);
+                       u64 capacity, u32 chunk_bytes, u32* meta, bool independent = false);
 hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_total,
                              const BatchFile* files_host, u32 count, u8* out, u64 out_total,
                              u32 chunk_bytes, u32* meta);

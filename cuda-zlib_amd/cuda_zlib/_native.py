@@ -25,6 +25,7 @@ _I64P = ctypes.POINTER(ctypes.c_int64)
 SIGNATURES = {
     "HipZlibCompress": [_P, _I64, _P, _U64, _P, _U64, _P, _U64],
     "HipZlibCompressNoAlloc": [_P, _I64, _P, _U64, _P, _U64, _P, _U64],
+    "HipZlibCompressIndependent": [_P, _I64, _P, _U64, _P, _U64, _P, _U64],
     "HipZlibDecompress": [_P, _I64, _I64, _P, _U64, _P, _U64, _P, _U64],
     "HipZlibDecompressFormat": [_P, ctypes.c_int32, _P, _U64, _I64, _I64, _P, _U64, _P, _U64, _P,
                                 _U64],

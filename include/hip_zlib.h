@@ -33,6 +33,17 @@ int HipZlibCompress(hipStream_t stream, int64_t chunk_bytes, const uint8_t* inpu
                     uint64_t input_size, uint8_t* output, uint64_t output_size,
                     uint32_t* metadata, uint64_t metadata_count);
 
+/* HipZlibCompress with every chunk's LZ77 window limited to the chunk itself
+ * (no matches into the bytes before it), the reference encoder's semantics
+ * ("Chunks have no shared history", src/cuda_zlib/_encode_kernels.py:6;
+ * encode_chunk 283-393, launched by Compress at codec_ffi.cu:551-612).  Same
+ * arguments, checks, statuses and metadata as HipZlibCompress; the stream is
+ * usually somewhat larger.  The reference has no separate handler for it: its
+ * one compress handler always encodes chunks this way. */
+int HipZlibCompressIndependent(hipStream_t stream, int64_t chunk_bytes, const uint8_t* input,
+                               uint64_t input_size, uint8_t* output, uint64_t output_size,
+                               uint32_t* metadata, uint64_t metadata_count);
+
 /* Decompress a zlib stream into exactly output_size bytes.
  * metadata (2 x u32, device): [status, 0].  Output is zero-filled on failure
  * (serial small-stream route: decoded prefix followed by zeros).

@@ -103,6 +103,42 @@ def test_incompressible_uses_stored_blocks_at_the_bound(gpu):
     assert len(stream) == len(data) + 5 * chunks + 6
 
 
+def _compress_independent(data, chunk=32768):
+    from cuda_zlib import compress_zlib_padded
+    out, meta = compress_zlib_padded(data, 0, chunk_bytes=chunk, independent_chunks=True)
+    length, status = (int(v) for v in meta.cpu().numpy())
+    assert status == 0
+    host = out.cpu().numpy().tobytes()
+    assert not any(host[length:]), "padding after the stream must be zero"
+    return host[:length]
+
+
+@pytest.mark.parametrize("chunk", [256, 4096, 32768])
+def test_independent_chunks_round_trip(gpu, chunk):
+    for kind, data in _kinds(200_003, chunk + 1):
+        stream = _compress_independent(data, chunk)
+        assert zlib.decompress(stream) == data, kind
+
+
+def test_independent_chunks_never_reach_into_the_previous_chunk(gpu):
+    """Two copies of a 32 KiB incompressible chunk: with history the second
+    chunk is one long match into the first; without it both must be stored."""
+    x = np.random.default_rng(21).integers(0, 256, 32768, dtype=np.uint8).tobytes()
+    data = x + x
+    shared = _compress(data)
+    alone = _compress_independent(data)
+    assert zlib.decompress(shared) == data and zlib.decompress(alone) == data
+    assert len(shared) < 32768 + 2000
+    assert len(alone) == len(data) + 5 * 2 + 6  # two stored chunks at the bound
+
+
+def test_independent_chunks_cost_ratio_on_text(gpu):
+    data = workloads.text_like(2 << 20, np.random.default_rng(23))
+    shared, alone = _compress(data), _compress_independent(data)
+    assert zlib.decompress(alone) == data
+    assert len(shared) < len(alone) < len(data)
+
+
 def test_deterministic(gpu):
     data = workloads.text_like(200_000, np.random.default_rng(11))
     assert _compress(data) == _compress(data)
