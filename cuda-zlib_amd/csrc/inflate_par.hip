@@ -3131,17 +3131,30 @@ __global__ __launch_bounds__(256) void g_batch_wide_finish(const BatchFile* file
   }
 }
 
-constexpr u32 kResolveLinks = 32;  // chain links a position follows per round
+// Chain links a position follows in resolve round r: 2, 4, 8, 16, then 32.
+// Early rounds see nearly every unresolved byte, and a wave waits for its
+// longest chain, so they take few links; the later rounds, which see only the
+// long chains, take more.
+__host__ __device__ constexpr u32 resolve_links(u32 round) { return round < 4 ? 2u << round : 32u; }
+
+// Resolve rounds for chains of up to `span` links: round r multiplies the
+// reach of every root link by resolve_links(r) (each round leaves every
+// position's root as far along its chain as it got).
+inline u32 resolve_rounds(u64 span) {
+  u32 rounds = 0;
+  for (u64 reach = 1; reach < span; reach *= resolve_links(rounds)) ++rounds;
+  return rounds ? rounds : 1;
+}
 
 // One resolution round: round r scans the unresolved bits of buffer (r & 1)
 // (round 0: the bits set by emission; counts[r] unresolved positions,
 // zero-filled before the first round) and writes every word of the other
 // buffer with the positions still unresolved, counted in counts[r + 1].  A
-// position follows up to kResolveLinks links of its root chain through this
+// position follows up to resolve_links(round) links of its root chain through this
 // round's snapshot (roots: any root read is an earlier byte of the same
 // chain, so concurrent updates are harmless); at a resolved byte it takes
 // that byte, else it keeps the root reached.  Round r thus covers
-// kResolveLinks^(r+1) links.  Only bytes written by earlier launches are
+// the product of resolve_links over rounds 0..r.  Only bytes written by earlier launches are
 // read.  The last round leaves its count in st->unresolved[1] (status 20 in
 // g_finish).
 // With `parts`, every resolved byte is added to this workgroup's Adler-32
@@ -3184,7 +3197,8 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
         const u32 u = u32((g * 64 + idx) * 32 + b);
         u32 r = roots[u];
         unres = (bits[r >> 5] >> (r & 31)) & 1u;
-        for (u32 k = 0; unres && k < kResolveLinks; ++k) {
+        const u32 links = resolve_links(round);
+        for (u32 k = 0; unres && k < links; ++k) {
           r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           unres = (bits[r >> 5] >> (r & 31)) & 1u;
         }
@@ -3467,12 +3481,9 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
 
   // Emission and cross-segment resolution.
   const u64 words = (out_total + 31) / 32 + 1;
-  // Round r covers kResolveLinks^(r+1) links of a chain.  A chain hops back
-  // across slices (or serially emitted segments), so its length is bounded
-  // by the number of slices plus segments.
-  u32 rounds = 1;
-  for (u64 span = kResolveLinks; span < group_capacity * 64 + u64(max_blocks); span *= kResolveLinks)
-    ++rounds;
+  // A chain hops back across slices (or serially emitted segments), so its
+  // length is bounded by the number of slices plus segments.
+  const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
   // Adler-32 partial pairs: kAdlerSlots each for the lane emitter, the
   // serial emitter and the resolve rounds (workgroups add theirs, so they
   // start at zero), summed by g_finish.  The pairs, the round counts and the
@@ -3558,9 +3569,7 @@ hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8
             encoded, max_blocks, st, slice_entry, slice_off, group_link, group_capacity, roots,
             bits0, redo, wanted);
   HZ_TRY(hipGetLastError());
-  u32 rounds = 1;
-  for (u64 span = kResolveLinks; span < group_capacity * 64 + u64(max_blocks); span *= kResolveLinks)
-    ++rounds;
+  const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
   u64* counts = nullptr;
   HZ_TRY(scratch.alloc(&counts, rounds + 1));
   HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
