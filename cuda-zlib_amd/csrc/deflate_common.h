@@ -711,7 +711,7 @@ template <bool kChecked>
 struct Win4 {
   const u32* words;
   u32 w, off, x0, x1, x2, x3, limit;
-  __device__ __forceinline__ void seek(u32 p) {
+  __host__ __device__ __forceinline__ void seek(u32 p) {
     w = p >> 5;
     off = p & 31u;
     x0 = words[w];
@@ -719,18 +719,18 @@ struct Win4 {
     x2 = words[w + 2];
     x3 = words[w + 3];
   }
-  __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
-  __device__ __forceinline__ u32 bits32() const { return __builtin_amdgcn_alignbit(x1, x0, off); }
-  __device__ __forceinline__ u64 bits64() const {
-    return u64(__builtin_amdgcn_alignbit(x1, x0, off)) |
-           (u64(__builtin_amdgcn_alignbit(x2, x1, off)) << 32);
+  __host__ __device__ __forceinline__ u32 pos() const { return (w << 5) + off; }
+  __host__ __device__ __forceinline__ u32 bits32() const { return funnel32(x1, x0, off); }
+  __host__ __device__ __forceinline__ u64 bits64() const {
+    return u64(funnel32(x1, x0, off)) |
+           (u64(funnel32(x2, x1, off)) << 32);
   }
-  __device__ __forceinline__ u32 avail() const {
+  __host__ __device__ __forceinline__ u32 avail() const {
     if (!kChecked) return 0xffffffffu;
     const u32 p = pos();
     return p < limit ? limit - p : 0u;
   }
-  __device__ __forceinline__ void advance(u32 n) {
+  __host__ __device__ __forceinline__ void advance(u32 n) {
     const u32 o = off + n;
     const u32 adv = o >> 5;  // 0, 1 or 2
     off = o & 31u;
@@ -738,7 +738,9 @@ struct Win4 {
     u32 c0 = x0, c1 = x1, c2 = x2, c3 = x3;
     // Opaque register values: keeps the compiler from turning the selects
     // below into a load through a selected pointer (into private memory).
+#if defined(__HIP_DEVICE_COMPILE__)
     asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+#endif
     x0 = adv >= 2 ? c2 : adv ? c1 : c0;
     x1 = adv >= 2 ? c3 : adv ? c2 : c1;
     x2 = words[w + 2];  // first used by the next advance
@@ -753,7 +755,7 @@ struct Win4 {
 // of block, an invalid symbol, or bits too close to the limit): the caller
 // then decodes that token with fast_token.  The token takes n <= 41 bits.
 template <bool kChecked>
-__device__ __forceinline__ bool quick_token(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
+__host__ __device__ __forceinline__ bool quick_token(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
                                             Win4<kChecked>& r, u32& length, u32& lit_or_dist) {
   const u64 b = r.bits64();
   const u32 b32 = u32(b);
@@ -775,6 +777,46 @@ __device__ __forceinline__ bool quick_token(const HuffTable<288, 10>& ll, const 
   lit_or_dist = (dist & is_len) | ((e >> 8) & 0xffu & ~is_len);
   r.advance(ok ? n : 0u);
   return ok;
+}
+
+// quick_token, extended to literal pairs: when the token is a literal whose
+// successor is also a literal in the primary LUT and starts before `stop`,
+// both are taken from the same window bits (the second lookup, which for a
+// match reads its distance code, then reads the next literal/length code).
+// Returns the tokens taken: 0 (nothing; the caller decodes with
+// fast_token), 1 (length/x as quick_token gives them) or 2 (two literals:
+// x and lit2, the second starting `first_bits` after the first).  The pair
+// takes n <= 30 bits.
+template <bool kChecked>
+__host__ __device__ __forceinline__ u32 quick_pair(const HuffTable<288, 10>& ll, const HuffTable<32, 8>& dd,
+                                          Win4<kChecked>& r, u32 stop, u32& length, u32& x,
+                                          u32& lit2, u32& first_bits) {
+  const u64 b = r.bits64();
+  const u32 b32 = u32(b);
+  const u32 e = ll.primary[b32 & 1023u];
+  const u32 l = e & 15u;
+  const u32 kind = (e >> 4) & 3u;
+  const bool is_len = kind == kKindLen;
+  const u32 nx = is_len ? (e >> 8) & 15u : 0u;
+  const u32 s = l + nx;  // <= 20
+  // One lookup serves both cases: a match's distance code, or the code
+  // after a literal.
+  const u32* p2 = is_len ? &dd.primary[(b32 >> s) & 255u] : &ll.primary[u32(b >> l) & 1023u];
+  const u32 e2 = *p2;
+  const u32 l2 = e2 & 15u, dx = (e2 >> 4) & 15u;
+  const bool lit = kind == kKindLit && l != 0;
+  bool pair = lit && l2 != 0 && dx == kKindLit && r.pos() + l < stop;  // dx: the code's kind
+  if (kChecked) pair = pair && l + l2 <= r.avail();
+  const bool dist_ok = l2 != 0 && !(e2 & 0x100u);
+  const u32 n = is_len ? s + l2 + dx : l + (pair ? l2 : 0u);
+  bool ok = lit || (is_len && l != 0 && dist_ok);
+  if (kChecked) ok = ok && n <= r.avail();
+  length = is_len ? (e >> 16) + ((b32 >> l) & ((1u << nx) - 1u)) : 1u;
+  x = is_len ? (e2 >> 16) + u32((b >> (s + l2)) & ((1u << dx) - 1u)) : (e >> 8) & 0xffu;
+  lit2 = (e2 >> 8) & 0xffu;
+  first_bits = l;
+  r.advance(ok ? n : 0u);
+  return ok ? (pair ? 2u : 1u) : 0u;
 }
 
 // Adler-32 partial sums of output bytes as they are produced: S = sum of the

@@ -1295,8 +1295,9 @@ __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u
     bits = (w == cw ? bits : 0ull) | (1ull << (off & 63));
     cw = w;
     visit[w * kDescThreads] = bits;
-    u32 length, x;
-    if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
+    u32 length, x, x2, l1;
+    const u32 got = quick_pair<kChecked>(t.ll, t.dd, r, stop, length, x, x2, l1);
+    if (!got) {
       u32 lit, distance;
       const u32 err = full_token<kChecked>(t, r, length, lit, distance);
       if (err || !length) {
@@ -1308,6 +1309,15 @@ __device__ void desc_slice(const DecodeTables& t, Win4<kChecked>& r, u32 stop, u
     }
     produced += length;  // <= 512 tokens of <= 258 bytes per slice
     ck[w * kDescThreads] = u16(produced);  // read back for words 0..6 only: < 2^16
+    if (got == 2) {
+      // The pair's second literal starts l1 bits after the first (before stop).
+      const u32 off2 = off + l1, w2 = off2 >> 6;
+      bits = (w2 == cw ? bits : 0ull) | (1ull << (off2 & 63));
+      cw = w2;
+      visit[w2 * kDescThreads] = bits;
+      ++produced;
+      ck[w2 * kDescThreads] = u16(produced);
+    }
   }
   count = produced;
 }
@@ -1319,8 +1329,10 @@ __device__ u32 desc_bytes_between(const DecodeTables& t, const Stage& sg, u32 li
   u32 bytes = 0;
   while (r.pos() < to) {
     const u32 p = r.pos();
-    u32 length, x;
-    if (!quick_token<kChecked>(t.ll, t.dd, r, length, x)) {
+    u32 length, x, x2, l1;
+    const u32 got = quick_pair<kChecked>(t.ll, t.dd, r, to, length, x, x2, l1);
+    bytes += got >> 1;  // a pair's second literal
+    if (!got) {
       u32 lit, distance;
       // Events are stepped over as desc_slice does.
       const u32 err = full_token<kChecked>(t, r, length, lit, distance);
@@ -1470,18 +1482,28 @@ __device__ void describe_round(u64 len, u64 limit, DescShared& sh, State* st, u6
           break;
         }
         const bool seen = desc_visited(sh, k, off);
-        u32 length, x;
-        const bool quick = quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x);
+        u32 length, x, x2, l1;
+        const u32 got = quick_pair<kChecked>(sh.tables.ll, sh.tables.dd, r, sk + slice, length, x,
+                                             x2, l1);
         if (seen) {
           if (k == t + 1) merge = off;
           else merge2 = off;
           break;
         }
-        if (!quick) {
+        if (!got) {
           u32 lit, distance;
           if (full_token<kChecked>(sh.tables, r, length, lit, distance) || !length) break;
         }
         tail += length;
+        if (got == 2) {
+          // A pair's second literal (inside slice k) may be where they meet.
+          if (desc_visited(sh, k, off + l1)) {
+            if (k == t + 1) merge = off + l1;
+            else merge2 = off + l1;
+            break;
+          }
+          ++tail;
+        }
       }
     }
     if (t + 1 < kDescThreads) sh.merge[t + 1] = merge;
@@ -2735,10 +2757,12 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
     // once every lane of the wave has finished decoding.
     const bool any_live = __ballot(live) != 0;
     if (live) {
-      u32 length = 0, x = 0;  // x: the literal (length 1) or the distance
+      u32 length = 0, x = 0, x2 = 0, l1;  // x: the literal (length 1) or the distance
+      u32 got = 1;                        // tokens taken (2: literals x, x2)
       if (r.pos() >= stop) {
         live = false;
-      } else if (!quick_token<kChecked>(sh.tables.ll, sh.tables.dd, r, length, x)) {
+      } else if (!(got = quick_pair<kChecked>(sh.tables.ll, sh.tables.dd, r, stop, length, x, x2,
+                                              l1))) {
         WordBits<kChecked> w;
         w.words = r.words;
         w.limit = r.limit;
@@ -2752,15 +2776,17 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
         } else {
           r.seek(w.pos());
           x = length == 1 ? lit : distance;
+          got = 1;
         }
       }
-      if (live && length > block_end - dst) {
+      if (live && length + (got >> 1) > block_end - dst) {
         err = kExtent;
         live = false;
       }
       if (live) {
         if (length == 1) {
           out.put(dst++, u8(x));
+          if (got == 2) out.put(dst++, u8(x2));
         } else if (x > window || x > dst - floor) {
           err = kBadDistance;
           live = false;

@@ -14,6 +14,7 @@
 //   staged the same body decoded with WordBits/fast_token over guarded words
 //   copy   copy_bytes over every length/alignment pair up to 96 bytes
 //   frame  parse_frame on every truncation, in each format
+//   pairs  quick_pair (literal pairs) against quick_token over guarded words
 //   guard  reads one byte past a guarded buffer (must crash: checks the guard)
 #include <sys/mman.h>
 #include <unistd.h>
@@ -152,6 +153,131 @@ u32 staged_body(const u8* body, u64 len, u64& produced) {
   return kBlockCapacity;
 }
 
+// The same body decoded twice over guarded staged words in slices of
+// `slice_bits`: A with quick_token (one token at a time), B with quick_pair
+// (literal pairs); both fall back to fast_token.  Each slice decodes the
+// tokens that start before its stop, so after every slice A and B must stand
+// at the same position, and their outputs must agree byte for byte.
+// Returns a status (kExtent when they disagree); `out` is B's output.
+u32 pairs_body(const u8* body, u64 len, u32 slice_bits, std::vector<u8>& out) {
+  static DecodeTables t;
+  const u32 margin_words = 16;
+  const u64 words = (len + 3) / 4 + margin_words;
+  std::vector<u32> host(words, 0u);
+  memcpy(host.data(), body, len);
+  Guarded g(reinterpret_cast<const u8*>(host.data()), words * 4);
+  const u32* w = reinterpret_cast<const u32*>(g.data);
+  BitIn hdr;
+  hdr.init(body, len, 0);
+  out.clear();
+  std::vector<u8> other;
+  for (u32 blocks = 0; blocks < 100000; ++blocks) {
+    u32 final_block, type;
+    if (!hdr.take(1, final_block) || !hdr.take(2, type)) return kTruncated;
+    if (type == 3) return kReservedBlock;
+    if (type == 0) {
+      hdr.seek((hdr.pos + 7) & ~u64(7));
+      u32 n, comp;
+      if (!hdr.take(16, n) || !hdr.take(16, comp)) return kTruncated;
+      if ((n ^ comp) != 0xffffu) return kBadSymbol;
+      if (u64(n) * 8 > hdr.avail()) return kTruncated;
+      for (u32 i = 0; i < n; ++i) out.push_back(body[(hdr.pos >> 3) + i]);
+      hdr.seek(hdr.pos + u64(n) * 8);
+      if (final_block) return (hdr.pos + 7) / 8 == len ? kOk : kExtent;
+      continue;
+    }
+    u32 err = type == 1 ? build_fixed_tables(t) : build_dynamic_tables(t, hdr);
+    if (err) return err;
+    fast_format(t.ll, true, 0, 1);
+    fast_format(t.dd, false, 0, 1);
+    other = out;
+    std::vector<u8> starts(len * 8 + 64, 0);  // token starts A met
+    Win4<true> a, b;
+    a.words = b.words = w;
+    a.limit = b.limit = u32(len * 8);
+    a.seek(u32(hdr.pos));
+    b.seek(u32(hdr.pos));
+    bool ended = false;
+    while (!ended) {
+      const u32 stop = a.pos() + slice_bits;
+      // A: one token at a time.
+      while (!ended && a.pos() < stop) {
+        starts[a.pos()] = 1;
+        u32 length, x;
+        if (!quick_token<true>(t.ll, t.dd, a, length, x)) {
+          WordBits<true> q;
+          q.words = w;
+          q.limit = a.limit;
+          q.seek(a.pos());
+          u32 lit, distance;
+          err = fast_token(t.ll, t.dd, q, lit, length, distance);
+          if (err) return err;
+          a.seek(q.pos());
+          if (!length) { ended = true; break; }
+          x = length == 1 ? lit : distance;
+        }
+        if (length == 1) { other.push_back(u8(x)); continue; }
+        if (x > other.size()) return kBadDistance;
+        for (u32 j = 0; j < length; ++j) other.push_back(other[other.size() - x]);
+      }
+      // B: literal pairs, the same stop.
+      bool b_ended = false;
+      while (!b_ended && b.pos() < stop) {
+        u32 length, x, x2, l1;
+        const u32 start = b.pos();
+        const u32 got = quick_pair<true>(t.ll, t.dd, b, stop, length, x, x2, l1);
+        // The second literal starts l1 bits in, at one of A's token starts.
+        if (got == 2 && (start + l1 >= stop || !starts[start + l1])) return kExtent;
+        if (!got) {
+          WordBits<true> q;
+          q.words = w;
+          q.limit = b.limit;
+          q.seek(b.pos());
+          u32 lit, distance;
+          err = fast_token(t.ll, t.dd, q, lit, length, distance);
+          if (err) return err;
+          b.seek(q.pos());
+          if (!length) { b_ended = true; break; }
+          x = length == 1 ? lit : distance;
+        }
+        if (length == 1) {
+          out.push_back(u8(x));
+          if (got == 2) out.push_back(u8(x2));
+          continue;
+        }
+        if (x > out.size()) return kBadDistance;
+        for (u32 j = 0; j < length; ++j) out.push_back(out[out.size() - x]);
+      }
+      if (a.pos() != b.pos() || ended != b_ended || out.size() != other.size()) return kExtent;
+    }
+    if (out != other) return kExtent;
+    hdr.seek(b.pos());
+    if (final_block) return (hdr.pos + 7) / 8 == len ? kOk : kExtent;
+  }
+  return kBlockCapacity;
+}
+
+int mode_pairs(int argc, char** argv) {
+  for (int i = 0; i < argc; ++i) {
+    const std::vector<u8> s = read_file(argv[i]);
+    printf("%s", argv[i]);
+    for (u32 slice : {29u, 97u, 512u}) {
+      Frame f;
+      std::vector<u8> out;
+      u32 st = parse_frame(s.data(), s.size(), kFormatZlib, false, f);
+      if (!st) st = pairs_body(s.data() + f.body, f.body_len, slice, out);
+      u32 a = 1, b = 0;
+      for (u8 c : out) {
+        a = (a + c) % 65521;
+        b = (b + a) % 65521;
+      }
+      printf(" s%u=%u bytes%u=%zu adler%u=%u", slice, st, slice, out.size(), slice, (b << 16) | a);
+    }
+    printf("\n");
+  }
+  return 0;
+}
+
 int mode_walk(int argc, char** argv, bool staged) {
   for (int i = 0; i < argc; ++i) {
     const std::vector<u8> s = read_file(argv[i]);
@@ -249,6 +375,7 @@ int main(int argc, char** argv) {
   if (!strcmp(mode, "staged")) return mode_walk(argc - 2, argv + 2, true);
   if (!strcmp(mode, "copy")) return mode_copy();
   if (!strcmp(mode, "frame")) return mode_frame(argc - 2, argv + 2);
+  if (!strcmp(mode, "pairs")) return mode_pairs(argc - 2, argv + 2);
   if (!strcmp(mode, "guard")) {
     const u8 byte = 1;
     Guarded g(&byte, 1);

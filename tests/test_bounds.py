@@ -112,6 +112,21 @@ def test_wrapper_parsing_of_every_truncation(harness, stream_files, tmp_path):
         assert got[p]["f0"] == "0" and got[p]["f1"] == "0" and got[p]["f2"] == "15"
 
 
+def test_literal_pairs_match_single_tokens(harness, stream_files):
+    """quick_pair (two literals per step) stops at every slice end where
+    quick_token does and decodes the same bytes: checked slice by slice in C,
+    and the result against the bytes zlib produced."""
+    valid = [(n, p, raw) for n, p, raw in stream_files if raw is not None]
+    proc = _run(harness, "pairs", [p for _, p, _ in valid])
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    got = _parse(proc.stdout)
+    for name, path, raw in valid:
+        for slice_bits in (29, 97, 512):
+            assert got[path]["s%d" % slice_bits] == "0", (name, slice_bits)
+            assert int(got[path]["bytes%d" % slice_bits]) == len(raw), name
+            assert int(got[path]["adler%d" % slice_bits]) == zlib.adler32(raw), name
+
+
 def test_copy_bytes_every_length_and_alignment(harness):
     proc = _run(harness, "copy")
     assert proc.returncode == 0, proc.stdout + proc.stderr[-2000:]
