@@ -61,6 +61,7 @@ struct State {
   u64 precount;      // entries of the dense pre-candidate array
   u64 tables_used;   // stored per-block decode tables
   u64 long_count;    // pre-candidates whose header walk left the per-lane window
+  u64 dense_count;   // ranges whose valid headers alone overflow their list (kind 2)
   u64 start_bit;     // body bit of the first block (0 unless a wrapper field precedes it)
   u64 floor;         // lowest output position a back-reference may read (history allowed: 0)
   u32 isize;         // gzip: the trailer's ISIZE
@@ -496,17 +497,23 @@ __device__ __forceinline__ u32 scan_slot(u32 e) { return e + e / kScanPer; }
 __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, ScanShared& sh) {
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   u64 carry = 0;
+  // The next tile's values load while the current tile is scanned.
+  u32 x[kScanPer];
+#pragma unroll
+  for (u32 k = 0; k < kScanPer; ++k) {
+    const u64 e = k * kScanThreads + t;
+    x[k] = e < count ? in[e] & mask : 0u;
+  }
   for (u64 base = 0; base < count; base += kScanTile) {
     const u32 m = u32(min<u64>(count - base, kScanTile));
-    u32 x[kScanPer];
-#pragma unroll
-    for (u32 k = 0; k < kScanPer; ++k) {
-      const u32 e = k * kScanThreads + t;
-      x[k] = e < m ? in[base + e] & mask : 0u;
-    }
 #pragma unroll
     for (u32 k = 0; k < kScanPer; ++k) sh.v[scan_slot(k * kScanThreads + t)] = x[k];
-    __syncthreads();
+#pragma unroll
+    for (u32 k = 0; k < kScanPer; ++k) {
+      const u64 e = base + kScanTile + k * kScanThreads + t;
+      x[k] = e < count ? in[e] & mask : 0u;
+    }
+    lds_barrier();  // LDS only: the next tile's loads stay in flight
     u32 mine = 0;
 #pragma unroll
     for (u32 k = 0; k < kScanPer; ++k) mine += sh.v[scan_slot(t * kScanPer + k)];
@@ -517,7 +524,7 @@ __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, S
       if (lane >= off) incl += y;
     }
     if (lane == 63) sh.wave[wave] = incl;
-    __syncthreads();
+    lds_barrier();
     u64 run = carry, tile_total = 0;
 #pragma unroll
     for (u32 w = 0; w < kScanThreads / 64; ++w) {
@@ -533,7 +540,7 @@ __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, S
       run += sh.v[scan_slot(e)];
     }
     carry += tile_total;
-    __syncthreads();  // the next tile reuses sh
+    lds_barrier();  // the next tile reuses sh
   }
   return carry;
 }
@@ -599,6 +606,7 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   st->precount = 0;
   st->tables_used = 0;
   st->long_count = 0;
+  st->dense_count = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -607,7 +615,8 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
 // overflow, leaves them to the gather pass (kind 2).  Also counts
 // stored-endpoint seeds.  Workgroups take ranges grid-stride.
 __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State* st,
-                                                  u32* wg_count, u64* wg_list, u64 groups) {
+                                                  u32* wg_count, u64* wg_list, u32* dense,
+                                                  u32* block_total, u64 groups, u64 per_block) {
   // The prefilter's lists are dead once its result is read, before any
   // validation uses the tables.
   __shared__ union {
@@ -631,19 +640,19 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
   // The next range's words are loaded while the current range is checked.
   static_assert(kPreStageWords <= 3 * kDiscThreads, "three words per thread hold a range");
   StagePrefetch<kPreStageWords, 3> next;
-  if (blockIdx.x < groups)
-    next.load(body, len, u64(blockIdx.x) * kDiscRange * 8, (u64(blockIdx.x) + 1) * kDiscRange * 8,
-              kPreMargin);
-  for (u64 wg = blockIdx.x; wg < groups; wg += gridDim.x) {
+  // This workgroup's ranges: per_block consecutive ones.
+  const u64 r0 = u64(blockIdx.x) * per_block, r1 = min(groups, r0 + per_block);
+  u32 entries = 0;  // listed entries of the block's ranges
+  if (r0 < r1) next.load(body, len, r0 * kDiscRange * 8, (r0 + 1) * kDiscRange * 8, kPreMargin);
+  for (u64 wg = r0; wg < r1; ++wg) {
     next.store(sg, body);
     for (u32 i = t; i < kDiscRange * 8 / 32; i += kDiscThreads) pass[i] = 0;
     __syncthreads();
     // Words past the staged ones read as zero, as body bits past the end do.
     for (u32 i = sg.count + t; i < kPreStageWords; i += kDiscThreads) sg.words[i] = 0;
     __syncthreads();
-    if (wg + gridDim.x < groups)
-      next.load(body, len, (wg + gridDim.x) * kDiscRange * 8, (wg + gridDim.x + 1) * kDiscRange * 8,
-                kPreMargin);
+    if (wg + 1 < r1)
+      next.load(body, len, (wg + 1) * kDiscRange * 8, (wg + 2) * kDiscRange * 8, kPreMargin);
     const u64 b0 = wg * kDiscRange + u64(t) * kDiscBytesPerThread;
     // The range starts at stage byte `a` (the stage begins at the aligned word
     // holding it); this thread's 64 offsets start at stage word 2t.
@@ -726,7 +735,12 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
       base = block_exclusive_scan(__popcll(mask), scan, total);
       kind = total > kDiscCap ? 2u : 1u;
     }
-    if (!threadIdx.x) wg_count[wg] = total | (kind << kKindShift);
+    if (!threadIdx.x) {
+      wg_count[wg] = total | (kind << kKindShift);
+      if (kind == 2)
+        dense[atomicAdd(reinterpret_cast<unsigned long long*>(&st->dense_count), 1ull)] = u32(wg);
+    }
+    entries += total;
     if (kind < 2) {
       while (mask) {
         const u32 k = __builtin_ctzll(mask);
@@ -736,17 +750,30 @@ __global__ __launch_bounds__(256) void g_discover(const u8* body, u64 len, State
     }
     __syncthreads();  // the next range reuses the stage and the lists
   }
+  if (!t) block_total[blockIdx.x] = entries;
   if (seeds) atomicAdd(reinterpret_cast<unsigned long long*>(&st->seeds), seeds);
 }
 
-// Discovery pass 2: one workgroup scans the per-range counts into offsets of
-// the dense pre-candidate array.
-__global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg_count,
-                                                        u64* wg_offset, u64 groups,
+// Offset in the dense array of range wg's list: its block's base plus the
+// lists of the block's earlier ranges (lanes load their counts, a wave sum
+// adds them).  Every lane of the wave calls it.
+__device__ __forceinline__ u64 range_offset(const u32* wg_count, const u64* block_base, u64 wg,
+                                            u64 per_block) {
+  const u64 b = wg / per_block, first = b * per_block;
+  u32 before = 0;
+  for (u64 j = first + lane_id(); j < wg; j += 64) before += wg_count[j] & kCountMask;
+  for (u32 off = 32; off; off >>= 1) before += __shfl_xor(before, off, 64);
+  return block_base[b] + before;
+}
+
+// Discovery pass 2: one workgroup scans the per-block entry totals into
+// offsets of the dense pre-candidate array.
+__global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* block_total,
+                                                        u64* block_base, u64 blocks,
                                                         u64 pre_capacity) {
   __shared__ ScanShared sh;
   if (st->status) return;
-  const u64 total = wg_exclusive_scan(wg_count, kCountMask, groups, wg_offset, sh);
+  const u64 total = wg_exclusive_scan(block_total, ~0u, blocks, block_base, sh);
   if (threadIdx.x == 0) {
     st->precount = total;
     // Only kind-2 ranges (valid headers alone overflowing a range) can push the
@@ -756,39 +783,59 @@ __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* wg
   }
 }
 
-// Discovery pass 3: the per-range lists in order into the dense array; kind-2
-// ranges recompute and validate here.
-__global__ __launch_bounds__(256) void g_discover_gather(const u8* body, u64 len, const State* st,
-                                                         const u32* wg_count, const u64* wg_list,
-                                                         const u64* wg_offset, u64* pre) {
+// Discovery pass 3: the per-range lists in order into the dense array, one
+// wave per range (kind-2 ranges are left to pass 3b).
+__global__ __launch_bounds__(256) void g_discover_gather(const State* st, const u32* wg_count,
+                                                         const u64* wg_list, const u64* block_base,
+                                                         u64* pre, u64 groups, u64 per_block) {
+  if (st->status) return;
+  const u64 wg = u64(blockIdx.x) * (kDiscThreads / 64) + (threadIdx.x >> 6);
+  if (wg >= groups) return;
+  const u32 c = wg_count[wg], lane = lane_id();
+  if ((c >> kKindShift) >= 2) return;
+  const u64 off = range_offset(wg_count, block_base, wg, per_block);
+  if (lane < (c & kCountMask)) pre[off + lane] = wg_list[wg * kDiscCap + lane];
+}
+
+// Discovery pass 3b: kind-2 ranges (listed by pass 1) recompute and
+// validate their offsets straight into the dense array.
+__global__ __launch_bounds__(256) void g_discover_dense(const u8* body, u64 len, const State* st,
+                                                        const u32* dense, const u32* wg_count,
+                                                        const u64* block_base, u64* pre,
+                                                        u64 per_block) {
+  __shared__ u64 range_off;
   __shared__ u8 luts[128][kDiscThreads];
   __shared__ u32 scan[kDiscThreads];
   __shared__ u16 kraft3[512];
   __shared__ PreStage sg;
   if (st->status) return;
-  const u64 wg = blockIdx.x;
-  const u32 count = wg_count[wg] & kCountMask, kind = wg_count[wg] >> kKindShift;
-  const u64 off = wg_offset[wg];
-  if (kind < 2) {
-    for (u32 i = threadIdx.x; i < count; i += kDiscThreads) pre[off + i] = wg_list[wg * kDiscCap + i];
-    return;
-  }
+  const u64 n = st->dense_count;
+  if (blockIdx.x >= n) return;
   build_kraft3(kraft3);
-  stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
-  __syncthreads();
-  const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
-  const u64 s0 = st->start_bit;
-  u64 first;
-  start_mask(s0, b0, first);
-  u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3, s0),
-                           &luts[0][threadIdx.x], kDiscThreads);
-  mask |= first;
-  u32 total;
-  u32 at = block_exclusive_scan(__popcll(mask), scan, total);
-  while (mask) {
-    const u32 k = __builtin_ctzll(mask);
-    mask &= mask - 1;
-    pre[off + at++] = (b0 * 8 + k) | kValidBit;
+  for (u64 k = blockIdx.x; k < n; k += gridDim.x) {
+    const u64 wg = dense[k];
+    if (threadIdx.x < 64) {
+      const u64 o = range_offset(wg_count, block_base, wg, per_block);
+      if (!threadIdx.x) range_off = o;
+    }
+    stage_range(body, len, wg * kDiscRange * 8, (wg + 1) * kDiscRange * 8, sg, kPreMargin);
+    __syncthreads();
+    const u64 b0 = wg * kDiscRange + u64(threadIdx.x) * kDiscBytesPerThread;
+    const u64 s0 = st->start_bit;
+    u64 first;
+    start_mask(s0, b0, first);
+    u64 mask = validate_mask(body, len, b0, prefilter_mask(len, b0, sg, kraft3, s0),
+                             &luts[0][threadIdx.x], kDiscThreads);
+    mask |= first;
+    u32 total;
+    u32 at = block_exclusive_scan(__popcll(mask), scan, total);  // (its barrier publishes range_off)
+    const u64 off = range_off;
+    while (mask) {
+      const u32 b = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      pre[off + at++] = (b0 * 8 + b) | kValidBit;
+    }
+    __syncthreads();  // the next range reuses the stage
   }
 }
 
@@ -3507,24 +3554,36 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 pre_capacity = groups * kDiscCap + u64(max_candidates) + 1;
   const u64 pre_blocks = (pre_capacity + kDiscThreads - 1) / kDiscThreads;
   u32 *wg_count = nullptr, *block_valid = nullptr;
-  u64 *wg_list = nullptr, *wg_offset = nullptr, *pre = nullptr, *block_offset = nullptr,
+  u64 *wg_list = nullptr, *pre = nullptr, *block_offset = nullptr,
       *cand = nullptr;
   HZ_TRY(scratch.alloc(&wg_count, groups));
   HZ_TRY(scratch.alloc(&wg_list, groups * kDiscCap));
-  HZ_TRY(scratch.alloc(&wg_offset, groups));
   HZ_TRY(scratch.alloc(&pre, pre_capacity));
   HZ_TRY(scratch.alloc(&block_valid, pre_blocks));
   HZ_TRY(scratch.alloc(&block_offset, pre_blocks));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
-  HZ_LAUNCH(g_discover, dim3(clamp_grid(groups, 8192)), dim3(kDiscThreads), 0, stream, body,
-            len, st, wg_count, wg_list, groups);
+  // Each discovery workgroup takes per_block consecutive ranges.
+  const u64 per_block = (groups + 8191) / 8192;
+  const u64 blocks = (groups + per_block - 1) / per_block;
+  u32* dense = nullptr;
+  u32* block_total = nullptr;
+  u64* block_base = nullptr;
+  HZ_TRY(scratch.alloc(&dense, groups));
+  HZ_TRY(scratch.alloc(&block_total, blocks));
+  HZ_TRY(scratch.alloc(&block_base, blocks));
+  HZ_LAUNCH(g_discover, dim3(u32(blocks)), dim3(kDiscThreads), 0, stream, body, len, st, wg_count,
+            wg_list, dense, block_total, groups, per_block);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, wg_count, wg_offset, groups,
+  HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, block_total, block_base, blocks,
             pre_capacity);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_discover_gather, dim3(u32(groups)), dim3(kDiscThreads), 0, stream, body, len, st,
-            wg_count, wg_list, wg_offset, pre);
+  HZ_LAUNCH(g_discover_gather, dim3(u32((groups + kDiscThreads / 64 - 1) / (kDiscThreads / 64))),
+            dim3(kDiscThreads), 0, stream, st, wg_count, wg_list, block_base, pre, groups,
+            per_block);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_discover_dense, dim3(64), dim3(kDiscThreads), 0, stream, body, len, st, dense,
+            wg_count, block_base, pre, per_block);
   HZ_TRY(hipGetLastError());
   u32* long_list = nullptr;
   HZ_TRY(scratch.alloc(&long_list, pre_capacity));
