@@ -830,6 +830,13 @@ struct AdlerAcc {
     w += weight * x;
     if (w >> 62) w %= kAdlerMod;
   }
+  // add_byte without the reduction: the caller folds (below) before w can
+  // pass 2^63 (a weight stays below 2^34, a product below 2^42).
+  __host__ __device__ __forceinline__ void add_byte_unfolded(u32 x, u64 weight) {
+    s += x;
+    w += weight * x;
+  }
+  __host__ __device__ __forceinline__ void fold() { w %= kAdlerMod; }
   // Sixteen bytes whose first weighs `weight0` (each next one 1 less).
   __host__ __device__ __forceinline__ void add16(const uint4& q, u64 weight0) {
     const u32 words[4] = {q.x, q.y, q.z, q.w};

@@ -2743,7 +2743,7 @@ struct RoundBytes {
       lds[u32(p - base)] = v;
     } else {
       out[p] = v;
-      acc->add_byte(v, end - p);
+      acc->add_byte_unfolded(v, end - p);  // folded once per round (at most 2^18 bytes a thread)
     }
   }
   __device__ __forceinline__ void zero(u64 p, u32 n) const {
@@ -3072,6 +3072,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
           }
           done += count;
           g = sh.next_g;
+          sums.fold();
           __syncthreads();
         }
       }
