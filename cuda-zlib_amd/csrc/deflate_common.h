@@ -819,6 +819,29 @@ __host__ __device__ __forceinline__ u32 quick_pair(const HuffTable<288, 10>& ll,
   return ok ? (pair ? 2u : 1u) : 0u;
 }
 
+// quick_pair extended to a third literal after a pair (a third lookup in
+// the same window bits): returns 0-3 tokens taken; with 3, lit3 is the third
+// literal.  Used by emission, which only needs the bytes.
+template <bool kChecked>
+__host__ __device__ __forceinline__ u32 quick_triple(const HuffTable<288, 10>& ll,
+                                                     const HuffTable<32, 8>& dd, Win4<kChecked>& r,
+                                                     u32 stop, u32& length, u32& x, u32& lit2,
+                                                     u32& lit3) {
+  const u32 p = r.pos();
+  const u64 b = r.bits64();
+  u32 l1;
+  const u32 got = quick_pair<kChecked>(ll, dd, r, stop, length, x, lit2, l1);
+  if (got != 2) return got;
+  const u32 l12 = r.pos() - p;  // both codes
+  const u32 e3 = ll.primary[u32(b >> l12) & 1023u];
+  const u32 l3 = e3 & 15u;
+  bool third = l3 != 0 && ((e3 >> 4) & 3u) == kKindLit && p + l12 < stop;
+  if (kChecked) third = third && l3 <= r.avail();
+  lit3 = (e3 >> 8) & 0xffu;
+  r.advance(third ? l3 : 0u);
+  return third ? 3u : 2u;
+}
+
 // Adler-32 partial sums of output bytes as they are produced: S = sum of the
 // bytes, W = sum of (end - position) * byte, where `end` is the stream's end
 // position, so that a byte at stream position i weighs n - i.  W is reduced

@@ -60,7 +60,6 @@ struct State {
   u64 groups_used;   // 64-slot slice groups handed out by describe
   u64 precount;      // entries of the dense pre-candidate array
   u64 tables_used;   // stored per-block decode tables
-  u64 long_count;    // pre-candidates whose header walk left the per-lane window
   u64 dense_count;   // ranges whose valid headers alone overflow their list (kind 2)
   u64 start_bit;     // body bit of the first block (0 unless a wrapper field precedes it)
   u64 floor;         // lowest output position a back-reference may read (history allowed: 0)
@@ -552,13 +551,22 @@ __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, S
 // wrapper field between it and the first block (a zlib DICTID, gzip's
 // optional fields) becomes start_bit.  A zlib stream with FDICT checks the
 // dictionary's Adler-32 against its DICTID (the workgroup sums the bytes).
+// Every workgroup also zeroes its grid-stride share of zero[0..zero_words):
+// the scratch that later kernels accumulate into (Adler-32 pairs, resolve
+// counts, the first unresolved bitmap).
 __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 format,
                                                const u8* dict, u64 dict_len, u64 body_off,
-                                               u64 out_base, State* st) {
+                                               u64 out_base, State* st, u32* zero,
+                                               u64 zero_words) {
   __shared__ Frame frame;
   __shared__ u32 status;
   __shared__ u64 red[2][4];
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  {
+    const u64 stride = u64(gridDim.x) * blockDim.x;
+    for (u64 i = u64(blockIdx.x) * blockDim.x + t; i < zero_words; i += stride) zero[i] = 0;
+  }
+  if (blockIdx.x) return;
   if (!t) status = parse_frame(in, in_size, format, dict_len > 0, frame);
   __syncthreads();
   if (!status && frame.needs_dict) {  // uniform
@@ -605,7 +613,6 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   st->groups_used = 0;
   st->precount = 0;
   st->tables_used = 0;
-  st->long_count = 0;
   st->dense_count = 0;
 }
 
@@ -847,7 +854,7 @@ namespace {
 // long header walk does not idle the other lanes.  A lane's header bits
 // are copied into its LDS window and its code-length symbols are decoded
 // arithmetically from the canonical code (no per-candidate table); a walk
-// that would leave the window goes to the long list, validated by pass 4b.
+// that reaches the window's end reloads the window from its position.
 constexpr u32 kValPerWave = 128;                    // pre-candidates per wave
 constexpr u32 kValRound = 16;                       // symbols between refills
 constexpr u32 kValWindowWords = 32;                 // LDS window per lane (dwords)
@@ -863,7 +870,8 @@ struct ValWalk {
   u32 x0, x1, x2;    // window words w, w+1, w+2 (x2 loaded for the next advance)
   u32 w, off;        // window position
   u32 limit;         // window-relative bit limit
-  bool body_end;     // limit is the body end (else leaving the window defers)
+  bool body_end;     // limit is the body end (else the window is reloaded there)
+  u64 bit0;          // body bit of window bit 0
   u32 nl, total, i, prev, eob, ll_kraft, d_kraft, ll_nnz, d_nnz;
   // Canonical code-length code (val_start): la[0..2] hold the left-justified
   // 7-bit starts of the codes of lengths 2..7 as 16-bit fields; lp and bp the
@@ -907,21 +915,26 @@ struct ValWalk {
 
 enum : u32 { kValRunning = 0, kValValid = 1, kValInvalid = 2, kValLong = 3 };
 
-
-// Load candidate `pos` (its BTYPE already known to be 2) into the lane's
-// window and parse HLIT/HDIST/HCLEN and the code-length code.  Returns
-// kValRunning or a final verdict.
-__device__ u32 val_start(const u8* body, u64 len, u64 pos, ValShared& sh, u32 lane, ValWalk& v) {
+// The lane's window: body bits from the dword holding bit `pos`, the walk
+// positioned at `pos`.  kBatch window words are loaded at a time (all of
+// them for a new candidate; fewer registers for a reload mid-walk).
+template <u32 kBatch>
+__device__ __forceinline__ void val_window(const u8* body, u64 len, u64 pos, ValShared& sh,
+                                           u32 lane, ValWalk& v) {
+  static_assert(kValWindowWords % kBatch == 0, "whole batches");
   const uintptr_t base = reinterpret_cast<uintptr_t>(body);
   const uintptr_t first = (base + (pos >> 3)) & ~uintptr_t(3);
   const uintptr_t end = base + len;  // body bytes end here
   const u32* g = reinterpret_cast<const u32*>(first);
   if (first + 4 * kValWindowWords <= end) {
-    u32 x[kValWindowWords];  // all loads in flight at once
+#pragma unroll 1
+    for (u32 j0 = 0; j0 < kValWindowWords; j0 += kBatch) {
+      u32 x[kBatch];  // a batch of loads in flight at once
 #pragma unroll
-    for (u32 j = 0; j < kValWindowWords; ++j) x[j] = g[j];
+      for (u32 j = 0; j < kBatch; ++j) x[j] = g[j0 + j];
 #pragma unroll
-    for (u32 j = 0; j < kValWindowWords; ++j) sh.win[j][lane] = x[j];
+      for (u32 j = 0; j < kBatch; ++j) sh.win[j0 + j][lane] = x[j];
+    }
   } else {
     for (u32 j = 0; j < kValWindowWords; ++j) {
       const uintptr_t a = first + 4 * j;
@@ -934,10 +947,19 @@ __device__ u32 val_start(const u8* body, u64 len, u64 pos, ValShared& sh, u32 la
     }
   }
   const u32 p0 = u32((base + (pos >> 3) - first) * 8 + (pos & 7));  // window bit of `pos`
-  const u64 rel_end = u64(p0) + (len * 8 - pos);                     // window bit of the body end
+  // Window bit of the body end (0 when even `pos` lies past it: nothing fits).
+  const u64 rel_end = u64(p0) + len * 8 > pos ? u64(p0) + len * 8 - pos : 0;
   v.body_end = rel_end <= kValUsableBits;
   v.limit = v.body_end ? u32(rel_end) : kValUsableBits;
-  v.seek(sh, lane, p0 + 3);
+  v.bit0 = pos - p0;
+  v.seek(sh, lane, p0);
+}
+
+// Load candidate `pos` (its BTYPE already known to be 2) into the lane's
+// window and parse HLIT/HDIST/HCLEN and the code-length code.  Returns
+// kValRunning or a final verdict.
+__device__ u32 val_start(const u8* body, u64 len, u64 pos, ValShared& sh, u32 lane, ValWalk& v) {
+  val_window<kValWindowWords>(body, len, pos + 3, sh, lane, v);
   // 14 + 57 bits of fields fit in the usable window (p0 < 32).
   if (v.pos() + 14 > v.limit) return kValInvalid;  // only at the body end
   const u32 f = v.bits();
@@ -998,7 +1020,8 @@ __device__ u32 val_start(const u8* body, u64 len, u64 pos, ValShared& sh, u32 la
   return kValRunning;
 }
 
-// One code-length symbol of the walk.
+// One code-length symbol of the walk.  kValLong: the symbol does not fit in
+// the window (nothing taken).
 __device__ __forceinline__ u32 val_step(const ValShared& sh, u32 lane, ValWalk& v) {
   const u32 b = v.bits();
   u32 l;
@@ -1037,9 +1060,8 @@ __device__ __forceinline__ u32 val_step(const ValShared& sh, u32 lane, ValWalk& 
 }  // namespace
 
 // Discovery pass 4 (one wave per workgroup; see above).  Valid entries get
-// kValidBit; deferred ones are appended to long_list.
-__global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre,
-                                                 u32* long_list) {
+// kValidBit.
+__global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre) {
   __shared__ ValShared sh;
   if (st->status) return;
   const u64 n = st->precount;
@@ -1067,39 +1089,24 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
       cursor += __popcll(idle);
     }
     if (!__ballot(active)) break;
+    // A walk that reaches its window's end pauses for the rest of the round
+    // and reloads the window after it (one copy of the reload, outside the
+    // unrolled steps); the step it could not take is taken next round.
+    bool reload = false;
     for (u32 k = 0; k < kValRound; ++k) {
       if (active) {
         const u32 r = val_step(sh, lane, v);
         if (r != kValRunning) {
           active = false;
           if (r == kValValid) pre[ci] |= kValidBit;
-          else if (r == kValLong)
-            long_list[atomicAdd(reinterpret_cast<unsigned long long*>(&st->long_count), 1ull)] =
-                u32(ci);
+          reload = r == kValLong;
         }
       }
     }
-  }
-}
-
-// Discovery pass 4b: one wave per deferred entry validates its header from
-// a staged copy of the longest possible header.
-__global__ __launch_bounds__(64) void g_validate_long(const u8* body, u64 len, const State* st,
-                                                      u64* pre, const u32* long_list) {
-  __shared__ StageT<kHeaderWords> stage;
-  __shared__ u8 lut[128];
-  if (st->status) return;
-  const u64 n = st->long_count;
-  for (u64 k = blockIdx.x; k < n; k += gridDim.x) {
-    const u32 ci = long_list[k];
-    const u64 pos = pre[ci] & kPosMask;
-    stage_range(body, len, pos, pos + 8, stage, kHeaderBytes);
-    __syncthreads();
-    if (!threadIdx.x) {
-      BitIn r = staged_reader(stage, len, pos + 3);
-      if (dynamic_header_fields_valid(r, lut, 1)) pre[ci] |= kValidBit;
+    if (reload) {
+      val_window<8>(body, len, v.bit0 + v.pos(), sh, lane, v);
+      active = true;
     }
-    __syncthreads();
   }
 }
 
@@ -2890,12 +2897,12 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
     // once every lane of the wave has finished decoding.
     const bool any_live = __ballot(live) != 0;
     if (live) {
-      u32 length = 0, x = 0, x2 = 0, l1;  // x: the literal (length 1) or the distance
-      u32 got = 1;                        // tokens taken (2: literals x, x2)
+      u32 length = 0, x = 0, x2 = 0, x3 = 0;  // x: the literal (length 1) or the distance
+      u32 got = 1;                            // tokens taken (2, 3: literals x, x2, x3)
       if (r.pos() >= stop) {
         live = false;
-      } else if (!(got = quick_pair<kChecked>(sh.tables.ll, sh.tables.dd, r, stop, length, x, x2,
-                                              l1))) {
+      } else if (!(got = quick_triple<kChecked>(sh.tables.ll, sh.tables.dd, r, stop, length, x, x2,
+                                                x3))) {
         WordBits<kChecked> w;
         w.words = r.words;
         w.limit = r.limit;
@@ -2912,14 +2919,15 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
           got = 1;
         }
       }
-      if (live && length + (got >> 1) > block_end - dst) {
+      if (live && length + got - 1 > block_end - dst) {
         err = kExtent;
         live = false;
       }
       if (live) {
         if (length == 1) {
           out.put(dst++, u8(x));
-          if (got == 2) out.put(dst++, u8(x2));
+          if (got >= 2) out.put(dst++, u8(x2));
+          if (got == 3) out.put(dst++, u8(x3));
         } else if (x > window || x > dst - floor) {
           err = kBadDistance;
           live = false;
@@ -3469,18 +3477,28 @@ __device__ u32 crc_from_tiles(const u64* parts, u64 n) {
   return crc_finish(reg[0], n);
 }
 
-// Final status: the trailer check over the output (`check`): Adler-32 from
-// the `nparts` pairs the emitters and resolve rounds accumulated (every
-// output byte is summed once, by whichever kernel wrote it), CRC-32 and size
-// from g_crc_tiles' tile registers, or nothing; one 256-thread workgroup.
+// Final status and the output on failure, over a grid of 256-thread
+// workgroups.  The status before the trailer check (the first error of the
+// decode, or unresolved references) is read by every workgroup: on a decode
+// error each zeroes its grid-stride share of out[0..n).  Workgroup 0 then
+// checks the trailer (`check`): Adler-32 from the `nparts` pairs the emitters
+// and resolve rounds accumulated (every output byte is summed once, by
+// whichever kernel wrote it), CRC-32 and size from g_crc_tiles' tile
+// registers, or nothing, and writes the metadata.  A trailer mismatch keeps
+// the output.
 __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, const u64* parts,
-                                                u32 nparts, u32 check) {
+                                                u32 nparts, u32 check, u8* out) {
   __shared__ u64 red[2][4];
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   u32 status = st->status;
   if (!status) status = st->emit_status;
   // References still unresolved after every round.
   if (!status && st->unresolved[1]) status = kReferenceDepth;
+  if (status) {  // uniform; st->status never holds a trailer mismatch here
+    const u64 stride = u64(gridDim.x) * blockDim.x;
+    for (u64 i = u64(blockIdx.x) * blockDim.x + t; i < n; i += stride) out[i] = 0;
+  }
+  if (blockIdx.x) return;
   if (!status && check == kCheckCrc) {  // uniform
     const u32 got = crc_from_tiles(parts, n);
     if (!t && (got != st->wanted || u32(n) != st->isize)) status = kGzipCheckMismatch;
@@ -3505,19 +3523,9 @@ __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, con
     if (((b << 16) | a) != st->wanted) status = kAdlerMismatch;
   }
   if (!t) {
-    st->status = status;
     meta[0] = status;
     meta[1] = 0;
   }
-}
-
-// Zero the output unless the stream decoded (status 0) or only its checksum failed.
-__global__ __launch_bounds__(256) void g_zero_on_failure(const State* st, u8* out, u64 n) {
-  const u32 status = st->status;
-  if (!status || status == kAdlerMismatch || status == kGzipCheckMismatch) return;
-  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
-  const u64 stride = u64(gridDim.x) * blockDim.x;
-  for (u64 i = tid; i < n; i += stride) out[i] = 0;
 }
 
 namespace {
@@ -3546,8 +3554,23 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   u8* stream_out = out + out_base;
   State* st = nullptr;
   HZ_TRY(scratch.alloc(&st, 1));
-  HZ_LAUNCH(g_frame, dim3(1), dim3(256), 0, stream, in, in_size, fmt.format, fmt.dict,
-            fmt.dict_len, body_off, out_base, st);
+  // Emission and resolution scratch sizes.  A resolve chain hops back across
+  // slices (or serially emitted segments), so its length is bounded by the
+  // number of slices plus segments.
+  const u64 group_capacity = (len * 8) / 8192 + 65536;
+  const u64 words = (out_total + 31) / 32 + 1;
+  const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
+  // Adler-32 partial pairs: kAdlerSlots each for the lane emitter, the
+  // serial emitter and the resolve rounds (workgroups add theirs, so they
+  // start at zero), summed by g_finish.  The pairs, the round counts and the
+  // first unresolved bitmap are zeroed by g_frame.
+  u8* zeroed = nullptr;
+  const u64 zero_u64 = 2 * u64(3 * kAdlerSlots) + rounds + 1;
+  const u64 zero_bytes = 8 * zero_u64 + 4 * words;
+  HZ_TRY(scratch.alloc(&zeroed, zero_bytes));
+  HZ_LAUNCH(g_frame, dim3(clamp_grid((zero_bytes / 4 + 255) / 256, 2048)), dim3(256), 0, stream,
+            in, in_size, fmt.format, fmt.dict, fmt.dict_len, body_off, out_base, st,
+            reinterpret_cast<u32*>(zeroed), zero_bytes / 4);
   HZ_TRY(hipGetLastError());
 
   // Discovery.
@@ -3586,12 +3609,8 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_discover_dense, dim3(64), dim3(kDiscThreads), 0, stream, body, len, st, dense,
             wg_count, block_base, pre, per_block);
   HZ_TRY(hipGetLastError());
-  u32* long_list = nullptr;
-  HZ_TRY(scratch.alloc(&long_list, pre_capacity));
   const u64 val_waves = (pre_capacity + kValPerWave - 1) / kValPerWave;
-  HZ_LAUNCH(g_validate, dim3(u32(val_waves)), dim3(64), 0, stream, body, len, st, pre, long_list);
-  HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_validate_long, dim3(2048), dim3(64), 0, stream, body, len, st, pre, long_list);
+  HZ_LAUNCH(g_validate, dim3(u32(val_waves)), dim3(64), 0, stream, body, len, st, pre);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_valid_count, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, st, pre,
             block_valid);
@@ -3617,7 +3636,6 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   // Block records and slice groups; running out only sends a segment to the
   // serial emitter.
   const u64 rec_capacity = u64(max_blocks) + cand_capacity + 1024;
-  const u64 group_capacity = (len * 8) / 8192 + 65536;
   BlockRec* recs = nullptr;
   u64* slice_entry = nullptr;
   u32 *slice_off = nullptr, *group_link = nullptr;
@@ -3652,26 +3670,14 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(hipGetLastError());
 
   // Emission and cross-segment resolution.
-  const u64 words = (out_total + 31) / 32 + 1;
-  // A chain hops back across slices (or serially emitted segments), so its
-  // length is bounded by the number of slices plus segments.
-  const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
-  // Adler-32 partial pairs: kAdlerSlots each for the lane emitter, the
-  // serial emitter and the resolve rounds (workgroups add theirs, so they
-  // start at zero), summed by g_finish.  The pairs, the round counts and the
-  // first unresolved bitmap share one zero fill.
   const u32 emit_grid = clamp_grid(max_blocks, 4096);
   const u32 resolve_grid = clamp_grid((words + 255) / 256, 2048);
-  u8* zeroed = nullptr;
-  const u64 zero_u64 = 2 * u64(3 * kAdlerSlots) + rounds + 1;
-  HZ_TRY(scratch.alloc(&zeroed, 8 * zero_u64 + 4 * words));
   u64* adler_parts = reinterpret_cast<u64*>(zeroed);
   u64* counts = adler_parts + 2 * u64(3 * kAdlerSlots);
   u32* bits0 = reinterpret_cast<u32*>(counts + rounds + 1);
   u32 *roots = nullptr, *bits1 = nullptr;
   HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
   HZ_TRY(scratch.alloc(&bits1, words));
-  HZ_TRY(launch_fill(stream, zeroed, 0, 8 * zero_u64 + 4 * words));
   const u64 out_end = out_total;  // a byte at position p is stream byte n - (out_end - p)
   HZ_LAUNCH(g_emit_lanes, dim3(emit_grid), dim3(kEmitThreads), 0, stream, body, len, st, acc,
             recs, slice_entry, slice_off, group_link, tables, out, roots, bits0, out_end,
@@ -3687,13 +3693,11 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   }
   u64* parts = nullptr;
   u32 nparts = 0;
+  const u32 finish_grid = clamp_grid((out_size + 255) / 256, 4096);
   if (check == kCheckAdler) {
     // The pairs of the emitters, then those of the resolve rounds.
-    HZ_LAUNCH(g_finish, dim3(1), dim3(256), 0, stream, st, out_size, meta, adler_parts,
-              3 * kAdlerSlots, check);
-    HZ_TRY(hipGetLastError());
-    HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
-              stream, st, stream_out, out_size);
+    HZ_LAUNCH(g_finish, dim3(finish_grid), dim3(256), 0, stream, st, out_size, meta, adler_parts,
+              3 * kAdlerSlots, check, stream_out);
     return hipGetLastError();
   }
   if (check == kCheckCrc) {
@@ -3705,10 +3709,8 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
       HZ_TRY(hipGetLastError());
     }
   }
-  HZ_LAUNCH(g_finish, dim3(1), dim3(256), 0, stream, st, out_size, meta, parts, nparts, check);
-  HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_zero_on_failure, dim3(clamp_grid((out_size + 255) / 256, 4096)), dim3(256), 0,
-                     stream, st, stream_out, out_size);
+  HZ_LAUNCH(g_finish, dim3(finish_grid), dim3(256), 0, stream, st, out_size, meta, parts, nparts,
+            check, stream_out);
   return hipGetLastError();
 }
 

@@ -191,12 +191,14 @@ u32 pairs_body(const u8* body, u64 len, u32 slice_bits, std::vector<u8>& out) {
     fast_format(t.ll, true, 0, 1);
     fast_format(t.dd, false, 0, 1);
     other = out;
+    std::vector<u8> third = out;
     std::vector<u8> starts(len * 8 + 64, 0);  // token starts A met
-    Win4<true> a, b;
-    a.words = b.words = w;
-    a.limit = b.limit = u32(len * 8);
+    Win4<true> a, b, c;
+    a.words = b.words = c.words = w;
+    a.limit = b.limit = c.limit = u32(len * 8);
     a.seek(u32(hdr.pos));
     b.seek(u32(hdr.pos));
+    c.seek(u32(hdr.pos));
     bool ended = false;
     while (!ended) {
       const u32 stop = a.pos() + slice_bits;
@@ -248,9 +250,38 @@ u32 pairs_body(const u8* body, u64 len, u32 slice_bits, std::vector<u8>& out) {
         if (x > out.size()) return kBadDistance;
         for (u32 j = 0; j < length; ++j) out.push_back(out[out.size() - x]);
       }
+      // C: up to three literals a step, the same stop; every step ends at
+      // one of A's token starts or at or past the stop.
+      bool c_ended = false;
+      while (!c_ended && c.pos() < stop) {
+        u32 length, x, x2, x3;
+        const u32 got = quick_triple<true>(t.ll, t.dd, c, stop, length, x, x2, x3);
+        if (got >= 2 && c.pos() < stop && !starts[c.pos()]) return kExtent;
+        if (!got) {
+          WordBits<true> q;
+          q.words = w;
+          q.limit = c.limit;
+          q.seek(c.pos());
+          u32 lit, distance;
+          err = fast_token(t.ll, t.dd, q, lit, length, distance);
+          if (err) return err;
+          c.seek(q.pos());
+          if (!length) { c_ended = true; break; }
+          x = length == 1 ? lit : distance;
+        }
+        if (length == 1) {
+          third.push_back(u8(x));
+          if (got >= 2) third.push_back(u8(x2));
+          if (got == 3) third.push_back(u8(x3));
+          continue;
+        }
+        if (x > third.size()) return kBadDistance;
+        for (u32 j = 0; j < length; ++j) third.push_back(third[third.size() - x]);
+      }
       if (a.pos() != b.pos() || ended != b_ended || out.size() != other.size()) return kExtent;
+      if (a.pos() != c.pos() || ended != c_ended || third.size() != other.size()) return kExtent;
     }
-    if (out != other) return kExtent;
+    if (out != other || third != other) return kExtent;
     hdr.seek(b.pos());
     if (final_block) return (hdr.pos + 7) / 8 == len ? kOk : kExtent;
   }

@@ -113,9 +113,10 @@ def test_wrapper_parsing_of_every_truncation(harness, stream_files, tmp_path):
 
 
 def test_literal_pairs_match_single_tokens(harness, stream_files):
-    """quick_pair (two literals per step) stops at every slice end where
-    quick_token does and decodes the same bytes: checked slice by slice in C,
-    and the result against the bytes zlib produced."""
+    """quick_pair (two literals per step) and quick_triple (three) stop at
+    every slice end where quick_token does, end every step at one of its token
+    starts and decode the same bytes: checked slice by slice in C, and the
+    result against the bytes zlib produced."""
     valid = [(n, p, raw) for n, p, raw in stream_files if raw is not None]
     proc = _run(harness, "pairs", [p for _, p, _ in valid])
     assert proc.returncode == 0, proc.stderr[-3000:]
