@@ -820,19 +820,21 @@ __host__ __device__ __forceinline__ u32 quick_pair(const HuffTable<288, 10>& ll,
 }
 
 // quick_pair extended to a third literal after a pair (a third lookup in
-// the same window bits): returns 0-3 tokens taken; with 3, lit3 is the third
-// literal.  Used by emission, which only needs the bytes.
+// the same window bits, taken when that code too is a literal in the primary
+// table and starts before `stop`): returns 0-3 tokens taken; with 3, lit3 is
+// the third literal.  The second and third literals start first_bits and
+// pair_bits after the first token's start.
 template <bool kChecked>
 __host__ __device__ __forceinline__ u32 quick_triple(const HuffTable<288, 10>& ll,
                                                      const HuffTable<32, 8>& dd, Win4<kChecked>& r,
                                                      u32 stop, u32& length, u32& x, u32& lit2,
-                                                     u32& lit3) {
+                                                     u32& lit3, u32& first_bits, u32& pair_bits) {
   const u32 p = r.pos();
   const u64 b = r.bits64();
-  u32 l1;
-  const u32 got = quick_pair<kChecked>(ll, dd, r, stop, length, x, lit2, l1);
-  if (got != 2) return got;
+  const u32 got = quick_pair<kChecked>(ll, dd, r, stop, length, x, lit2, first_bits);
   const u32 l12 = r.pos() - p;  // both codes
+  pair_bits = l12;
+  if (got != 2) return got;
   const u32 e3 = ll.primary[u32(b >> l12) & 1023u];
   const u32 l3 = e3 & 15u;
   bool third = l3 != 0 && ((e3 >> 4) & 3u) == kKindLit && p + l12 < stop;

@@ -2899,10 +2899,11 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
     if (live) {
       u32 length = 0, x = 0, x2 = 0, x3 = 0;  // x: the literal (length 1) or the distance
       u32 got = 1;                            // tokens taken (2, 3: literals x, x2, x3)
+      u32 l1, l12;
       if (r.pos() >= stop) {
         live = false;
       } else if (!(got = quick_triple<kChecked>(sh.tables.ll, sh.tables.dd, r, stop, length, x, x2,
-                                                x3))) {
+                                                x3, l1, l12))) {
         WordBits<kChecked> w;
         w.words = r.words;
         w.limit = r.limit;

@@ -14,7 +14,8 @@
 //   staged the same body decoded with WordBits/fast_token over guarded words
 //   copy   copy_bytes over every length/alignment pair up to 96 bytes
 //   frame  parse_frame on every truncation, in each format
-//   pairs  quick_pair (literal pairs) against quick_token over guarded words
+//   pairs  quick_pair (literal pairs) and quick_triple (three literals)
+//          against quick_token over guarded words
 //   guard  reads one byte past a guarded buffer (must crash: checks the guard)
 #include <sys/mman.h>
 #include <unistd.h>
@@ -153,12 +154,13 @@ u32 staged_body(const u8* body, u64 len, u64& produced) {
   return kBlockCapacity;
 }
 
-// The same body decoded twice over guarded staged words in slices of
+// The same body decoded three times over guarded staged words in slices of
 // `slice_bits`: A with quick_token (one token at a time), B with quick_pair
-// (literal pairs); both fall back to fast_token.  Each slice decodes the
-// tokens that start before its stop, so after every slice A and B must stand
-// at the same position, and their outputs must agree byte for byte.
-// Returns a status (kExtent when they disagree); `out` is B's output.
+// (literal pairs), C with quick_triple (up to three literals); all fall back
+// to fast_token.  Each slice decodes the tokens that start before its stop,
+// so after every slice A, B and C must stand at the same position, and their
+// outputs must agree byte for byte.  Returns a status (kExtent when they
+// disagree); `out` is B's output.
 u32 pairs_body(const u8* body, u64 len, u32 slice_bits, std::vector<u8>& out) {
   static DecodeTables t;
   const u32 margin_words = 16;
@@ -254,9 +256,13 @@ u32 pairs_body(const u8* body, u64 len, u32 slice_bits, std::vector<u8>& out) {
       // one of A's token starts or at or past the stop.
       bool c_ended = false;
       while (!c_ended && c.pos() < stop) {
-        u32 length, x, x2, x3;
-        const u32 got = quick_triple<true>(t.ll, t.dd, c, stop, length, x, x2, x3);
+        u32 length, x, x2, x3, l1, l12;
+        const u32 start = c.pos();
+        const u32 got = quick_triple<true>(t.ll, t.dd, c, stop, length, x, x2, x3, l1, l12);
         if (got >= 2 && c.pos() < stop && !starts[c.pos()]) return kExtent;
+        // The second and third literals start at A's token starts before the stop.
+        if (got >= 2 && (start + l1 >= stop || !starts[start + l1])) return kExtent;
+        if (got == 3 && (start + l12 >= stop || !starts[start + l12])) return kExtent;
         if (!got) {
           WordBits<true> q;
           q.words = w;
