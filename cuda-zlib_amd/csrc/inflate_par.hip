@@ -1060,8 +1060,9 @@ __device__ __forceinline__ u32 val_step(const ValShared& sh, u32 lane, ValWalk& 
 }  // namespace
 
 // Discovery pass 4 (one wave per workgroup; see above).  Valid entries get
-// kValidBit.
-__global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre) {
+// kValidBit; wave_valid[w] counts the valid entries of wave w's range.
+__global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre,
+                                                 u32* wave_valid) {
   __shared__ ValShared sh;
   if (st->status) return;
   const u64 n = st->precount;
@@ -1073,6 +1074,7 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
   u64 ci = 0;
   bool active = false;
   ValWalk v;
+  u32 found = 0;  // this lane's valid verdicts
   for (;;) {
     // Give every idle lane the next entry that needs a walk.
     for (;;) {
@@ -1082,8 +1084,8 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
         ci = cursor + __popcll(idle & lanemask_lt());
         if (ci < q1) {
           const u64 e = pre[ci];
-          if (!(e & kValidBit))
-            active = val_start(body, len, e & kPosMask, sh, lane, v) == kValRunning;
+          if (e & kValidBit) ++found;  // validated by discovery
+          else active = val_start(body, len, e & kPosMask, sh, lane, v) == kValRunning;
         }
       }
       cursor += __popcll(idle);
@@ -1098,7 +1100,10 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
         const u32 r = val_step(sh, lane, v);
         if (r != kValRunning) {
           active = false;
-          if (r == kValValid) pre[ci] |= kValidBit;
+          if (r == kValValid) {
+            pre[ci] |= kValidBit;
+            ++found;
+          }
           reload = r == kValLong;
         }
       }
@@ -1108,58 +1113,60 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
       active = true;
     }
   }
+  for (u32 off = 32; off; off >>= 1) found += __shfl_xor(found, off, 64);
+  if (!lane) wave_valid[blockIdx.x] = found;
 }
 
-// Discovery pass 4c: valid entries per 256-entry block.
-__global__ __launch_bounds__(256) void g_valid_count(const State* st, const u64* pre,
-                                                     u32* block_valid) {
-  __shared__ u32 count;
+// Discovery pass 5: valid entries in order into the candidate array, one
+// 256-entry block (two validation waves) per workgroup.  The block's offset
+// is the sum of the earlier waves' valid counts, added up by the workgroup;
+// the workgroup holding the last entry sets the candidate count and checks
+// the candidate limit (valid headers + bit 0 + stored seeds, as the
+// reference counts them).
+__global__ __launch_bounds__(256) void g_valid_scatter(State* st, const u64* pre,
+                                                       const u32* wave_valid, u64* cand,
+                                                       u64 cand_capacity, u64 max_candidates) {
+  static_assert(kDiscThreads == 2 * kValPerWave, "a block covers two validation waves");
+  __shared__ u32 wave_count[kDiscThreads / 64];
+  __shared__ u64 red[kDiscThreads / 64];
   if (st->status) return;
   const u64 n = st->precount;
   if (u64(blockIdx.x) * kDiscThreads >= n) return;
-  if (!threadIdx.x) count = 0;
+  const u32 t = threadIdx.x, wave = t >> 6, lane = lane_id();
+  // Valid entries before the block: waves 0 .. 2 * blockIdx.x - 1.
+  const u64 before_waves = 2 * u64(blockIdx.x);
+  u64 part = 0;
+  for (u64 w = t; w < before_waves; w += 4 * kDiscThreads) {
+    const u64 w1 = w + kDiscThreads, w2 = w + 2 * kDiscThreads, w3 = w + 3 * kDiscThreads;
+    const u32 a = wave_valid[w];
+    const u32 b = w1 < before_waves ? wave_valid[w1] : 0u;
+    const u32 c = w2 < before_waves ? wave_valid[w2] : 0u;
+    const u32 d = w3 < before_waves ? wave_valid[w3] : 0u;
+    part += u64(a) + b + c + d;
+  }
+  for (u32 off = 32; off; off >>= 1) part += __shfl_xor(part, off, 64);
+  const u64 i = u64(blockIdx.x) * kDiscThreads + t;
+  const u64 e = i < n ? pre[i] : 0;
+  const bool valid = i < n && (e & kValidBit);
+  const u64 bal = __ballot(valid);
+  if (!lane) {
+    wave_count[wave] = __popcll(bal);
+    red[wave] = part;
+  }
   __syncthreads();
-  const u64 i = u64(blockIdx.x) * kDiscThreads + threadIdx.x;
-  const u64 bal = __ballot(i < n && (pre[i] & kValidBit));
-  if (lane_id() == 0 && bal) atomicAdd(&count, u32(__popcll(bal)));
-  __syncthreads();
-  if (!threadIdx.x) block_valid[blockIdx.x] = count;
-}
-
-// Discovery pass 5: one workgroup scans the valid counts; the candidate limit
-// (valid headers + bit 0 + stored seeds, as the reference counts them).
-__global__ __launch_bounds__(1024) void g_valid_scan(State* st, const u32* block_valid,
-                                                     u64* block_offset, u64 max_candidates) {
-  __shared__ ScanShared sh;
-  if (st->status) return;
-  const u64 blocks = (st->precount + kDiscThreads - 1) / kDiscThreads;
-  const u64 total = wg_exclusive_scan(block_valid, ~0u, blocks, block_offset, sh);
-  if (threadIdx.x == 0) {
+  u64 at = 0;
+  for (u32 w = 0; w < kDiscThreads / 64; ++w) at += red[w];
+  const u64 block_base = at;
+  for (u32 w = 0; w < wave; ++w) at += wave_count[w];
+  at += __popcll(bal & lanemask_lt());
+  if (valid && at < cand_capacity) cand[at] = e & kPosMask;
+  if (!t && (u64(blockIdx.x) + 1) * kDiscThreads >= n) {
+    u64 total = block_base;
+    for (u32 w = 0; w < kDiscThreads / 64; ++w) total += wave_count[w];
     st->candidates = total;
     st->tables_used = total;  // table slots 0 .. total-1 belong to the candidates
     if (total + st->seeds > max_candidates) st->status = kCandidateOverflow;
   }
-}
-
-// Discovery pass 6: valid entries in order into the candidate array.
-__global__ __launch_bounds__(256) void g_valid_scatter(const State* st, const u64* pre,
-                                                       const u64* block_offset, u64* cand,
-                                                       u64 cand_capacity) {
-  __shared__ u32 wave_count[kDiscThreads / 64];
-  if (st->status) return;
-  const u64 n = st->precount;
-  if (u64(blockIdx.x) * kDiscThreads >= n) return;
-  const u64 i = u64(blockIdx.x) * kDiscThreads + threadIdx.x;
-  const u64 e = i < n ? pre[i] : 0;
-  const bool valid = i < n && (e & kValidBit);
-  const u64 bal = __ballot(valid);
-  const u32 wave = threadIdx.x >> 6, lane = lane_id();
-  if (!lane) wave_count[wave] = __popcll(bal);
-  __syncthreads();
-  u64 at = block_offset[blockIdx.x];
-  for (u32 w = 0; w < wave; ++w) at += wave_count[w];
-  at += __popcll(bal & (lane ? (~0ull >> (64 - lane)) : 0ull));
-  if (valid && at < cand_capacity) cand[at] = e & kPosMask;
 }
 
 namespace {
@@ -3578,14 +3585,13 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 groups = len ? (len + kDiscRange - 1) / kDiscRange : 1;
   const u64 pre_capacity = groups * kDiscCap + u64(max_candidates) + 1;
   const u64 pre_blocks = (pre_capacity + kDiscThreads - 1) / kDiscThreads;
-  u32 *wg_count = nullptr, *block_valid = nullptr;
-  u64 *wg_list = nullptr, *pre = nullptr, *block_offset = nullptr,
-      *cand = nullptr;
+  const u64 val_waves = (pre_capacity + kValPerWave - 1) / kValPerWave;
+  u32 *wg_count = nullptr, *wave_valid = nullptr;
+  u64 *wg_list = nullptr, *pre = nullptr, *cand = nullptr;
   HZ_TRY(scratch.alloc(&wg_count, groups));
   HZ_TRY(scratch.alloc(&wg_list, groups * kDiscCap));
   HZ_TRY(scratch.alloc(&pre, pre_capacity));
-  HZ_TRY(scratch.alloc(&block_valid, pre_blocks));
-  HZ_TRY(scratch.alloc(&block_offset, pre_blocks));
+  HZ_TRY(scratch.alloc(&wave_valid, val_waves));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
   // Each discovery workgroup takes per_block consecutive ranges.
@@ -3610,17 +3616,11 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_discover_dense, dim3(64), dim3(kDiscThreads), 0, stream, body, len, st, dense,
             wg_count, block_base, pre, per_block);
   HZ_TRY(hipGetLastError());
-  const u64 val_waves = (pre_capacity + kValPerWave - 1) / kValPerWave;
-  HZ_LAUNCH(g_validate, dim3(u32(val_waves)), dim3(64), 0, stream, body, len, st, pre);
-  HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_valid_count, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, st, pre,
-            block_valid);
-  HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_valid_scan, dim3(1), dim3(1024), 0, stream, st, block_valid, block_offset,
-            u64(max_candidates));
+  HZ_LAUNCH(g_validate, dim3(u32(val_waves)), dim3(64), 0, stream, body, len, st, pre,
+            wave_valid);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_valid_scatter, dim3(u32(pre_blocks)), dim3(kDiscThreads), 0, stream, st, pre,
-            block_offset, cand, cand_capacity);
+            wave_valid, cand, cand_capacity, u64(max_candidates));
   HZ_TRY(hipGetLastError());
 
   // Describe every candidate's segment.
