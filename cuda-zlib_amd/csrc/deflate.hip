@@ -64,6 +64,12 @@ constexpr u32 kNear = 2;
 constexpr u32 kWalkMatches = 4;  // waves with at most this many match lanes walk their orbit
 constexpr u32 kMaxDist = 32768;
 constexpr u32 kHistory = 32768;
+constexpr u32 kMaxSteps = 65536 / 1024 + 1;  // parse steps of the largest chunk
+// A continued chunk's bytes are loaded into registers during the previous
+// chunk's last kAheadSteps parse steps (chunks up to kAheadWords dwords per
+// thread of the parse workgroup).
+constexpr u32 kAheadWords = 8;
+constexpr u32 kAheadSteps = 2;
 constexpr u32 kLdsBudget = 160 * 1024;
 constexpr u32 kEmitThreads = 256;
 constexpr u32 kEmitWaves = kEmitThreads / 64;
@@ -114,6 +120,10 @@ struct ParseShared {
   u32 adv;                      // step advance: first orbit point at or past the step's end
   u32 extra_bits;
   u64 red_s[kParseWaves], red_l[kParseWaves];
+  // Positions a step skipped (inside a match past the step's end), which the
+  // parse never hashed: [skip_lo, skip_hi) per range, window-relative.
+  u32 skip_lo[kMaxSteps], skip_hi[kMaxSteps];
+  u32 nskip;
 };
 
 constexpr u32 kParseShared = (sizeof(ParseShared) + 15) & ~u32(15);
@@ -610,8 +620,16 @@ __global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 c
   }
 }
 
-// LZ77 parse of one chunk per workgroup (grid-stride).  Dynamic LDS:
-// ParseShared + window.
+// LZ77 parse of consecutive chunks per workgroup.  Dynamic LDS: ParseShared
+// + window.
+//
+// A chunk that continues the workgroup's previous chunk in the same file
+// keeps the hash table: its entries move down by the window's shift and
+// those that leave the window are cleared.  The table then holds exactly
+// what hashing every history position into an empty table gives (a bucket
+// keeps the largest position that hashed to it), once the positions the
+// previous parse never hashed are added: its last three (their four bytes
+// reach into this chunk) and those its steps skipped inside matches.
 __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const ChunkDesc* descs,
                                                          u32 chunks, u32* tokens,
                                                          ChunkStats* stats) {
@@ -619,12 +637,73 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
   ParseShared& sh = *reinterpret_cast<ParseShared*>(dyn);
   u32* win = reinterpret_cast<u32*>(dyn + kParseShared);
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
-  for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
-    const ChunkDesc d = descs[c];
+  const u32 per = (chunks + gridDim.x - 1) / gridDim.x;
+  const u32 c0 = blockIdx.x * per, c1 = min(chunks, c0 + per);
+  u64 prev_in = 0, prev_start = 0;  // previous chunk: input offset, window start
+  u32 prev_len = 0, prev_file = 0;
+  bool have_prev = false;
+  u32 ahead[kAheadWords];  // this chunk's dwords t + 1024 j, loaded during the previous parse
+  bool have_ahead = false;
+  ChunkDesc d = c0 < c1 ? descs[c0] : ChunkDesc{};
+  for (u32 c = c0; c < c1; ++c) {
+    const ChunkDesc nd = c + 1 < c1 ? descs[c + 1] : ChunkDesc{};
     const u32 hist = d.hist, end = d.hist + d.len;
+    // This window starts `shift` bytes into the previous one.
+    const bool carry = have_prev && hist && d.file == prev_file && d.in_off == prev_in + prev_len;
+    const u32 shift = carry ? u32(d.in_off - hist - prev_start) : 0u;
+    const u32 prev_skips = sh.nskip;  // read before thread 0 resets it (after a barrier)
+    // The next chunk continues this one with dword-aligned bytes and window:
+    // its bytes are loaded during this chunk's last steps.
+    const u64 next_shift = nd.in_off - nd.hist - (d.in_off - hist);
+    bool want_ahead = c + 1 < c1 && nd.hist && nd.file == d.file && nd.in_off == d.in_off + d.len &&
+                      nd.len <= 4 * kAheadWords * kParseThreads && !(nd.hist & 3) &&
+                      !(next_shift & 3) && !(reinterpret_cast<uintptr_t>(in + nd.in_off) & 3);
+    if (carry) {
+      for (u32 i = t; i < kBuckets * kWays; i += kParseThreads) {
+        const u32 e = sh.table[i];
+        sh.table[i] = e > shift ? e - shift : 0u;
+      }
+    } else {
+      for (u32 i = t; i < kBuckets * kWays; i += kParseThreads) sh.table[i] = 0;
+    }
 
     // ---- stage the window as aligned dwords; Adler partials of the chunk ----
-    {
+    if (carry && have_ahead) {
+      // History: the previous window's dwords from `shift` on, moved down
+      // (all read before any is written); then the chunk's loaded dwords.
+      const u32 hw = hist / 4, cw = (d.len + 3) / 4;
+      u32 hv[kAheadWords];
+#pragma unroll
+      for (u32 j = 0; j < kAheadWords; ++j) {
+        const u32 k = t + j * kParseThreads;
+        hv[j] = k < hw ? win[shift / 4 + k] : 0u;
+      }
+      lds_barrier();
+      u64 s = 0, l = 0;
+#pragma unroll
+      for (u32 j = 0; j < kAheadWords; ++j) {
+        const u32 k = t + j * kParseThreads;
+        if (k < hw) win[k] = hv[j];
+        if (k < cw) {
+          u32 v = ahead[j];
+          if (4 * k + 4 > d.len) v &= (1u << (8 * (d.len - 4 * k))) - 1;
+          win[hw + k] = v;
+          const u32 sum = __builtin_amdgcn_udot4(v, 0x01010101u, 0u, false);
+          const u32 wsum = __builtin_amdgcn_udot4(v, 0x03020100u, 0u, false);
+          s += sum;
+          l += u64(4 * k) * sum + wsum;
+        }
+      }
+      for (u32 k = hw + cw + t; k < hw + cw + 4; k += kParseThreads) win[k] = 0;
+      for (u32 off = 32; off; off >>= 1) {
+        s += __shfl_down(s, off, 64);
+        l += __shfl_down(l, off, 64);
+      }
+      if (!lane) {
+        sh.red_s[wave] = s;
+        sh.red_l[wave] = l;
+      }
+    } else {
       const uintptr_t addr = reinterpret_cast<uintptr_t>(in + d.in_off - hist);
       const u32 a = u32(addr & 3);
       const u32* g = reinterpret_cast<const u32*>(addr - a);
@@ -676,19 +755,33 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         sh.red_l[wave] = l;
       }
     }
-    for (u32 i = t; i < kBuckets * kWays; i += kParseThreads) sh.table[i] = 0;
+    have_ahead = false;
     for (u32 i = t; i < 288; i += kParseThreads) sh.freq_ll[i] = 0;
     if (t < 32) sh.freq_d[t] = 0;
     if (!t) sh.extra_bits = 0;
     lds_barrier();
 
     // ---- history positions enter the table ----
+    if (carry) {
+      // The previous chunk's skipped ranges and last three positions.
+      // In the previous window's positions; those before `shift` left.
+      const u32 n = prev_skips, prev_end = shift + hist;
+      for (u32 k = 0; k <= n; ++k) {
+        const u32 lo_p = k < n ? sh.skip_lo[k] : (prev_end > 3 ? prev_end - 3 : 0u);
+        const u32 hi_p = k < n ? sh.skip_hi[k] : prev_end;
+        const u32 lo = max(lo_p, shift) - shift, hi = hi_p > shift ? hi_p - shift : 0u;
+        for (u32 q = lo + t; q < hi; q += kParseThreads)
+          if (q + 4 <= end) atomicMax(&sh.table[hash4(win_u32(win, q))], q + 1);
+      }
+    } else {
 #pragma unroll 4
-    for (u32 base = 0; base < hist; base += kStep) {
-      const u32 q = base + t;
-      if (q < hist && q + 4 <= end) atomicMax(&sh.table[hash4(win_u32(win, q))], q + 1);
+      for (u32 base = 0; base < hist; base += kStep) {
+        const u32 q = base + t;
+        if (q < hist && q + 4 <= end) atomicMax(&sh.table[hash4(win_u32(win, q))], q + 1);
+      }
     }
     lds_barrier();
+    if (!t) sh.nskip = 0;  // every thread read it before the barrier above
 
     // ---- parse ----
     u32* tok = tokens + d.in_off;
@@ -713,6 +806,17 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       ntok += u32(__builtin_amdgcn_readlane(int(inc), int(kParseWaves - 1)));
     };
     for (u32 p = hist; p < end;) {
+      if (want_ahead && p + kAheadSteps * kStep >= end) {  // uniform
+        const u32* g = reinterpret_cast<const u32*>(in + nd.in_off);
+        const u32 cw = (nd.len + 3) / 4;
+#pragma unroll
+        for (u32 j = 0; j < kAheadWords; ++j) {
+          const u32 k = t + j * kParseThreads;
+          ahead[j] = k < cw ? g[k] : 0u;  // an aligned dword holding a chunk byte
+        }
+        want_ahead = false;
+        have_ahead = true;
+      }
       const u32 q = p + t;
       const bool hashable = q + 4 <= end;
       const u32 v = hashable ? win_u32(win, q) : 0u;
@@ -864,6 +968,12 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       pend_buf = cur_buf;
       cur_buf ^= 1u;
       pending = true;
+      if (!t && adv > lim && p + lim < end && sh.nskip < kMaxSteps) {
+        // Positions [p + lim, p + adv) were skipped.
+        sh.skip_lo[sh.nskip] = p + lim;
+        sh.skip_hi[sh.nskip] = min(p + adv, end);
+        ++sh.nskip;
+      }
       p += adv;
       // No barrier here: the next step writes exitv before its first
       // barrier, and went, adv, mark and the other count buffer after it;
@@ -890,6 +1000,12 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       st.sum_s = s;
       st.sum_l = l;
     }
+    prev_in = d.in_off;
+    prev_start = d.in_off - hist;
+    prev_len = d.len;
+    prev_file = d.file;
+    have_prev = true;
+    d = nd;
     lds_barrier();
   }
 }
@@ -1268,8 +1384,14 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_emit),
                              hipFuncAttributeMaxDynamicSharedMemorySize, int(emit_lds)));
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
-  HZ_LAUNCH(e_parse, dim3(grid), dim3(kParseThreads), parse_lds, stream, in, b.descs, u32(chunks),
-            b.tokens, b.stats);
+  // One parse workgroup per CU (its LDS fills one), each taking a run of
+  // consecutive chunks.
+  int device = 0, cus = 0;
+  HZ_TRY(hipGetDevice(&device));
+  HZ_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  const u32 parse_grid = u32(std::min<u64>(chunks, u64(cus > 0 ? cus : 1)));
+  HZ_LAUNCH(e_parse, dim3(parse_grid), dim3(kParseThreads), parse_lds, stream, in, b.descs,
+            u32(chunks), b.tokens, b.stats);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), emit_lds, stream, in, b.descs, u32(chunks),
             b.tokens, b.stats, words, u32(slot_bytes), b.slots, b.results);
