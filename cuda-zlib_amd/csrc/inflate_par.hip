@@ -2273,20 +2273,28 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
 constexpr u32 kChainLdsNodes = 12288;  // candidates whose exits g_chain keeps in LDS
 
 // One 1024-thread workgroup: path from candidate 0, output prefixes and
-// acceptance of the whole chain.
-__global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, const u64* seg_end,
-                                                const u64* seg_size, const u32* seg_blocks,
-                                                const u32* seg_next, const u32* seg_flags,
-                                                const u32* seg_rec,
-                                                u32* exit_node, u64 len,
-                                                u64 out_size, u32 max_blocks, Segment* acc,
-                                                u64 out_base) {
+// acceptance of the whole chain.  Thread t owns the candidates [lo, hi) of
+// range t.  When the candidates fit in LDS (kChainLdsNodes), a thread keeps
+// its candidates' links, sizes and block counts in registers, loaded at once,
+// and walks them in candidate order (a link always points to a later
+// candidate), so no step waits on a chain of dependent loads.
+__global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict__ cand,
+                                                const u64* __restrict__ seg_end,
+                                                const u64* __restrict__ seg_size,
+                                                const u32* __restrict__ seg_blocks,
+                                                const u32* __restrict__ seg_next,
+                                                const u32* __restrict__ seg_flags,
+                                                const u32* __restrict__ seg_rec,
+                                                u32* __restrict__ exit_node, u64 len,
+                                                u64 out_size, u32 max_blocks,
+                                                Segment* __restrict__ acc, u64 out_base) {
+  constexpr u32 kPer = kChainLdsNodes / 1024;  // candidates per thread in LDS mode
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
   __shared__ u32 lexit[kChainLdsNodes];  // exit_node in LDS when the candidates fit
   __shared__ u32 wexit[kChainLdsNodes];  // first node outside the wave's span (LDS mode)
   __shared__ u32 wentry[16];
-  __shared__ u32 last_node, last_wave;
+  __shared__ u32 last_node, last_wave, path_end;
   __shared__ u32 ok;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -2301,15 +2309,35 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
   const bool in_lds = n <= kChainLdsNodes;
   const u64 per = (n + 1023) / 1024;
   const u64 lo = min<u64>(n, u64(t) * per), hi = min<u64>(n, lo + per);
-  // 1. exits: first node outside [lo, hi) reached from each node.
-  for (u64 c = hi; c-- > lo;) {
-    const u32 nx = seg_next[c];
-    const u32 ex = (nx == kNone || nx >= hi) ? nx : in_lds ? lexit[nx] : exit_node[nx];
-    if (in_lds) lexit[c] = ex;
-    else exit_node[c] = ex;
+  u32 bl[kPer];
+  u64 sz[kPer];
+#pragma unroll
+  for (u32 i = 0; i < kPer; ++i) {
+    const u64 c = lo + i;
+    const bool mine = in_lds && c < hi;
+    if (mine) wexit[c] = seg_next[c];  // the links, staged in LDS
+    sz[i] = mine ? seg_size[c] : 0ull;
+    bl[i] = mine ? seg_blocks[c] : 0u;
+  }
+  if (in_lds) {  // uniform
+    // 1. exits: first node outside [lo, hi) reached from each node.
+#pragma unroll
+    for (u32 j = 0; j < kPer; ++j) {
+      const u64 c = lo + kPer - 1 - j;
+      if (c < hi) {
+        const u32 x = wexit[c];
+        lexit[c] = (x == kNone || x >= hi) ? x : lexit[x];
+      }
+    }
+  } else {
+    for (u64 c = hi; c-- > lo;) {
+      const u32 x = seg_next[c];
+      exit_node[c] = (x == kNone || x >= hi) ? x : exit_node[x];
+    }
   }
   entry[t] = kNone;
   if (t < 16) wentry[t] = kNone;
+  if (!t) path_end = kNone;
   __syncthreads();
   // 2. entry node of every range on the path from node 0.
   if (in_lds) {
@@ -2358,14 +2386,38 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
     last_node = last;
   }
   __syncthreads();
-  // 3. mark path nodes inside each range and sum their sizes.
+  // The links again, into LDS (wexit is done with; a thread reads back only
+  // its own candidates'): independent loads, one latency.
+  u32* lnext = wexit;
+  if (in_lds) {
+#pragma unroll
+    for (u32 i = 0; i < kPer; ++i)
+      if (lo + i < hi) lnext[lo + i] = seg_next[lo + i];
+  }
+  // 3. mark path nodes inside each range and sum their sizes; the range
+  // where the path ends records its last node.
   u64 s = 0, b = 0, k = 0;
-  u32 cur = entry[t];
-  while (cur != kNone && cur < hi) {
-    s += seg_size[cur];
-    b += seg_blocks[cur];
-    ++k;
-    cur = seg_next[cur];
+  if (in_lds) {
+    u32 cur = entry[t];
+#pragma unroll
+    for (u32 i = 0; i < kPer; ++i) {
+      const u64 c = lo + i;
+      if (c < hi && c == cur) {
+        s += sz[i];
+        b += bl[i];
+        ++k;
+        cur = lnext[c];
+        if (cur == kNone) path_end = u32(c);
+      }
+    }
+  } else {
+    u32 cur = entry[t];
+    while (cur != kNone && cur < hi) {
+      s += seg_size[cur];
+      b += seg_blocks[cur];
+      ++k;
+      cur = seg_next[cur];
+    }
   }
   psize[t] = s;
   pblocks[t] = b;
@@ -2382,9 +2434,12 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
     __syncthreads();
   }
   if (!t) {
-    // The path's last node: follow next pointers inside the last entered range.
+    // The path's last node: recorded in LDS mode, else followed by next
+    // pointers inside the last entered range.
     u32 z = last_node;
-    while (seg_next[z] != kNone) z = seg_next[z];
+    if (in_lds && path_end != kNone) z = path_end;
+    else
+      while (seg_next[z] != kNone) z = seg_next[z];
     const u32 flags = seg_flags[z];
     const u64 total = psize[1023], blocks = pblocks[1023], count = pcount[1023];
     const bool good = (flags & 0x7fffffffu) == 0 && (flags & 0x80000000u) && total == out_size &&
@@ -2397,17 +2452,36 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* cand, cons
   if (!ok) return;
   // 4. write accepted segments in order.
   u64 offset = out_base + psize[t] - s, index = pcount[t] - k;
-  cur = entry[t];
-  while (cur != kNone && cur < hi) {
-    acc[index].start = cand[cur];
-    acc[index].end = seg_end[cur];
-    acc[index].prefix = offset;
-    acc[index].size = seg_size[cur];
-    acc[index].rec_first = seg_rec[cur];
-    acc[index].rec_count = seg_blocks[cur];
-    offset += seg_size[cur];
-    ++index;
-    cur = seg_next[cur];
+  if (in_lds) {
+    u32 cur = entry[t];
+#pragma unroll
+    for (u32 i = 0; i < kPer; ++i) {
+      const u64 c = lo + i;
+      if (c < hi && c == cur) {
+        acc[index].start = cand[c];
+        acc[index].end = seg_end[c];
+        acc[index].prefix = offset;
+        acc[index].size = sz[i];
+        acc[index].rec_first = seg_rec[c];
+        acc[index].rec_count = bl[i];
+        offset += sz[i];
+        ++index;
+        cur = lnext[c];
+      }
+    }
+  } else {
+    u32 cur = entry[t];
+    while (cur != kNone && cur < hi) {
+      acc[index].start = cand[cur];
+      acc[index].end = seg_end[cur];
+      acc[index].prefix = offset;
+      acc[index].size = seg_size[cur];
+      acc[index].rec_first = seg_rec[cur];
+      acc[index].rec_count = seg_blocks[cur];
+      offset += seg_size[cur];
+      ++index;
+      cur = seg_next[cur];
+    }
   }
 }
 
