@@ -14,12 +14,14 @@
 // (run_deflate with `independent`) limits every window to its own chunk, as
 // the reference's per-chunk encoder does.
 //
-// e_parse, one 1024-thread workgroup per chunk (the LDS holds the window and
-// the hash table, so one workgroup per CU; 16 waves hide LDS latency):
+// e_parse, one 1024-thread workgroup per chunk; the LDS holds the window and
+// the hash table.  For chunks up to about 35 KiB two workgroups share a CU
+// (80 KiB each, up to 11 KiB of history for 32 KiB chunks), so that one
+// runs while the other waits at a barrier; larger chunks take a whole CU:
 //   stage    window (history + chunk) into LDS as aligned dwords; Adler-32
 //            partial sums of the chunk bytes
 //   history  every history position enters the hash table
-//   parse    steps of 1024 positions, one per thread: 4-byte hash into 16384
+//   parse    steps of 1024 positions, one per thread: 4-byte hash into 8192
 //            one-way buckets; candidates = the bucket plus the nearest of the
 //            2 previous positions of the same wave with an equal hash; longest
 //            match (ties: nearest); one-step lazy rule (a position yields to a
@@ -57,7 +59,7 @@ constexpr u32 kParseWaves = kParseThreads / 64;
 static_assert(kParseWaves <= 16, "the wave-count scan covers one 16-lane DPP row");
 constexpr u32 kStep = kParseThreads;  // parse positions per step
 constexpr u32 kLog2Step = 10;
-constexpr u32 kHashBits = 14;
+constexpr u32 kHashBits = 13;
 constexpr u32 kBuckets = 1u << kHashBits;
 constexpr u32 kWays = 1;
 constexpr u32 kNear = 2;
@@ -65,12 +67,13 @@ constexpr u32 kWalkMatches = 4;  // waves with at most this many match lanes wal
 constexpr u32 kMaxDist = 32768;
 constexpr u32 kHistory = 32768;
 constexpr u32 kMaxSteps = 65536 / 1024 + 1;  // parse steps of the largest chunk
-// A continued chunk's bytes are loaded into registers during the previous
-// chunk's last kAheadSteps parse steps (chunks up to kAheadWords dwords per
-// thread of the parse workgroup).
-constexpr u32 kAheadWords = 8;
-constexpr u32 kAheadSteps = 2;
+// LDS of a CU, and of each of two parse workgroups sharing one.  Two
+// workgroups per CU fill each other's barrier waits (the chain of wave
+// entries and the slowest wave's lookups); they need 8 waves per SIMD, so
+// the parse kernel keeps to 64 VGPRs.
 constexpr u32 kLdsBudget = 160 * 1024;
+constexpr u32 kPairBudget = kLdsBudget / 2;
+constexpr u32 kPairMinHistory = 8192;  // least history that keeps the paired layout
 constexpr u32 kEmitThreads = 256;
 constexpr u32 kEmitWaves = kEmitThreads / 64;
 constexpr u32 kTokensPerThread = 4;
@@ -128,12 +131,20 @@ struct ParseShared {
 
 constexpr u32 kParseShared = (sizeof(ParseShared) + 15) & ~u32(15);
 
-// Largest history that fits the LDS budget next to a chunk of `chunk` bytes.
+// LDS of one parse workgroup for chunks of `chunk` bytes: half a CU when
+// that leaves at least kPairMinHistory bytes of history, else the whole CU.
+constexpr u32 parse_budget(u32 chunk) {
+  return kParseShared + chunk + 32 + kPairMinHistory <= kPairBudget ? kPairBudget : kLdsBudget;
+}
+
+// Largest history that fits the parse budget next to a chunk of `chunk` bytes.
 constexpr u32 history_limit(u32 chunk) {
-  return kLdsBudget - kParseShared - chunk - 32 < kHistory ? kLdsBudget - kParseShared - chunk - 32
-                                                           : kHistory;
+  return parse_budget(chunk) - kParseShared - chunk - 32 < kHistory
+             ? parse_budget(chunk) - kParseShared - chunk - 32
+             : kHistory;
 }
 static_assert(kParseShared + 65535 + 32 + 16384 < kLdsBudget, "parse LDS layout exceeds the budget");
+static_assert(parse_budget(32768) == kPairBudget, "32 KiB chunks parse two workgroups per CU");
 
 constexpr u32 kPmItems = 640;               // items of one package-merge level (< 2 * 320)
 constexpr u32 kPmWords = kPmItems / 32;
@@ -630,9 +641,8 @@ __global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 c
 // keeps the largest position that hashed to it), once the positions the
 // previous parse never hashed are added: its last three (their four bytes
 // reach into this chunk) and those its steps skipped inside matches.
-__global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const ChunkDesc* descs,
-                                                         u32 chunks, u32* tokens,
-                                                         ChunkStats* stats) {
+__global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8))) void e_parse(
+    const u8* in, const ChunkDesc* descs, u32 chunks, u32* tokens, ChunkStats* stats) {
   extern __shared__ __align__(16) u8 dyn[];
   ParseShared& sh = *reinterpret_cast<ParseShared*>(dyn);
   u32* win = reinterpret_cast<u32*>(dyn + kParseShared);
@@ -642,8 +652,6 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
   u64 prev_in = 0, prev_start = 0;  // previous chunk: input offset, window start
   u32 prev_len = 0, prev_file = 0;
   bool have_prev = false;
-  u32 ahead[kAheadWords];  // this chunk's dwords t + 1024 j, loaded during the previous parse
-  bool have_ahead = false;
   ChunkDesc d = c0 < c1 ? descs[c0] : ChunkDesc{};
   for (u32 c = c0; c < c1; ++c) {
     const ChunkDesc nd = c + 1 < c1 ? descs[c + 1] : ChunkDesc{};
@@ -652,12 +660,6 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
     const bool carry = have_prev && hist && d.file == prev_file && d.in_off == prev_in + prev_len;
     const u32 shift = carry ? u32(d.in_off - hist - prev_start) : 0u;
     const u32 prev_skips = sh.nskip;  // read before thread 0 resets it (after a barrier)
-    // The next chunk continues this one with dword-aligned bytes and window:
-    // its bytes are loaded during this chunk's last steps.
-    const u64 next_shift = nd.in_off - nd.hist - (d.in_off - hist);
-    bool want_ahead = c + 1 < c1 && nd.hist && nd.file == d.file && nd.in_off == d.in_off + d.len &&
-                      nd.len <= 4 * kAheadWords * kParseThreads && !(nd.hist & 3) &&
-                      !(next_shift & 3) && !(reinterpret_cast<uintptr_t>(in + nd.in_off) & 3);
     if (carry) {
       for (u32 i = t; i < kBuckets * kWays; i += kParseThreads) {
         const u32 e = sh.table[i];
@@ -668,50 +670,16 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
     }
 
     // ---- stage the window as aligned dwords; Adler partials of the chunk ----
-    if (carry && have_ahead) {
-      // History: the previous window's dwords from `shift` on, moved down
-      // (all read before any is written); then the chunk's loaded dwords.
-      const u32 hw = hist / 4, cw = (d.len + 3) / 4;
-      u32 hv[kAheadWords];
-#pragma unroll
-      for (u32 j = 0; j < kAheadWords; ++j) {
-        const u32 k = t + j * kParseThreads;
-        hv[j] = k < hw ? win[shift / 4 + k] : 0u;
-      }
-      lds_barrier();
-      u64 s = 0, l = 0;
-#pragma unroll
-      for (u32 j = 0; j < kAheadWords; ++j) {
-        const u32 k = t + j * kParseThreads;
-        if (k < hw) win[k] = hv[j];
-        if (k < cw) {
-          u32 v = ahead[j];
-          if (4 * k + 4 > d.len) v &= (1u << (8 * (d.len - 4 * k))) - 1;
-          win[hw + k] = v;
-          const u32 sum = __builtin_amdgcn_udot4(v, 0x01010101u, 0u, false);
-          const u32 wsum = __builtin_amdgcn_udot4(v, 0x03020100u, 0u, false);
-          s += sum;
-          l += u64(4 * k) * sum + wsum;
-        }
-      }
-      for (u32 k = hw + cw + t; k < hw + cw + 4; k += kParseThreads) win[k] = 0;
-      for (u32 off = 32; off; off >>= 1) {
-        s += __shfl_down(s, off, 64);
-        l += __shfl_down(l, off, 64);
-      }
-      if (!lane) {
-        sh.red_s[wave] = s;
-        sh.red_l[wave] = l;
-      }
-    } else {
+    {
       const uintptr_t addr = reinterpret_cast<uintptr_t>(in + d.in_off - hist);
       const u32 a = u32(addr & 3);
       const u32* g = reinterpret_cast<const u32*>(addr - a);
       const u32 nw = (end + 3) / 4;
       u64 s = 0, l = 0;
       // A thread's dwords are loaded kStageBatch at a time, all loads in
-      // flight before the first is used (one memory latency per batch).
-      constexpr u32 kStageBatch = 16;
+      // flight before the first is used (one memory latency per batch; the
+      // CU's other parse workgroup runs meanwhile).
+      constexpr u32 kStageBatch = 4;
       for (u32 k0 = t; k0 < nw; k0 += kStageBatch * kParseThreads) {
         u32 lo[kStageBatch], hi[kStageBatch];
 #pragma unroll
@@ -755,7 +723,6 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
         sh.red_l[wave] = l;
       }
     }
-    have_ahead = false;
     for (u32 i = t; i < 288; i += kParseThreads) sh.freq_ll[i] = 0;
     if (t < 32) sh.freq_d[t] = 0;
     if (!t) sh.extra_bits = 0;
@@ -806,17 +773,6 @@ __global__ __launch_bounds__(kParseThreads) void e_parse(const u8* in, const Chu
       ntok += u32(__builtin_amdgcn_readlane(int(inc), int(kParseWaves - 1)));
     };
     for (u32 p = hist; p < end;) {
-      if (want_ahead && p + kAheadSteps * kStep >= end) {  // uniform
-        const u32* g = reinterpret_cast<const u32*>(in + nd.in_off);
-        const u32 cw = (nd.len + 3) / 4;
-#pragma unroll
-        for (u32 j = 0; j < kAheadWords; ++j) {
-          const u32 k = t + j * kParseThreads;
-          ahead[j] = k < cw ? g[k] : 0u;  // an aligned dword holding a chunk byte
-        }
-        want_ahead = false;
-        have_ahead = true;
-      }
       const u32 q = p + t;
       const bool hashable = q + 4 <= end;
       const u32 v = hashable ? win_u32(win, q) : 0u;
@@ -1384,12 +1340,13 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_emit),
                              hipFuncAttributeMaxDynamicSharedMemorySize, int(emit_lds)));
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
-  // One parse workgroup per CU (its LDS fills one), each taking a run of
-  // consecutive chunks.
+  // One or two parse workgroups per CU (as many as their LDS allows), each
+  // taking a run of consecutive chunks.
   int device = 0, cus = 0;
   HZ_TRY(hipGetDevice(&device));
   HZ_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-  const u32 parse_grid = u32(std::min<u64>(chunks, u64(cus > 0 ? cus : 1)));
+  const u64 per_cu = kLdsBudget / parse_budget(chunk_bytes);
+  const u32 parse_grid = u32(std::min<u64>(chunks, per_cu * u64(cus > 0 ? cus : 1)));
   HZ_LAUNCH(e_parse, dim3(parse_grid), dim3(kParseThreads), parse_lds, stream, in, b.descs,
             u32(chunks), b.tokens, b.stats);
   HZ_TRY(hipGetLastError());

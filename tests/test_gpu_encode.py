@@ -120,15 +120,17 @@ def test_independent_chunks_round_trip(gpu, chunk):
         assert zlib.decompress(stream) == data, kind
 
 
-def test_independent_chunks_never_reach_into_the_previous_chunk(gpu):
-    """Two copies of a 32 KiB incompressible chunk: with history the second
-    chunk is one long match into the first; without it both must be stored."""
-    x = np.random.default_rng(21).integers(0, 256, 32768, dtype=np.uint8).tobytes()
+@pytest.mark.parametrize("chunk", [8192, 16384])
+def test_independent_chunks_never_reach_into_the_previous_chunk(gpu, chunk):
+    """Two copies of an incompressible chunk: with history the second chunk is
+    matches into the first (chunks up to 16 KiB keep at least a chunk of
+    history); without history both chunks must be stored."""
+    x = np.random.default_rng(21).integers(0, 256, chunk, dtype=np.uint8).tobytes()
     data = x + x
-    shared = _compress(data)
-    alone = _compress_independent(data)
+    shared = _compress(data, chunk)
+    alone = _compress_independent(data, chunk)
     assert zlib.decompress(shared) == data and zlib.decompress(alone) == data
-    assert len(shared) < 32768 + 2000
+    assert len(shared) < chunk + chunk // 8
     assert len(alone) == len(data) + 5 * 2 + 6  # two stored chunks at the bound
 
 
