@@ -77,6 +77,7 @@ constexpr u32 kPairMinHistory = 8192;  // least history that keeps the paired la
 constexpr u32 kEmitThreads = 256;
 constexpr u32 kEmitWaves = kEmitThreads / 64;
 constexpr u32 kTokensPerThread = 4;
+constexpr u32 kTreeThreads = 128;
 
 struct ChunkDesc {
   u64 in_off;    // absolute input offset of the chunk
@@ -146,21 +147,23 @@ constexpr u32 history_limit(u32 chunk) {
 static_assert(kParseShared + 65535 + 32 + 16384 < kLdsBudget, "parse LDS layout exceeds the budget");
 static_assert(parse_budget(32768) == kPairBudget, "32 KiB chunks parse two workgroups per CU");
 
-constexpr u32 kPmItems = 640;               // items of one package-merge level (< 2 * 320)
-constexpr u32 kPmWords = kPmItems / 32;
-struct HuffScratch {
-  u16 list[320];
-  u16 sorted[320];
-  u32 leaf[320];                  // leaf weights in sorted order
-  u32 items[2][kPmItems];         // item weights of two consecutive levels
-  u32 leafbits[16][kPmWords];     // per level: which items are leaves
+// Package-merge scratch of one tree of at most N symbols (one wave).
+template <u32 N>
+struct HuffScratchT {
+  static constexpr u32 kItems = 2 * N;           // items of one level (< 2 * symbols)
+  static constexpr u32 kWords = (kItems + 31) / 32;
+  u16 list[N];
+  u16 sorted[N];
+  u32 leaf[N];                   // leaf weights in sorted order
+  u32 items[2][kItems];          // item weights of two consecutive levels
+  u32 leafbits[16][kWords];      // per level: which items are leaves
 };
+using HuffScratchLL = HuffScratchT<320>;  // literal/length tree (286), then code lengths (19)
+using HuffScratchD = HuffScratchT<32>;    // distance tree (30)
 
-// e_emit LDS; the bit buffer (which first serves as HuffScratch) follows it.
-struct EmitShared {
-  u32 freq_ll[288];
-  u32 freq_d[32];
-  u32 freq_cl[20];
+// A chunk's block coding, from e_tree to e_emit: code lengths, canonical
+// codes (bit-reversed), the code-length RLE and the chosen block.
+struct alignas(16) CodeTables {
   u8 len_ll[288];
   u8 len_d[32];
   u8 len_cl[20];
@@ -168,21 +171,33 @@ struct EmitShared {
   u16 code_d[32];
   u16 code_cl[20];
   u16 rle[320];  // code-length RLE: symbol | extra << 5
+  u32 nrle, hlit, hdist, hclen, mode, extent, hdr_bits;
+};
+static_assert(sizeof(CodeTables) % 16 == 0, "code tables copy as uint4");
+
+// e_tree LDS.
+struct TreeShared {
+  u32 freq_ll[288];
+  u32 freq_d[32];
+  u32 freq_cl[20];
+  CodeTables tab;
+  HuffScratchLL hs_ll;
+  HuffScratchD hs_d;
+};
+
+// e_emit LDS; the bit buffer follows it.
+struct EmitShared {
+  CodeTables tab;
   u32 scan[kEmitWaves];
-  u32 nrle, hlit, hdist, hclen, mode, extent, hdr_bits, status;
+  u32 status;
 };
 
 constexpr u32 kEmitShared = (sizeof(EmitShared) + 15) & ~u32(15);
 
 // Bit buffer words for a chunk: a fixed/dynamic block is only chosen when it
-// is shorter than the stored form (len + 5 bytes).
-// The bit buffer also holds two HuffScratch (waves 0 and 1) before emission.
-constexpr u32 stage_words(u32 chunk) {
-  // A multiple of 4 words: the stage is cleared and copied out as uint4.
-  return (((chunk + 8) / 4 + 16) * 4 > 2 * sizeof(HuffScratch)
-              ? (chunk + 8) / 4 + 16 + 3
-              : u32(2 * sizeof(HuffScratch) / 4 + 1 + 3)) & ~3u;
-}
+// is shorter than the stored form (len + 5 bytes).  A multiple of 4 words:
+// the stage is cleared and copied out as uint4.
+constexpr u32 stage_words(u32 chunk) { return ((chunk + 8) / 4 + 16 + 3) & ~3u; }
 
 __device__ __forceinline__ u32 win_u32(const u32* win, u32 q) {
   return __builtin_amdgcn_alignbyte(win[(q >> 2) + 1], win[q >> 2], q & 3);
@@ -249,14 +264,6 @@ __device__ __forceinline__ u32 fixed_len(u32 s) {
   return s < 144 ? 8u : s < 256 ? 9u : s < 280 ? 7u : 8u;
 }
 
-// Code lengths for `n` symbols from frequencies, at most `limit` bits; called
-// by all 64 lanes of one wave.  At least two codes are always assigned
-// (zero-frequency symbols of lowest index get weight 1), so every code is
-// complete, as zlib's trees are.  Leaves are ranked by (weight, symbol) in
-// parallel; lane 0 runs the two-queue merge for optimal depths, folds depths
-// above the limit back with the JPEG count adjustment (ITU T.81 K.3, which
-// keeps the Kraft sum at 1) and gives the shortest lengths to the heaviest
-// symbols.
 // Optimal length-limited code lengths by package-merge (one wave; every lane
 // calls).  Leaves are sorted by (frequency, symbol) with a bitonic network.  Level
 // `limit` holds the sorted leaves; level j merges the leaves with the
@@ -266,8 +273,9 @@ __device__ __forceinline__ u32 fixed_len(u32 s) {
 // a taken package takes its two children, so the taken items of every level
 // are a prefix, and a leaf's length is the number of levels whose taken
 // prefix holds it.  Unused symbols get length 0 (at least two symbols get a
-// code).
-__device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 limit, u8* len) {
+// code).  The sort covers 64 * kRegs slots, at least n.
+template <u32 kRegs, class HS>
+__device__ void huffman_lengths(HS& hs, const u32* freq, u32 n, u32 limit, u8* len) {
   const u32 lane = lane_id();
   u32 m = 0;
   for (u32 base = 0; base < n; base += 64) {
@@ -286,12 +294,12 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
       }
   }
   wave_sync();
-  // Bitonic sort of the keys (weight << 9 | symbol) over 512 slots: slot
+  // Bitonic sort of the keys (weight << 9 | symbol) over 64 * kRegs slots: slot
   // r * 64 + lane in register r; partners within a lane swap registers,
   // partners across lanes exchange by shuffles.
-  u32 key[8];
+  u32 key[kRegs];
 #pragma unroll
-  for (u32 r = 0; r < 8; ++r) {
+  for (u32 r = 0; r < kRegs; ++r) {
     const u32 i = r * 64 + lane;
     if (i < m) {
       const u32 s = hs.list[i];
@@ -301,13 +309,13 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
     }
   }
 #pragma clang loop unroll(full)
-  for (u32 k = 2; k <= 512; k <<= 1) {
+  for (u32 k = 2; k <= 64 * kRegs; k <<= 1) {
 #pragma clang loop unroll(full)
     for (u32 j = k >> 1; j; j >>= 1) {
       if (j >= 64) {
         const u32 rj = j >> 6;
 #pragma clang loop unroll(full)
-        for (u32 r = 0; r < 8; ++r) {
+        for (u32 r = 0; r < kRegs; ++r) {
           if (r & rj) continue;
           const u32 e = r * 64 + lane;
           const bool up = (e & k) == 0;
@@ -318,7 +326,7 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
         }
       } else {
 #pragma clang loop unroll(full)
-        for (u32 r = 0; r < 8; ++r) {
+        for (u32 r = 0; r < kRegs; ++r) {
           const u32 e = r * 64 + lane;
           const u32 other = __shfl_xor(key[r], j, 64);
           const bool up = (e & k) == 0, lower = (lane & j) == 0;
@@ -330,14 +338,14 @@ __device__ void huffman_lengths(HuffScratch& hs, const u32* freq, u32 n, u32 lim
     }
   }
 #pragma unroll
-  for (u32 r = 0; r < 8; ++r) {
+  for (u32 r = 0; r < kRegs; ++r) {
     const u32 i = r * 64 + lane;
     if (i < m) {
       hs.sorted[i] = u16(key[r] & 511);
       hs.leaf[i] = key[r] >> 9;
     }
   }
-  for (u32 i = lane; i < 16 * kPmWords; i += 64) (&hs.leafbits[0][0])[i] = 0;
+  for (u32 i = lane; i < 16 * HS::kWords; i += 64) (&hs.leafbits[0][0])[i] = 0;
   wave_sync();
   // Level `limit`: the leaves.
   u32* prev = hs.items[0];
@@ -481,10 +489,11 @@ __device__ __forceinline__ void rle_run(u32 v, u32 run, F&& emit) {
 // same symbols as a serial left-to-right pass.  Each lane owns the runs that
 // start at its positions; run ends come from the start ballots, outputs from
 // a scan of per-run symbol counts.
-__device__ void rle_lengths_wave(EmitShared& sh) {
+__device__ void rle_lengths_wave(TreeShared& sh) {
+  CodeTables& tab = sh.tab;
   const u32 lane = lane_id();
-  const u32 total = sh.hlit + sh.hdist;  // <= 316: five ballot words
-  auto at = [&](u32 k) -> u32 { return k < sh.hlit ? sh.len_ll[k] : sh.len_d[k - sh.hlit]; };
+  const u32 total = tab.hlit + tab.hdist;  // <= 316: five ballot words
+  auto at = [&](u32 k) -> u32 { return k < tab.hlit ? tab.len_ll[k] : tab.len_d[k - tab.hlit]; };
   if (lane < 20) sh.freq_cl[lane] = 0;
   u64 starts[5];
 #pragma unroll
@@ -526,11 +535,11 @@ __device__ void rle_lengths_wave(EmitShared& sh) {
     carry += __shfl(x, 63, 64);
     if (cnt[c])
       rle_run(v[c], run[c], [&](u32 sym) {
-        sh.rle[at_sym++] = u16(sym);
+        tab.rle[at_sym++] = u16(sym);
         atomicAdd(&sh.freq_cl[sym & 31], 1u);
       });
   }
-  if (!lane) sh.nrle = carry;
+  if (!lane) tab.nrle = carry;
   wave_sync();
 }
 
@@ -561,19 +570,19 @@ __device__ __forceinline__ void or_bits(u32* words, u32 cap, u32 pos, u64 v) {
 
 // Block-wide exclusive scan of one u32 per thread of e_emit; returns the
 // prefix and writes the total.  Contains barriers: every thread must call it.
-__device__ __forceinline__ u32 block_scan(EmitShared& sh, u32 v, u32& total) {
+__device__ __forceinline__ u32 block_scan(u32* scan, u32 v, u32& total) {
   const u32 lane = lane_id(), wave = threadIdx.x >> 6;
   u32 x = v;
   for (u32 off = 1; off < 64; off <<= 1) {
     const u32 y = __shfl_up(x, off, 64);
     if (lane >= off) x += y;
   }
-  if (lane == 63) sh.scan[wave] = x;
+  if (lane == 63) scan[wave] = x;
   lds_barrier();
   u32 before = 0;
   total = 0;
   for (u32 w = 0; w < kEmitWaves; ++w) {
-    const u32 s = sh.scan[w];
+    const u32 s = scan[w];
     if (w < wave) before += s;
     total += s;
   }
@@ -582,7 +591,7 @@ __device__ __forceinline__ u32 block_scan(EmitShared& sh, u32 v, u32& total) {
 }
 
 // Code bits of one token (LSB first) and their count.
-__device__ __forceinline__ u32 token_bits(const EmitShared& sh, u32 tk, u64& bits) {
+__device__ __forceinline__ u32 token_bits(const CodeTables& sh, u32 tk, u64& bits) {
   if (!(tk >> 31)) {
     bits = sh.code_ll[tk];
     return sh.len_ll[tk];
@@ -966,48 +975,46 @@ __global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8
   }
 }
 
-// Block coding and bit emission of one chunk per workgroup (grid-stride).
-// Dynamic LDS: EmitShared + bit buffer of `words` words.
-__global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const ChunkDesc* descs,
-                                                       u32 chunks, const u32* tokens,
-                                                       const ChunkStats* stats, u32 words,
-                                                       u32 slot_bytes, u8* slots,
+// Block coding of one chunk per workgroup of two waves (grid-stride): code
+// lengths (literal/length tree on wave 0, distance tree on wave 1), the
+// code-length RLE and its tree, exact costs and the block type (wave 0),
+// canonical codes; the tables go to the chunk's CodeTables.  The trees are
+// chains of dependent LDS accesses, so many small workgroups per CU hide
+// their latency (about 13 KiB of LDS each).
+__global__ __launch_bounds__(kTreeThreads) __attribute__((amdgpu_waves_per_eu(4))) void e_tree(const ChunkDesc* descs, u32 chunks,
+                                                       const ChunkStats* stats,
+                                                       CodeTables* tables,
                                                        ChunkResult* results) {
-  extern __shared__ __align__(16) u8 dyn[];
-  EmitShared& sh = *reinterpret_cast<EmitShared*>(dyn);
-  u32* stage = reinterpret_cast<u32*>(dyn + kEmitShared);
+  __shared__ TreeShared sh;
+  CodeTables& tab = sh.tab;
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
     const ChunkDesc d = descs[c];
     const ChunkStats& st = stats[c];
-    for (u32 i = t; i < 288; i += kEmitThreads) sh.freq_ll[i] = i < 286 ? st.freq_ll[i] : 0u;
+    for (u32 i = t; i < 288; i += kTreeThreads) sh.freq_ll[i] = i < 286 ? st.freq_ll[i] : 0u;
     if (t < 32) sh.freq_d[t] = t < 30 ? st.freq_d[t] : 0u;
     lds_barrier();
-
-    // ---- code lengths (waves 0 and 1), RLE, costs, block type (wave 0),
-    // canonical codes (waves 0-2) ----
-    HuffScratch* hsw = reinterpret_cast<HuffScratch*>(stage);  // one per wave
-    if (wave == 0) huffman_lengths(hsw[0], sh.freq_ll, 286, 15, sh.len_ll);
-    else if (wave == 1) huffman_lengths(hsw[1], sh.freq_d, 30, 15, sh.len_d);
+    if (wave == 0) huffman_lengths<8>(sh.hs_ll, sh.freq_ll, 286, 15, tab.len_ll);
+    else huffman_lengths<1>(sh.hs_d, sh.freq_d, 30, 15, tab.len_d);
     lds_barrier();
     if (wave == 0) {
-      sh.hlit = used_extent(sh.len_ll, 286, 257);
-      sh.hdist = used_extent(sh.len_d, 30, 1);
+      tab.hlit = used_extent(tab.len_ll, 286, 257);
+      tab.hdist = used_extent(tab.len_d, 30, 1);
       wave_sync();
       rle_lengths_wave(sh);
-      huffman_lengths(hsw[0], sh.freq_cl, 19, 7, sh.len_cl);
+      huffman_lengths<1>(sh.hs_ll, sh.freq_cl, 19, 7, tab.len_cl);
       u32 dyn_bits = 0, fix_bits = 0, hdr = 0;
       for (u32 sy = lane; sy < 286; sy += 64) {
-        dyn_bits += sh.freq_ll[sy] * sh.len_ll[sy];
+        dyn_bits += sh.freq_ll[sy] * tab.len_ll[sy];
         fix_bits += sh.freq_ll[sy] * fixed_len(sy);
       }
       if (lane < 30) {
-        dyn_bits += sh.freq_d[lane] * sh.len_d[lane];
+        dyn_bits += sh.freq_d[lane] * tab.len_d[lane];
         fix_bits += sh.freq_d[lane] * 5;
       }
-      for (u32 i = lane; i < sh.nrle; i += 64) {
-        const u32 sy = sh.rle[i] & 31;
-        hdr += sh.len_cl[sy] + (sy == 16 ? 2 : sy == 17 ? 3 : sy == 18 ? 7 : 0);
+      for (u32 i = lane; i < tab.nrle; i += 64) {
+        const u32 sy = tab.rle[i] & 31;
+        hdr += tab.len_cl[sy] + (sy == 16 ? 2 : sy == 17 ? 3 : sy == 18 ? 7 : 0);
       }
       for (u32 off = 32; off; off >>= 1) {
         dyn_bits += __shfl_down(dyn_bits, off, 64);
@@ -1015,11 +1022,11 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         hdr += __shfl_down(hdr, off, 64);
       }
       // HCLEN: one past the last nonzero code-length length in RFC order.
-      const u64 cl_used = __ballot(lane < 19 && sh.len_cl[cl_order(lane)] != 0);
+      const u64 cl_used = __ballot(lane < 19 && tab.len_cl[cl_order(lane)] != 0);
       if (!lane) {
         const u32 last = cl_used ? 64 - __builtin_clzll(cl_used) : 0u;
         const u32 hc = last > 4 ? last : 4u;
-        sh.hclen = hc;
+        tab.hclen = hc;
         hdr += 3 + 14 + 3 * hc;
         const u64 dyn_total = u64(hdr) + dyn_bits + st.extra_bits;
         const u64 fix_total = 3ull + fix_bits + st.extra_bits;
@@ -1032,10 +1039,9 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         u64 best = e_stored;
         if (e_fixed < best) { mode = 1; best = e_fixed; }
         if (e_dyn < best) { mode = 2; best = e_dyn; }
-        sh.mode = mode;
-        sh.extent = u32(best);
-        sh.hdr_bits = mode == 2 ? hdr : 3u;
-        sh.status = 0;
+        tab.mode = mode;
+        tab.extent = u32(best);
+        tab.hdr_bits = mode == 2 ? hdr : 3u;
         const u64 S = st.sum_s % kAdlerMod, L = st.sum_l % kAdlerMod;
         results[c].adler_s = S;
         results[c].adler_b =
@@ -1043,18 +1049,48 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
       }
     }
     lds_barrier();
+    const u32 mode = tab.mode;
+    if (mode == 1) {
+      for (u32 i = t; i < 288; i += kTreeThreads) tab.len_ll[i] = u8(fixed_len(i));
+      if (t < 30) tab.len_d[t] = 5;
+      lds_barrier();
+    }
+    if (mode) {
+      if (wave == 0) {
+        canonical_codes_wave(tab.len_ll, mode == 1 ? 288 : 286, tab.code_ll);
+      } else {
+        canonical_codes_wave(tab.len_d, 30, tab.code_d);
+        if (mode == 2) canonical_codes_wave(tab.len_cl, 19, tab.code_cl);
+      }
+    }
+    lds_barrier();
+    uint4* dst = reinterpret_cast<uint4*>(tables + c);
+    const uint4* src = reinterpret_cast<const uint4*>(&tab);
+    for (u32 i = t; i < sizeof(CodeTables) / 16; i += kTreeThreads) dst[i] = src[i];
+    lds_barrier();
+  }
+}
+
+// Bit emission of one chunk per workgroup (grid-stride) with the chunk's
+// CodeTables.  Dynamic LDS: EmitShared + bit buffer of `words` words.
+__global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const ChunkDesc* descs,
+                                                       u32 chunks, const u32* tokens,
+                                                       const ChunkStats* stats,
+                                                       const CodeTables* tables, u32 words,
+                                                       u32 slot_bytes, u8* slots,
+                                                       ChunkResult* results) {
+  extern __shared__ __align__(16) u8 dyn[];
+  EmitShared& es = *reinterpret_cast<EmitShared*>(dyn);
+  CodeTables& sh = es.tab;
+  u32* stage = reinterpret_cast<u32*>(dyn + kEmitShared);
+  const u32 t = threadIdx.x;
+  for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const ChunkDesc d = descs[c];
     {
-      const u32 mode = sh.mode;
-      if (mode == 1) {
-        for (u32 i = t; i < 288; i += kEmitThreads) sh.len_ll[i] = u8(fixed_len(i));
-        if (t < 30) sh.len_d[t] = 5;
-        lds_barrier();
-      }
-      if (mode) {
-        if (wave == 0) canonical_codes_wave(sh.len_ll, mode == 1 ? 288 : 286, sh.code_ll);
-        else if (wave == 1) canonical_codes_wave(sh.len_d, 30, sh.code_d);
-        else if (wave == 2 && mode == 2) canonical_codes_wave(sh.len_cl, 19, sh.code_cl);
-      }
+      const uint4* src = reinterpret_cast<const uint4*>(tables + c);
+      uint4* dst = reinterpret_cast<uint4*>(&sh);
+      for (u32 i = t; i < sizeof(CodeTables) / 16; i += kEmitThreads) dst[i] = src[i];
+      if (!t) es.status = 0;
     }
     lds_barrier();
 
@@ -1111,16 +1147,16 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         hmine += hn[k];
       }
       u32 htotal;
-      u32 hoff = fixed_bits + block_scan(sh, hmine, htotal);
+      u32 hoff = fixed_bits + block_scan(es.scan, hmine, htotal);
 #pragma unroll
       for (u32 k = 0; k < 2; ++k) {
         if (hn[k]) or_bits(stage, words, hoff, hb[k]);
         hoff += hn[k];
       }
-      if (!t && fixed_bits + htotal != sh.hdr_bits) sh.status = kCompressionOverflow;
+      if (!t && fixed_bits + htotal != sh.hdr_bits) es.status = kCompressionOverflow;
       lds_barrier();
       const u32* tok = tokens + d.in_off;
-      const u32 ntokens = st.ntok;
+      const u32 ntokens = stats[c].ntok;
       u32 pos = sh.hdr_bits;
       // The tokens of the next round are loaded (one 16-byte load per
       // thread) while the current round is coded, so the global-memory
@@ -1154,7 +1190,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
           mine += nbits[k];
         }
         u32 total;
-        u32 off = pos + block_scan(sh, mine, total);
+        u32 off = pos + block_scan(es.scan, mine, total);
 #pragma unroll
         for (u32 k = 0; k < kTokensPerThread; ++k) {
           if (nbits[k]) or_bits(stage, words, off, bits[k]);
@@ -1173,7 +1209,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
           out.put(0xffff, 16);
         }
         const u32 bytes = (out.pos + 7) / 8;
-        if (bytes != sh.extent) sh.status = kCompressionOverflow;
+        if (bytes != sh.extent) es.status = kCompressionOverflow;
         results[c].extent = sh.extent;
       }
       lds_barrier();
@@ -1183,7 +1219,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
       uint4* slot128 = reinterpret_cast<uint4*>(slot);
       const uint4* stage128 = reinterpret_cast<const uint4*>(stage);
       for (u32 i = t; i < copy4; i += kEmitThreads) slot128[i] = stage128[i];
-      if (!t) results[c].status = sh.status;
+      if (!t) results[c].status = es.status;
     }
     lds_barrier();
   }
@@ -1311,6 +1347,7 @@ struct ChunkBuffers {
   u32* tokens = nullptr;
   u8* slots = nullptr;
   ChunkStats* stats = nullptr;
+  CodeTables* tables = nullptr;
   ChunkResult* results = nullptr;
   u64* sums = nullptr;
   u32* file_ok = nullptr;
@@ -1323,6 +1360,7 @@ hipError_t alloc_chunks(Scratch& scratch, u64 chunks, u32 file_count, u64 in_tot
   HZ_TRY(scratch.alloc(&b.tokens, in_total ? in_total : 1));
   HZ_TRY(scratch.alloc(&b.slots, chunks * slot_size(chunk_bytes)));
   HZ_TRY(scratch.alloc(&b.stats, chunks));
+  HZ_TRY(scratch.alloc(&b.tables, chunks));
   HZ_TRY(scratch.alloc(&b.results, chunks));
   HZ_TRY(scratch.alloc(&b.sums, 4 * (chunks + 1)));
   HZ_TRY(scratch.alloc(&b.file_ok, file_count));
@@ -1350,8 +1388,11 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_LAUNCH(e_parse, dim3(parse_grid), dim3(kParseThreads), parse_lds, stream, in, b.descs,
             u32(chunks), b.tokens, b.stats);
   HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(e_tree, dim3(grid), dim3(kTreeThreads), 0, stream, b.descs, u32(chunks), b.stats,
+            b.tables, b.results);
+  HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), emit_lds, stream, in, b.descs, u32(chunks),
-            b.tokens, b.stats, words, u32(slot_bytes), b.slots, b.results);
+            b.tokens, b.stats, b.tables, words, u32(slot_bytes), b.slots, b.results);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, b.results, u32(chunks), b.sums);
   HZ_TRY(hipGetLastError());
