@@ -22,8 +22,8 @@
 //            partial sums of the chunk bytes
 //   history  every history position enters the hash table
 //   parse    steps of 1024 positions, one per thread: 4-byte hash into 8192
-//            one-way buckets; candidates = the bucket plus the nearest of the
-//            2 previous positions of the same wave with an equal hash; longest
+//            one-way buckets; candidates = the bucket plus the previous
+//            position of the same wave when its hash is equal; longest
 //            match (ties: nearest); one-step lazy rule (a position yields to a
 //            longer match at the next position).  With f(j) = j + max(1, L_j)
 //            the greedy token starts are the orbit of 0 under f: every wave
@@ -62,7 +62,7 @@ constexpr u32 kLog2Step = 10;
 constexpr u32 kHashBits = 13;
 constexpr u32 kBuckets = 1u << kHashBits;
 constexpr u32 kWays = 1;
-constexpr u32 kNear = 2;
+constexpr u32 kNear = 1;
 constexpr u32 kWalkMatches = 4;  // waves with at most this many match lanes walk their orbit
 constexpr u32 kMaxDist = 32768;
 constexpr u32 kHistory = 32768;
