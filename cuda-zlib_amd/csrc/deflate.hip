@@ -192,12 +192,15 @@ struct EmitShared {
   u32 status;
 };
 
-constexpr u32 kEmitShared = (sizeof(EmitShared) + 15) & ~u32(15);
 
-// Bit buffer words for a chunk: a fixed/dynamic block is only chosen when it
-// is shorter than the stored form (len + 5 bytes).  A multiple of 4 words:
-// the stage is cleared and copied out as uint4.
-constexpr u32 stage_words(u32 chunk) { return ((chunk + 8) / 4 + 16 + 3) & ~3u; }
+// e_emit's bit buffer is a ring: word w of the chunk's stream lives at
+// ring[w % kRingWords].  A round of 1024 tokens writes at most 1536 words,
+// and the words below a round's first bit leave for the slot during the
+// next round, so the live words always fit.
+constexpr u32 kRingWords = 4096;
+constexpr u32 kRingMask = kRingWords - 1;
+static_assert(2 * (kEmitThreads * kTokensPerThread * 48 / 32) + 8 < kRingWords,
+              "two rounds of the longest tokens fit the ring");
 
 __device__ __forceinline__ u32 win_u32(const u32* win, u32 q) {
   return __builtin_amdgcn_alignbyte(win[(q >> 2) + 1], win[q >> 2], q & 3);
@@ -546,26 +549,25 @@ __device__ void rle_lengths_wave(TreeShared& sh) {
 // Serial LSB-first writer into the LDS bit buffer (header and block tail);
 // ORs into words that the caller has cleared.
 struct StageWriter {
-  u32* words;
-  u32 cap;
+  u32* ring;
   u32 pos;
   __device__ __forceinline__ void put(u32 v, u32 n) {
     if (!n) return;
     const u32 w = pos >> 5, s = pos & 31;
     const u64 x = u64(v) << s;
-    if (w < cap) words[w] |= u32(x);
-    if (s + n > 32 && w + 1 < cap) words[w + 1] |= u32(x >> 32);
+    ring[w & kRingMask] |= u32(x);
+    if (s + n > 32) ring[(w + 1) & kRingMask] |= u32(x >> 32);
     pos += n;
   }
 };
 
-__device__ __forceinline__ void or_bits(u32* words, u32 cap, u32 pos, u64 v) {
+__device__ __forceinline__ void or_bits(u32* ring, u32 pos, u64 v) {
   const u32 w = pos >> 5, s = pos & 31;
   const u64 lo = v << s;
   const u32 hi = s ? u32(v >> (64 - s)) : 0u;
-  if (u32(lo) && w < cap) atomicOr(&words[w], u32(lo));
-  if (u32(lo >> 32) && w + 1 < cap) atomicOr(&words[w + 1], u32(lo >> 32));
-  if (hi && w + 2 < cap) atomicOr(&words[w + 2], hi);
+  if (u32(lo)) atomicOr(&ring[w & kRingMask], u32(lo));
+  if (u32(lo >> 32)) atomicOr(&ring[(w + 1) & kRingMask], u32(lo >> 32));
+  if (hi) atomicOr(&ring[(w + 2) & kRingMask], hi);
 }
 
 // Block-wide exclusive scan of one u32 per thread of e_emit; returns the
@@ -1072,17 +1074,16 @@ __global__ __launch_bounds__(kTreeThreads) __attribute__((amdgpu_waves_per_eu(4)
 }
 
 // Bit emission of one chunk per workgroup (grid-stride) with the chunk's
-// CodeTables.  Dynamic LDS: EmitShared + bit buffer of `words` words.
-__global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const ChunkDesc* descs,
-                                                       u32 chunks, const u32* tokens,
-                                                       const ChunkStats* stats,
-                                                       const CodeTables* tables, u32 words,
-                                                       u32 slot_bytes, u8* slots,
-                                                       ChunkResult* results) {
-  extern __shared__ __align__(16) u8 dyn[];
-  EmitShared& es = *reinterpret_cast<EmitShared*>(dyn);
+// CodeTables, through an LDS bit ring (18 KiB of LDS in all, so eight
+// workgroups share a CU): every round, after the scan that places its
+// tokens, the words below the round's first bit are complete and move to
+// the slot (and are cleared for reuse).
+__global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8))) void e_emit(
+    const u8* in, const ChunkDesc* descs, u32 chunks, const u32* tokens, const ChunkStats* stats,
+    const CodeTables* tables, u32 slot_bytes, u8* slots, ChunkResult* results) {
+  __shared__ EmitShared es;
+  __shared__ __align__(16) u32 stage[kRingWords];
   CodeTables& sh = es.tab;
-  u32* stage = reinterpret_cast<u32*>(dyn + kEmitShared);
   const u32 t = threadIdx.x;
   for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
     const ChunkDesc d = descs[c];
@@ -1112,16 +1113,30 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         results[c].status = 0;
       }
     } else {
-      const u32 used4 = min(((sh.extent + 3) / 4 + 1 + 3) / 4, words / 4);
-      for (u32 i = t; i < used4; i += kEmitThreads)
-        reinterpret_cast<uint4*>(stage)[i] = uint4{0u, 0u, 0u, 0u};
+      uint4* ring4 = reinterpret_cast<uint4*>(stage);
+      for (u32 i = t; i < kRingWords / 4; i += kEmitThreads) ring4[i] = uint4{0u, 0u, 0u, 0u};
+      // Ring words [0, flushed) are in the slot already (flushed: uniform, a
+      // multiple of 4).  The slot takes whole uint4s: its size is a multiple
+      // of 16 bytes, and ring words past the stream are zero.
+      uint4* slot128 = reinterpret_cast<uint4*>(slot);
+      const u32 slot4 = slot_bytes / 16;
+      u32 flushed = 0;
+      const auto flush = [&](u32 upto) {  // words [flushed, upto) are complete
+        const u32 hi4 = min(upto / 4, slot4);
+        for (u32 i = flushed / 4 + t; i < hi4; i += kEmitThreads) {
+          uint4& r = ring4[i & (kRingMask / 4)];
+          slot128[i] = r;
+          r = uint4{0u, 0u, 0u, 0u};
+        }
+        if (hi4 * 4 > flushed) flushed = hi4 * 4;
+      };
       lds_barrier();
       // Header: the fixed fields by thread 0 (before the scan's barriers),
       // then the code-length RLE symbols, two per thread, placed by a scan.
       const u32 nrle = mode == 2 ? sh.nrle : 0u;
       const u32 fixed_bits = mode == 2 ? 17 + 3 * sh.hclen : 3u;
       if (!t) {
-        StageWriter out = {stage, words, 0};
+        StageWriter out = {stage, 0};
         out.put(d.last ? 1u : 0u, 1);
         out.put(mode == 1 ? 1u : 2u, 2);
         if (mode == 2) {
@@ -1150,7 +1165,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
       u32 hoff = fixed_bits + block_scan(es.scan, hmine, htotal);
 #pragma unroll
       for (u32 k = 0; k < 2; ++k) {
-        if (hn[k]) or_bits(stage, words, hoff, hb[k]);
+        if (hn[k]) or_bits(stage, hoff, hb[k]);
         hoff += hn[k];
       }
       if (!t && fixed_bits + htotal != sh.hdr_bits) es.status = kCompressionOverflow;
@@ -1191,16 +1206,18 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         }
         u32 total;
         u32 off = pos + block_scan(es.scan, mine, total);
+        // Every earlier round's bits are in the ring (the scan's barriers).
+        flush((pos >> 5) & ~3u);
 #pragma unroll
         for (u32 k = 0; k < kTokensPerThread; ++k) {
-          if (nbits[k]) or_bits(stage, words, off, bits[k]);
+          if (nbits[k]) or_bits(stage, off, bits[k]);
           off += nbits[k];
         }
         pos += total;
       }
       lds_barrier();
       if (!t) {
-        StageWriter out = {stage, words, pos};
+        StageWriter out = {stage, pos};
         out.put(sh.code_ll[256], sh.len_ll[256]);
         if (!d.last) {
           out.put(0, 3);
@@ -1213,12 +1230,7 @@ __global__ __launch_bounds__(kEmitThreads) void e_emit(const u8* in, const Chunk
         results[c].extent = sh.extent;
       }
       lds_barrier();
-      // Whole uint4s: the slot size and the stage size are multiples of 16
-      // bytes, and the stage is zero past the stream up to used4.
-      const u32 copy4 = min(((sh.extent + 3) / 4 + 3) / 4, min(slot_bytes / 16, words / 4));
-      uint4* slot128 = reinterpret_cast<uint4*>(slot);
-      const uint4* stage128 = reinterpret_cast<const uint4*>(stage);
-      for (u32 i = t; i < copy4; i += kEmitThreads) slot128[i] = stage128[i];
+      flush(4 * ((sh.extent + 15) / 16));
       if (!t) results[c].status = es.status;
     }
     lds_barrier();
@@ -1371,12 +1383,9 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
                       u32 file_count, u8* out, u32 chunk_bytes, u32* meta) {
   const u64 slot_bytes = slot_size(chunk_bytes);
   const u32 parse_lds = kParseShared + history_limit(chunk_bytes) + chunk_bytes + 32;
-  const u32 words = stage_words(chunk_bytes);
-  const u32 emit_lds = kEmitShared + 4 * words;
+
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_parse),
                              hipFuncAttributeMaxDynamicSharedMemorySize, int(parse_lds)));
-  HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_emit),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, int(emit_lds)));
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
   // One or two parse workgroups per CU (as many as their LDS allows), each
   // taking a run of consecutive chunks.
@@ -1391,8 +1400,8 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_LAUNCH(e_tree, dim3(grid), dim3(kTreeThreads), 0, stream, b.descs, u32(chunks), b.stats,
             b.tables, b.results);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), emit_lds, stream, in, b.descs, u32(chunks),
-            b.tokens, b.stats, b.tables, words, u32(slot_bytes), b.slots, b.results);
+  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), 0, stream, in, b.descs, u32(chunks),
+            b.tokens, b.stats, b.tables, u32(slot_bytes), b.slots, b.results);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, b.results, u32(chunks), b.sums);
   HZ_TRY(hipGetLastError());
