@@ -220,7 +220,7 @@ __device__ __forceinline__ u32 hash4(u32 v) { return (v * 2654435761u) >> (32 - 
 __device__ __forceinline__ u32 match_len(const u32* win, u32 a, u32 b, u32 maxlen) {
   {
     const u32 x = win_u32(win, a) ^ win_u32(win, b);
-    if (x) return min(maxlen, __builtin_ctz(x) >> 3);
+    if (x) return min(maxlen, u32(__builtin_ctz(x)) >> 3);
   }
   const u32 sa = a & 3, sb = b & 3;
   const u32* pa = win + (a >> 2) + 1;
@@ -236,7 +236,7 @@ __device__ __forceinline__ u32 match_len(const u32* win, u32 a, u32 b, u32 maxle
     for (u32 k = 0; k < 4; ++k) {
       const u32 x = __builtin_amdgcn_alignbyte(da[k + 1], da[k], sa) ^
                     __builtin_amdgcn_alignbyte(db[k + 1], db[k], sb);
-      if (x) return min(maxlen, m + 4 * k + (__builtin_ctz(x) >> 3));
+      if (x) return min(maxlen, m + 4 * k + (u32(__builtin_ctz(x)) >> 3));
     }
   }
   return maxlen;

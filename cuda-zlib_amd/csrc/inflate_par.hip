@@ -504,7 +504,7 @@ __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, S
     x[k] = e < count ? in[e] & mask : 0u;
   }
   for (u64 base = 0; base < count; base += kScanTile) {
-    const u32 m = u32(min<u64>(count - base, kScanTile));
+    const u32 m = count - base < kScanTile ? u32(count - base) : kScanTile;
 #pragma unroll
     for (u32 k = 0; k < kScanPer; ++k) sh.v[scan_slot(k * kScanThreads + t)] = x[k];
 #pragma unroll
