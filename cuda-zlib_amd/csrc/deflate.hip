@@ -845,13 +845,18 @@ __global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8
       // by shuffles; J[k] = f^(2^k) while inside the wave); wave 0 chains the
       // waves' entries; each wave then finds its orbit from its entry.
       const u32 w0 = wave * 64, wend = w0 + 64;
+      const u64 matches = __ballot(L != 0);
       u32 J[6];
       u32 x = f;
+      if (matches) {
 #pragma unroll
-      for (u32 k = 0; k < 6; ++k) {
-        J[k] = x;
-        const u32 y = __shfl(x, int((x - w0) & 63), 64);
-        x = x < wend ? y : x;
+        for (u32 k = 0; k < 6; ++k) {
+          J[k] = x;
+          const u32 y = __shfl(x, int((x - w0) & 63), 64);
+          x = x < wend ? y : x;
+        }
+      } else {
+        x = wend;  // all literals: every orbit in the wave leaves it at its end
       }
       sh.exitv[t] = u16(x);
       lds_barrier();
@@ -889,7 +894,6 @@ __global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8
       // walk resumes past that match, in scalar registers.  Otherwise marks
       // are pushed from the entry, 2^k hops in round k.
       u64 starts = 0;
-      const u64 matches = __ballot(L != 0);
       if (__popcll(matches) > kWalkMatches) {
         sh.mark[t] = t == entry;
         wave_sync();
