@@ -117,6 +117,7 @@ struct ParseShared {
   u32 table[kBuckets * kWays];  // position + 1 per way, 0 = empty
   u16 exitv[kStep];             // first orbit point past the position's wave
   u16 went[kParseWaves];        // orbit entry of each wave (0xffff: none)
+  u8 wave_match[kParseWaves];   // the wave has a match in the current step
   u8 mark[kStep];               // token starts of waves that mark by doubling
   u32 freq_ll[288];
   u32 freq_d[32];
@@ -859,6 +860,7 @@ __global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8
         x = wend;  // all literals: every orbit in the wave leaves it at its end
       }
       sh.exitv[t] = u16(x);
+      if (!lane) sh.wave_match[wave] = matches != 0;
       lds_barrier();
       // Every lookup of the step is done: its positions enter the table.
       if (hashable) atomicMax(&sh.table[h], q + 1);
@@ -870,19 +872,25 @@ __global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8
         // the hops are scalar work, and the scalar unit is shared by the
         // CU): lane l holds the exits of position l of every wave; each hop
         // leaves its wave, so wave w is entered at most once, at iteration w.
-        u32 ex[kParseWaves];
+        if (!__ballot(lane < kParseWaves && sh.wave_match[lane])) {
+          // No match in the step: every wave is entered at its first position.
+          if (lane < kParseWaves) sh.went[lane] = u16(lane * 64 < lim ? lane * 64 : 0xffffu);
+          if (!lane) sh.adv = (lim + 63) & ~63u;
+        } else {
+          u32 ex[kParseWaves];
 #pragma unroll
-        for (u32 w = 0; w < kParseWaves; ++w) ex[w] = sh.exitv[w * 64 + lane];
-        u32 e = 0, went = 0xffffu;  // e is uniform; lane w keeps wave w's entry
+          for (u32 w = 0; w < kParseWaves; ++w) ex[w] = sh.exitv[w * 64 + lane];
+          u32 e = 0, went = 0xffffu;  // e is uniform; lane w keeps wave w's entry
 #pragma unroll
-        for (u32 w = 0; w < kParseWaves; ++w) {
-          if (e < lim && (e >> 6) == w) {
-            went = lane == w ? e : went;
-            e = u32(__builtin_amdgcn_readlane(int(ex[w]), int(e & 63)));
+          for (u32 w = 0; w < kParseWaves; ++w) {
+            if (e < lim && (e >> 6) == w) {
+              went = lane == w ? e : went;
+              e = u32(__builtin_amdgcn_readlane(int(ex[w]), int(e & 63)));
+            }
           }
+          if (lane < kParseWaves) sh.went[lane] = u16(went);
+          if (!lane) sh.adv = e;
         }
-        if (lane < kParseWaves) sh.went[lane] = u16(went);
-        if (!lane) sh.adv = e;
       }
       lds_barrier();
       if (pending && wave == 0) flush();
