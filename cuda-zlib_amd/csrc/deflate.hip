@@ -34,17 +34,18 @@
 //            Tokens go to a global list, histograms by LDS atomics; the step's
 //            positions enter the table by atomicMax, so the newest position
 //            wins independently of execution order.
-// e_emit, one 256-thread workgroup per chunk (small LDS, several per CU):
-//   huffman  waves 0 and 1: optimal code lengths limited to 15/7 bits
-//            (leaves sorted by a bitonic network, package-merge with each
-//            level merged along merge paths); wave-parallel code-length
-//            RLE and canonical codes
-//   choose   exact bit costs of stored / fixed / dynamic
-//   emit     4 tokens per thread per round: bit lengths, block-wide
-//            exclusive scan, atomicOr into an LDS bit buffer; one coalesced
-//            copy into the chunk's slot
-// Then a scan of chunk extents, per-file wrapper/metadata, and packing, all on
-// device (no host synchronisation).
+// e_tree, one two-wave workgroup per chunk (eight per CU):
+//   huffman  optimal code lengths limited to 15/7 bits (leaves sorted by a
+//            bitonic network, package-merge with each level merged along
+//            merge paths); wave-parallel code-length RLE and canonical codes
+//   choose   exact bit costs of stored / fixed / dynamic, hence the chunk's
+//            compressed extent
+// e_scan places every chunk from the extents; then e_emit, one 256-thread
+// workgroup per chunk (eight per CU): 4 tokens per thread per round, bit
+// lengths, block-wide exclusive scan, atomicOr into an LDS bit ring whose
+// complete 16-byte lines go straight to the chunk's place in the output.
+// Then per-file wrapper and metadata, all on device (no host
+// synchronisation).
 #include <algorithm>
 #include <vector>
 
@@ -83,7 +84,6 @@ struct ChunkDesc {
   u64 in_off;    // absolute input offset of the chunk
   u64 file_off;  // chunk offset inside its file
   u64 file_len;  // length of the chunk's file
-  u64 slot;      // byte offset of the chunk's slot
   u32 len;       // chunk bytes
   u32 hist;      // history bytes staged before the chunk (same file)
   u32 file;
@@ -194,9 +194,9 @@ struct EmitShared {
 };
 
 
-// e_emit's bit buffer is a ring: word w of the chunk's stream lives at
+// e_emit's bit buffer is a ring: word w of the chunk's output lines lives at
 // ring[w % kRingWords].  A round of 1024 tokens writes at most 1536 words,
-// and the words below a round's first bit leave for the slot during the
+// and the lines below a round's first bit leave for the output during the
 // next round, so the live words always fit.
 constexpr u32 kRingWords = 4096;
 constexpr u32 kRingMask = kRingWords - 1;
@@ -620,7 +620,6 @@ __global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 c
                                ChunkDesc* descs, FileDesc* file) {
   const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x;
   const u64 stride = u64(gridDim.x) * blockDim.x;
-  const u64 slot_bytes = (u64(chunk) + 16 + 15) & ~u64(15);
   for (u64 c = tid; c < chunks; c += stride) {
     ChunkDesc d;
     d.in_off = c * chunk;
@@ -630,7 +629,6 @@ __global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 c
     d.hist = u32(min<u64>(hist_max, d.in_off));
     d.file = 0;
     d.last = c + 1 == chunks;
-    d.slot = c * slot_bytes;
     descs[c] = d;
   }
   if (!tid) {
@@ -1056,6 +1054,8 @@ __global__ __launch_bounds__(kTreeThreads) __attribute__((amdgpu_waves_per_eu(4)
         tab.mode = mode;
         tab.extent = u32(best);
         tab.hdr_bits = mode == 2 ? hdr : 3u;
+        results[c].extent = u32(best);
+        results[c].status = 0;
         const u64 S = st.sum_s % kAdlerMod, L = st.sum_l % kAdlerMod;
         results[c].adler_s = S;
         results[c].adler_b =
@@ -1086,69 +1086,83 @@ __global__ __launch_bounds__(kTreeThreads) __attribute__((amdgpu_waves_per_eu(4)
 }
 
 // Bit emission of one chunk per workgroup (grid-stride) with the chunk's
-// CodeTables, through an LDS bit ring (18 KiB of LDS in all, so eight
-// workgroups share a CU): every round, after the scan that places its
-// tokens, the words below the round's first bit are complete and move to
-// the slot (and are cleared for reuse).
+// CodeTables, straight into the chunk's place in the output stream (after
+// its file's 2-byte header and the earlier chunks, from the extent scan).
+// The bits go through an LDS bit ring (18 KiB of LDS in all, so eight
+// workgroups share a CU) that starts at the chunk's byte offset inside an
+// aligned 16-byte line: ring line k is output line k.  After each round's
+// scan the lines below the round's first bit are complete and are stored
+// (whole lines as 16-byte stores, the chunk's partial first and last lines
+// byte by byte, so that neighbouring chunks' bytes are never written) and
+// cleared for reuse.  A chunk whose bits do not match its extent (an
+// internal inconsistency) marks its file failed; nothing is written past
+// the extent.
 __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8))) void e_emit(
-    const u8* in, const ChunkDesc* descs, u32 chunks, const u32* tokens, const ChunkStats* stats,
-    const CodeTables* tables, u32 slot_bytes, u8* slots, ChunkResult* results) {
+    const u8* in, const ChunkDesc* descs, const FileDesc* files, u32 chunks, const u32* tokens,
+    const ChunkStats* stats, const CodeTables* tables, const u64* sums, u8* out,
+    u32* file_bad) {
   __shared__ EmitShared es;
   __shared__ __align__(16) u32 stage[kRingWords];
   CodeTables& sh = es.tab;
   const u32 t = threadIdx.x;
   for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
     const ChunkDesc d = descs[c];
+    const FileDesc f = files[d.file];
+    u8* dst = out + f.out_off + 2 + (sums[4 * u64(c)] - sums[4 * u64(f.first_chunk)]);
     {
       const uint4* src = reinterpret_cast<const uint4*>(tables + c);
-      uint4* dst = reinterpret_cast<uint4*>(&sh);
-      for (u32 i = t; i < sizeof(CodeTables) / 16; i += kEmitThreads) dst[i] = src[i];
+      uint4* dst4 = reinterpret_cast<uint4*>(&sh);
+      for (u32 i = t; i < sizeof(CodeTables) / 16; i += kEmitThreads) dst4[i] = src[i];
       if (!t) es.status = 0;
     }
     lds_barrier();
 
     // ---- emission ----
     const u32 mode = sh.mode;
-    u8* slot = slots + d.slot;
     if (mode == 0) {
       if (!t) {
-        slot[0] = u8(d.last ? 1 : 0);
-        slot[1] = u8(d.len & 0xff);
-        slot[2] = u8(d.len >> 8);
-        slot[3] = u8(~d.len & 0xff);
-        slot[4] = u8((~d.len >> 8) & 0xff);
+        dst[0] = u8(d.last ? 1 : 0);
+        dst[1] = u8(d.len & 0xff);
+        dst[2] = u8(d.len >> 8);
+        dst[3] = u8(~d.len & 0xff);
+        dst[4] = u8((~d.len >> 8) & 0xff);
       }
       const u8* src = in + d.in_off;
-      for (u32 i = t; i < d.len; i += kEmitThreads) slot[5 + i] = src[i];
-      if (!t) {
-        results[c].extent = sh.extent;
-        results[c].status = 0;
-      }
+      copy_bytes(dst + 5, src, d.len, src + d.len, t, kEmitThreads);
     } else {
       uint4* ring4 = reinterpret_cast<uint4*>(stage);
       for (u32 i = t; i < kRingWords / 4; i += kEmitThreads) ring4[i] = uint4{0u, 0u, 0u, 0u};
-      // Ring words [0, flushed) are in the slot already (flushed: uniform, a
-      // multiple of 4).  The slot takes whole uint4s: its size is a multiple
-      // of 16 bytes, and ring words past the stream are zero.
-      uint4* slot128 = reinterpret_cast<uint4*>(slot);
-      const u32 slot4 = slot_bytes / 16;
-      u32 flushed = 0;
-      const auto flush = [&](u32 upto) {  // words [flushed, upto) are complete
-        const u32 hi4 = min(upto / 4, slot4);
-        for (u32 i = flushed / 4 + t; i < hi4; i += kEmitThreads) {
-          uint4& r = ring4[i & (kRingMask / 4)];
-          slot128[i] = r;
+      // Output line k is bytes [16k, 16k + 16) from `line0`; the chunk's
+      // bytes are [lead, lead + extent) of them.
+      const u32 lead = u32(reinterpret_cast<uintptr_t>(dst) & 15);
+      u8* line0 = dst - lead;
+      const u32 last_byte = lead + sh.extent;
+      u32 stored = 0;  // output lines stored and cleared (uniform)
+      const auto store_lines = [&](u32 upto) {  // lines [stored, upto) are complete
+        for (u32 k = stored + t; k < upto; k += kEmitThreads) {
+          uint4& r = ring4[k & (kRingMask / 4)];
+          const u32 lo = max(16 * k, lead), hi = min(16 * k + 16, last_byte);
+          if (lo == 16 * k && hi == 16 * k + 16) {
+            *reinterpret_cast<uint4*>(line0 + 16 * k) = r;
+          } else {
+            for (u32 b = lo; b < hi; ++b) {
+              const u32 q = (b >> 2) & 3;
+              const u32 word = q == 0 ? r.x : q == 1 ? r.y : q == 2 ? r.z : r.w;
+              line0[b] = u8(word >> (8 * (b & 3)));
+            }
+          }
           r = uint4{0u, 0u, 0u, 0u};
         }
-        if (hi4 * 4 > flushed) flushed = hi4 * 4;
+        if (upto > stored) stored = upto;
       };
       lds_barrier();
       // Header: the fixed fields by thread 0 (before the scan's barriers),
       // then the code-length RLE symbols, two per thread, placed by a scan.
       const u32 nrle = mode == 2 ? sh.nrle : 0u;
       const u32 fixed_bits = mode == 2 ? 17 + 3 * sh.hclen : 3u;
+      const u32 bit0 = 8 * lead;
       if (!t) {
-        StageWriter out = {stage, 0};
+        StageWriter out = {stage, bit0};
         out.put(d.last ? 1u : 0u, 1);
         out.put(mode == 1 ? 1u : 2u, 2);
         if (mode == 2) {
@@ -1174,7 +1188,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8)
         hmine += hn[k];
       }
       u32 htotal;
-      u32 hoff = fixed_bits + block_scan(es.scan, hmine, htotal);
+      u32 hoff = bit0 + fixed_bits + block_scan(es.scan, hmine, htotal);
 #pragma unroll
       for (u32 k = 0; k < 2; ++k) {
         if (hn[k]) or_bits(stage, hoff, hb[k]);
@@ -1184,7 +1198,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8)
       lds_barrier();
       const u32* tok = tokens + d.in_off;
       const u32 ntokens = stats[c].ntok;
-      u32 pos = sh.hdr_bits;
+      u32 pos = bit0 + sh.hdr_bits;
       // The tokens of the next round are loaded (one 16-byte load per
       // thread) while the current round is coded, so the global-memory
       // latency overlaps the scan's barriers.
@@ -1219,7 +1233,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8)
         u32 total;
         u32 off = pos + block_scan(es.scan, mine, total);
         // Every earlier round's bits are in the ring (the scan's barriers).
-        flush((pos >> 5) & ~3u);
+        store_lines(min(pos / 128, last_byte / 16));
 #pragma unroll
         for (u32 k = 0; k < kTokensPerThread; ++k) {
           if (nbits[k]) or_bits(stage, off, bits[k]);
@@ -1237,13 +1251,12 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8)
           out.put(0, 16);
           out.put(0xffff, 16);
         }
-        const u32 bytes = (out.pos + 7) / 8;
+        const u32 bytes = (out.pos + 7) / 8 - lead;
         if (bytes != sh.extent) es.status = kCompressionOverflow;
-        results[c].extent = sh.extent;
       }
       lds_barrier();
-      flush(4 * ((sh.extent + 15) / 16));
-      if (!t) results[c].status = es.status;
+      store_lines((last_byte + 15) / 16);
+      if (!t && es.status) atomicOr(&file_bad[d.file], 1u);
     }
     lds_barrier();
   }
@@ -1251,9 +1264,12 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(8)
 
 // One workgroup: exclusive scans of chunk extents, Adler partial sums and
 // failed-chunk counts; sums[4 * i + k] holds the prefix before chunk i.
-__global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 chunks, u64* sums) {
+// Also clears the files' failure flags, which e_emit sets.
+__global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 chunks, u64* sums,
+                                               u32* file_bad, u32 file_count) {
   __shared__ u64 part[4][1024];
   const u32 t = threadIdx.x;
+  for (u32 fi = t; fi < file_count; fi += 1024) file_bad[fi] = 0;
   const u64 per = (u64(chunks) + 1023) / 1024;
   const u64 lo = min<u64>(chunks, t * per), hi = min<u64>(chunks, lo + per);
   u64 acc[4] = {0, 0, 0, 0};
@@ -1287,12 +1303,13 @@ __global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 c
 
 // Per file: status, wrapper and metadata [length, status].
 __global__ void e_wrap(const FileDesc* files, u32 count, const ChunkResult* results,
-                       const u64* sums, u8* out, u32* meta, u32* file_ok) {
+                       const u64* sums, u8* out, u32* meta, u32* file_ok,
+                       const u32* file_bad) {
   const u32 tid = blockIdx.x * blockDim.x + threadIdx.x;
   for (u32 fi = tid; fi < count; fi += gridDim.x * blockDim.x) {
     const FileDesc f = files[fi];
     const u64 a0 = f.first_chunk, a1 = f.first_chunk + f.chunks;
-    u32 status = sums[4 * a1 + 3] != sums[4 * a0 + 3] ? kCompressionOverflow : 0u;
+    u32 status = sums[4 * a1 + 3] != sums[4 * a0 + 3] || file_bad[fi] ? kCompressionOverflow : 0u;
     const u64 body = sums[4 * a1] - sums[4 * a0];
     const u64 total = body + 6;
     if (total > f.capacity) status = kCompressionOverflow;
@@ -1317,39 +1334,14 @@ __global__ void e_wrap(const FileDesc* files, u32 count, const ChunkResult* resu
   }
 }
 
-// Copy chunk slots to their final places (after each file's 2-byte header).
-__global__ __launch_bounds__(256) void e_pack(const ChunkDesc* descs, const FileDesc* files,
-                                              u32 chunks, const ChunkResult* results,
-                                              const u64* sums, const u8* slots, u8* out,
-                                              const u32* file_ok) {
-  for (u32 c = blockIdx.x; c < chunks; c += gridDim.x) {
-    const ChunkDesc d = descs[c];
-    const FileDesc f = files[d.file];
-    if (!file_ok[d.file]) continue;
-    const u64 rel = sums[4 * u64(c)] - sums[4 * u64(f.first_chunk)];
-    u8* dst = out + f.out_off + 2 + rel;
-    const u8* src = slots + d.slot;
-    const u32 n = results[c].extent;
-    // Bytes up to the first 16-byte boundary of dst, then 16-byte stores of
-    // source dwords realigned with v_alignbyte (a slot is 16-byte aligned and
-    // has at least 16 bytes past any extent, so the fifth dword is in it),
-    // then the tail bytes.
-    const u32 head = min(n, u32((16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15));
-    const u32 blocks = (n - head) / 16;
-    for (u32 i = threadIdx.x; i < head; i += blockDim.x) dst[i] = src[i];
-    const u32* s32 = reinterpret_cast<const u32*>(src);
-    const u32 sh = head & 3;
-    for (u32 j = threadIdx.x; j < blocks; j += blockDim.x) {
-      const u32 w = (head + 16 * j) >> 2;
-      const u32 x0 = s32[w], x1 = s32[w + 1], x2 = s32[w + 2], x3 = s32[w + 3], x4 = s32[w + 4];
-      uint4 o;
-      o.x = __builtin_amdgcn_alignbyte(x1, x0, sh);
-      o.y = __builtin_amdgcn_alignbyte(x2, x1, sh);
-      o.z = __builtin_amdgcn_alignbyte(x3, x2, sh);
-      o.w = __builtin_amdgcn_alignbyte(x4, x3, sh);
-      *reinterpret_cast<uint4*>(dst + head + 16 * j) = o;
-    }
-    for (u32 i = head + 16 * blocks + threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+// Zeroes the output slot of every failed file of a batch (e_emit has already
+// written its chunks); one workgroup per file, grid-stride.
+__global__ __launch_bounds__(256) void e_clear_failed(const FileDesc* files, u32 count,
+                                                      const u32* file_ok, u8* out) {
+  for (u32 fi = blockIdx.x; fi < count; fi += gridDim.x) {
+    if (file_ok[fi]) continue;
+    const FileDesc f = files[fi];
+    for (u64 i = threadIdx.x; i < f.capacity; i += blockDim.x) out[f.out_off + i] = 0;
   }
 }
 
@@ -1361,7 +1353,6 @@ namespace {
     if (_e != hipSuccess) return _e; \
   } while (0)
 
-u64 slot_size(u32 chunk_bytes) { return (u64(chunk_bytes) + 16 + 15) & ~u64(15); }
 
 // Scratch of one encode call.  Every buffer is carved before the first
 // launch, so that a call which cannot get its scratch enqueues nothing.
@@ -1369,12 +1360,12 @@ struct ChunkBuffers {
   ChunkDesc* descs = nullptr;
   FileDesc* files = nullptr;
   u32* tokens = nullptr;
-  u8* slots = nullptr;
   ChunkStats* stats = nullptr;
   CodeTables* tables = nullptr;
   ChunkResult* results = nullptr;
   u64* sums = nullptr;
   u32* file_ok = nullptr;
+  u32* file_bad = nullptr;
 };
 
 hipError_t alloc_chunks(Scratch& scratch, u64 chunks, u32 file_count, u64 in_total,
@@ -1382,18 +1373,17 @@ hipError_t alloc_chunks(Scratch& scratch, u64 chunks, u32 file_count, u64 in_tot
   HZ_TRY(scratch.alloc(&b.descs, chunks));
   HZ_TRY(scratch.alloc(&b.files, file_count));
   HZ_TRY(scratch.alloc(&b.tokens, in_total ? in_total : 1));
-  HZ_TRY(scratch.alloc(&b.slots, chunks * slot_size(chunk_bytes)));
   HZ_TRY(scratch.alloc(&b.stats, chunks));
   HZ_TRY(scratch.alloc(&b.tables, chunks));
   HZ_TRY(scratch.alloc(&b.results, chunks));
   HZ_TRY(scratch.alloc(&b.sums, 4 * (chunks + 1)));
   HZ_TRY(scratch.alloc(&b.file_ok, file_count));
+  HZ_TRY(scratch.alloc(&b.file_bad, file_count));
   return hipSuccess;
 }
 
 hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u64 chunks,
-                      u32 file_count, u8* out, u32 chunk_bytes, u32* meta) {
-  const u64 slot_bytes = slot_size(chunk_bytes);
+                      u32 file_count, u8* out, u32 chunk_bytes, u32* meta, bool clear_failed) {
   const u32 parse_lds = kParseShared + history_limit(chunk_bytes) + chunk_bytes + 32;
 
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_parse),
@@ -1412,16 +1402,21 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_LAUNCH(e_tree, dim3(grid), dim3(kTreeThreads), 0, stream, b.descs, u32(chunks), b.stats,
             b.tables, b.results);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), 0, stream, in, b.descs, u32(chunks),
-            b.tokens, b.stats, b.tables, u32(slot_bytes), b.slots, b.results);
+  // The extents are known from the trees: their scan places every chunk
+  // before any is emitted.
+  HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, b.results, u32(chunks), b.sums, b.file_bad,
+            file_count);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_scan, dim3(1), dim3(1024), 0, stream, b.results, u32(chunks), b.sums);
+  HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), 0, stream, in, b.descs, b.files, u32(chunks),
+            b.tokens, b.stats, b.tables, b.sums, out, b.file_bad);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, b.files, file_count,
-            b.results, b.sums, out, meta, b.file_ok);
+            b.results, b.sums, out, meta, b.file_ok, b.file_bad);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_pack, dim3(grid), dim3(256), 0, stream, b.descs, b.files, u32(chunks), b.results,
-            b.sums, b.slots, out, b.file_ok);
+  if (clear_failed) {
+    HZ_LAUNCH(e_clear_failed, dim3(std::min<u32>(file_count, 65536)), dim3(256), 0, stream,
+              b.files, file_count, b.file_ok, out);
+  }
   return hipGetLastError();
 }
 
@@ -1429,7 +1424,7 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
 
 // Zeros the single stream's slot after its stream: [meta[0], capacity), which
 // is the whole slot when compression failed (meta[0] is then 0).  The stream
-// itself is written in full by e_wrap and e_pack.
+// itself is written in full by e_emit and e_wrap.
 __global__ __launch_bounds__(256) void e_zero_tail(u8* out, u64 capacity, const u32* meta) {
   const u64 from = min<u64>(meta[0], capacity);
   const u64 first16 = (from + 15) & ~u64(15), end16 = capacity & ~u64(15);
@@ -1455,7 +1450,7 @@ hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 i
             stream, in_size, chunk_bytes, u32(chunks), independent ? 0u : history_limit(chunk_bytes),
             capacity, b.descs, b.files);
   HZ_TRY(hipGetLastError());
-  HZ_TRY(run_chunks(stream, b, in, chunks, 1, out, chunk_bytes, meta));
+  HZ_TRY(run_chunks(stream, b, in, chunks, 1, out, chunk_bytes, meta, false));
   HZ_LAUNCH(e_zero_tail, dim3(u32(std::min<u64>(1024, (capacity / 16 + 255) / 256 + 1))), dim3(256),
             0, stream, out, capacity, meta);
   return hipGetLastError();
@@ -1482,7 +1477,6 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
   (void)out_total;
   std::vector<ChunkDesc> descs;
   std::vector<FileDesc> files(count);
-  const u64 slot_bytes = slot_size(chunk_bytes);
   const u32 hist_max = history_limit(chunk_bytes);
   for (u32 f = 0; f < count; ++f) {
     const BatchFile& bf = files_host[f];
@@ -1498,7 +1492,6 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
       d.hist = u32(std::min<u64>(hist_max, j * chunk_bytes));
       d.file = f;
       d.last = j + 1 == k;
-      d.slot = descs.size() * slot_bytes;
       descs.push_back(d);
     }
   }
@@ -1509,7 +1502,7 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
                         hipMemcpyHostToDevice, stream));
   HZ_TRY(hipMemcpyAsync(b.files, files.data(), count * sizeof(FileDesc), hipMemcpyHostToDevice,
                         stream));
-  return run_chunks(stream, b, in, descs.size(), count, out, chunk_bytes, meta);
+  return run_chunks(stream, b, in, descs.size(), count, out, chunk_bytes, meta, true);
 }
 
 }  // namespace hz

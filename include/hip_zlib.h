@@ -96,7 +96,7 @@ int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_sizes, uint6
  * library holds on each GPU for the life of the process, instead of the pool.
  * It calls no hipMalloc/hipFree or allocating routine, for callers that cannot
  * allocate (code under HIP graph capture, allocation-free serving loops).
- * Inputs are limited by that array: with 32 KiB chunks up to about 9.5 MiB
+ * Inputs are limited by that array: with 32 KiB chunks up to about 11 MiB
  * (scratch is about 5 bytes per input byte).  A larger input returns
  * HIP_ZLIB_INVALID_ARGUMENT, with the bytes it would need in
  * HipZlibErrorString(-1), and enqueues nothing.  Calls on one GPU share the
