@@ -2823,15 +2823,18 @@ struct RoundBytes {
   u8* lds;
   u64 base, split;  // split = base + stage bytes
   u8* out;
-  AdlerAcc* acc;
   u64 end;
+  // Sums of the bytes written straight to the output, held in the sink (not
+  // behind a pointer to the caller's sums, which kept those in scratch
+  // memory); the caller adds them after the slice.
+  mutable AdlerAcc acc;
   __device__ __forceinline__ u8 get(u64 p) const { return p < split ? lds[u32(p - base)] : out[p]; }
   __device__ __forceinline__ void put(u64 p, u8 v) const {
     if (p < split) {
       lds[u32(p - base)] = v;
     } else {
       out[p] = v;
-      acc->add_byte_unfolded(v, end - p);  // folded once per round (at most 2^18 bytes a thread)
+      acc.add_byte_unfolded(v, end - p);  // folded once per round (at most 2^18 bytes a thread)
     }
   }
   __device__ __forceinline__ void zero(u64 p, u32 n) const {
@@ -3128,7 +3131,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
             // Writes stay inside the round: a slice that would pass its end
             // is an extent error.
             const u64 rend = min(block_out + rec.size, hi);
-            const RoundBytes sink{sh.ostage, lo16, split, out, &sums, out_end};
+            const RoundBytes sink{sh.ostage, lo16, split, out, out_end, AdlerAcc{}};
             // Unchecked decoding when the slice and a token of overshoot lie
             // before the body end.
             if (dst0 < lo)
@@ -3139,6 +3142,8 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
             else
               lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
                                       unres, unres_total, floor);
+            sums.s += sink.acc.s;
+            sums.w += sink.acc.w;
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
           // The staged part in whole 16-byte lines (bytes of the neighbouring
