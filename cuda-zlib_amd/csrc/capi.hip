@@ -99,7 +99,7 @@ class DeviceScope {
     return hipSuccess;
   }
   ~DeviceScope() {
-    if (switched_) hipSetDevice(previous_);
+    if (switched_) (void)hipSetDevice(previous_);
   }
   int device() const { return device_; }
 
@@ -181,7 +181,7 @@ class Workspace final : public Scratch {
     }
     return first;
   }
-  ~Workspace() override { release(); }
+  ~Workspace() override { (void)release(); }
 
  private:
   hipError_t acquire() {
@@ -607,7 +607,7 @@ extern "C" int HipZlibTrimWorkspacePool(int device) {
     keep(hipEventDestroy(a->last_use));
   }
   if (first == hipSuccess) first = hipMemPoolTrimTo(pool, 0);
-  if (previous != device) hipSetDevice(previous);
+  if (previous != device) (void)hipSetDevice(previous);
   return int(first);
 }
 

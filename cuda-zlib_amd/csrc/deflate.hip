@@ -59,7 +59,6 @@ constexpr u32 kParseThreads = 1024;
 constexpr u32 kParseWaves = kParseThreads / 64;
 static_assert(kParseWaves <= 16, "the wave-count scan covers one 16-lane DPP row");
 constexpr u32 kStep = kParseThreads;  // parse positions per step
-constexpr u32 kLog2Step = 10;
 constexpr u32 kHashBits = 13;
 constexpr u32 kBuckets = 1u << kHashBits;
 constexpr u32 kWays = 1;
@@ -1302,9 +1301,8 @@ __global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 c
 }
 
 // Per file: status, wrapper and metadata [length, status].
-__global__ void e_wrap(const FileDesc* files, u32 count, const ChunkResult* results,
-                       const u64* sums, u8* out, u32* meta, u32* file_ok,
-                       const u32* file_bad) {
+__global__ void e_wrap(const FileDesc* files, u32 count, const u64* sums, u8* out, u32* meta,
+                       u32* file_ok, const u32* file_bad) {
   const u32 tid = blockIdx.x * blockDim.x + threadIdx.x;
   for (u32 fi = tid; fi < count; fi += gridDim.x * blockDim.x) {
     const FileDesc f = files[fi];
@@ -1369,7 +1367,7 @@ struct ChunkBuffers {
 };
 
 hipError_t alloc_chunks(Scratch& scratch, u64 chunks, u32 file_count, u64 in_total,
-                        u32 chunk_bytes, ChunkBuffers& b) {
+                        ChunkBuffers& b) {
   HZ_TRY(scratch.alloc(&b.descs, chunks));
   HZ_TRY(scratch.alloc(&b.files, file_count));
   HZ_TRY(scratch.alloc(&b.tokens, in_total ? in_total : 1));
@@ -1411,7 +1409,7 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
             b.tokens, b.stats, b.tables, b.sums, out, b.file_bad);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, b.files, file_count,
-            b.results, b.sums, out, meta, b.file_ok, b.file_bad);
+            b.sums, out, meta, b.file_ok, b.file_bad);
   HZ_TRY(hipGetLastError());
   if (clear_failed) {
     HZ_LAUNCH(e_clear_failed, dim3(std::min<u32>(file_count, 65536)), dim3(256), 0, stream,
@@ -1445,7 +1443,7 @@ hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 i
                        u64 capacity, u32 chunk_bytes, u32* meta, bool independent) {
   const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
   ChunkBuffers b;
-  HZ_TRY(alloc_chunks(scratch, chunks, 1, in_size, chunk_bytes, b));
+  HZ_TRY(alloc_chunks(scratch, chunks, 1, in_size, b));
   HZ_LAUNCH(e_single_descs, dim3(u32(std::min<u64>(1024, (chunks + 255) / 256))), dim3(256), 0,
             stream, in_size, chunk_bytes, u32(chunks), independent ? 0u : history_limit(chunk_bytes),
             capacity, b.descs, b.files);
@@ -1467,7 +1465,7 @@ u64 deflate_scratch_bytes(u64 in_size, u32 chunk_bytes) {
   } sizing;
   const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
   ChunkBuffers b;
-  alloc_chunks(sizing, chunks, 1, in_size, chunk_bytes, b);
+  (void)alloc_chunks(sizing, chunks, 1, in_size, b);
   return sizing.total;
 }
 
@@ -1496,7 +1494,7 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
     }
   }
   ChunkBuffers b;
-  HZ_TRY(alloc_chunks(scratch, descs.size(), count, in_total, chunk_bytes, b));
+  HZ_TRY(alloc_chunks(scratch, descs.size(), count, in_total, b));
   // Pageable sources: the runtime copies them before these calls return.
   HZ_TRY(hipMemcpyAsync(b.descs, descs.data(), descs.size() * sizeof(ChunkDesc),
                         hipMemcpyHostToDevice, stream));

@@ -105,9 +105,7 @@ struct BlockTables {
 constexpr u32 kStageBytes = 16384;                 // LDS bitstream window per wave
 constexpr u32 kStageMargin = 64;                   // bytes staged past the last slice
 constexpr u32 kStageWords = (kStageBytes + kStageMargin) / 4 + 4;
-constexpr u64 kMinSlice = 64;                      // bits; > longest token (48 bits)
 constexpr u64 kMaxSlice = (u64(kStageBytes) * 8) / 64;
-constexpr u32 kWindowSlots = 32;                   // token starts recorded per slice window
 constexpr u32 kHeaderBytes = 640;  // > longest dynamic header (< 566 bytes)
 constexpr u32 kHeaderWords = kHeaderBytes / 4 + 4;
 

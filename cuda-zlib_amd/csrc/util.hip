@@ -45,7 +45,7 @@ std::string profile_collect(bool reset) {
   std::vector<unsigned long long> counts;
   for (const ProfileEntry& e : r.entries) {
     float ms = 0.f;
-    if (hipEventSynchronize(e.stop) == hipSuccess) hipEventElapsedTime(&ms, e.start, e.stop);
+    if (hipEventSynchronize(e.stop) == hipSuccess) (void)hipEventElapsedTime(&ms, e.start, e.stop);
     size_t i = 0;
     while (i < names.size() && names[i] != e.name) ++i;
     if (i == names.size()) {
@@ -58,8 +58,8 @@ std::string profile_collect(bool reset) {
   }
   if (reset) {
     for (const ProfileEntry& e : r.entries) {
-      hipEventDestroy(e.start);
-      hipEventDestroy(e.stop);
+      (void)hipEventDestroy(e.start);
+      (void)hipEventDestroy(e.stop);
     }
     r.entries.clear();
   }
