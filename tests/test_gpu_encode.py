@@ -55,7 +55,9 @@ def test_round_trip_sizes(gpu, n):
         assert int.from_bytes(stream[-4:], "big") == zlib.adler32(data), kind
 
 
-@pytest.mark.parametrize("chunk", [256, 1000, 4096, 32768, 65535])
+# 35000-byte chunks still parse two workgroups per CU (with less than 9 KiB
+# of history), 36864-byte chunks take a whole CU.
+@pytest.mark.parametrize("chunk", [256, 1000, 4096, 32768, 35000, 36864, 65535])
 def test_round_trip_chunk_sizes(gpu, chunk):
     for kind, data in _kinds(300_001, chunk):
         stream = _compress(data, chunk)
