@@ -2417,18 +2417,37 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
       cur = seg_next[cur];
     }
   }
-  psize[t] = s;
-  pblocks[t] = b;
-  pcount[t] = k;
-  __syncthreads();
-  for (u32 off = 1; off < 1024; off <<= 1) {
-    const u64 xs = t >= off ? psize[t - off] : 0ull;
-    const u64 xb = t >= off ? pblocks[t - off] : 0ull;
-    const u64 xk = t >= off ? pcount[t - off] : 0ull;
+  // Inclusive prefix sums over the 1024 ranges: wave scans by shuffles, then
+  // the earlier waves' totals (one barrier in between).
+  {
+    const u32 lane = t & 63, wave = t >> 6;
+    u64 xs = s, xb = b, xk = k;
+#pragma unroll
+    for (u32 off = 1; off < 64; off <<= 1) {
+      const u64 ys = __shfl_up(xs, off, 64), yb = __shfl_up(xb, off, 64),
+                yk = __shfl_up(xk, off, 64);
+      if (lane >= off) {
+        xs += ys;
+        xb += yb;
+        xk += yk;
+      }
+    }
+    if (lane == 63) {
+      psize[wave] = xs;
+      pblocks[wave] = xb;
+      pcount[wave] = xk;
+    }
     __syncthreads();
-    psize[t] += xs;
-    pblocks[t] += xb;
-    pcount[t] += xk;
+    u64 ws = 0, wb = 0, wk = 0;
+    for (u32 w = 0; w < wave; ++w) {
+      ws += psize[w];
+      wb += pblocks[w];
+      wk += pcount[w];
+    }
+    __syncthreads();
+    psize[t] = ws + xs;
+    pblocks[t] = wb + xb;
+    pcount[t] = wk + xk;
     __syncthreads();
   }
   if (!t) {
