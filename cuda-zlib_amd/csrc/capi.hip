@@ -526,6 +526,12 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
         large.push_back(u32(f));
         large_bits += layout[f].in_size * 8;
       }
+    // Largest files first: a file's workgroup decodes its blocks one after
+    // another, so the longest decodes start while the grid fills and the
+    // short ones fill in behind them.  The order only schedules work.
+    std::stable_sort(large.begin(), large.end(), [&](u32 a, u32 b) {
+      return layout[a].out_size > layout[b].out_size;
+    });
     err = launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
                                metadata, encoded, kBatchWideBytes);
     if (err != hipSuccess || large.empty()) return err;

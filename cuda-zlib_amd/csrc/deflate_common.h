@@ -1071,4 +1071,177 @@ __device__ __forceinline__ u64 lanemask_lt() {
   return lane ? (~0ull >> (64 - lane)) : 0ull;
 }
 
+// Status of a wave header walk that would read past its words.
+constexpr u32 kHeaderWalkStuck = 0xffffffffu;
+
+// Position of code-length symbol s in the header's order of lengths (the
+// inverse of cl_order), 5 bits per symbol.
+__device__ __forceinline__ u32 cl_index(u32 s) {
+  return s < 12 ? u32((0x520c429d2b6be23ull >> (5 * s)) & 31)
+                : u32((0x820941ccull >> (5 * (s - 12))) & 31);
+}
+
+// 32 bits from bit q of a dword array (words q/32 and q/32 + 1).
+__device__ __forceinline__ u32 stage_bits(const u32* words, u32 q) {
+  return __builtin_amdgcn_alignbit(words[(q >> 5) + 1], words[q >> 5], q & 31);
+}
+
+// Fields and code-length code of a dynamic header, by the whole wave, from
+// `count` dwords in which body bit b is bit b - bit0 (mod 2^64); `start` is
+// the body bit after BTYPE.  Returns false when a read could pass the
+// given words or the body end (the caller then runs parse_dynamic_lengths
+// from the same start, so statuses and their order are that function's);
+// otherwise sets err (kBadTree: HLIT above 29 or an incomplete code-length
+// code, as build_cl_table rules) and `after` (the bit after the fields read),
+// and with err == 0 the code-length table's
+// primary LUT is built and p (first length's bit in the words) / lim (read
+// limit there) / nl / nd describe the walk over the lengths.  Lane s < 19 holds symbol s: its length, its rank among the
+// symbols of that length (ballots) and so its canonical code, whose LUT
+// entries it fills.
+__device__ inline bool header_prelude_wave(const u32* words, u64 bit0, u32 count,
+                                           DecodeTables& tables, u64 len, u64 start, u32& nl,
+                                           u32& nd, u32& err, u64& after, u32& p, u32& lim32) {
+  const u32 lane = lane_id();
+  // A read of bit q touches words q/32 and q/32 + 1.
+  const u64 staged = count > 1 ? u64(count - 1) * 32 : 0;
+  const u64 body_end = len * 8 - bit0;
+  const u64 lim = min(staged, body_end);
+  const u64 q0 = start - bit0;
+  if (q0 + 14 > lim) return false;
+  const u32 f = stage_bits(words, u32(q0));
+  const u32 hlit = f & 31u, hdist = (f >> 5) & 31u, hclen = (f >> 10) & 15u;
+  nl = hlit + 257;
+  nd = hdist + 1;
+  const u32 nc = hclen + 4;
+  after = start + 14;
+  if (nl > 286) {
+    err = kBadTree;
+    return true;
+  }
+  if (q0 + 14 + 3 * nc > lim) return false;
+  after += 3 * nc;
+  u32 l = 0;
+  if (lane < 19) {
+    const u32 k = cl_index(lane);
+    if (k < nc) l = stage_bits(words, u32(q0 + 14 + 3 * k)) & 7u;
+  }
+  // Kraft sum and the first canonical code of each length.
+  u32 kraft = 0, code = 0, mine = 0, count_prev = 0;
+#pragma unroll
+  for (u32 k = 1; k < 8; ++k) {
+    const u64 b = __ballot(l == k);
+    const u32 c = u32(__popcll(b));
+    code = (code + count_prev) << 1;  // first code of length k
+    if (l == k) mine = code + u32(__popcll(b & lanemask_lt()));
+    count_prev = c;
+    kraft += c << (7 - k);
+  }
+  if (kraft != 128) {  // the code must be complete
+    err = kBadTree;
+    return true;
+  }
+  if (l) {
+    const u32 e = (lane << 16) | l;
+    for (u32 k = bit_reverse(mine, l); k < 128; k += 1u << l) tables.cl.primary[k] = e;
+  }
+  p = u32(q0 + 14 + 3 * nc);
+  lim32 = u32(lim);
+  err = kOk;
+  wave_sync();
+  return true;
+}
+
+// The code lengths of a dynamic header by the whole wave, after
+// header_prelude_wave.  The code-length code is complete, so every 7-bit
+// pattern starts a code: each lane decodes the symbol (and extra bits) at its
+// own bit of a 64-bit batch.  The true path through the batch (its offsets,
+// from 0, one hop per symbol) is the only serial part; the path lanes then
+// place their runs together: the lengths before each (a prefix sum of the
+// repeat counts), the value a 16 repeats (the last other symbol before it, a
+// max scan), and the first path symbol that ends the walk (unreadable within
+// the limit, a 16 first, a repeat past the end, or the last length).
+// Lanes then fill the lengths from the runs (`runs`: LDS, >= 320 entries).
+// Returns kOk, an error status (the one parse_dynamic_lengths gives: every
+// read on the path lies before the limit), or kHeaderWalkStuck when the walk
+// would read past it.  `p` advances to the bit after the lengths.
+__device__ inline u32 header_lengths_wave(const u32* words, DecodeTables& tables, u32* runs, u32 total,
+                                   u32& p, u32 lim) {
+  const u32 lane = lane_id();
+  u32 i = 0, prev = 0, nruns = 0;
+  while (i < total) {
+    // This lane's symbol at bit p + lane: its advance (0: past the limit),
+    // symbol and repeat count.
+    const u32 q = p + lane;
+    u32 adv = 0, sym = 0, rep = 1;
+    if (q + 14 <= lim) {
+      const u32 b = stage_bits(words, q);
+      const u32 e = tables.cl.primary[b & 127];
+      const u32 l = e & 15u;
+      sym = e >> 16;
+      const u32 x = b >> l;
+      adv = sym < 16 ? l : sym == 16 ? l + 2 : sym == 17 ? l + 3 : l + 7;
+      rep = sym < 16 ? 1u : sym == 16 ? 3 + (x & 3u) : sym == 17 ? 3 + (x & 7u) : 11 + (x & 127u);
+      if (!l) adv = 0;
+    }
+    // The path's offsets (uniform hops).
+    u64 path = 0;
+    u32 off = 0;
+    while (off < 64) {
+      const u32 a = u32(__builtin_amdgcn_readlane(int(adv), int(off)));
+      path |= 1ull << off;
+      if (!a) break;
+      off += a;
+    }
+    const bool on = (path >> lane) & 1;
+    // Lengths before each path symbol.
+    const u32 r_on = on ? rep : 0u;
+    u32 incl = r_on;
+#pragma unroll
+    for (u32 o = 1; o < 64; o <<= 1) {
+      const u32 y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    const u32 before = i + incl - r_on;
+    // The first path symbol that ends the walk, and how.
+    const bool stuck = !adv;
+    const bool bad = (sym == 16 && before == 0) || before + rep > total;
+    const u64 term = __ballot(on && (stuck || bad || before + rep == total));
+    const u32 end = term ? u32(__builtin_ctzll(term)) : 64u;
+    if (end < 64) {
+      if (__builtin_amdgcn_readlane(int(stuck), int(end))) return kHeaderWalkStuck;
+      if (__builtin_amdgcn_readlane(int(bad), int(end))) return kBadRepeat;
+    }
+    const u64 valid = end < 64 ? path & ((2ull << end) - 1) : path;
+    // The value a 16 repeats: that of the last other path symbol before it
+    // (17 and 18 give 0), or the value carried from the earlier batches.
+    int last = (valid >> lane) & 1 && sym != 16 ? int(lane) : -1;
+#pragma unroll
+    for (u32 o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(last, o, 64);
+      if (lane >= o && y > last) last = y;
+    }
+    const u32 src_sym = u32(__shfl(int(sym), last < 0 ? 0 : last, 64));
+    const u32 base = last < 0 ? prev : src_sym < 16 ? src_sym : 0u;
+    const u32 value = sym < 16 ? sym : sym == 16 ? base : 0u;
+    if ((valid >> lane) & 1)
+      runs[nruns + __popcll(valid & lanemask_lt())] = before | (value << 9) | (rep << 13);
+    nruns += u32(__popcll(valid));
+    const u32 tail = 63 - u32(__builtin_clzll(valid));
+    i = u32(__builtin_amdgcn_readlane(int(before + rep), int(tail)));
+    prev = u32(__builtin_amdgcn_readlane(int(value), int(tail)));
+    p += end < 64 ? end + u32(__builtin_amdgcn_readlane(int(adv), int(end))) : off;
+  }
+  wave_sync();
+  u32 status = kOk;
+  for (u32 k = lane; k < nruns; k += 64) {
+    const u32 e = runs[k];
+    const u32 first = e & 511u, value = (e >> 9) & 15u, r = e >> 13;
+    for (u32 j = 0; j < r; ++j) tables.lens[first + j] = u8(value);
+  }
+  wave_sync();
+  if (!tables.lens[256]) status = kBadTree;
+  wave_sync();
+  return status;
+}
+
 }  // namespace hz

@@ -1270,6 +1270,7 @@ struct DescShared {
     // Phases 1-3: bytes lane j produced by the tokens starting in visit words
     // 0..w (read for w <= 6: at most 32 * 7 tokens of <= 258 bytes, 16 bits).
     u16 ck[kVisitWords][kDescThreads];
+    u32 hruns[320];  // block_header: code-length runs of the wave walk
     struct {
       u32 before[kDescThreads];   // bytes lane j produced before its merge point
       u32 prefix[kDescThreads];   // inclusive prefix of per-slice bytes
@@ -1435,11 +1436,14 @@ __device__ __forceinline__ u32 prev_bit(const u64* mask, u32 at) {
   }
 }
 
-// Reads a block header at sh.pos from the stage (lane 0): stored fields, or
-// dynamic code lengths; then the wave builds fixed/dynamic tables.  Sets
+// Reads a block header at sh.pos from the stage: lane 0 the block type and a
+// stored block's fields, wave 0 a dynamic block's code lengths (the wave walk,
+// or lane 0's serial parse where the walk cannot finish within the stage or
+// without kWalk, which leaves sh.hruns out of the shared layout); then wave 0
+// builds the fixed/dynamic tables.  Sets
 // sh.type, sh.final_block, sh.status, sh.d0 (first token or payload bit) and,
 // for stored blocks, sh.end/sh.size.
-template <bool kOneWave = false, bool kFast = false, typename Shared>
+template <bool kOneWave = false, bool kFast = false, bool kWalk = true, typename Shared>
 __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
   const u32 lane = threadIdx.x;
   if (!staged_covers(sh.stage, body, len, sh.pos, sh.pos + 4096)) {
@@ -1465,25 +1469,59 @@ __device__ void block_header(const u8* body, u64 len, u64 limit, Shared& sh) {
         sh.size = nlen;
       }
     } else if (type == 1) {
-      for (u32 i = 0; i < 320; ++i) sh.tables.lens[i] = i < 144 ? 8 : i < 256 ? 9 : i < 280 ? 7 : i < 288 ? 8 : 5;
       sh.nl = 288;
       sh.nd = 32;
-    } else {
-      u32 nl = 0, nd = 0;
-      err = parse_dynamic_lengths(sh.tables, r, nl, nd);
-      sh.nl = nl;
-      sh.nd = nd;
     }
-    sh.d0 = r.pos;
+    sh.d0 = r.pos;  // a dynamic block: the bit after BTYPE
     sh.type = type;
     sh.final_block = fin;
     sh.status = err;
   }
   __syncthreads();
+  if (sh.type == 2 && !sh.status) {
+    const u64 start = sh.d0;
+    if constexpr (kWalk) {
+      if (lane < 64) {
+        u32 nl = 0, nd = 0, err = kOk, p = 0, lim = 0;
+        u64 after = start;
+        if (!header_prelude_wave(sh.stage.words, sh.stage.bit0, sh.stage.count, sh.tables, len,
+                                 start, nl, nd, err, after, p, lim)) {
+          err = kHeaderWalkStuck;
+        } else if (!err) {
+          err = header_lengths_wave(sh.stage.words, sh.tables, sh.hruns, nl + nd, p, lim);
+          after = sh.stage.bit0 + p;
+        }
+        if (!lane) {
+          sh.status = err;
+          sh.nl = nl;
+          sh.nd = nd;
+          sh.d0 = after;
+        }
+      }
+    } else {
+      if (!lane) sh.status = kHeaderWalkStuck;
+    }
+    __syncthreads();
+    if (!lane && sh.status == kHeaderWalkStuck) {
+      BitIn r = staged_reader(sh.stage, len, start);
+      u32 nl = 0, nd = 0;
+      sh.status = parse_dynamic_lengths(sh.tables, r, nl, nd);
+      sh.nl = nl;
+      sh.nd = nd;
+      sh.d0 = r.pos;
+    }
+    __syncthreads();
+  }
   if (sh.type && !sh.status) {
     // The tables are built by one wave (wave 0 of a larger workgroup).
     if (!kOneWave || lane < 64) {
       const bool fixed = sh.type == 1;
+      if (fixed) {
+        for (u32 i = lane; i < 320; i += 64)
+          sh.tables.lens[i] = i < 144 ? 8 : i < 256 ? 9 : i < 280 ? 7 : i < 288 ? 8 : 5;
+        if (kOneWave) wave_sync();
+        else __syncthreads();
+      }
       u32 err = huff_build_wave<288, 10, kOneWave>(sh.tables.ll, sh.tables.lens, sh.nl, false,
                                                    true, 15, sh.codes, &sh.build_status);
       if (!err)
@@ -1867,177 +1905,9 @@ struct HeaderShared {
   u32 runs[320];  // code-length runs of the wave walk: first index | value << 9 | repeat << 13
   u64 d0;
   u32 status, type, fin, nl, nd, build_status;
-  u32 walk, p, lim, nruns;  // wave walk: start (stage bit), read limit, runs found
+  u32 walk;  // the wave walk runs
 };
 
-// Position of code-length symbol s in the header's order of lengths (the
-// inverse of cl_order), 5 bits per symbol.
-__device__ __forceinline__ u32 cl_index(u32 s) {
-  return s < 12 ? u32((0x520c429d2b6be23ull >> (5 * s)) & 31)
-                : u32((0x820941ccull >> (5 * (s - 12))) & 31);
-}
-
-// 32 stage bits from stage-relative bit q (words q/32 and q/32 + 1).
-__device__ __forceinline__ u32 stage_bits(const u32* words, u32 q) {
-  return __builtin_amdgcn_alignbit(words[(q >> 5) + 1], words[q >> 5], q & 31);
-}
-
-// Fields and code-length code of a dynamic header, by the whole wave; `start`
-// is the body bit after BTYPE.  Returns false when a read could pass the
-// staged words or the body end (the caller then runs parse_dynamic_lengths
-// from the same start, so statuses and their order are that function's);
-// otherwise sets err (kBadTree: HLIT above 29 or an incomplete code-length
-// code, as build_cl_table rules) and `after` (the bit after the fields read),
-// and with err == 0 the code-length table's
-// primary LUT is built and sh.p / sh.lim / nl / nd describe the walk over the
-// lengths.  Lane s < 19 holds symbol s: its length, its rank among the
-// symbols of that length (ballots) and so its canonical code, whose LUT
-// entries it fills.
-__device__ bool header_prelude_wave(HeaderShared& sh, u64 len, u64 start, u32& nl, u32& nd,
-                                    u32& err, u64& after) {
-  const u32 lane = lane_id();
-  const u64 bit0 = sh.stage.bit0;
-  // A read of bit q touches words q/32 and q/32 + 1.
-  const u64 staged = sh.stage.count > 1 ? u64(sh.stage.count - 1) * 32 : 0;
-  const u64 body_end = len * 8 - bit0;
-  const u64 lim = min(staged, body_end);
-  const u64 q0 = start - bit0;
-  if (q0 + 14 > lim) return false;
-  const u32 f = stage_bits(sh.stage.words, u32(q0));
-  const u32 hlit = f & 31u, hdist = (f >> 5) & 31u, hclen = (f >> 10) & 15u;
-  nl = hlit + 257;
-  nd = hdist + 1;
-  const u32 nc = hclen + 4;
-  after = start + 14;
-  if (nl > 286) {
-    err = kBadTree;
-    return true;
-  }
-  if (q0 + 14 + 3 * nc > lim) return false;
-  after += 3 * nc;
-  u32 l = 0;
-  if (lane < 19) {
-    const u32 k = cl_index(lane);
-    if (k < nc) l = stage_bits(sh.stage.words, u32(q0 + 14 + 3 * k)) & 7u;
-  }
-  // Kraft sum and the first canonical code of each length.
-  u32 kraft = 0, code = 0, mine = 0, count_prev = 0;
-#pragma unroll
-  for (u32 k = 1; k < 8; ++k) {
-    const u64 b = __ballot(l == k);
-    const u32 c = u32(__popcll(b));
-    code = (code + count_prev) << 1;  // first code of length k
-    if (l == k) mine = code + u32(__popcll(b & lanemask_lt()));
-    count_prev = c;
-    kraft += c << (7 - k);
-  }
-  if (kraft != 128) {  // the code must be complete
-    err = kBadTree;
-    return true;
-  }
-  if (l) {
-    const u32 e = (lane << 16) | l;
-    for (u32 k = bit_reverse(mine, l); k < 128; k += 1u << l) sh.tables.cl.primary[k] = e;
-  }
-  sh.p = u32(q0 + 14 + 3 * nc);
-  sh.lim = u32(lim);
-  err = kOk;
-  wave_sync();
-  return true;
-}
-
-// The code lengths of a dynamic header by the whole wave, after
-// header_prelude_wave.  The code-length code is complete, so every 7-bit
-// pattern starts a code: each lane decodes the symbol (and extra bits) at its
-// own bit of a 64-bit batch.  The true path through the batch (its offsets,
-// from 0, one hop per symbol) is the only serial part; the path lanes then
-// place their runs together: the lengths before each (a prefix sum of the
-// repeat counts), the value a 16 repeats (the last other symbol before it, a
-// max scan), and the first path symbol that ends the walk (unreadable within
-// the limit, a 16 first, a repeat past the end, or the last length).
-// Lanes then fill the lengths from the runs.  Returns kOk, an error status
-// (the one parse_dynamic_lengths gives: every read on the path lies before the
-// limit), or kNone when the walk would read past it.
-__device__ u32 header_lengths_wave(HeaderShared& sh, u32 total) {
-  const u32 lane = lane_id();
-  const u32 lim = sh.lim;
-  u32 p = sh.p, i = 0, prev = 0, nruns = 0;
-  while (i < total) {
-    // This lane's symbol at bit p + lane: its advance (0: past the limit),
-    // symbol and repeat count.
-    const u32 q = p + lane;
-    u32 adv = 0, sym = 0, rep = 1;
-    if (q + 14 <= lim) {
-      const u32 b = stage_bits(sh.stage.words, q);
-      const u32 e = sh.tables.cl.primary[b & 127];
-      const u32 l = e & 15u;
-      sym = e >> 16;
-      const u32 x = b >> l;
-      adv = sym < 16 ? l : sym == 16 ? l + 2 : sym == 17 ? l + 3 : l + 7;
-      rep = sym < 16 ? 1u : sym == 16 ? 3 + (x & 3u) : sym == 17 ? 3 + (x & 7u) : 11 + (x & 127u);
-      if (!l) adv = 0;
-    }
-    // The path's offsets (uniform hops).
-    u64 path = 0;
-    u32 off = 0;
-    while (off < 64) {
-      const u32 a = u32(__builtin_amdgcn_readlane(int(adv), int(off)));
-      path |= 1ull << off;
-      if (!a) break;
-      off += a;
-    }
-    const bool on = (path >> lane) & 1;
-    // Lengths before each path symbol.
-    const u32 r_on = on ? rep : 0u;
-    u32 incl = r_on;
-#pragma unroll
-    for (u32 o = 1; o < 64; o <<= 1) {
-      const u32 y = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += y;
-    }
-    const u32 before = i + incl - r_on;
-    // The first path symbol that ends the walk, and how.
-    const bool stuck = !adv;
-    const bool bad = (sym == 16 && before == 0) || before + rep > total;
-    const u64 term = __ballot(on && (stuck || bad || before + rep == total));
-    const u32 end = term ? u32(__builtin_ctzll(term)) : 64u;
-    if (end < 64) {
-      if (__builtin_amdgcn_readlane(int(stuck), int(end))) return kNone;
-      if (__builtin_amdgcn_readlane(int(bad), int(end))) return kBadRepeat;
-    }
-    const u64 valid = end < 64 ? path & ((2ull << end) - 1) : path;
-    // The value a 16 repeats: that of the last other path symbol before it
-    // (17 and 18 give 0), or the value carried from the earlier batches.
-    int last = (valid >> lane) & 1 && sym != 16 ? int(lane) : -1;
-#pragma unroll
-    for (u32 o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(last, o, 64);
-      if (lane >= o && y > last) last = y;
-    }
-    const u32 src_sym = u32(__shfl(int(sym), last < 0 ? 0 : last, 64));
-    const u32 base = last < 0 ? prev : src_sym < 16 ? src_sym : 0u;
-    const u32 value = sym < 16 ? sym : sym == 16 ? base : 0u;
-    if ((valid >> lane) & 1)
-      sh.runs[nruns + __popcll(valid & lanemask_lt())] = before | (value << 9) | (rep << 13);
-    nruns += u32(__popcll(valid));
-    const u32 tail = 63 - u32(__builtin_clzll(valid));
-    i = u32(__builtin_amdgcn_readlane(int(before + rep), int(tail)));
-    prev = u32(__builtin_amdgcn_readlane(int(value), int(tail)));
-    p += end < 64 ? end + u32(__builtin_amdgcn_readlane(int(adv), int(end))) : off;
-  }
-  wave_sync();
-  u32 status = kOk;
-  for (u32 k = lane; k < nruns; k += 64) {
-    const u32 e = sh.runs[k];
-    const u32 first = e & 511u, value = (e >> 9) & 15u, r = e >> 13;
-    for (u32 j = 0; j < r; ++j) sh.tables.lens[first + j] = u8(value);
-  }
-  wave_sync();
-  if (!sh.tables.lens[256]) status = kBadTree;
-  if (!lane) sh.p = p;
-  wave_sync();
-  return status;
-}
 }  // namespace
 
 // One wave per candidate (below the table capacity): parse its dynamic
@@ -2073,12 +1943,14 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
       sh.walk = 0;
     }
     __syncthreads();
+    u32 p = 0, lim = 0;  // the wave walk's start and read limit (stage bits)
     if (!sh.status && sh.type == 2) {
       u32 nl = 0, nd = 0, err = kOk;
       u64 after = start;
-      const bool staged = header_prelude_wave(sh, len, start, nl, nd, err, after);
+      const bool staged = header_prelude_wave(sh.stage.words, sh.stage.bit0, sh.stage.count,
+                                              sh.tables, len, start, nl, nd, err, after, p, lim);
       if (!lane) {
-        sh.status = staged ? err : kNone;
+        sh.status = staged ? err : kHeaderWalkStuck;
         sh.walk = staged && !err;
         sh.nl = nl;
         sh.nd = nd;
@@ -2087,14 +1959,15 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
     }
     __syncthreads();
     if (sh.walk) {
-      const u32 st_walk = header_lengths_wave(sh, sh.nl + sh.nd);
+      const u32 st_walk =
+          header_lengths_wave(sh.stage.words, sh.tables, sh.runs, sh.nl + sh.nd, p, lim);
       if (!lane) {
         sh.status = st_walk;
-        sh.d0 = sh.stage.bit0 + sh.p;
+        sh.d0 = sh.stage.bit0 + p;
       }
     }
     __syncthreads();
-    if (!lane && sh.status == kNone) {
+    if (!lane && sh.status == kHeaderWalkStuck) {
       BitIn r = staged_reader(sh.stage, len, start);
       u32 nl = 0, nd = 0;
       sh.status = parse_dynamic_lengths(sh.tables, r, nl, nd);
@@ -3088,7 +2961,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
                    &sums, out_end - block_out);
       } else {
         if (rec.table == kNone) {
-          block_header<true, true>(body, len, ~0ull, sh);
+          block_header<true, true, false>(body, len, ~0ull, sh);
           if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
         }
         bool tables_pending = rec.table != kNone;

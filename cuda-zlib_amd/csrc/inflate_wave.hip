@@ -18,7 +18,13 @@ constexpr u32 kCoopMatch = 32;  // matches at least this long are copied by the 
 
 struct WaveShared {
   DecodeTables tables;
-  u32 action;  // 0 done, 1 match copy, 2 stored copy
+  union {
+    u16 codes[320];  // table build scratch
+    u32 runs[320];   // code-length runs of the header walk
+  };
+  u64 hdr_start;  // a dynamic header: the body bit after BTYPE
+  u32 nl, nd, fixed, build_status;
+  u32 action;  // 0 done, 1 match copy, 2 stored copy, 3 table build
   u32 error;
   u64 begin, length, distance, src;
   Frame frame;
@@ -119,6 +125,7 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
   bool need_header = true, complete = false;
   BitIn r;
   if (!lane) {
+    sh.action = 0;
     sh.error = parse_frame(in, in_size, fmt.format, fmt.dict_len > 0, sh.frame);
     // Only a zlib stream that asks for a dictionary (FDICT) uses one.
     if (fmt.format == kFormatZlib && !sh.frame.needs_dict) sh.frame.dict_id = 0;
@@ -146,6 +153,7 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
   while (true) {
     if (!lane) {
       u32 action = 0;
+      if (sh.action == 3) error = sh.build_status;
       while (!error && !complete) {
         if (need_header) {
           if (blocks >= max_blocks) { error = kBlockCapacity; break; }
@@ -169,9 +177,15 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
             action = 2;
             break;
           }
-          error = type == 1 ? build_fixed_tables(sh.tables) : build_dynamic_tables(sh.tables, r);
+          // The wave reads a dynamic header's code lengths and builds the
+          // tables (action 3); lane 0 resumes after the header.
           need_header = false;
-          if (error) break;
+          sh.nl = 288;
+          sh.nd = 32;
+          sh.hdr_start = r.pos;
+          sh.fixed = type == 1;
+          action = 3;
+          break;
         }
         u32 lit = 0, length = 0, distance = 0;
         error = decode_token(sh.tables, r, window, lit, length, distance);
@@ -221,9 +235,67 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
     __syncthreads();
     const u32 action = sh.action;
     if (!action) break;
-    if (action == 1) wave_match(out, sh.begin, sh.distance, sh.length, lane);
-    else
+    if (action == 1) {
+      wave_match(out, sh.begin, sh.distance, sh.length, lane);
+    } else if (action == 2) {
       for (u64 j = lane; j < sh.length; j += kWave) out[sh.begin + j] = in[sh.src + j];
+    } else {
+      // Same tables and statuses as build_fixed_tables / build_dynamic_tables.
+      const bool fixed = sh.fixed;
+      u32 err = kOk;
+      if (fixed) {
+        for (u32 i = lane; i < 320; i += kWave)
+          sh.tables.lens[i] = i < 144 ? 8 : i < 256 ? 9 : i < 280 ? 7 : i < 288 ? 8 : 5;
+      } else {
+        // The lengths by the wave walk over the body's dwords from the one
+        // holding the header (at most 256 of them, so positions stay small),
+        // or by lane 0's serial parse where the walk cannot finish there.
+        const u64 start = sh.hdr_start, len = sh.frame.body_len;
+        const uintptr_t addr = reinterpret_cast<uintptr_t>(in + sh.frame.body);
+        const u64 lead = u64(addr & 3u) * 8;  // body bit b is bit b + lead of the dwords
+        const u64 all = (u64(addr & 3u) + len + 3) >> 2;
+        const u64 first = (start + lead) >> 5;
+        const u32* words = reinterpret_cast<const u32*>(addr & ~uintptr_t(3)) + first;
+        const u64 bit0 = first * 32 - lead;
+        const u32 count = u32(min(all - first, u64(256)));
+        u32 nl = 0, nd = 0, p = 0, lim = 0;
+        u64 after = start;
+        if (!header_prelude_wave(words, bit0, count, sh.tables, len, start, nl, nd, err, after, p,
+                                 lim)) {
+          err = kHeaderWalkStuck;
+        } else if (!err) {
+          err = header_lengths_wave(words, sh.tables, sh.runs, nl + nd, p, lim);
+          after = bit0 + p;
+        }
+        if (err == kHeaderWalkStuck) {  // uniform
+          if (!lane) {
+            r.seek(start);
+            err = parse_dynamic_lengths(sh.tables, r, nl, nd);
+            sh.nl = nl;
+            sh.nd = nd;
+            sh.build_status = err;
+            after = r.pos;
+          }
+          __syncthreads();
+          err = sh.build_status;
+          nl = sh.nl;
+          nd = sh.nd;
+        }
+        if (!lane) {
+          r.seek(after);
+          sh.nl = nl;
+          sh.nd = nd;
+        }
+      }
+      __syncthreads();
+      if (!err)
+        err = huff_build_wave(sh.tables.ll, sh.tables.lens, sh.nl, false, true, 15, sh.codes,
+                              &sh.build_status);
+      if (!err)
+        err = huff_build_wave(sh.tables.dd, sh.tables.lens + sh.nl, sh.nd, !fixed, true, 15,
+                              sh.codes, &sh.build_status);
+      if (!lane) sh.build_status = err;
+    }
     __syncthreads();
   }
 
@@ -242,6 +314,54 @@ __device__ void inflate_one_wave(const u8* in, u64 in_size, u8* out, u64 out_siz
   }
 }
 
+// Copies n bytes with the wave: dwords when both ends are dword-aligned,
+// bytes otherwise.
+__device__ __forceinline__ void wave_copy(u8* dst, const u8* src, u64 n, u32 lane) {
+  u64 i = lane;
+  if (!((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 3u)) {
+    const u64 words = n >> 2;
+    for (; i < words; i += kWave)
+      reinterpret_cast<u32*>(dst)[i] = reinterpret_cast<const u32*>(src)[i];
+    i = (words << 2) + lane;
+  }
+  for (; i < n; i += kWave) dst[i] = src[i];
+}
+
+// inflate_one_wave with the output, and the stream when it fits too, copied
+// into `stage` (LDS, 16-byte aligned, `capacity` bytes).  Lane 0's walk then
+// waits on LDS rather than on global memory for each dword of the bit stream
+// and for each source byte of a short match.  `out` receives the same bytes
+// as an unstaged decode: the staged output starts zeroed and is copied whole.
+__device__ void inflate_staged(const u8* in, u64 in_size, u8* out, u64 out_size, u32 max_blocks,
+                               u32* meta, WaveShared& sh, u8* stage, u64 capacity,
+                               const WaveFormat fmt = WaveFormat()) {
+  const u32 lane = threadIdx.x;
+  const u64 out_room = (out_size + 15) & ~u64(15), in_room = (in_size + 15) & ~u64(15);
+  // Invalid limits leave `out` untouched, so they stay on the direct path.
+  const bool staged = max_blocks && max_blocks <= kMaxBlocks && in_size <= kMaxBytes &&
+                      out_room <= capacity;
+  const u8* src = in;
+  if (staged && out_room + in_room <= capacity) {
+    u8* copy = stage + out_room;
+    wave_copy(copy, in, in_size, lane);
+    // The dword reads of the bit reader see zeros, not stale bytes, past the end.
+    if (lane < in_room - in_size) copy[in_size + lane] = 0;
+    src = copy;
+  }
+  __syncthreads();
+  inflate_one_wave(src, in_size, staged ? stage : out, out_size, max_blocks, meta, sh, fmt);
+  if (staged) {
+    __syncthreads();
+    wave_copy(out, stage, out_size, lane);
+  }
+}
+
+// LDS staging capacities: the one-stream kernel (one workgroup, streams of at
+// most 64 KiB of output on the small route) and the batch kernel (many
+// resident workgroups; files under 256 B of output).
+constexpr u64 kSingleStage = 128 * 1024;
+constexpr u64 kBatchStage = 2048;
+
 }  // namespace
 
 __global__ __launch_bounds__(64) void inflate_single_kernel(const u8* in, u64 in_size, u8* out,
@@ -249,11 +369,12 @@ __global__ __launch_bounds__(64) void inflate_single_kernel(const u8* in, u64 in
                                                             u32* meta, u32 format, const u8* dict,
                                                             u64 dict_len) {
   __shared__ WaveShared sh;
+  __shared__ __align__(16) u8 stage[kSingleStage];
   WaveFormat fmt;
   fmt.format = format;
   fmt.dict = dict;
   fmt.dict_len = dict_len;
-  inflate_one_wave(in, in_size, out, out_size, max_blocks, meta, sh, fmt);
+  inflate_staged(in, in_size, out, out_size, max_blocks, meta, sh, stage, kSingleStage, fmt);
 }
 
 // One workgroup per file.  With encoded metadata (compression's
@@ -268,6 +389,7 @@ __global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out
                                                            const u32* encoded, u64 skip_from,
                                                            const u32* list, const u32* redo) {
   __shared__ WaveShared sh;
+  __shared__ __align__(16) u8 stage[kBatchStage];
   for (u32 i = blockIdx.x; i < count; i += gridDim.x) {
     const u32 f = list ? list[i] : i;
     if (list ? !redo[f] : files[f].out_size >= skip_from) continue;  // uniform
@@ -290,8 +412,8 @@ __global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out
       }
       in_size = enc_len;
     }
-    inflate_one_wave(in + file.in_offset, in_size, out + file.out_offset, file.out_size, max_blocks,
-                     meta + 2 * u64(f), sh);
+    inflate_staged(in + file.in_offset, in_size, out + file.out_offset, file.out_size, max_blocks,
+                   meta + 2 * u64(f), sh, stage, kBatchStage);
     __syncthreads();
   }
 }
