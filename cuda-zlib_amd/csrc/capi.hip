@@ -40,6 +40,7 @@ struct Arena {
 struct PoolRegistry {
   std::mutex mutex;
   std::vector<PoolEntry> pools;
+  std::vector<std::pair<int, hipStream_t>> side_streams;
   std::vector<std::unique_ptr<Arena>> arenas;
   u64 retention = 1ull << 30;
 };
@@ -70,6 +71,55 @@ hipError_t get_pool(int device, hipMemPool_t* out) {
   *out = pool;
   return hipSuccess;
 }
+
+// A second stream of the device, for work that overlaps the caller's stream
+// inside one call (created on first use with the default priority and kept,
+// like the pools, for the process lifetime).
+hipError_t get_side_stream(int device, hipStream_t* out) {
+  PoolRegistry& reg = registry();
+  std::lock_guard<std::mutex> lock(reg.mutex);
+  for (const auto& e : reg.side_streams)
+    if (e.first == device) { *out = e.second; return hipSuccess; }
+  hipStream_t side = nullptr;
+  hipError_t err = hipStreamCreateWithFlags(&side, hipStreamNonBlocking);
+  if (err != hipSuccess) return err;
+  reg.side_streams.push_back({device, side});
+  *out = side;
+  return hipSuccess;
+}
+
+// Work forked from `main` onto `side`: side starts after what main holds at
+// fork(), and main continues past join() (or the destructor, on every path)
+// only once side's work is done.  Events belong to the one call.
+class SideWork {
+ public:
+  SideWork(hipStream_t main, hipStream_t side) : main_(main), side_(side) {}
+  hipError_t fork() {
+    hipError_t err = hipEventCreateWithFlags(&fork_, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&join_, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventRecord(fork_, main_);
+    if (err == hipSuccess) err = hipStreamWaitEvent(side_, fork_, 0);
+    forked_ = err == hipSuccess;
+    return err;
+  }
+  hipError_t join() {
+    if (!forked_) return hipSuccess;
+    forked_ = false;
+    hipError_t err = hipEventRecord(join_, side_);
+    if (err == hipSuccess) err = hipStreamWaitEvent(main_, join_, 0);
+    return err;
+  }
+  ~SideWork() {
+    (void)join();
+    if (fork_) (void)hipEventDestroy(fork_);
+    if (join_) (void)hipEventDestroy(join_);
+  }
+
+ private:
+  hipStream_t main_, side_;
+  hipEvent_t fork_ = nullptr, join_ = nullptr;
+  bool forked_ = false;
+};
 
 bool find_pool(int device, hipMemPool_t* out) {
   PoolRegistry& reg = registry();
@@ -121,6 +171,7 @@ class Workspace final : public Scratch {
  public:
   Workspace(hipStream_t stream, hipMemPool_t pool, int device)
       : stream_(stream), pool_(pool), device_(device) {}
+  int device() const { return device_; }
   hipError_t alloc_bytes(void** p, u64 bytes) override {
     *p = nullptr;
     bytes = scratch_round(bytes);
@@ -532,9 +583,22 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
     std::stable_sort(large.begin(), large.end(), [&](u32 a, u32 b) {
       return layout[a].out_size > layout[b].out_size;
     });
-    err = launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
+    if (large.empty())
+      return launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
+                                  metadata, encoded, kBatchWideBytes);
+    // The small files decode on a second stream while the large ones take
+    // the parallel route here (they share no output bytes or metadata rows,
+    // and resolution writes single bytes of large files only); the caller's
+    // stream then waits for both.
+    hipStream_t side_stream = nullptr;
+    err = get_side_stream(ws.device(), &side_stream);
+    if (err != hipSuccess) return err;
+    SideWork side(stream, side_stream);
+    err = side.fork();
+    if (err != hipSuccess) return err;
+    err = launch_inflate_batch(side_stream, input, output, device_files, u32(files), kMaxBlocks,
                                metadata, encoded, kBatchWideBytes);
-    if (err != hipSuccess || large.empty()) return err;
+    if (err != hipSuccess) return err;
     u32 *device_large = nullptr, *redo = nullptr;
     err = ws.alloc(&device_large, large.size());
     if (err == hipSuccess) err = ws.alloc(&redo, files);
@@ -546,8 +610,10 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
                                  device_large, u32(large.size()), large_bits, encoded, kMaxBlocks,
                                  redo, metadata);
     if (err != hipSuccess) return err;
-    return launch_inflate_batch(stream, input, output, device_files, u32(large.size()), kMaxBlocks,
-                                metadata, encoded, ~0ull, device_large, redo);
+    err = launch_inflate_batch(stream, input, output, device_files, u32(large.size()), kMaxBlocks,
+                               metadata, encoded, ~0ull, device_large, redo);
+    if (err != hipSuccess) return err;
+    return side.join();
   });
 }
 

@@ -465,35 +465,44 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
     }
   }
   if (lane < 16) t.count[lane] = u16(cnt);
-  sync();
-  if (!lane) {
-    u32 st = kOk, maximum = 0;
-    if (n > u32(N)) st = kBadTree;
-    for (u32 l = limit + 1; l < 16 && !st; ++l)
-      if (t.count[l]) st = kBadTree;
-    for (u32 l = 1; l <= limit && l < 16; ++l)
-      if (t.count[l]) maximum = l;
-    t.maximum = maximum;
-    if (!st && !maximum && !empty_ok) st = kBadTree;
-    if (!st && maximum) {
-      i32 left = 1;
-      for (u32 l = 1; l <= limit && !st; ++l) {
-        left = (left << 1) - i32(t.count[l]);
-        if (left < 0) st = kBadTree;
-      }
-      if (!st && left && !(single_ok && maximum == 1 && t.count[1] == 1)) st = kBadTree;
-    }
-    if (!st && maximum) {
-      offs[1] = 0;
-      for (u32 l = 1; l < 15; ++l) offs[l + 1] = u16(offs[l] + t.count[l]);
-      u32 code = 0;
-      next[1] = 0;
-      for (u32 l = 2; l < 16; ++l) {
-        code = (code + t.count[l - 1]) << 1;
-        next[l] = u16(code);
+  // Kraft sum, offsets and first codes by scans over lanes 1..15.  With
+  // weights count[l] << (15 - l), the serial running balance of huff_build
+  // goes negative exactly when the total passes 2^15 (the partial sums only
+  // grow), the code is complete exactly at 2^15, and the first code of
+  // length l is the exclusive weighted sum below l shifted down by 15 - l
+  // (exact: every term below l is a multiple of 2^(16 - l)).
+  {
+    const bool used = lane >= 1 && lane <= limit && lane < 16;
+    const u32 c = used ? cnt : 0u;
+    u32 wsum = c << (15 - (lane & 15)), csum = c;
+#pragma unroll
+    for (u32 o = 1; o < 16; o <<= 1) {
+      const u32 wy = __shfl_up(wsum, o, 64), cy = __shfl_up(csum, o, 64);
+      if (lane >= o) {
+        wsum += wy;
+        csum += cy;
       }
     }
-    *status = st;
+    const u32 total = u32(__builtin_amdgcn_readlane(int(wsum), 15));
+    const u64 lens_used = __ballot(used && cnt);
+    const u64 over_limit = __ballot(lane > limit && lane < 16 && cnt);
+    const u32 maximum = lens_used ? 63u - u32(__builtin_clzll(lens_used)) : 0u;
+    const u32 ones = u32(__builtin_amdgcn_readlane(int(cnt), 1));
+    if (lane >= 1 && lane < 16) {
+      offs[lane] = u16(csum - c);
+      next[lane] = u16((wsum - (c << (15 - lane))) >> (15 - lane));
+    }
+    if (!lane) {
+      u32 st = kOk;
+      if (n > u32(N) || over_limit) st = kBadTree;
+      t.maximum = maximum;
+      if (!st && !maximum && !empty_ok) st = kBadTree;
+      if (!st && maximum) {
+        if (total > 32768u) st = kBadTree;
+        else if (total != 32768u && !(single_ok && maximum == 1 && ones == 1)) st = kBadTree;
+      }
+      *status = st;
+    }
   }
   for (u32 i = lane; i < (1u << P); i += 64) t.primary[i] = 0;
   sync();
