@@ -3243,11 +3243,36 @@ __global__ __launch_bounds__(256) void g_batch_wide_finish(const BatchFile* file
     const BatchFile file = files[f];
     const u8* o = out + file.out_offset;
     const u64 len = file.out_size;
+    // Bytes before the first 16-byte boundary and after the last one singly,
+    // the rest as 16-byte loads (byte k weighs len - k).
+    const u64 lead = (16 - (reinterpret_cast<uintptr_t>(o) & 15)) & 15;
+    const u64 head = lead < len ? lead : len;
+    const u64 mid = (len - head) & ~u64(15);
     u64 s = 0, w = 0;
-    for (u64 k = t; k < len; k += 256) {
+    if (t < head + (len - head - mid)) {  // at most 15 + 15 single bytes
+      const u64 k = t < head ? t : head + mid + (t - head);
       const u64 v = o[k];
-      s += v;
-      w += (len - k) * v;
+      s = v;
+      w = (len - k) * v;
+    }
+    const uint4* q = reinterpret_cast<const uint4*>(o + head);
+    for (u64 g = t; g < mid / 16; g += 256) {
+      const uint4 x = q[g];
+      u32 bs = 0, bw = 0;  // sum of the 16 bytes, and of each times its index
+      auto take = [&](u32 word, u32 j0) {
+#pragma unroll
+        for (u32 j = 0; j < 4; ++j) {
+          const u32 b = (word >> (8 * j)) & 255u;
+          bs += b;
+          bw += (j0 + j) * b;
+        }
+      };
+      take(x.x, 0);
+      take(x.y, 4);
+      take(x.z, 8);
+      take(x.w, 12);
+      s += bs;
+      w += (len - head - 16 * g) * bs - bw;
       if (w >> 62) w %= kAdlerMod;
     }
     s %= kAdlerMod;
