@@ -651,13 +651,17 @@ __global__ void e_single_descs(u64 n, u32 chunk, u32 chunks, u32 hist_max, u64 c
 // previous parse never hashed are added: its last three (their four bytes
 // reach into this chunk) and those its steps skipped inside matches.
 __global__ __launch_bounds__(kParseThreads) __attribute__((amdgpu_waves_per_eu(8))) void e_parse(
-    const u8* in, const ChunkDesc* descs, u32 chunks, u32* tokens, ChunkStats* stats) {
+    const u8* in, const ChunkDesc* descs, u32 chunks, const u32* runs, u32* tokens,
+    ChunkStats* stats) {
   extern __shared__ __align__(16) u8 dyn[];
   ParseShared& sh = *reinterpret_cast<ParseShared*>(dyn);
   u32* win = reinterpret_cast<u32*>(dyn + kParseShared);
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  // This workgroup's run of consecutive chunks: [runs[b], runs[b + 1]), or
+  // an equal share of the chunks.
   const u32 per = (chunks + gridDim.x - 1) / gridDim.x;
-  const u32 c0 = blockIdx.x * per, c1 = min(chunks, c0 + per);
+  const u32 c0 = runs ? runs[blockIdx.x] : blockIdx.x * per;
+  const u32 c1 = runs ? runs[blockIdx.x + 1] : min(chunks, c0 + per);
   u64 prev_in = 0, prev_start = 0;  // previous chunk: input offset, window start
   u32 prev_len = 0, prev_file = 0;
   bool have_prev = false;
@@ -1356,6 +1360,7 @@ namespace {
 // launch, so that a call which cannot get its scratch enqueues nothing.
 struct ChunkBuffers {
   ChunkDesc* descs = nullptr;
+  u32* runs = nullptr;  // optional: e_parse workgroup b takes chunks [runs[b], runs[b + 1])
   FileDesc* files = nullptr;
   u32* tokens = nullptr;
   ChunkStats* stats = nullptr;
@@ -1380,6 +1385,20 @@ hipError_t alloc_chunks(Scratch& scratch, u64 chunks, u32 file_count, u64 in_tot
   return hipSuccess;
 }
 
+// Parse workgroups for `chunks` chunks: one or two per CU (as many as their
+// LDS allows), each taking a run of consecutive chunks.  Batches launch
+// kBatchParseRuns times as many shorter runs, so that workgroups that finish
+// early take further runs.
+constexpr u64 kBatchParseRuns = 2;
+hipError_t parse_grid_size(u64 chunks, u32 chunk_bytes, u32* grid) {
+  int device = 0, cus = 0;
+  HZ_TRY(hipGetDevice(&device));
+  HZ_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  const u64 per_cu = kLdsBudget / parse_budget(chunk_bytes);
+  *grid = u32(std::min<u64>(chunks, per_cu * u64(cus > 0 ? cus : 1)));
+  return hipSuccess;
+}
+
 hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u64 chunks,
                       u32 file_count, u8* out, u32 chunk_bytes, u32* meta, bool clear_failed) {
   const u32 parse_lds = kParseShared + history_limit(chunk_bytes) + chunk_bytes + 32;
@@ -1387,15 +1406,11 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_parse),
                              hipFuncAttributeMaxDynamicSharedMemorySize, int(parse_lds)));
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
-  // One or two parse workgroups per CU (as many as their LDS allows), each
-  // taking a run of consecutive chunks.
-  int device = 0, cus = 0;
-  HZ_TRY(hipGetDevice(&device));
-  HZ_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-  const u64 per_cu = kLdsBudget / parse_budget(chunk_bytes);
-  const u32 parse_grid = u32(std::min<u64>(chunks, per_cu * u64(cus > 0 ? cus : 1)));
+  u32 parse_grid = 0;
+  HZ_TRY(parse_grid_size(chunks, chunk_bytes, &parse_grid));
+  if (b.runs) parse_grid = u32(std::min<u64>(chunks, u64(parse_grid) * kBatchParseRuns));
   HZ_LAUNCH(e_parse, dim3(parse_grid), dim3(kParseThreads), parse_lds, stream, in, b.descs,
-            u32(chunks), b.tokens, b.stats);
+            u32(chunks), b.runs, b.tokens, b.stats);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(e_tree, dim3(grid), dim3(kTreeThreads), 0, stream, b.descs, u32(chunks), b.stats,
             b.tables, b.results);
@@ -1495,7 +1510,26 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
   }
   ChunkBuffers b;
   HZ_TRY(alloc_chunks(scratch, descs.size(), count, in_total, b));
+  // Parse runs of about equal work (bytes plus a fixed cost per chunk) rather
+  // than of equal chunk counts: a batch's chunks range from a few bytes to a
+  // full chunk, and a run that collects many full chunks would finish last.
+  u32 parse_grid = 0;
+  HZ_TRY(parse_grid_size(descs.size(), chunk_bytes, &parse_grid));
+  parse_grid = u32(std::min<u64>(descs.size(), u64(parse_grid) * kBatchParseRuns));
+  constexpr u64 kChunkCost = 4096;
+  std::vector<u32> runs(u64(parse_grid) + 1, u32(descs.size()));
+  u64 work = 0, done = 0;
+  for (const ChunkDesc& d : descs) work += d.len + kChunkCost;
+  runs[0] = 0;
+  u32 next = 1;
+  for (u64 c = 0; c < descs.size(); ++c) {
+    done += descs[c].len + kChunkCost;
+    while (next < parse_grid && done * parse_grid >= work * next) runs[next++] = u32(c + 1);
+  }
+  HZ_TRY(scratch.alloc(&b.runs, runs.size()));
   // Pageable sources: the runtime copies them before these calls return.
+  HZ_TRY(hipMemcpyAsync(b.runs, runs.data(), runs.size() * sizeof(u32), hipMemcpyHostToDevice,
+                        stream));
   HZ_TRY(hipMemcpyAsync(b.descs, descs.data(), descs.size() * sizeof(ChunkDesc),
                         hipMemcpyHostToDevice, stream));
   HZ_TRY(hipMemcpyAsync(b.files, files.data(), count * sizeof(FileDesc), hipMemcpyHostToDevice,
