@@ -267,39 +267,13 @@ __device__ __forceinline__ u32 fixed_len(u32 s) {
   return s < 144 ? 8u : s < 256 ? 9u : s < 280 ? 7u : 8u;
 }
 
-// Optimal length-limited code lengths by package-merge (one wave; every lane
-// calls).  Leaves are sorted by (frequency, symbol) with a bitonic network.  Level
-// `limit` holds the sorted leaves; level j merges the leaves with the
-// packages of level j + 1 (sums of its consecutive item pairs), each lane
-// merging one stretch of the output along the merge path (leaves before
-// packages of equal weight).  The first 2m - 2 items of level 1 are taken;
-// a taken package takes its two children, so the taken items of every level
-// are a prefix, and a leaf's length is the number of levels whose taken
-// prefix holds it.  Unused symbols get length 0 (at least two symbols get a
-// code).  The sort covers 64 * kRegs slots, at least n.
+// Bitonic sort of the m leaf keys (weight << 9 | symbol) over 64 * kRegs
+// slots, m <= 64 * kRegs, into hs.sorted / hs.leaf: slot r * 64 + lane in
+// register r; partners within a lane swap registers, partners across lanes
+// exchange by shuffles.  Padding keys sort last, so every width that holds
+// the m keys gives the same order.
 template <u32 kRegs, class HS>
-__device__ void huffman_lengths(HS& hs, const u32* freq, u32 n, u32 limit, u8* len) {
-  const u32 lane = lane_id();
-  u32 m = 0;
-  for (u32 base = 0; base < n; base += 64) {
-    const u32 s = base + lane;
-    const bool used = s < n && freq[s] != 0;
-    if (s < n) len[s] = 0;
-    const u64 bal = __ballot(used);
-    if (used) hs.list[m + __popcll(bal & lanemask_lt())] = u16(s);
-    m += __popcll(bal);
-  }
-  if (m < 2) {
-    for (u32 s = 0; m < 2 && s < n; ++s)
-      if (!freq[s]) {
-        if (!lane) hs.list[m] = u16(s);
-        ++m;
-      }
-  }
-  wave_sync();
-  // Bitonic sort of the keys (weight << 9 | symbol) over 64 * kRegs slots: slot
-  // r * 64 + lane in register r; partners within a lane swap registers,
-  // partners across lanes exchange by shuffles.
+__device__ void sort_leaves(HS& hs, const u32* freq, u32 m, u32 lane) {
   u32 key[kRegs];
 #pragma unroll
   for (u32 r = 0; r < kRegs; ++r) {
@@ -348,6 +322,43 @@ __device__ void huffman_lengths(HS& hs, const u32* freq, u32 n, u32 limit, u8* l
       hs.leaf[i] = key[r] >> 9;
     }
   }
+}
+
+// Optimal length-limited code lengths by package-merge (one wave; every lane
+// calls).  Leaves are sorted by (frequency, symbol) with a bitonic network.  Level
+// `limit` holds the sorted leaves; level j merges the leaves with the
+// packages of level j + 1 (sums of its consecutive item pairs), each lane
+// merging one stretch of the output along the merge path (leaves before
+// packages of equal weight).  The first 2m - 2 items of level 1 are taken;
+// a taken package takes its two children, so the taken items of every level
+// are a prefix, and a leaf's length is the number of levels whose taken
+// prefix holds it.  Unused symbols get length 0 (at least two symbols get a
+// code).  64 * kRegs slots hold at least n leaves.
+template <u32 kRegs, class HS>
+__device__ void huffman_lengths(HS& hs, const u32* freq, u32 n, u32 limit, u8* len) {
+  const u32 lane = lane_id();
+  u32 m = 0;
+  for (u32 base = 0; base < n; base += 64) {
+    const u32 s = base + lane;
+    const bool used = s < n && freq[s] != 0;
+    if (s < n) len[s] = 0;
+    const u64 bal = __ballot(used);
+    if (used) hs.list[m + __popcll(bal & lanemask_lt())] = u16(s);
+    m += __popcll(bal);
+  }
+  if (m < 2) {
+    for (u32 s = 0; m < 2 && s < n; ++s)
+      if (!freq[s]) {
+        if (!lane) hs.list[m] = u16(s);
+        ++m;
+      }
+  }
+  wave_sync();
+  // The narrowest sort that holds the m leaves (short chunks use few symbols).
+  if (kRegs >= 8 && m > 256) sort_leaves<(kRegs >= 8 ? 8u : 1u)>(hs, freq, m, lane);
+  else if (kRegs >= 4 && m > 128) sort_leaves<(kRegs >= 4 ? 4u : 1u)>(hs, freq, m, lane);
+  else if (kRegs >= 2 && m > 64) sort_leaves<(kRegs >= 2 ? 2u : 1u)>(hs, freq, m, lane);
+  else sort_leaves<1>(hs, freq, m, lane);
   for (u32 i = lane; i < 16 * HS::kWords; i += 64) (&hs.leafbits[0][0])[i] = 0;
   wave_sync();
   // Level `limit`: the leaves.
