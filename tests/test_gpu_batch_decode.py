@@ -115,3 +115,62 @@ def test_encoded_rows_route_large_files_like_small_ones(gpu):
         got = host[at:at + len(raw)]
         assert got == (raw if status[i] == 0 else bytes(len(raw)))
         at += len(raw)
+
+
+def _small_dynamic(rng, n):
+    """A stream of under 256 B of output in one dynamic-Huffman block."""
+    raw = bytes(rng.choice(b"abcdefg"[:rng.randrange(2, 8)]) for _ in range(n))
+    c = zlib.compressobj(9, zlib.DEFLATED, 15, 9, zlib.Z_HUFFMAN_ONLY)
+    return raw, c.compress(raw) + c.flush()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_small_dynamic_headers_match_the_serial_oracle(gpu, seed):
+    """Files under 256 B decode one wave per file, staged in LDS, their
+    dynamic headers read by the wave walk (lane 0's serial parse where the
+    walk stops); valid, header-corrupted and truncated ones against the
+    oracle, beside large files so both routes run together."""
+    rng = random.Random(40 + seed)
+    streams, expected = [], []
+    for i in range(60):
+        raw, payload = _small_dynamic(rng, rng.randrange(1, 256))
+        data = bytearray(payload)
+        kind = rng.randrange(4)
+        if kind == 1:  # a bit of the header fields, the code-length code or the lengths
+            bit = rng.randrange(16 + 3, min(len(data) - 4, 40) * 8)
+            data[bit // 8] ^= 1 << (bit % 8)
+        elif kind == 2 and len(data) > 10:  # truncated inside the header
+            del data[rng.randrange(3, min(len(data) - 1, 12)):]
+        streams.append(bytes(data))
+        expected.append(len(raw))
+        if i % 10 == 0:  # a large neighbour for the parallel route
+            big = workloads.text_like(rng.randrange(3000, 40000), np.random.default_rng(seed * 100 + i))
+            streams.append(zlib.compress(big, 6))
+            expected.append(len(big))
+    _check(streams, expected)
+
+
+def test_batch_on_a_side_stream_is_complete_when_that_stream_is(gpu):
+    """Small files decode on a second stream beside the large ones; the
+    caller's stream alone must cover both once synchronized."""
+    import torch
+    from cuda_zlib import decompress_zlib_batch_checked
+    rng = random.Random(77)
+    raws = []
+    for i in range(200):
+        if i % 4 == 0:
+            raws.append(workloads.text_like(rng.randrange(2000, 60000), np.random.default_rng(i)))
+        else:
+            raws.append(_small_dynamic(rng, rng.randrange(1, 256))[0])
+    streams = [zlib.compress(r, 6) for r in raws]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        out, meta = decompress_zlib_batch_checked(b"".join(streams), [len(s) for s in streams],
+                                                  [len(r) for r in raws], 0)
+        host_out = torch.empty(out.numel(), dtype=torch.uint8, pin_memory=True)
+        host_meta = torch.empty(meta.shape, dtype=meta.dtype, pin_memory=True)
+        host_out.copy_(out, non_blocking=True)
+        host_meta.copy_(meta, non_blocking=True)
+    stream.synchronize()
+    assert host_meta.numpy()[:, 0].tolist() == [0] * len(raws)
+    assert host_out.numpy().tobytes() == b"".join(raws)
