@@ -1372,6 +1372,7 @@ namespace {
 struct ChunkBuffers {
   ChunkDesc* descs = nullptr;
   u32* runs = nullptr;  // optional: e_parse workgroup b takes chunks [runs[b], runs[b + 1])
+  u32 run_count = 0;    // workgroups (runs) that `runs` describes
   FileDesc* files = nullptr;
   u32* tokens = nullptr;
   ChunkStats* stats = nullptr;
@@ -1419,7 +1420,7 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   const u32 grid = u32(chunks < 65536 ? chunks : 65536);
   u32 parse_grid = 0;
   HZ_TRY(parse_grid_size(chunks, chunk_bytes, &parse_grid));
-  if (b.runs) parse_grid = u32(std::min<u64>(chunks, u64(parse_grid) * kBatchParseRuns));
+  if (b.runs) parse_grid = b.run_count;
   HZ_LAUNCH(e_parse, dim3(parse_grid), dim3(kParseThreads), parse_lds, stream, in, b.descs,
             u32(chunks), b.runs, b.tokens, b.stats);
   HZ_TRY(hipGetLastError());
@@ -1538,6 +1539,7 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
     while (next < parse_grid && done * parse_grid >= work * next) runs[next++] = u32(c + 1);
   }
   HZ_TRY(scratch.alloc(&b.runs, runs.size()));
+  b.run_count = parse_grid;
   // Pageable sources: the runtime copies them before these calls return.
   HZ_TRY(hipMemcpyAsync(b.runs, runs.data(), runs.size() * sizeof(u32), hipMemcpyHostToDevice,
                         stream));
