@@ -190,6 +190,22 @@ class Workspace final : public Scratch {
     allocations_.push_back(*p);
     return hipSuccess;
   }
+  // Starts carving again from the arena's beginning: the work enqueued so
+  // far keeps its scratch in stream order (later work on the stream runs
+  // after it), so a call made of independent phases reuses one phase's
+  // scratch for the next.  Pool allocations are freed on the stream.
+  hipError_t rewind() {
+    hipError_t first = hipSuccess;
+    for (void* p : allocations_) {
+      const hipError_t err = hipFreeAsync(p, stream_);
+      if (first == hipSuccess) first = err;
+    }
+    allocations_.clear();
+    peak_ = std::max(peak_, total_);
+    total_ = 0;
+    used_ = 0;
+    return first;
+  }
   hipError_t release() {
     hipError_t first = hipSuccess;
     auto keep = [&](hipError_t err) { if (first == hipSuccess) first = err; };
@@ -197,6 +213,7 @@ class Workspace final : public Scratch {
     allocations_.clear();
     if (!acquired_) return first;
     acquired_ = false;
+    total_ = std::max(peak_, total_);
     PoolRegistry& reg = registry();
     std::lock_guard<std::mutex> lock(reg.mutex);
     const u64 want = (total_ + kArenaGranule - 1) / kArenaGranule * kArenaGranule;
@@ -253,7 +270,7 @@ class Workspace final : public Scratch {
   int device_;
   Arena* arena_ = nullptr;
   bool acquired_ = false;
-  u64 used_ = 0, total_ = 0;
+  u64 used_ = 0, total_ = 0, peak_ = 0;
   std::vector<void*> allocations_;
 };
 
@@ -282,6 +299,80 @@ int execute(hipStream_t stream, Body&& body) {
 }
 
 u64 chunk_count(u64 size, u64 chunk) { return std::max<u64>(1, (size + chunk - 1) / chunk); }
+
+// Input bytes an open-ended member decode first looks at: at least this
+// many, or four times the previous member's.  Discovery covers what a decode
+// is given, so a window keeps a long run of small members linear in the
+// input; a member that does not end inside its window is decoded again over
+// the whole rest of the input.
+constexpr u64 kMemberWindowMin = 16ull << 20;
+
+// A concatenation of zlib streams or gzip members (HIP_ZLIB_FORMAT_MEMBERS):
+// each member by an open-ended general-route decode into the output after
+// the previous member's bytes, the host reading back (one stream
+// synchronisation per member) where the member ended and how many bytes it
+// produced.
+hipError_t decode_members(hipStream_t stream, Workspace& ws, u32 format, int64_t max_candidates,
+                          int64_t max_blocks, const uint8_t* input, uint64_t input_size,
+                          uint8_t* output, uint64_t output_size, uint32_t* metadata) {
+  if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, kInvalidBounds, 0);
+  hipError_t err = launch_fill(stream, output, 0, output_size);
+  if (err != hipSuccess) return err;
+  if (input_size > kMaxBytes || max_candidates < 1 || max_candidates > kMaxCandidates ||
+      max_blocks < 1 || max_blocks > kMaxBlocks)
+    return launch_set_meta(stream, metadata, kInvalidBounds, 0);
+  const u64 fixed = format == kFormatGzip ? 18 : 8;
+  u64 in_off = 0, out_off = 0, last_in = 0;
+  u32 status = kOk;
+  while (!status) {
+    const u64 rest_in = input_size - in_off, rest_out = output_size - out_off;
+    if (rest_in < fixed) {
+      status = kTruncatedZlib;
+      break;
+    }
+    u64 window = std::min(rest_in, std::max(kMemberWindowMin, 4 * last_in));
+    u64 report_host[3] = {0, 0, 0};
+    for (;;) {
+      err = ws.rewind();
+      if (err != hipSuccess) return err;
+      u64* report = nullptr;
+      u32* member_meta = nullptr;
+      err = ws.alloc(&report, 3);
+      if (err == hipSuccess) err = ws.alloc(&member_meta, 2);
+      if (err != hipSuccess) return err;
+      StreamFormat fmt;
+      fmt.format = format;
+      fmt.open = true;
+      fmt.windowed = window < rest_in;
+      fmt.report = report;
+      err = run_inflate_general(stream, ws, input + in_off, window, output + out_off, rest_out,
+                                u32(max_candidates), u32(max_blocks), member_meta, fmt);
+      if (err == hipSuccess)
+        err = hipMemcpyAsync(report_host, report, sizeof(report_host), hipMemcpyDeviceToHost,
+                             stream);
+      if (err == hipSuccess) err = hipStreamSynchronize(stream);
+      if (err != hipSuccess) return err;
+      if (report_host[0] && window < rest_in) {
+        window = rest_in;  // the member may run past its window: decode it over all the rest
+        continue;
+      }
+      break;
+    }
+    status = u32(report_host[0]);
+    if (status) break;
+    in_off += report_host[1];
+    out_off += report_host[2];
+    last_in = report_host[1];
+    if (in_off >= input_size) break;
+  }
+  if (!status && out_off != output_size) status = kSizeMismatch;
+  // A checksum mismatch keeps the output, as a single stream's does.
+  if (status && status != kAdlerMismatch && status != kGzipCheckMismatch) {
+    err = launch_fill(stream, output, 0, output_size);
+    if (err != hipSuccess) return err;
+  }
+  return launch_set_meta(stream, metadata, status, 0);
+}
 
 }  // namespace
 }  // namespace hz
@@ -322,11 +413,20 @@ extern "C" int HipZlibDecompressFormat(hipStream_t stream, int32_t format,
                                        uint64_t output_size, uint32_t* metadata,
                                        uint64_t metadata_count) {
   if (!metadata || metadata_count != 2) return invalid("codec metadata must have shape (2,)");
+  const bool members = (format & HIP_ZLIB_FORMAT_MEMBERS) != 0;
+  format &= ~HIP_ZLIB_FORMAT_MEMBERS;
   if (format != kFormatZlib && format != kFormatRaw && format != kFormatGzip)
     return invalid("unknown stream format (0 zlib, 1 raw DEFLATE, 2 gzip)");
   if (format == kFormatGzip && dictionary_size) return invalid("gzip streams take no dictionary");
+  if (members && (format == kFormatRaw || dictionary_size))
+    return invalid("concatenated members are zlib streams or gzip members, without a dictionary");
   if (dictionary_size && !dictionary) return invalid("missing preset dictionary");
   if (dictionary_size > kMaxBytes) return invalid("preset dictionary exceeds 2**32 - 1 bytes");
+  if (members)
+    return execute(stream, [&](Workspace& ws) -> hipError_t {
+      return decode_members(stream, ws, u32(format), max_candidates, max_blocks, input, input_size,
+                            output, output_size, metadata);
+    });
   return execute(stream, [&](Workspace& ws) -> hipError_t {
     if (output_size > kMaxBytes) return launch_set_meta(stream, metadata, kInvalidBounds, 0);
     auto fail = [&](u32 status) -> hipError_t {

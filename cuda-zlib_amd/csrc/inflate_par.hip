@@ -65,6 +65,22 @@ struct State {
   u64 floor;         // lowest output position a back-reference may read (history allowed: 0)
   u32 isize;         // gzip: the trailer's ISIZE
   u32 pad2;
+  // Open-ended decode (one member of a concatenation): the accepted path's
+  // end bit and output bytes, which the trailer and the next member follow.
+  u64 stream_end;
+  u64 produced;
+};
+
+// An open-ended decode's stream may end before the input does (other members
+// follow it) and produce fewer bytes than the output holds; `trailer` is the
+// wrapper's trailer length, which must fit after the last block.  A
+// `windowed` decode sees only a prefix of the input: when the fast chain does
+// not accept it, it reports kTruncated at once (no exact walk), and the
+// caller decodes the member again over the whole input.
+struct OpenEnd {
+  u32 open;
+  u32 trailer;
+  u32 windowed;
 };
 
 struct Segment {
@@ -612,6 +628,8 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   st->precount = 0;
   st->tables_used = 0;
   st->dense_count = 0;
+  st->stream_end = 0;
+  st->produced = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -2158,7 +2176,8 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
                                                 const u32* __restrict__ seg_rec,
                                                 u32* __restrict__ exit_node, u64 len,
                                                 u64 out_size, u32 max_blocks,
-                                                Segment* __restrict__ acc, u64 out_base) {
+                                                Segment* __restrict__ acc, u64 out_base,
+                                                OpenEnd open) {
   constexpr u32 kPer = kChainLdsNodes / 1024;  // candidates per thread in LDS mode
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
@@ -2332,11 +2351,18 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
       while (seg_next[z] != kNone) z = seg_next[z];
     const u32 flags = seg_flags[z];
     const u64 total = psize[1023], blocks = pblocks[1023], count = pcount[1023];
-    const bool good = (flags & 0x7fffffffu) == 0 && (flags & 0x80000000u) && total == out_size &&
-                      blocks <= max_blocks && (seg_end[z] + 7) / 8 == len;
+    const u64 end_byte = (seg_end[z] + 7) / 8;
+    const bool fits = open.open ? total <= out_size && end_byte + open.trailer <= len
+                                : total == out_size && end_byte == len;
+    const bool good = (flags & 0x7fffffffu) == 0 && (flags & 0x80000000u) && fits &&
+                      blocks <= max_blocks;
     ok = good ? 1u : 0u;
     st->chain_ok = ok;
     st->accepted = good ? count : 0;
+    if (good) {
+      st->stream_end = seg_end[z];
+      st->produced = total;
+    }
   }
   __syncthreads();
   if (!ok) return;
@@ -2387,9 +2413,13 @@ struct WalkShared {
 // accepted list one block per entry.
 __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, State* st,
                                                    u64 out_size, u32 max_blocks, Segment* acc,
-                                                   u64 out_base) {
+                                                   u64 out_base, OpenEnd open) {
   __shared__ WalkShared sh;
   if (st->status || st->chain_ok || threadIdx.x) return;
+  if (open.windowed) {
+    st->status = kTruncated;
+    return;
+  }
   const u64 start = st->start_bit;
   u64 next = start, output = 0, n = 0;
   u32 status = 0;
@@ -2427,13 +2457,21 @@ __global__ __launch_bounds__(64) void g_exact_walk(const u8* body, u64 len, Stat
     output += size;
     next = end;
     if (final_block) {
-      if (output != out_size) status = kSizeMismatch;
-      else if ((next + 7) / 8 != len) status = kExtent;
+      if (open.open) {
+        // The member's trailer must follow its last block.
+        if ((next + 7) / 8 + open.trailer > len) status = kTruncatedZlib;
+      } else if (output != out_size) {
+        status = kSizeMismatch;
+      } else if ((next + 7) / 8 != len) {
+        status = kExtent;
+      }
       break;
     }
   }
   st->status = status;
   st->accepted = status ? 0 : n;
+  st->stream_end = next;
+  st->produced = output;
 }
 
 namespace {
@@ -3407,11 +3445,15 @@ constexpr u32 kCrcTile = 16384;  // output bytes per CRC-32 tile (256 threads x 
 // at 0 unchanged, so every thread's 64-byte piece has full length and the
 // pieces join with one factor per tree level (x^(8 * 64 * 2^l)).
 __global__ __launch_bounds__(256) void g_crc_tiles(const State* st, const u8* out, u64 n,
-                                                   u64* parts, u64 tiles) {
+                                                   u64* parts, u64 tiles, u32 open) {
   __shared__ u32 table[256];
   __shared__ u32 factor[8];
   __shared__ u32 red[256];
   if (st->status || st->emit_status) return;
+  if (open) {  // an open-ended decode's output is the bytes its path produced
+    n = min(n, st->produced);
+    tiles = (n + kCrcTile - 1) / kCrcTile;
+  }
   const u32 t = threadIdx.x;
   table[t] = crc_byte_update(0, t);
   if (t < 8) factor[t] = crc_shift_bytes(u64(64) << t);
@@ -3488,22 +3530,43 @@ __device__ u32 crc_from_tiles(const u64* parts, u64 n) {
 // whichever kernel wrote it), CRC-32 and size from g_crc_tiles' tile
 // registers, or nothing, and writes the metadata.  A trailer mismatch keeps
 // the output.
+// Open-ended decode (`open.open`, one member of a concatenation): n is the
+// output's capacity, the member's size is what its path produced, and its
+// trailer is read after its last block in `body`; the output is left as it
+// is (the caller clears it on failure), and report[0..2] gets the status, the
+// member's input bytes (body_off + body bytes + trailer) and its output bytes.
 __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, const u64* parts,
-                                                u32 nparts, u32 check, u8* out) {
+                                                u32 nparts, u32 check, u8* out, OpenEnd open,
+                                                const u8* body, u64 body_off, u64* report) {
   __shared__ u64 red[2][4];
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   u32 status = st->status;
   if (!status) status = st->emit_status;
   // References still unresolved after every round.
   if (!status && st->unresolved[1]) status = kReferenceDepth;
-  if (status) {  // uniform; st->status never holds a trailer mismatch here
+  if (status && !open.open) {  // uniform; st->status never holds a trailer mismatch here
     const u64 stride = u64(gridDim.x) * blockDim.x;
     for (u64 i = u64(blockIdx.x) * blockDim.x + t; i < n; i += stride) out[i] = 0;
   }
   if (blockIdx.x) return;
+  // Adler-32 weights were taken against the capacity's end: W = sum (cap - i) x_i.
+  const u64 cap = n;
+  u32 wanted = st->wanted, isize = st->isize;
+  u64 end_byte = 0;
+  if (open.open) {
+    n = status ? 0 : st->produced;
+    end_byte = (st->stream_end + 7) / 8;
+    const u8* tr = body + end_byte;  // inside the input: the walk checked that it fits
+    if (!status && check == kCheckAdler)
+      wanted = (u32(tr[0]) << 24) | (u32(tr[1]) << 16) | (u32(tr[2]) << 8) | u32(tr[3]);
+    if (!status && check == kCheckCrc) {
+      wanted = u32(tr[0]) | (u32(tr[1]) << 8) | (u32(tr[2]) << 16) | (u32(tr[3]) << 24);
+      isize = u32(tr[4]) | (u32(tr[5]) << 8) | (u32(tr[6]) << 16) | (u32(tr[7]) << 24);
+    }
+  }
   if (!status && check == kCheckCrc) {  // uniform
     const u32 got = crc_from_tiles(parts, n);
-    if (!t && (got != st->wanted || u32(n) != st->isize)) status = kGzipCheckMismatch;
+    if (!t && (got != wanted || u32(n) != isize)) status = kGzipCheckMismatch;
   }
   if (!status && check == kCheckAdler) {  // uniform: every emitter and round wrote its pair
     u64 s = 0, w = 0;
@@ -3520,13 +3583,23 @@ __global__ __launch_bounds__(256) void g_finish(State* st, u64 n, u32* meta, con
       red[1][wave] = w;
     }
     __syncthreads();
-    const u32 a = u32((red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1) % kAdlerMod);
-    const u32 b = u32((red[1][0] + red[1][1] + red[1][2] + red[1][3] + n % kAdlerMod) % kAdlerMod);
-    if (((b << 16) | a) != st->wanted) status = kAdlerMismatch;
+    const u64 s_all = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) % kAdlerMod;
+    const u32 a = u32((s_all + 1) % kAdlerMod);
+    // sum (n - i) x_i = W - (cap - n) * S (mod 65521).
+    const u64 shift = ((cap - n) % kAdlerMod) * s_all % kAdlerMod;
+    const u32 b = u32((red[1][0] + red[1][1] + red[1][2] + red[1][3] + kAdlerMod - shift +
+                       n % kAdlerMod) %
+                      kAdlerMod);
+    if (((b << 16) | a) != wanted) status = kAdlerMismatch;
   }
   if (!t) {
     meta[0] = status;
     meta[1] = 0;
+    if (open.open) {
+      report[0] = status;
+      report[1] = body_off + end_byte + open.trailer;
+      report[2] = n;
+    }
   }
 }
 
@@ -3548,7 +3621,10 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 body_off = fmt.format == kFormatGzip ? 10 : fmt.format == kFormatRaw ? 0 : 2;
   const u64 trailer = fmt.format == kFormatGzip ? 8 : fmt.format == kFormatRaw ? 0 : 4;
   const u8* body = in + body_off;
-  const u64 len = in_size - body_off - trailer;
+  // An open-ended decode's body runs to the input's end: its trailer (and any
+  // later member) lies somewhere inside.
+  const u64 len = in_size - body_off - (fmt.open ? 0 : trailer);
+  const OpenEnd open{fmt.open ? 1u : 0u, u32(trailer), fmt.windowed ? 1u : 0u};
   const u32 check = fmt.format == kFormatGzip ? kCheckCrc
                     : fmt.format == kFormatRaw ? kCheckNone : kCheckAdler;
   // The stream's output starts `out_base` bytes into `out` (dictionary history).
@@ -3658,10 +3734,11 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   Segment* acc = nullptr;
   HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
   HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size, seg_blocks,
-            seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc, out_base);
+            seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc, out_base,
+            open);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size, max_blocks,
-            acc, out_base);
+            acc, out_base, open);
   HZ_TRY(hipGetLastError());
 
   // Emission and cross-segment resolution.
@@ -3692,7 +3769,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   if (check == kCheckAdler) {
     // The pairs of the emitters, then those of the resolve rounds.
     HZ_LAUNCH(g_finish, dim3(finish_grid), dim3(256), 0, stream, st, out_size, meta, adler_parts,
-              3 * kAdlerSlots, check, stream_out);
+              3 * kAdlerSlots, check, stream_out, open, body, body_off, fmt.report);
     return hipGetLastError();
   }
   if (check == kCheckCrc) {
@@ -3700,12 +3777,12 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
     HZ_TRY(scratch.alloc(&parts, tiles ? tiles : 1));
     if (tiles) {
       HZ_LAUNCH(g_crc_tiles, dim3(clamp_grid(tiles, 4096)), dim3(256), 0, stream, st, stream_out,
-                out_size, parts, tiles);
+                out_size, parts, tiles, open.open);
       HZ_TRY(hipGetLastError());
     }
   }
   HZ_LAUNCH(g_finish, dim3(finish_grid), dim3(256), 0, stream, st, out_size, meta, parts, nparts,
-            check, stream_out);
+            check, stream_out, open, body, body_off, fmt.report);
   return hipGetLastError();
 }
 

@@ -78,6 +78,17 @@ struct StreamFormat {
   const u8* dict = nullptr;
   u64 dict_len = 0;
   u64 out_base = 0;
+  // Open-ended decode of the first member of in[0..in_size): its stream may
+  // end before in_size (other members follow its trailer) and produce at most
+  // out_size bytes.  `report` (device, 3 x u64) then receives
+  // [status, input bytes of the member, output bytes]; the output is not
+  // cleared on failure.
+  // `windowed`: in_size is a prefix of the member's input, so a stream the
+  // fast path cannot accept reports kTruncated (1) at once, and the caller
+  // decodes it again over all of its input.
+  bool open = false;
+  bool windowed = false;
+  u64* report = nullptr;
 };
 
 // inflate_par.hip: general-route decode.  The stream's out_size bytes go to

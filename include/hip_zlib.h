@@ -65,7 +65,21 @@ int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int64_t max_bl
  * (such as a second gzip member) give status 12.  Format 0 without a
  * dictionary is exactly HipZlibDecompress.  No counterpart in the reference,
  * which rejects gzip with status 16 and dictionaries with 17
- * (src/cuda_zlib/_codec.py:105-111). */
+ * (src/cuda_zlib/_codec.py:105-111).
+ *
+ * format | HIP_ZLIB_FORMAT_MEMBERS (zlib or gzip, no dictionary) decodes a
+ * concatenation: one member after another (each zlib stream or gzip member
+ * with its own header, window and Adler-32 or CRC-32/ISIZE check) until the
+ * input ends, their outputs placed one after another.  The members' outputs
+ * must add up to output_size (else status 11; 7 when they exceed it), and an
+ * input that ends inside a member gives that member's status (14 for a
+ * missing trailer).  The first failing member's status is reported; on a
+ * checksum mismatch (21, 24) the output decoded so far is kept, otherwise the
+ * output is zero-filled.  This mode synchronises the stream with the host
+ * once per member (the next member starts where the previous one ended), so
+ * it must not be used under graph capture.  The reference rejects a second
+ * stream after the first (tests/test_decode.py:679-713). */
+#define HIP_ZLIB_FORMAT_MEMBERS 0x100
 int HipZlibDecompressFormat(hipStream_t stream, int32_t format, const uint8_t* dictionary,
                             uint64_t dictionary_size, int64_t max_candidates, int64_t max_blocks,
                             const uint8_t* input, uint64_t input_size, uint8_t* output,
