@@ -943,6 +943,50 @@ __host__ __device__ __forceinline__ u32 check_framing(const u8* in, u64 size, u3
   return kOk;
 }
 
+// ---- fixed-Huffman tokens without tables ----------------------------------------
+// One token of a fixed-Huffman block (RFC 1951 3.2.6) at the low bits of `b`
+// (LSB first; at least 31 meaningful bits, the longest fixed token).  The
+// first nine stream bits, reversed, are the code MSB first: 7-bit codes
+// 0000000-0010111 are symbols 256-279, 8-bit 00110000-10111111 literals
+// 0-143 and 11000000-11000111 symbols 280-287, 9-bit 110010000-111111111
+// literals 144-255.  Distance codes are five bits.  Returns kKindLit (value =
+// the byte), kKindLen (length, value = distance), kKindEob or kKindBad
+// (symbols 286-287, distance codes 30-31), and the bits the token takes.
+__host__ __device__ __forceinline__ u32 fixed_token(u64 b, u32& nbits, u32& length, u32& value) {
+  const u32 r9 = __builtin_bitreverse32(u32(b)) >> 23;
+  u32 sym, l;
+  if ((r9 >> 2) < 24) {
+    sym = 256 + (r9 >> 2);
+    l = 7;
+  } else if ((r9 >> 1) < 0xC0) {
+    sym = (r9 >> 1) - 0x30;
+    l = 8;
+  } else if ((r9 >> 1) < 0xC8) {
+    sym = 280 + ((r9 >> 1) - 0xC0);
+    l = 8;
+  } else {
+    sym = r9 - 256;  // 0x190 -> 144
+    l = 9;
+  }
+  length = 1;
+  value = sym;
+  nbits = l;
+  if (sym < 256) return kKindLit;
+  if (sym == 256) return kKindEob;
+  if (sym > 285) return kKindBad;
+  const u32 li = sym - 257, e = length_extra(li);
+  length = length_base(li) + (u32(b >> l) & ((1u << e) - 1u));
+  l += e;
+  const u32 d = __builtin_bitreverse32(u32(b >> l)) >> 27;
+  l += 5;
+  nbits = l;
+  if (d > 29) return kKindBad;
+  const u32 de = dist_extra(d);
+  value = dist_base(d) + (u32(b >> l) & ((1u << de) - 1u));
+  nbits = l + de;
+  return kKindLen;
+}
+
 // ---- wrapper formats -----------------------------------------------------------
 // zlib (RFC 1950), raw DEFLATE (RFC 1951 alone) and gzip (RFC 1952, one
 // member).  The drop-in zlib entry points use kFormatZlib without a

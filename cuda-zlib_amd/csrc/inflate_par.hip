@@ -69,6 +69,11 @@ struct State {
   // end bit and output bytes, which the trailer and the next member follow.
   u64 stream_end;
   u64 produced;
+  // Long fixed-Huffman runs: regions deferred by describe, run records and
+  // tile slots handed out by the walk.
+  u64 fix_regions;
+  u64 fix_runs;
+  u64 fix_rt;
 };
 
 // An open-ended decode's stream may end before the input does (other members
@@ -630,6 +635,9 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   st->dense_count = 0;
   st->stream_end = 0;
   st->produced = 0;
+  st->fix_regions = 0;
+  st->fix_runs = 0;
+  st->fix_rt = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -1245,6 +1253,153 @@ __device__ u32 describe_block(BitIn& r, DecodeTables& t, u64 limit, u32& final_b
   }
   size = produced;
   return err;
+}
+
+// ---- long fixed-Huffman runs ------------------------------------------------
+// A fixed block has a 3-bit header, so discovery cannot find where one starts,
+// and a run of fixed blocks (Z_FIXED data, a text segment of the stress
+// stream) would otherwise belong to the segment of the candidate before it and
+// be described by one workgroup.  Instead describe defers such a run (a
+// "region"), and three passes decode it across the whole GPU:
+//   summaries  every 2 KiB tile of the region, from each of the 32 bit
+//              offsets at which the tile's first token can start (a fixed
+//              token is at most 31 bits): where decoding leaves the tile,
+//              bytes produced, headers crossed, first EOB, or how it ended
+//   walk       one wave per region chains the summaries from the run's first
+//              token (stored blocks between runs parsed in place), giving the
+//              true entry and output offset of every tile, the segment's end
+//              and block records; a tile without a summary is decoded there
+//   slices     every tile on a run decodes once more from its true entry to
+//              place the 512-bit emission slices inside it
+// Emission then decodes a run's slices like a block's, crossing the fixed
+// headers inside a slice.  The reference keeps per-2 KiB-tile summaries of 32
+// entries for its serial chain walk (FixedSummary, scan_fixed_region,
+// _decode_kernels.py:376-472, 1181-1207, 1274).
+constexpr u32 kFixTileBits = 16384;
+constexpr u32 kFixEntries = 32;
+constexpr u32 kFixSliceBits = 512;
+constexpr u32 kFixTileSlices = kFixTileBits / kFixSliceBits;
+constexpr u32 kFixProbeTokens = 512;  // tokens a fixed block is probed before it is deferred
+constexpr u32 kFixMarginBytes = 64;   // staged past a tile: its last token, an EOB and a header
+constexpr u32 kFixStageWords = (2 * kFixTileBits / 8 + kFixMarginBytes) / 4 + 4;
+enum : u32 { kFixGo = 0, kFixEnd = 1, kFixHeader = 2, kFixError = 3 };
+constexpr u32 kFixInFinal = 0x10;       // kind flag: the exit lies inside the final block
+constexpr u16 kFixNoEob = 0xffffu;
+constexpr u32 kSegPaused = 0x40000000u;  // seg_flags: the segment continues in a fixed run
+constexpr u32 kSegRecsLost = 0x20000000u;  // seg_flags with kSegPaused: records ran out
+constexpr u32 kRecFixedRun = 1u;         // BlockRec.pad: slices cross fixed block headers
+
+// Decoding from one entry bit of one tile (tile-relative bit positions).
+struct FixSummary {
+  u32 bytes;      // output bytes up to the exit or terminal
+  u32 eob_bytes;  // output bytes before the first EOB
+  u16 exit;       // kFixGo: first token start at or after the tile's end; else the terminal
+                  // bit (kFixEnd: after the final EOB; kFixHeader: the non-fixed header;
+                  // kFixError: the failing token)
+  u16 eob;        // bit after the first EOB, or kFixNoEob
+  u16 blocks;     // block headers crossed (all fixed, non-final or final)
+  u8 kind;        // kFix* | kFixInFinal
+  u8 status;      // kFixError: the status
+};
+static_assert(sizeof(FixSummary) == 16, "summary layout");
+
+// A run of fixed blocks on a walked path, for the slice pass: its slices are
+// the 512-bit windows b0 .. b0 + lanes - 1 (slice i starts at the first token
+// at or after bit 512 * (b0 + i); slice 0 at the run's first token).
+struct FixRun {
+  u64 tok;      // first token bit
+  u64 end;      // bit after the last EOB
+  u64 b0;
+  u32 lanes;
+  u32 group;    // first of the run's consecutive slice groups
+  u64 hdr;      // header bit of the run's first block
+  u64 seg_off;  // output offset of the run inside its segment
+  u64 size;     // output bytes
+  u32 cand;     // the candidate whose segment holds the run
+  u32 pad;
+};
+
+// One tile of a run: its true entry and the run's output bytes before it.
+struct FixTile {
+  u64 pos;
+  u32 off;
+  u32 run;  // kNone: unused slot
+  u64 k;    // tile index
+};
+
+// 64 bits starting at stage bit p, words past `n` reading as zero.
+struct FixPeek {
+  const u32* w;
+  u32 n;
+  __device__ __forceinline__ u64 operator()(u32 p) const {
+    const u32 i = p >> 5, sh = p & 31u;
+    const u64 x0 = i < n ? w[i] : 0u, x1 = i + 1 < n ? w[i + 1] : 0u, x2 = i + 2 < n ? w[i + 2] : 0u;
+    const u64 lo = x0 | (x1 << 32);
+    return sh ? (lo >> sh) | (x2 << (64 - sh)) : lo;
+  }
+};
+
+// Fixed-Huffman decode from token start `p` until the first token start at or
+// after `stop`, crossing non-final and final fixed headers, within `body_end`
+// (stage bits past it do not exist).  `in_final`: the decode starts inside the
+// stream's final block, so its first EOB ends the stream.  Positions in the
+// result are relative to `rel0`.  With kMaxTokens, a decode that has taken
+// that many tokens stops as if it had reached `stop` (the probe).
+template <u32 kMaxTokens = 0>
+__device__ FixSummary fix_scan(const FixPeek& pk, u32 p, u32 stop, u32 body_end, bool in_final,
+                               u32 rel0) {
+  FixSummary s;
+  s.bytes = 0;
+  s.eob_bytes = 0;
+  s.eob = kFixNoEob;
+  s.blocks = 0;
+  s.status = 0;
+  u32 kind = kFixGo, tokens = 0;
+  for (;;) {
+    if (p >= stop || (kMaxTokens && tokens == kMaxTokens)) break;
+    ++tokens;
+    const u64 b = pk(p);
+    u32 nb, length, value;
+    const u32 k = fixed_token(b, nb, length, value);
+    if (k == kKindBad || p + nb > body_end) {
+      kind = kFixError;
+      s.status = k == kKindBad ? kBadSymbol : kTruncated;
+      break;
+    }
+    if (k == kKindEob) {
+      const u32 q = p + 7;
+      if (s.eob == kFixNoEob) {
+        s.eob = u16(q - rel0);
+        s.eob_bytes = s.bytes;
+      }
+      if (in_final) {
+        kind = kFixEnd;
+        p = q;
+        break;
+      }
+      if (q + 3 > body_end) {
+        kind = kFixError;
+        s.status = kTruncated;
+        p = q;
+        break;
+      }
+      const u32 h = u32(pk(q)) & 7u;  // BFINAL, then BTYPE
+      if ((h >> 1) != 1u) {
+        kind = kFixHeader;
+        p = q;
+        break;
+      }
+      ++s.blocks;
+      in_final = h & 1u;
+      p = q + 3;
+      continue;
+    }
+    s.bytes += length;
+    p += nb;
+  }
+  s.exit = u16(p - rel0);
+  s.kind = u8(kind | (kind == kFixGo && in_final ? kFixInFinal : 0u));
+  return s;
 }
 
 constexpr u32 kNoMerge = 0xffffffffu;
@@ -2022,14 +2177,37 @@ __global__ __launch_bounds__(64) void g_headers(const u8* body, u64 len, const S
   }
 }
 
+namespace {
+
+// Marks tiles k0 .. k1 of the summary bitmap.
+__device__ void fix_mark_tiles(u32* need, u64 k0, u64 k1) {
+  for (u64 w = k0 >> 5; w <= (k1 >> 5); ++w) {
+    const u32 lo = w == (k0 >> 5) ? ~0u << (k0 & 31) : ~0u;
+    const u32 hi = w == (k1 >> 5) ? ~0u >> (31 - (k1 & 31)) : ~0u;
+    atomicOr(need + w, lo & hi);
+  }
+}
+
+// Candidates a region's marking looks past (their segments failed: header
+// look-alikes inside the run's data) before it stops and leaves the rest of
+// the run to the walk.
+constexpr u32 kFixMarkScan = 4096;
+
+}  // namespace
+
 // One workgroup per candidate: describe the candidate's segment (its block and
 // the following stored/fixed blocks up to the next candidate) with parallel
-// token decoding, and record per-block slices for emission.
+// token decoding, and record per-block slices for emission.  A fixed block
+// whose decode is still going after kFixProbeTokens tokens starts a region:
+// the segment stops there (kSegPaused; seg_end = the block's header bit,
+// seg_last = its last block record) and g_fix_walk continues it from where
+// workgroup's records go on (g_fix_mark marks the tiles to summarise).
 __global__ __launch_bounds__(kDescThreads) void g_describe(
     const u8* body, u64 len, const u64* cand, State* st, u64 out_size, u64* seg_end,
     u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags, u32* seg_rec, BlockRec* recs,
     u64 rec_capacity, u64* slice_entry, u32* slice_off, u32* group_link, u64 group_capacity,
-    BlockTables* tables, u64 table_capacity, const u64* hdr_d0, const u32* hdr_info) {
+    BlockTables* tables, u64 table_capacity, const u64* hdr_d0, const u32* hdr_info,
+    u32* seg_last, u32* region_cand, u64* seg_prefix) {
   __shared__ DescShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -2037,6 +2215,7 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
   for (u64 c = blockIdx.x; c < n; c += gridDim.x) {
     u64 produced = 0;
     u32 blocks = 0, status = 0, final_block = 0, next = kNone, first_rec = kNone, last_rec = kNone;
+    bool paused = false;
     // Thread 0: every candidate before this index lies at or before sh.pos
     // (the list is sorted and sh.pos only grows).
     u64 search_from = c + 1;
@@ -2070,6 +2249,32 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
       const bool pre = first && pre0;
       if (!pre) block_header<true, true>(body, len, out_size, sh);
       first = false;
+      if (sh.type == 1 && !sh.status) {  // uniform
+        // Probe the fixed run: a long one becomes a region.  Decoding garbage
+        // (a header look-alike's block) meets an invalid code within a few
+        // dozen tokens, so regions start only on real fixed data.
+        constexpr u64 kProbeBits = u64(kFixProbeTokens) * 34;
+        if (!staged_covers(sh.stage, body, len, sh.d0, sh.d0 + kProbeBits)) {
+          __syncthreads();
+          stage_range(body, len, sh.pos, sh.pos + 64 * kMaxSlice, sh.stage);
+          __syncthreads();
+        }
+        if (!t) {
+          const FixPeek pk{sh.stage.words, sh.stage.count};
+          const u32 d0 = u32(sh.d0 - sh.stage.bit0);
+          const FixSummary f = fix_scan<kFixProbeTokens>(pk, d0, 0xffffffffu,
+                                                         stage_limit(sh.stage, len),
+                                                         sh.final_block != 0, d0);
+          sh.need = (f.kind & 15u) == kFixGo ? 1u : 0u;
+          if (sh.need) {
+            const u64 r = atomicAdd(reinterpret_cast<unsigned long long*>(&st->fix_regions), 1ull);
+            region_cand[r] = u32(c);
+            paused = true;
+          }
+        }
+        __syncthreads();
+        if (sh.need) break;  // uniform
+      }
       if (!t && sh.type && !sh.status) {
         const u64 idx = lower_bound_from(cand, n, search_from, sh.pos + 1);
         search_from = idx;
@@ -2148,14 +2353,444 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
       if (!sh.go) break;
     }
     if (!t) {
-      seg_end[c] = sh.end;
-      seg_size[c] = produced;
-      seg_blocks[c] = blocks;
-      seg_next[c] = next;
-      seg_flags[c] = status | (final_block ? 0x80000000u : 0u);
-      seg_rec[c] = recs_ok ? first_rec : kNone;
+      seg_prefix[c] = ~0ull;  // set by g_chain for segments on the path
+      if (paused) {
+        seg_end[c] = sh.pos;
+        seg_size[c] = produced;
+        seg_blocks[c] = blocks;
+        seg_next[c] = kNone;
+        seg_flags[c] = kSegPaused | (recs_ok ? 0u : kSegRecsLost);
+        seg_rec[c] = first_rec;
+        seg_last[c] = last_rec;
+      } else {
+        seg_end[c] = sh.end;
+        seg_size[c] = produced;
+        seg_blocks[c] = blocks;
+        seg_next[c] = next;
+        seg_flags[c] = status | (final_block ? 0x80000000u : 0u);
+        seg_rec[c] = recs_ok ? first_rec : kNone;
+      }
     }
     __syncthreads();
+  }
+}
+
+// Marks the tiles of every region for g_fix_sum: from the region's start to
+// the first later candidate whose own segment did not fail (header
+// look-alikes inside a run fail), at most kFixMarkScan candidates on.
+__global__ __launch_bounds__(256) void g_fix_mark(const State* st, const u64* cand, u64 len,
+                                                  const u64* seg_end, const u32* seg_flags,
+                                                  const u32* region_cand, u32* fix_need,
+                                                  u64 tiles) {
+  if (st->status) return;
+  const u64 regions = st->fix_regions, n = st->candidates;
+  for (u64 r = threadIdx.x; r < regions; r += blockDim.x) {
+    const u32 c = region_cand[r];
+    const u64 x = seg_end[c];
+    u64 j = lower_bound_from(cand, n, c + 1, x + 1);
+    u64 h = len * 8;
+    for (u32 k = 0; j < n; ++j, ++k) {
+      if (k == kFixMarkScan || (seg_flags[j] & 0xffffu) == 0) {
+        h = cand[j];
+        break;
+      }
+    }
+    if (tiles) fix_mark_tiles(fix_need, x / kFixTileBits, min<u64>(h / kFixTileBits, tiles - 1));
+  }
+}
+
+namespace {
+
+// One wave's tile pair for g_fix_sum.
+__device__ void fix_sum_pair(const u8* body, u64 len, const u32* need, FixSummary* sum, u64 tiles,
+                             u64 k0, u32 pair, u32* w, u32 lane) {
+  // The wave stages body bits [k0 T, (k0 + 2) T) and the margin.
+  const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+  const u64 byte0 = k0 * (kFixTileBits / 8);
+  const u64 first_word = (base + byte0) >> 2;
+  u64 last_byte = byte0 + 2 * (kFixTileBits / 8) + kFixMarginBytes;
+  if (last_byte > len) last_byte = len;
+  const u64 end_word = (base + last_byte + 3) >> 2;
+  const u32 nwords = u32(min<u64>(end_word > first_word ? end_word - first_word : 0, kFixStageWords));
+  const u32* g = reinterpret_cast<const u32*>(first_word << 2);
+  wave_sync();  // the previous pair's reads of the stage are done
+  for (u32 i = lane; i < nwords; i += 64) w[i] = g[i];
+  wave_sync();
+  const u32 half = lane >> 5, e = lane & 31u;
+  const u64 k = k0 + half;
+  if (k >= tiles || !((pair >> half) & 1u)) return;
+  const u32 skew = u32((base + byte0) & 3u) * 8;  // stage bit of body bit k0 T
+  const u32 rel = skew + half * kFixTileBits;
+  const u64 body_end = len * 8 - k0 * kFixTileBits + skew;
+  const FixPeek pk{w, nwords};
+  sum[k * kFixEntries + e] = fix_scan(pk, rel + e, rel + kFixTileBits,
+                                      u32(min<u64>(body_end, 0xffffffffull)), false, rel);
+}
+
+}  // namespace
+
+// Summaries of the marked tiles (one wave per two tiles: lane e decodes the
+// first tile from its entry bit e, lane 32 + e the second), over the tiles
+// and a margin staged in LDS.  Waves take tile pairs grid-stride.
+__global__ __launch_bounds__(256) void g_fix_sum(const u8* body, u64 len, const State* st,
+                                                 const u32* need, FixSummary* sum, u64 tiles) {
+  __shared__ u32 words[kDescThreads / 64][kFixStageWords];
+  if (st->status || !st->fix_regions) return;
+  const u32 lane = lane_id(), wave = threadIdx.x >> 6;
+  const u64 waves = u64(gridDim.x) * (kDescThreads / 64);
+  for (u64 k0 = (u64(blockIdx.x) * (kDescThreads / 64) + wave) * 2; k0 < tiles; k0 += 2 * waves) {
+    const u32 pair = (need[k0 >> 5] >> (k0 & 31)) & 3u;  // k0 is even: one need word
+    if (pair) fix_sum_pair(body, len, need, sum, tiles, k0, pair, words[wave], lane);
+  }
+}
+
+
+
+namespace {
+
+constexpr u32 kFixBatch = 16;  // tiles of summaries a walk holds in LDS at once
+
+struct FixWalkShared {
+  FixSummary batch[kFixBatch][kFixEntries];
+  u32 words[kFixStageWords / 2 + 8];  // one tile and its margin, for decodes without a summary
+};
+
+// An atomic add by lane 0, its old value given to every lane.
+__device__ __forceinline__ u64 wave_fetch_add(u64* p, u64 v) {
+  u64 old = 0;
+  if (!lane_id()) old = atomicAdd(reinterpret_cast<unsigned long long*>(p), v);
+  return __shfl(old, 0, 64);
+}
+
+}  // namespace
+
+// One wave per region: continue the paused segment from the fixed block at
+// its seg_end.  Every lane follows the same walk (uniform loads; lane 0
+// stores), and the wave loads summaries and stages tiles together.  Fixed
+// runs are followed by summaries (a tile entered at a bit offset above 31, or
+// not marked, is decoded from the stage); stored blocks are parsed in place;
+// the segment ends at a final block, at a block boundary that is a candidate,
+// or at an error, as describe ends it.  Each finished run gets a block record
+// (kRecFixedRun) with consecutive slice groups and a FixRun; each of its tiles
+// a FixTile slot for g_fix_slices.  When records, groups or slots run out the
+// segment keeps no records (serial emission).
+__global__ __launch_bounds__(64) void g_fix_walk(
+    const u8* body, u64 len, State* st, const u64* cand, const u32* need, const FixSummary* sum,
+    u64 tiles, u64* seg_end, u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags,
+    u32* seg_rec, const u32* seg_last, const u32* region_cand, BlockRec* recs, u64 rec_capacity,
+    FixRun* runs, u64 run_capacity, FixTile* rt, u64 rt_capacity, u32* group_link,
+    u64 group_capacity, u64 out_size) {
+  __shared__ FixWalkShared sh;
+  if (st->status) return;
+  const u64 regions = st->fix_regions;
+  const u64 n = st->candidates;
+  const u32 lane = lane_id();
+  const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+  for (u64 ri = blockIdx.x; ri < regions; ri += gridDim.x) {
+    const u32 c = region_cand[ri];
+    u64 pos = seg_end[c];  // the header of the region's first fixed block
+    u64 out = seg_size[c];
+    u64 blocks = seg_blocks[c];
+    bool recs_ok = !(seg_flags[c] & kSegRecsLost);
+    u32 first_rec = seg_rec[c], last_rec = seg_last[c];
+    u64 search_from = c + 1;
+    const u64 start_pos = pos;
+    bool at_header = true, in_final = false, final_seg = false;
+    u32 status = 0, next = kNone;
+    bool run_on = false;
+    u64 run_hdr = 0, run_tok = 0, run_out0 = 0;
+    u32 run_id = kNone;
+    u64 slot_base = 0;
+    u32 slot_used = 64;
+    bool chunk = false;  // slots slot_base .. +63 are this walk's (unused ones marked at the end)
+    u64 batch_k = ~0ull;
+    // Finishes the open run at bit `e_end`: its record, slice groups and FixRun.
+    auto close_run = [&](u64 e_end) {
+      run_on = false;
+      if (run_id == kNone || !recs_ok) return;
+      const u64 b0 = run_tok / kFixSliceBits, bl = (e_end - 1) / kFixSliceBits;
+      const u64 lanes = bl - b0 + 1, ng = (lanes + 63) / 64;
+      const u64 g = wave_fetch_add(&st->groups_used, ng);
+      const u64 ri2 = wave_fetch_add(&st->recs_used, 1);
+      if (g + ng > group_capacity || ri2 >= rec_capacity || ri2 >= kNone || lanes >= kNone) {
+        recs_ok = false;
+        return;
+      }
+      for (u64 i = lane; i < ng; i += 64) group_link[g + i] = i + 1 < ng ? u32(g + i + 1) : kNone;
+      if (!lane) {
+        FixRun fr;
+        fr.tok = run_tok;
+        fr.end = e_end;
+        fr.b0 = b0;
+        fr.lanes = u32(lanes);
+        fr.group = u32(g);
+        fr.hdr = run_hdr;
+        fr.seg_off = run_out0;
+        fr.size = out - run_out0;
+        fr.cand = c;
+        fr.pad = 0;
+        runs[run_id] = fr;
+        BlockRec rec;
+        rec.start = run_hdr;
+        rec.data = run_tok;
+        rec.end = e_end;
+        rec.size = out - run_out0;
+        rec.type = 1;
+        rec.lanes = u32(lanes);
+        rec.group = u32(g);
+        rec.next = kNone;
+        rec.table = kNone;
+        rec.pad = kRecFixedRun;
+        recs[ri2] = rec;
+        if (last_rec != kNone) recs[last_rec].next = u32(ri2);
+      }
+      if (last_rec == kNone) first_rec = u32(ri2);
+      last_rec = u32(ri2);
+    };
+    for (;;) {
+      if (at_header) {
+        if (pos != start_pos) {  // a block boundary: a candidate there ends the segment
+          const u64 idx = lower_bound_from(cand, n, search_from, pos);
+          search_from = idx;
+          if (idx < n && cand[idx] == pos) {
+            next = u32(idx);
+            break;
+          }
+        }
+        BitIn h;
+        h.init(body, len, pos);
+        u32 fin = 0, type = 0;
+        if (!h.take(1, fin) || !h.take(2, type)) { status = kTruncated; break; }
+        if (type == 3) { status = kReservedBlock; break; }
+        if (type == 2) { status = kUndiscovered; break; }
+        if (++blocks > kMaxBlocks) { status = kBlockCapacity; break; }
+        if (type == 1) {
+          if (!run_on) {
+            run_on = true;
+            run_hdr = pos;
+            run_tok = pos + 3;
+            run_out0 = out;
+            run_id = kNone;
+            if (recs_ok) {
+              const u64 id = wave_fetch_add(&st->fix_runs, 1);
+              if (id < run_capacity) {
+                run_id = u32(id);
+                if (!lane) runs[id].lanes = 0;  // until the run is finished
+              } else {
+                recs_ok = false;
+              }
+            }
+          }
+          in_final = fin != 0;
+          pos += 3;
+          at_header = false;
+          continue;
+        }
+        // A stored block (RFC 1951 3.2.4), as describe_block reads it.
+        if (run_on) close_run(pos);
+        h.seek((h.pos + 7) & ~u64(7));
+        u32 nlen = 0, comp = 0;
+        if (!h.take(16, nlen) || !h.take(16, comp)) { status = kTruncated; break; }
+        if ((nlen ^ comp) != 0xffffu) { status = kBadSymbol; break; }
+        if (nlen > out_size - out) { status = kOutputOverflow; break; }
+        if (u64(nlen) * 8 > h.avail()) { status = kTruncated; break; }
+        if (recs_ok) {
+          const u64 ri2 = wave_fetch_add(&st->recs_used, 1);
+          if (ri2 >= rec_capacity || ri2 >= kNone) {
+            recs_ok = false;
+          } else {
+            if (!lane) {
+              BlockRec rec;
+              rec.start = pos;
+              rec.data = h.pos;
+              rec.end = h.pos + u64(nlen) * 8;
+              rec.size = nlen;
+              rec.type = 0;
+              rec.lanes = 0;
+              rec.group = kNone;
+              rec.next = kNone;
+              rec.table = kNone;
+              rec.pad = 0;
+              recs[ri2] = rec;
+              if (last_rec != kNone) recs[last_rec].next = u32(ri2);
+            }
+            if (last_rec == kNone) first_rec = u32(ri2);
+            last_rec = u32(ri2);
+          }
+        }
+        out += nlen;
+        pos = h.pos + u64(nlen) * 8;
+        if (fin) {
+          final_seg = true;
+          break;
+        }
+        continue;
+      }
+      // Inside a fixed run, at the token start `pos` of tile k.
+      if (pos >= len * 8) { status = kTruncated; break; }
+      const u64 k = pos / kFixTileBits;
+      const u32 e = u32(pos - k * kFixTileBits);
+      if (recs_ok && run_id != kNone) {
+        if (slot_used == 64) {
+          slot_base = wave_fetch_add(&st->fix_rt, 64);
+          slot_used = 0;
+          chunk = slot_base + 64 <= rt_capacity;
+          if (!chunk) {
+            // Mark what fits of the chunk unused, and keep no records.
+            if (slot_base + lane < rt_capacity) rt[slot_base + lane].run = kNone;
+            recs_ok = false;
+          }
+        }
+        if (recs_ok) {
+          if (!lane) {
+            FixTile ft;
+            ft.pos = pos;
+            ft.off = u32(out - run_out0);
+            ft.run = run_id;
+            ft.k = k;
+            rt[slot_base + slot_used] = ft;
+          }
+          ++slot_used;
+        }
+      }
+      FixSummary f;
+      const bool have = e < kFixEntries && k < tiles && ((need[k >> 5] >> (k & 31)) & 1u);
+      if (have) {
+        if (k < batch_k || k >= batch_k + kFixBatch) {
+          // The next kFixBatch tiles' summaries, 16 bytes a load.
+          const uint4* src = reinterpret_cast<const uint4*>(sum + k * kFixEntries);
+          uint4* dst = reinterpret_cast<uint4*>(&sh.batch[0][0]);
+          const u64 avail = min<u64>(kFixBatch, tiles - k) * kFixEntries;
+          for (u32 i = lane; i < kFixBatch * kFixEntries; i += 64)
+            if (i < avail) dst[i] = src[i];
+          wave_sync();
+          batch_k = k;
+        }
+        f = sh.batch[k - batch_k][e];
+        if (in_final && f.eob != kFixNoEob) {
+          // The stream's last block ends at its first EOB.
+          f.kind = kFixEnd;
+          f.exit = f.eob;
+          f.bytes = f.eob_bytes;
+          f.blocks = 0;
+        }
+      } else {
+        // Decode from the stage: tile k and its margin.
+        const u64 byte0 = k * (kFixTileBits / 8);
+        const u64 first_word = (base + byte0) >> 2;
+        u64 last_byte = byte0 + kFixTileBits / 8 + kFixMarginBytes;
+        if (last_byte > len) last_byte = len;
+        const u64 end_word = (base + last_byte + 3) >> 2;
+        const u32 nwords = u32(min<u64>(end_word > first_word ? end_word - first_word : 0,
+                                        kFixStageWords / 2 + 8));
+        const u32* gw = reinterpret_cast<const u32*>(first_word << 2);
+        wave_sync();  // earlier reads of the stage are done
+        for (u32 i = lane; i < nwords; i += 64) sh.words[i] = gw[i];
+        wave_sync();
+        const u32 skew = u32((base + byte0) & 3u) * 8;
+        const u64 body_end = len * 8 - k * kFixTileBits + skew;
+        const FixPeek pk{sh.words, nwords};
+        f = fix_scan(pk, skew + e, skew + kFixTileBits, u32(min<u64>(body_end, 0xffffffffull)),
+                     in_final, skew);
+      }
+      out += f.bytes;
+      blocks += f.blocks;
+      if (out > out_size) { status = kOutputOverflow; break; }
+      if (blocks > kMaxBlocks) { status = kBlockCapacity; break; }
+      const u32 kind = f.kind & 15u;
+      if (kind == kFixGo) {
+        in_final = (f.kind & kFixInFinal) != 0 || (have && in_final);
+        pos = k * kFixTileBits + f.exit;
+      } else if (kind == kFixEnd) {
+        pos = k * kFixTileBits + f.exit;
+        close_run(pos);
+        final_seg = true;
+        break;
+      } else if (kind == kFixHeader) {
+        pos = k * kFixTileBits + f.exit;
+        close_run(pos);
+        at_header = true;
+      } else {
+        pos = k * kFixTileBits + f.exit;
+        status = f.status ? f.status : u32(kBadSymbol);
+        break;
+      }
+    }
+    // Unused slots of the last chunk.
+    if (chunk && lane >= slot_used) rt[slot_base + lane].run = kNone;
+    if (!lane) {
+      seg_end[c] = pos;
+      seg_size[c] = out;
+      seg_blocks[c] = u32(min<u64>(blocks, 0xffffffffull));
+      seg_next[c] = next;
+      seg_flags[c] = status | (final_seg && !status ? 0x80000000u : 0u);
+      seg_rec[c] = recs_ok ? first_rec : kNone;
+    }
+    wave_sync();
+  }
+}
+
+// Slices of the walked runs: one thread per tile slot decodes the tile from
+// its true entry and places the slices whose 512-bit windows start inside
+// it (slice b - b0 of the run starts at the first token at or after bit
+// 512 b; where the run ends first, at the run's end, with nothing to decode).
+__global__ __launch_bounds__(256) void g_fix_slices(const u8* body, u64 len, const State* st,
+                                                    const FixTile* rt, u64 rt_capacity,
+                                                    const FixRun* runs, u64 run_capacity,
+                                                    u64* slice_entry, u32* slice_off) {
+  if (st->status || !st->fix_regions) return;
+  const u64 used = min<u64>(st->fix_rt, rt_capacity);
+  const u64 nruns = min<u64>(st->fix_runs, run_capacity);
+  const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+  const u32* words = reinterpret_cast<const u32*>(base & ~uintptr_t(3));
+  const u64 skew = u64(base & 3u) * 8;
+  const u64 nwords = (u64(base & 3u) + len + 3) / 4;
+  for (u64 i = u64(blockIdx.x) * blockDim.x + threadIdx.x; i < used;
+       i += u64(gridDim.x) * blockDim.x) {
+    const FixTile ft = rt[i];
+    if (ft.run == kNone || ft.run >= nruns) continue;
+    const FixRun run = runs[ft.run];
+    if (!run.lanes) continue;
+    const u64 bl = run.b0 + run.lanes - 1;
+    const u64 bf = max<u64>(run.b0, ft.k * kFixTileSlices);
+    const u64 bt = min<u64>(bl, ft.k * kFixTileSlices + kFixTileSlices - 1);
+    const u64 at = u64(run.group) * 64 - run.b0;  // slice index of window b: at + b
+    slice_entry[at + bf] = ft.pos;
+    slice_off[at + bf] = ft.off;
+    u64 p = ft.pos;
+    u32 off = ft.off;
+    // Windows up to bt; the tile whose decode reaches the run's end also
+    // places the windows after it (the run's last EOB may end past the tile).
+    const u64 tile_end = (ft.k + 1) * kFixTileBits;
+    for (u64 b = bf + 1; b <= bl;) {
+      if (p >= run.end || (b <= bt && p >= b * kFixSliceBits)) {
+        if (p > run.end) p = run.end;
+        slice_entry[at + b] = p;
+        slice_off[at + b] = off;
+        ++b;
+        continue;
+      }
+      if (b > bt && p >= tile_end) break;  // the next tile places the rest
+      // 64 body bits at p (bits past the body's words read as zero).
+      const u64 a = p + skew, wi = a >> 5;
+      const u32 sh = u32(a & 31u);
+      const u64 x0 = wi < nwords ? words[wi] : 0u, x1 = wi + 1 < nwords ? words[wi + 1] : 0u,
+                x2 = wi + 2 < nwords ? words[wi + 2] : 0u;
+      const u64 lo = x0 | (x1 << 32);
+      const u64 bits = sh ? (lo >> sh) | (x2 << (64 - sh)) : lo;
+      u32 nb, length, value;
+      const u32 kind = fixed_token(bits, nb, length, value);
+      if (kind == kKindBad) {
+        p = run.end;  // never on a walked run; emission then reports an extent error
+        continue;
+      }
+      if (kind == kKindEob) {
+        p = p + 7 >= run.end ? run.end : p + 10;  // past the next fixed header
+        continue;
+      }
+      off += length;
+      p += nb;
+    }
   }
 }
 
@@ -2177,7 +2812,7 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
                                                 u32* __restrict__ exit_node, u64 len,
                                                 u64 out_size, u32 max_blocks,
                                                 Segment* __restrict__ acc, u64 out_base,
-                                                OpenEnd open) {
+                                                OpenEnd open, u64* __restrict__ seg_prefix) {
   constexpr u32 kPer = kChainLdsNodes / 1024;  // candidates per thread in LDS mode
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
@@ -2374,12 +3009,14 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
     for (u32 i = 0; i < kPer; ++i) {
       const u64 c = lo + i;
       if (c < hi && c == cur) {
+        const u32 rf = seg_rec[c];
         acc[index].start = cand[c];
         acc[index].end = seg_end[c];
         acc[index].prefix = offset;
         acc[index].size = sz[i];
-        acc[index].rec_first = seg_rec[c];
+        acc[index].rec_first = rf;
         acc[index].rec_count = bl[i];
+        if (rf != kNone) seg_prefix[c] = offset;
         offset += sz[i];
         ++index;
         cur = lnext[c];
@@ -2388,12 +3025,14 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
   } else {
     u32 cur = entry[t];
     while (cur != kNone && cur < hi) {
+      const u32 rf = seg_rec[cur];
       acc[index].start = cand[cur];
       acc[index].end = seg_end[cur];
       acc[index].prefix = offset;
       acc[index].size = seg_size[cur];
-      acc[index].rec_first = seg_rec[cur];
+      acc[index].rec_first = rf;
       acc[index].rec_count = seg_blocks[cur];
+      if (rf != kNone) seg_prefix[cur] = offset;
       offset += seg_size[cur];
       ++index;
       cur = seg_next[cur];
@@ -2891,11 +3530,13 @@ struct MatchQueue {
 // Decode one slice [entry, stop) into out[dst0 ..], within the block's output
 // [.., block_end) of a stream whose output starts at out[floor]; adds the
 // slice's unresolved bytes to `unres_total`.  Returns 0 or an error.  `sh`
-// holds the block's tables and the staged bits.
+// holds the block's tables and the staged bits.  With `cross` (a run of
+// fixed blocks), an EOB before `stop` is followed by the next block's fixed
+// header, and decoding goes on after it.
 template <bool kChecked, class Shared, class Sink>
 __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u64 block_end,
                           u32 window, const Sink& out, u32* roots, u32* unres, u64& unres_total,
-                          u64 floor = 0) {
+                          u64 floor = 0, bool cross = false) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
   r.limit = blim;
@@ -2926,17 +3567,27 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
           live = false;
         } else if (!length) {
           live = false;
+          if (cross && w.pos() < stop) {
+            // The run's next block: a non-final or final fixed header.
+            if (w.avail() < 3 || ((w.bits32() >> 1) & 3u) != 1u) {
+              err = kExtent;
+            } else {
+              r.seek(w.pos() + 3);
+              live = true;
+              got = 0;  // no token to emit this step
+            }
+          }
         } else {
           r.seek(w.pos());
           x = length == 1 ? lit : distance;
           got = 1;
         }
       }
-      if (live && length + got - 1 > block_end - dst) {
+      if (live && got && length + got - 1 > block_end - dst) {
         err = kExtent;
         live = false;
       }
-      if (live) {
+      if (live && got) {
         if (length == 1) {
           out.put(dst++, u8(x));
           if (got >= 2) out.put(dst++, u8(x2));
@@ -2963,7 +3614,8 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
 // described slices in parallel, one slice per thread, with the tables that
 // describe stored (or rebuilt from the header), writing output in place.  A
 // byte copied from before its slice's output start is queued as unresolved
-// (root = source position).
+// (root = source position).  A run of fixed blocks (kRecFixedRun) decodes its
+// slices across the run's block headers.
 __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4))) void g_emit_lanes(
     const u8* body, u64 len, State* st, const Segment* acc, const BlockRec* recs,
     const u64* slice_entry, const u32* slice_off, const u32* group_link,
@@ -3003,6 +3655,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
           if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
         }
         bool tables_pending = rec.table != kNone;
+        const bool cross = (rec.pad & kRecFixedRun) != 0;
         u32 g = rec.group;
         u32 done = 0;
         while (g != kNone && done < rec.lanes) {
@@ -3066,10 +3719,10 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
               lerr = kExtent;  // offsets out of order: never from a consistent describe
             else if (stop + 64 <= len * 8)
               lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
-                                       unres, unres_total, floor);
+                                       unres, unres_total, floor, cross);
             else
               lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
-                                      unres, unres_total, floor);
+                                      unres, unres_total, floor, cross);
             sums.s += sink.acc.s;
             sums.w += sink.acc.w;
           }
@@ -3638,13 +4291,16 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 group_capacity = (len * 8) / 8192 + 65536;
   const u64 words = (out_total + 31) / 32 + 1;
   const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
+  // Fixed-run tiles of the body and their bitmap (zeroed with the rest).
+  const u64 tiles = (len * 8 + kFixTileBits - 1) / kFixTileBits;
+  const u64 need_words = tiles / 32 + 1;
   // Adler-32 partial pairs: kAdlerSlots each for the lane emitter, the
   // serial emitter and the resolve rounds (workgroups add theirs, so they
   // start at zero), summed by g_finish.  The pairs, the round counts and the
   // first unresolved bitmap are zeroed by g_frame.
   u8* zeroed = nullptr;
   const u64 zero_u64 = 2 * u64(3 * kAdlerSlots) + rounds + 1;
-  const u64 zero_bytes = 8 * zero_u64 + 4 * words;
+  const u64 zero_bytes = 8 * zero_u64 + 4 * words + 4 * need_words;
   HZ_TRY(scratch.alloc(&zeroed, zero_bytes));
   HZ_LAUNCH(g_frame, dim3(clamp_grid((zero_bytes / 4 + 255) / 256, 2048)), dim3(256), 0, stream,
             in, in_size, fmt.format, fmt.dict, fmt.dict_len, body_off, out_base, st,
@@ -3724,10 +4380,41 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
   HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
   HZ_TRY(scratch.alloc(&group_link, group_capacity));
+  u32 *seg_last = nullptr, *region_cand = nullptr;
+  u64* seg_prefix = nullptr;
+  HZ_TRY(scratch.alloc(&seg_last, cand_capacity));
+  HZ_TRY(scratch.alloc(&region_cand, cand_capacity));
+  HZ_TRY(scratch.alloc(&seg_prefix, cand_capacity));
+  u32* fix_need = reinterpret_cast<u32*>(zeroed + 8 * zero_u64 + 4 * words);
   HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kDescThreads), 0, stream, body, len,
             cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
             rec_capacity, slice_entry, slice_off, group_link, group_capacity, tables,
-            table_capacity, hdr_d0, hdr_info);
+            table_capacity, hdr_d0, hdr_info, seg_last, region_cand, seg_prefix);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_fix_mark, dim3(1), dim3(256), 0, stream, st, cand, len, seg_end, seg_flags,
+            region_cand, fix_need, tiles);
+  HZ_TRY(hipGetLastError());
+
+  // Long fixed-Huffman runs deferred by describe (each launch returns at once
+  // when there are none).
+  FixSummary* fix_sum = nullptr;
+  FixRun* fix_runs = nullptr;
+  FixTile* fix_rt = nullptr;
+  const u64 run_capacity = cand_capacity + 1024;
+  const u64 rt_capacity = tiles + 64 * 4096;
+  HZ_TRY(scratch.alloc(&fix_sum, (tiles ? tiles : 1) * kFixEntries));
+  HZ_TRY(scratch.alloc(&fix_runs, run_capacity));
+  HZ_TRY(scratch.alloc(&fix_rt, rt_capacity));
+  HZ_LAUNCH(g_fix_sum, dim3(clamp_grid((tiles + 7) / 8, 2048)), dim3(256), 0, stream, body, len,
+            st, fix_need, fix_sum, tiles);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_fix_walk, dim3(clamp_grid(cand_capacity, 2048)), dim3(kWave), 0, stream, body, len, st,
+            cand, fix_need, fix_sum, tiles, seg_end, seg_size, seg_blocks, seg_next, seg_flags,
+            seg_rec, seg_last, region_cand, recs, rec_capacity, fix_runs, run_capacity, fix_rt,
+            rt_capacity, group_link, group_capacity, out_size);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_fix_slices, dim3(clamp_grid((rt_capacity + 255) / 256, 2048)), dim3(256), 0, stream,
+            body, len, st, fix_rt, rt_capacity, fix_runs, run_capacity, slice_entry, slice_off);
   HZ_TRY(hipGetLastError());
 
   // Chain selection, then the exact walk if the fast chain declined.
@@ -3735,7 +4422,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
   HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size, seg_blocks,
             seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc, out_base,
-            open);
+            open, seg_prefix);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size, max_blocks,
             acc, out_base, open);
