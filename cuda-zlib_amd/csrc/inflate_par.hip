@@ -1312,11 +1312,6 @@ struct FixRun {
   u64 b0;
   u32 lanes;
   u32 group;    // first of the run's consecutive slice groups
-  u64 hdr;      // header bit of the run's first block
-  u64 seg_off;  // output offset of the run inside its segment
-  u64 size;     // output bytes
-  u32 cand;     // the candidate whose segment holds the run
-  u32 pad;
 };
 
 // One tile of a run: its true entry and the run's output bytes before it.
@@ -2207,7 +2202,7 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
     u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags, u32* seg_rec, BlockRec* recs,
     u64 rec_capacity, u64* slice_entry, u32* slice_off, u32* group_link, u64 group_capacity,
     BlockTables* tables, u64 table_capacity, const u64* hdr_d0, const u32* hdr_info,
-    u32* seg_last, u32* region_cand, u64* seg_prefix) {
+    u32* seg_last, u32* region_cand) {
   __shared__ DescShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -2353,7 +2348,6 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
       if (!sh.go) break;
     }
     if (!t) {
-      seg_prefix[c] = ~0ull;  // set by g_chain for segments on the path
       if (paused) {
         seg_end[c] = sh.pos;
         seg_size[c] = produced;
@@ -2524,11 +2518,6 @@ __global__ __launch_bounds__(64) void g_fix_walk(
         fr.b0 = b0;
         fr.lanes = u32(lanes);
         fr.group = u32(g);
-        fr.hdr = run_hdr;
-        fr.seg_off = run_out0;
-        fr.size = out - run_out0;
-        fr.cand = c;
-        fr.pad = 0;
         runs[run_id] = fr;
         BlockRec rec;
         rec.start = run_hdr;
@@ -2812,7 +2801,7 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
                                                 u32* __restrict__ exit_node, u64 len,
                                                 u64 out_size, u32 max_blocks,
                                                 Segment* __restrict__ acc, u64 out_base,
-                                                OpenEnd open, u64* __restrict__ seg_prefix) {
+                                                OpenEnd open) {
   constexpr u32 kPer = kChainLdsNodes / 1024;  // candidates per thread in LDS mode
   __shared__ u32 entry[1024];
   __shared__ u64 psize[1024], pblocks[1024], pcount[1024];
@@ -3009,14 +2998,12 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
     for (u32 i = 0; i < kPer; ++i) {
       const u64 c = lo + i;
       if (c < hi && c == cur) {
-        const u32 rf = seg_rec[c];
         acc[index].start = cand[c];
         acc[index].end = seg_end[c];
         acc[index].prefix = offset;
         acc[index].size = sz[i];
-        acc[index].rec_first = rf;
+        acc[index].rec_first = seg_rec[c];
         acc[index].rec_count = bl[i];
-        if (rf != kNone) seg_prefix[c] = offset;
         offset += sz[i];
         ++index;
         cur = lnext[c];
@@ -3025,14 +3012,12 @@ __global__ __launch_bounds__(1024) void g_chain(State* st, const u64* __restrict
   } else {
     u32 cur = entry[t];
     while (cur != kNone && cur < hi) {
-      const u32 rf = seg_rec[cur];
       acc[index].start = cand[cur];
       acc[index].end = seg_end[cur];
       acc[index].prefix = offset;
       acc[index].size = seg_size[cur];
-      acc[index].rec_first = rf;
+      acc[index].rec_first = seg_rec[cur];
       acc[index].rec_count = seg_blocks[cur];
-      if (rf != kNone) seg_prefix[cur] = offset;
       offset += seg_size[cur];
       ++index;
       cur = seg_next[cur];
@@ -4381,15 +4366,13 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
   HZ_TRY(scratch.alloc(&group_link, group_capacity));
   u32 *seg_last = nullptr, *region_cand = nullptr;
-  u64* seg_prefix = nullptr;
   HZ_TRY(scratch.alloc(&seg_last, cand_capacity));
   HZ_TRY(scratch.alloc(&region_cand, cand_capacity));
-  HZ_TRY(scratch.alloc(&seg_prefix, cand_capacity));
   u32* fix_need = reinterpret_cast<u32*>(zeroed + 8 * zero_u64 + 4 * words);
   HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kDescThreads), 0, stream, body, len,
             cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
             rec_capacity, slice_entry, slice_off, group_link, group_capacity, tables,
-            table_capacity, hdr_d0, hdr_info, seg_last, region_cand, seg_prefix);
+            table_capacity, hdr_d0, hdr_info, seg_last, region_cand);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_fix_mark, dim3(1), dim3(256), 0, stream, st, cand, len, seg_end, seg_flags,
             region_cand, fix_need, tiles);
@@ -4422,7 +4405,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&acc, u64(max_blocks) + 1));
   HZ_LAUNCH(g_chain, dim3(1), dim3(1024), 0, stream, st, cand, seg_end, seg_size, seg_blocks,
             seg_next, seg_flags, seg_rec, exit_node, len, out_size, max_blocks, acc, out_base,
-            open, seg_prefix);
+            open);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_exact_walk, dim3(1), dim3(kWave), 0, stream, body, len, st, out_size, max_blocks,
             acc, out_base, open);
