@@ -161,6 +161,12 @@ class DeviceScope {
 constexpr u64 kArenaGranule = 64ull << 20;
 // Batch files of at least this many output bytes decode by parallel slices.
 constexpr u64 kBatchWideBytes = 256;
+// Single streams of the small route with at least this many output bytes are
+// decoded by the parallel route first; the serial one-wave decoder (the
+// reference's small route, codec_ffi.cu:681-693) runs only when that reports
+// a failure, to give its status and its failed output (decoded prefix, then
+// zeros).  Below it the serial decoder alone is faster than the launches.
+constexpr u64 kSmallParallelBytes = 256;
 
 // Stream-ordered scratch for one call, carved from an arena of the device
 // (taken on the first allocation).  Requests the arena cannot hold come from
@@ -396,11 +402,20 @@ extern "C" int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int
       return fail(kInvalidBounds);
     if (input_size < 8) return fail(kTruncatedZlib);
     const bool default_limits = max_candidates == kMaxCandidates && max_blocks == kMaxBlocks;
-    // Small streams decode serially in one wave (the reference's small route,
-    // codec_ffi.cu:681-693); everything else takes the parallel route.
-    if (default_limits && output_size <= 65536 && input_size <= 131072)
+    // The reference's small route (codec_ffi.cu:681-693): tiny streams decode
+    // serially in one wave; the others take the parallel route first, and the
+    // serial decoder redoes only a failed one.  Everything else takes the
+    // parallel route.
+    if (default_limits && output_size <= 65536 && input_size <= 131072) {
+      if (output_size < kSmallParallelBytes)
+        return launch_inflate_single(stream, input, input_size, output, output_size,
+                                     u32(max_blocks), metadata);
+      hipError_t err = run_inflate_general(stream, ws, input, input_size, output, output_size,
+                                           u32(max_candidates), u32(max_blocks), metadata);
+      if (err != hipSuccess) return err;
       return launch_inflate_single(stream, input, input_size, output, output_size,
-                                   u32(max_blocks), metadata);
+                                   u32(max_blocks), metadata, kFormatZlib, nullptr, 0, true);
+    }
     return run_inflate_general(stream, ws, input, input_size, output, output_size,
                                u32(max_candidates), u32(max_blocks), metadata);
   });
@@ -440,10 +455,20 @@ extern "C" int HipZlibDecompressFormat(hipStream_t stream, int32_t format,
     const u64 fixed = format == kFormatZlib ? 8 : format == kFormatGzip ? 18 : 0;
     if (input_size < fixed) return fail(kTruncatedZlib);
     const bool default_limits = max_candidates == kMaxCandidates && max_blocks == kMaxBlocks;
-    if (default_limits && output_size <= 65536 && input_size <= 131072)
+    if (default_limits && output_size <= 65536 && input_size <= 131072) {
+      // As HipZlibDecompress's small route; with a dictionary, serially.
+      if (output_size < kSmallParallelBytes || dictionary_size)
+        return launch_inflate_single(stream, input, input_size, output, output_size,
+                                     u32(max_blocks), metadata, u32(format), dictionary,
+                                     dictionary_size);
+      StreamFormat first;
+      first.format = u32(format);
+      hipError_t err = run_inflate_general(stream, ws, input, input_size, output, output_size,
+                                           u32(max_candidates), u32(max_blocks), metadata, first);
+      if (err != hipSuccess) return err;
       return launch_inflate_single(stream, input, input_size, output, output_size,
-                                   u32(max_blocks), metadata, u32(format), dictionary,
-                                   dictionary_size);
+                                   u32(max_blocks), metadata, u32(format), nullptr, 0, true);
+    }
     StreamFormat fmt;
     fmt.format = u32(format);
     fmt.dict = dictionary;

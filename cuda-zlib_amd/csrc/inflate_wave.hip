@@ -364,12 +364,16 @@ constexpr u64 kBatchStage = 2048;
 
 }  // namespace
 
+// With `redo`, the stream was already decoded by the parallel route, which
+// left its status in meta[0]: the kernel decodes it again only when that
+// status is not 0, to give the serial route's status and failed output.
 __global__ __launch_bounds__(64) void inflate_single_kernel(const u8* in, u64 in_size, u8* out,
                                                             u64 out_size, u32 max_blocks,
                                                             u32* meta, u32 format, const u8* dict,
-                                                            u64 dict_len) {
+                                                            u64 dict_len, u32 redo) {
   __shared__ WaveShared sh;
   __shared__ __align__(16) u8 stage[kSingleStage];
+  if (redo && !meta[0]) return;  // uniform
   WaveFormat fmt;
   fmt.format = format;
   fmt.dict = dict;
@@ -420,9 +424,9 @@ __global__ __launch_bounds__(64) void inflate_batch_kernel(const u8* in, u8* out
 
 hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
                                  u64 out_size, u32 max_blocks, u32* meta, u32 format,
-                                 const u8* dict, u64 dict_len) {
+                                 const u8* dict, u64 dict_len, bool redo) {
   HZ_LAUNCH(inflate_single_kernel, dim3(1), dim3(kWave), 0, stream, in, in_size, out,
-                     out_size, max_blocks, meta, format, dict, dict_len);
+                     out_size, max_blocks, meta, format, dict, dict_len, redo ? 1u : 0u);
   return hipGetLastError();
 }
 

@@ -44,11 +44,13 @@ hipError_t launch_set_meta_rows(hipStream_t stream, u32* meta, u64 rows, u32 fir
 // inflate_wave.hip: serial-route decode (one wave per stream).
 // format: kFormatZlib / kFormatRaw / kFormatGzip; dict (dict_len bytes, device)
 // is the preset dictionary of a zlib stream with FDICT or the history of a
-// raw stream (null and 0: none).
+// raw stream (null and 0: none).  With `redo`, meta[0] already holds the
+// parallel route's status for the same stream, and the serial decode runs
+// only when it is not 0.
 hipError_t launch_inflate_single(hipStream_t stream, const u8* in, u64 in_size, u8* out,
                                  u64 out_size, u32 max_blocks, u32* meta,
                                  u32 format = kFormatZlib, const u8* dict = nullptr,
-                                 u64 dict_len = 0);
+                                 u64 dict_len = 0, bool redo = false);
 // Files of at least skip_from output bytes are skipped; with `list`, only the
 // listed files whose `redo` flag is set are decoded.
 hipError_t launch_inflate_batch(hipStream_t stream, const u8* in, u8* out, const BatchFile* files,
