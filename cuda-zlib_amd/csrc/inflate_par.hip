@@ -144,7 +144,7 @@ using Stage = StageT<kStageWords>;
 // (capped at the body end and at the stage capacity).  Every thread of the
 // workgroup takes part.
 template <u32 W>
-__device__ void stage_range(const u8* body, u64 len, u64 bit0, u64 bit1, StageT<W>& sg,
+__device__ __forceinline__ void stage_range(const u8* body, u64 len, u64 bit0, u64 bit1, StageT<W>& sg,
                             u64 margin = kStageMargin) {
   const uintptr_t base = reinterpret_cast<uintptr_t>(body);
   const u64 first_word = (base + (bit0 >> 3)) >> 2;
@@ -1341,7 +1341,7 @@ struct FixPeek {
 // result are relative to `rel0`.  With kMaxTokens, a decode that has taken
 // that many tokens stops as if it had reached `stop` (the probe).
 template <u32 kMaxTokens = 0>
-__device__ FixSummary fix_scan(const FixPeek& pk, u32 p, u32 stop, u32 body_end, bool in_final,
+__device__ __forceinline__ FixSummary fix_scan(const FixPeek& pk, u32 p, u32 stop, u32 body_end, bool in_final,
                                u32 rel0) {
   FixSummary s;
   s.bytes = 0;
@@ -2247,7 +2247,8 @@ __global__ __launch_bounds__(kDescThreads) void g_describe(
       if (sh.type == 1 && !sh.status) {  // uniform
         // Probe the fixed run: a long one becomes a region.  Decoding garbage
         // (a header look-alike's block) meets an invalid code within a few
-        // dozen tokens, so regions start only on real fixed data.
+        // dozen tokens, so regions start only on real fixed data.  The scan is
+        // inlined: as an outlined call it cost the pass a fifth of its time.
         constexpr u64 kProbeBits = u64(kFixProbeTokens) * 34;
         if (!staged_covers(sh.stage, body, len, sh.d0, sh.d0 + kProbeBits)) {
           __syncthreads();
