@@ -3319,7 +3319,7 @@ struct LaneEmitShared {
   u64 first, chunk_end, round_lo, round_hi;
   u32 count, next_g, need;
   u64 red[2][kEmitThreads / 64];
-  __align__(16) u8 ostage[kOutStage + 16];
+  __align__(16) u8 ostage[kOutStage + 16];  // a whole number of 16-byte lines
   // block_header interface
   u64 pos, d0, end, size;
   u32 type, final_block, status, nl, nd, build_status;
@@ -3371,7 +3371,9 @@ struct StagedBytes {
 
 // A round's output: positions [base, base + kOutStage) in the LDS stage
 // (copied out and summed when the round is done), later ones straight to
-// the output buffer (summed as they are written).
+// the output buffer (summed as they are written).  The stage is all zero
+// when a round starts (the copy-out clears what it read), so the bytes a
+// resolve round provides are zero without a store each.
 struct RoundBytes {
   u8* lds;
   u64 base, split;  // split = base + stage bytes
@@ -3390,11 +3392,21 @@ struct RoundBytes {
       acc.add_byte_unfolded(v, end - p);  // folded once per round (at most 2^18 bytes a thread)
     }
   }
-  __device__ __forceinline__ void zero(u64 p, u32 n) const {
-    for (u32 j = 0; j < n; ++j)
-      if (p + j < split) lds[u32(p + j - base)] = 0;
-  }
+  __device__ __forceinline__ void zero(u64, u32) const {}
 };
+
+// roots[dst + j] = root + j * step for j < n, four roots a store where the
+// positions are 16-byte aligned (a run's positions are its own: no other
+// thread writes them).
+__device__ __forceinline__ void roots_fill(u32* roots, u64 dst, u32 n, u32 root, u32 step) {
+  u32 j = 0;
+  for (; j < n && ((dst + j) & 3u); ++j) roots[dst + j] = root + j * step;
+  for (; j + 4 <= n; j += 4) {
+    const u32 r = root + j * step;
+    *reinterpret_cast<uint4*>(roots + dst + j) = make_uint4(r, r + step, r + 2 * step, r + 3 * step);
+  }
+  for (; j < n; ++j) roots[dst + j] = root + j * step;
+}
 
 // out[dst + j] = out[src0 + j] for j < length where src0 + distance = dst:
 // an overlapping copy repeats the first `distance` bytes, so every byte is
@@ -3437,7 +3449,7 @@ __device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u
   const u64 src0 = dst - distance;
   if (src0 + length <= dst0) {
     // Every source precedes the slice: unresolved, rooted at the source.
-    for (u32 j = 0; j < length; ++j) roots[dst + j] = u32(src0 + j);
+    roots_fill(roots, dst, length, u32(src0), 1);
     bits_set_range(unres, dst, length);
     out.zero(dst, length);
     nunres += length;
@@ -3450,7 +3462,7 @@ __device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u
     const bool before = p < dst0;
     if (before || (nunres && bit_get(unres, p))) {
       const u32 root = before ? u32(p) : roots[p];
-      for (u32 j = 0; j < length; ++j) roots[dst + j] = root;
+      roots_fill(roots, dst, length, root, 0);
       bits_set_range(unres, dst, length);
       out.zero(dst, length);
       nunres += length;
@@ -3614,6 +3626,10 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
   const u64 floor = st->floor;
   u64 unres_total = 0;  // this thread's unresolved bytes, counted once per wave at the end
   AdlerAcc sums;        // Adler-32 sums of the bytes this thread writes
+  // The output stage starts all zero (ordered before the first round by the
+  // barrier of its segment's set-up).
+  for (u32 k = t; 16 * k < sizeof(sh.ostage); k += kEmitThreads)
+    *reinterpret_cast<uint4*>(sh.ostage + 16 * k) = make_uint4(0, 0, 0, 0);
   for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
     const Segment seg = acc[si];
     if (seg.rec_first == kNone) continue;
@@ -3731,6 +3747,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
                 sums.add_byte(v, out_end - (a + j));
               }
             }
+            *reinterpret_cast<uint4*>(sh.ostage + r0) = make_uint4(0, 0, 0, 0);  // for the next round
           }
           done += count;
           g = sh.next_g;
