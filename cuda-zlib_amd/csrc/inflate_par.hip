@@ -74,6 +74,7 @@ struct State {
   u64 fix_regions;
   u64 fix_runs;
   u64 fix_rt;
+  u64 fix_tasks;  // remainder tasks queued by the summary pass
 };
 
 // An open-ended decode's stream may end before the input does (other members
@@ -638,6 +639,7 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   st->fix_regions = 0;
   st->fix_runs = 0;
   st->fix_rt = 0;
+  st->fix_tasks = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -1280,6 +1282,7 @@ constexpr u32 kFixEntries = 32;
 constexpr u32 kFixSliceBits = 512;
 constexpr u32 kFixTileSlices = kFixTileBits / kFixSliceBits;
 constexpr u32 kFixProbeTokens = 512;  // tokens a fixed block is probed before it is deferred
+constexpr u32 kFixSyncBits = 256;     // entries decoded apart before those that meet share a task
 constexpr u32 kFixMarginBytes = 64;   // staged past a tile: its last token, an EOB and a header
 constexpr u32 kFixStageWords = (2 * kFixTileBits / 8 + kFixMarginBytes) / 4 + 4;
 enum : u32 { kFixGo = 0, kFixEnd = 1, kFixHeader = 2, kFixError = 3 };
@@ -1302,6 +1305,31 @@ struct FixSummary {
   u8 status;      // kFixError: the status
 };
 static_assert(sizeof(FixSummary) == 16, "summary layout");
+
+// The rest of one tile for the entries whose decodes reached the same token
+// start `p` (tile-relative, at or after kFixSyncBits) in the same state.
+struct FixTask {
+  u64 tile;
+  u32 entries;  // bit e: entry e
+  u16 p;
+  u16 in_final;
+};
+static_assert(sizeof(FixTask) == 16, "task layout");
+
+// A decode's summary from its prefix p (which ended, kind kFixGo, where r
+// starts) and the rest r.
+__device__ __forceinline__ FixSummary fix_join(const FixSummary& p, const FixSummary& r) {
+  FixSummary s;
+  const bool had_eob = p.eob != kFixNoEob;
+  s.bytes = p.bytes + r.bytes;
+  s.eob_bytes = had_eob ? p.eob_bytes : p.bytes + r.eob_bytes;
+  s.exit = r.exit;
+  s.eob = had_eob ? p.eob : r.eob;
+  s.blocks = u16(p.blocks + r.blocks);
+  s.kind = r.kind;
+  s.status = r.status;
+  return s;
+}
 
 // A run of fixed blocks on a walked path, for the slice pass: its slices are
 // the 512-bit windows b0 .. b0 + lanes - 1 (slice i starts at the first token
@@ -2396,9 +2424,22 @@ __global__ __launch_bounds__(256) void g_fix_mark(const State* st, const u64* ca
 
 namespace {
 
-// One wave's tile pair for g_fix_sum.
+__device__ __forceinline__ u64 wave_fetch_add(u64* p, u64 v) {
+  u64 old = 0;
+  if (!lane_id()) old = atomicAdd(reinterpret_cast<unsigned long long*>(p), v);
+  return __shfl(old, 0, 64);
+}
+
+// One wave's tile pair for g_fix_sum.  Every entry decodes to the first token
+// start at or after kFixSyncBits; entries that reach the same one in the same
+// state decode the same rest of the tile, which the lowest of them queues as
+// one task for g_fix_rem (with the queue full, each entry decodes it here).
+// The summaries of queued entries hold their prefixes until g_fix_rem joins
+// the rest.  Fixed codes resynchronize slowly: after 256 bits the 32 entries
+// of a tile typically still follow one to three token paths.
 __device__ void fix_sum_pair(const u8* body, u64 len, const u32* need, FixSummary* sum, u64 tiles,
-                             u64 k0, u32 pair, u32* w, u32 lane) {
+                             u64 k0, u32 pair, u32* w, u32 lane, State* st, FixTask* tasks,
+                             u64 task_capacity) {
   // The wave stages body bits [k0 T, (k0 + 2) T) and the margin.
   const uintptr_t base = reinterpret_cast<uintptr_t>(body);
   const u64 byte0 = k0 * (kFixTileBits / 8);
@@ -2413,13 +2454,43 @@ __device__ void fix_sum_pair(const u8* body, u64 len, const u32* need, FixSummar
   wave_sync();
   const u32 half = lane >> 5, e = lane & 31u;
   const u64 k = k0 + half;
-  if (k >= tiles || !((pair >> half) & 1u)) return;
+  const bool mine = k < tiles && ((pair >> half) & 1u);
   const u32 skew = u32((base + byte0) & 3u) * 8;  // stage bit of body bit k0 T
   const u32 rel = skew + half * kFixTileBits;
-  const u64 body_end = len * 8 - k0 * kFixTileBits + skew;
+  const u32 body_end = u32(min<u64>(len * 8 - k0 * kFixTileBits + skew, 0xffffffffull));
   const FixPeek pk{w, nwords};
-  sum[k * kFixEntries + e] = fix_scan(pk, rel + e, rel + kFixTileBits,
-                                      u32(min<u64>(body_end, 0xffffffffull)), false, rel);
+  FixSummary f{};
+  if (mine) f = fix_scan(pk, rel + e, rel + kFixSyncBits, body_end, false, rel);
+  const bool go = mine && (f.kind & 15u) == kFixGo;
+  const u32 key = go ? u32(f.exit) | ((f.kind & kFixInFinal) ? 1u << 16 : 0u) | (half << 17) : ~0u;
+  // Each lane's representative: the lowest lane with its key.
+  u32 rep = lane, entries = 0;
+  for (u64 todo = __ballot(go); todo;) {
+    const u32 l = u32(__builtin_ctzll(todo));
+    const u32 kl = __shfl(key, int(l), 64);
+    const u64 same = __ballot(key == kl);
+    todo &= ~same;
+    if (key == kl) rep = l;
+    if (lane == l) entries = u32(same >> (32 * half));
+  }
+  const bool lead = go && rep == lane;
+  const u64 leads = __ballot(lead);
+  const u64 slot0 = leads ? wave_fetch_add(&st->fix_tasks, u64(__popcll(leads))) : 0;
+  const u64 slot = slot0 + u64(__popcll(leads & ((1ull << lane) - 1)));
+  const bool queued = lead && slot < task_capacity;
+  if (queued) {
+    FixTask tk;
+    tk.tile = k;
+    tk.entries = entries;
+    tk.p = f.exit;
+    tk.in_final = (f.kind & kFixInFinal) ? 1 : 0;
+    tasks[slot] = tk;
+  }
+  const u64 taken = __ballot(queued);
+  if (go && !((taken >> rep) & 1u))
+    f = fix_join(f, fix_scan(pk, rel + f.exit, rel + kFixTileBits, body_end,
+                             (f.kind & kFixInFinal) != 0, rel));
+  if (mine) sum[k * kFixEntries + e] = f;
 }
 
 }  // namespace
@@ -2427,15 +2498,49 @@ __device__ void fix_sum_pair(const u8* body, u64 len, const u32* need, FixSummar
 // Summaries of the marked tiles (one wave per two tiles: lane e decodes the
 // first tile from its entry bit e, lane 32 + e the second), over the tiles
 // and a margin staged in LDS.  Waves take tile pairs grid-stride.
-__global__ __launch_bounds__(256) void g_fix_sum(const u8* body, u64 len, const State* st,
-                                                 const u32* need, FixSummary* sum, u64 tiles) {
+__global__ __launch_bounds__(256) void g_fix_sum(const u8* body, u64 len, State* st,
+                                                 const u32* need, FixSummary* sum, u64 tiles,
+                                                 FixTask* tasks, u64 task_capacity) {
   __shared__ u32 words[kDescThreads / 64][kFixStageWords];
   if (st->status || !st->fix_regions) return;
   const u32 lane = lane_id(), wave = threadIdx.x >> 6;
   const u64 waves = u64(gridDim.x) * (kDescThreads / 64);
   for (u64 k0 = (u64(blockIdx.x) * (kDescThreads / 64) + wave) * 2; k0 < tiles; k0 += 2 * waves) {
     const u32 pair = (need[k0 >> 5] >> (k0 & 31)) & 3u;  // k0 is even: one need word
-    if (pair) fix_sum_pair(body, len, need, sum, tiles, k0, pair, words[wave], lane);
+    if (pair)
+      fix_sum_pair(body, len, need, sum, tiles, k0, pair, words[wave], lane, st, tasks,
+                   task_capacity);
+  }
+}
+
+// The queued rests of tiles: one thread per task decodes from the task's
+// token start to the tile's end (the body read through the cache) and joins
+// the result to the summaries of the task's entries.
+__global__ __launch_bounds__(256) void g_fix_rem(const u8* body, u64 len, const State* st,
+                                                 const FixTask* tasks, u64 task_capacity,
+                                                 FixSummary* sum) {
+  if (st->status || !st->fix_regions) return;
+  const u64 n = min<u64>(st->fix_tasks, task_capacity);
+  const uintptr_t base = reinterpret_cast<uintptr_t>(body);
+  for (u64 i = u64(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += u64(gridDim.x) * blockDim.x) {
+    const FixTask tk = tasks[i];
+    // The tile and its margin, as g_fix_sum staged them.
+    const u64 byte0 = tk.tile * (kFixTileBits / 8);
+    const u64 first_word = (base + byte0) >> 2;
+    u64 last_byte = byte0 + kFixTileBits / 8 + kFixMarginBytes;
+    if (last_byte > len) last_byte = len;
+    const u64 end_word = (base + last_byte + 3) >> 2;
+    const u32 nwords = u32(end_word > first_word ? end_word - first_word : 0);
+    const u32 skew = u32((base + byte0) & 3u) * 8;
+    const u32 body_end = u32(min<u64>(len * 8 - tk.tile * kFixTileBits + skew, 0xffffffffull));
+    const FixPeek pk{reinterpret_cast<const u32*>(first_word << 2), nwords};
+    const FixSummary r =
+        fix_scan(pk, skew + tk.p, skew + kFixTileBits, body_end, tk.in_final != 0, skew);
+    for (u32 m = tk.entries; m; m &= m - 1) {
+      FixSummary* s = sum + tk.tile * kFixEntries + __builtin_ctz(m);
+      *s = fix_join(*s, r);
+    }
   }
 }
 
@@ -2451,12 +2556,6 @@ struct FixWalkShared {
 };
 
 // An atomic add by lane 0, its old value given to every lane.
-__device__ __forceinline__ u64 wave_fetch_add(u64* p, u64 v) {
-  u64 old = 0;
-  if (!lane_id()) old = atomicAdd(reinterpret_cast<unsigned long long*>(p), v);
-  return __shfl(old, 0, 64);
-}
-
 }  // namespace
 
 // One wave per region: continue the paused segment from the fixed block at
@@ -4403,11 +4502,17 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   FixTile* fix_rt = nullptr;
   const u64 run_capacity = cand_capacity + 1024;
   const u64 rt_capacity = tiles + 64 * 4096;
+  FixTask* fix_tasks = nullptr;
+  const u64 task_capacity = 4 * tiles + 4096;  // beyond it, g_fix_sum decodes the rests itself
   HZ_TRY(scratch.alloc(&fix_sum, (tiles ? tiles : 1) * kFixEntries));
+  HZ_TRY(scratch.alloc(&fix_tasks, task_capacity));
   HZ_TRY(scratch.alloc(&fix_runs, run_capacity));
   HZ_TRY(scratch.alloc(&fix_rt, rt_capacity));
   HZ_LAUNCH(g_fix_sum, dim3(clamp_grid((tiles + 7) / 8, 2048)), dim3(256), 0, stream, body, len,
-            st, fix_need, fix_sum, tiles);
+            st, fix_need, fix_sum, tiles, fix_tasks, task_capacity);
+  HZ_TRY(hipGetLastError());
+  HZ_LAUNCH(g_fix_rem, dim3(clamp_grid((task_capacity + 255) / 256, 2048)), dim3(256), 0, stream,
+            body, len, st, fix_tasks, task_capacity, fix_sum);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_fix_walk, dim3(clamp_grid(cand_capacity, 2048)), dim3(kWave), 0, stream, body, len, st,
             cand, fix_need, fix_sum, tiles, seg_end, seg_size, seg_blocks, seg_next, seg_flags,
