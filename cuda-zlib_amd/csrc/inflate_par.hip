@@ -75,6 +75,7 @@ struct State {
   u64 fix_runs;
   u64 fix_rt;
   u64 fix_tasks;  // remainder tasks queued by the summary pass
+  u64 emit_units;  // emission units of long fixed runs queued for the unit pass
 };
 
 // An open-ended decode's stream may end before the input does (other members
@@ -640,6 +641,7 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   st->fix_runs = 0;
   st->fix_rt = 0;
   st->fix_tasks = 0;
+  st->emit_units = 0;
 }
 
 // Discovery pass 1, per 2 KiB range: prefiltered offsets in order (kind 0,
@@ -3404,6 +3406,23 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
 
 namespace {
 constexpr u32 kEmitThreads = kDescThreads;
+// A long fixed run is emitted in units of this many slices (two rounds): its
+// segment's workgroup takes the first and queues the others for the unit
+// pass, so that the run spreads over the grid.
+constexpr u32 kUnitLanes = 2 * kEmitThreads;
+// Longest slice emission accepts, in bits (describe's slices are at most
+// 512 bits plus a token, a fixed run's windows 512 bits plus a token and an
+// end of block with its header): a longer one is an extent error.
+constexpr u64 kMaxEmitSlice = 4096;
+
+// Slices first .. first + kUnitLanes - 1 (at most) of the run in record
+// `rec`, whose output starts at block_out.  rec = kNone: a slot reserved
+// past the queue's end, skipped.
+struct EmitUnit {
+  u64 block_out;
+  u32 rec;
+  u32 first;
+};
 
 // Output bytes of one round (256 slices) that g_emit_lanes stages in LDS
 // before writing them out in 16-byte stores; rounds with more output write
@@ -3415,8 +3434,8 @@ struct LaneEmitShared {
   Stage stage;
   u16 codes[320];
   BlockRec rec;
-  u64 first, chunk_end, round_lo, round_hi;
-  u32 count, next_g, need;
+  u64 first, chunk_end, round_lo, round_hi, unit_q;
+  u32 count, next_g, need, unit_end, unit_more;
   u64 red[2][kEmitThreads / 64];
   __align__(16) u8 ostage[kOutStage + 16];  // a whole number of 16-byte lines
   // block_header interface
@@ -3716,11 +3735,12 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
 __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4))) void g_emit_lanes(
     const u8* body, u64 len, State* st, const Segment* acc, const BlockRec* recs,
     const u64* slice_entry, const u32* slice_off, const u32* group_link,
-    const BlockTables* tables, u8* out, u32* roots, u32* unres, u64 out_end, u64* parts) {
+    const BlockTables* tables, u8* out, u32* roots, u32* unres, u64 out_end, u64* parts,
+    EmitUnit* units, u64 unit_capacity, u32 unit_pass) {
   __shared__ LaneEmitShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
-  const u64 segments = st->accepted;
+  const u64 items = unit_pass ? min<u64>(st->emit_units, unit_capacity) : st->accepted;
   const u32 window = st->window;
   const u64 floor = st->floor;
   u64 unres_total = 0;  // this thread's unresolved bytes, counted once per wave at the end
@@ -3729,11 +3749,20 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
   // barrier of its segment's set-up).
   for (u32 k = t; 16 * k < sizeof(sh.ostage); k += kEmitThreads)
     *reinterpret_cast<uint4*>(sh.ostage + 16 * k) = make_uint4(0, 0, 0, 0);
-  for (u64 si = blockIdx.x; si < segments; si += gridDim.x) {
-    const Segment seg = acc[si];
-    if (seg.rec_first == kNone) continue;
-    u32 ri = seg.rec_first;
-    u64 block_out = seg.prefix;
+  for (u64 si = blockIdx.x; si < items; si += gridDim.x) {
+    u32 ri, first = 0;
+    u64 block_out;
+    if (unit_pass) {
+      const EmitUnit u = units[si];
+      ri = u.rec;
+      block_out = u.block_out;
+      first = u.first;
+    } else {
+      const Segment seg = acc[si];
+      ri = seg.rec_first;
+      block_out = seg.prefix;
+    }
+    if (ri == kNone) continue;
     u32 error = 0;
     if (!t) {
       sh.stage.count = 0;
@@ -3747,6 +3776,10 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
       }
       __syncthreads();
       const BlockRec rec = sh.rec;
+      if (unit_pass && (rec.type != 1 || !(rec.pad & kRecFixedRun) || first >= rec.lanes)) {
+        error = kExtent;  // never queued: units are slices of fixed runs
+        break;
+      }
       if (rec.type == 0) {
         copy_bytes(out + block_out, body + (rec.data >> 3), rec.size, body + len, t, kEmitThreads,
                    &sums, out_end - block_out);
@@ -3757,9 +3790,41 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
         }
         bool tables_pending = rec.table != kNone;
         const bool cross = (rec.pad & kRecFixedRun) != 0;
-        u32 g = rec.group;
-        u32 done = 0;
-        while (g != kNone && done < rec.lanes) {
+        if (!t) {
+          // The slices this workgroup emits: a unit of the unit pass; else the
+          // record's, or only the first unit of a long fixed run, whose other
+          // units are queued (all of them here when they do not fit).
+          u32 end = rec.lanes, more = 0;
+          u64 q = 0;
+          if (unit_pass) {
+            end = min(first + kUnitLanes, rec.lanes);
+          } else if (cross && rec.lanes > kUnitLanes) {
+            more = (rec.lanes - 1) / kUnitLanes;
+            q = atomicAdd(reinterpret_cast<unsigned long long*>(&st->emit_units), u64(more));
+            if (q + more <= unit_capacity) end = kUnitLanes;
+          }
+          sh.unit_end = end;
+          sh.unit_more = more;
+          sh.unit_q = q;
+        }
+        __syncthreads();
+        if (sh.unit_more) {  // uniform
+          const u64 q = sh.unit_q;
+          const u32 more = sh.unit_more;
+          const bool queued = sh.unit_end < rec.lanes;
+          for (u32 i = t; i < more && q + i < unit_capacity; i += kEmitThreads) {
+            EmitUnit u;
+            u.block_out = block_out;
+            u.rec = queued ? ri : kNone;
+            u.first = (i + 1) * kUnitLanes;
+            units[q + i] = u;
+          }
+        }
+        const u32 unit_end = sh.unit_end;
+        // A fixed run's slice groups are consecutive.
+        u32 g = rec.group + first / 64;
+        u32 done = first;
+        while (g != kNone && done < unit_end) {
           // One describe round: up to 256 slices in consecutive groups.  The
           // round's slice entries and offsets, and in the first round the
           // block's tables, load together (one memory latency).
@@ -3816,8 +3881,8 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
             const RoundBytes sink{sh.ostage, lo16, split, out, out_end, AdlerAcc{}};
             // Unchecked decoding when the slice and a token of overshoot lie
             // before the body end.
-            if (dst0 < lo)
-              lerr = kExtent;  // offsets out of order: never from a consistent describe
+            if (dst0 < lo || dst0 > rend || stop < entry || stop - entry > kMaxEmitSlice)
+              lerr = kExtent;  // never from a consistent describe or walk
             else if (stop + 64 <= len * 8)
               lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
                                        unres, unres_total, floor, cross);
@@ -3855,7 +3920,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
         }
       }
       block_out += rec.size;
-      ri = rec.next;
+      ri = unit_pass ? kNone : rec.next;
       __syncthreads();
     }
     if (!t && error) atomicMax(&st->emit_status, error);
@@ -4544,10 +4609,16 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
   HZ_TRY(scratch.alloc(&bits1, words));
   const u64 out_end = out_total;  // a byte at position p is stream byte n - (out_end - p)
-  HZ_LAUNCH(g_emit_lanes, dim3(emit_grid), dim3(kEmitThreads), 0, stream, body, len, st, acc,
-            recs, slice_entry, slice_off, group_link, tables, out, roots, bits0, out_end,
-            adler_parts);
-  HZ_TRY(hipGetLastError());
+  // Emission by segments, then the queued units of long fixed runs.
+  EmitUnit* units = nullptr;
+  const u64 unit_capacity = group_capacity * 64 / kUnitLanes + 64;
+  HZ_TRY(scratch.alloc(&units, unit_capacity));
+  for (u32 pass = 0; pass < 2; ++pass) {
+    HZ_LAUNCH(g_emit_lanes, dim3(emit_grid), dim3(kEmitThreads), 0, stream, body, len, st, acc,
+              recs, slice_entry, slice_off, group_link, tables, out, roots, bits0, out_end,
+              adler_parts, units, unit_capacity, pass);
+    HZ_TRY(hipGetLastError());
+  }
   HZ_LAUNCH(g_emit_serial, dim3(emit_grid), dim3(kWave), 0, stream, body, len, st, acc, out,
             roots, bits0, out_end, adler_parts + 2 * kAdlerSlots);
   HZ_TRY(hipGetLastError());
