@@ -1364,15 +1364,50 @@ struct FixPeek {
   }
 };
 
+// 64 bits at bit p of words in memory for one thread's forward decode: 128
+// bits in registers and the next 64 in flight, loaded when the position
+// moves past the first 64 (so a load has a few tokens of decoding to arrive).
+// Positions must not decrease by more than the window or jump more than 64
+// bits past it without a reload, which seek() does.  Words past `n` read as
+// zero.
+struct FixStream {
+  const u32* w;
+  u32 n;
+  u32 i0;  // even word index of `cur`
+  u64 cur, nxt, pend;
+  __device__ __forceinline__ u64 pair(u32 i) const {
+    return u64(i < n ? w[i] : 0u) | (u64(i + 1 < n ? w[i + 1] : 0u) << 32);
+  }
+  __device__ __forceinline__ void seek(u32 p) {
+    i0 = (p >> 5) & ~1u;
+    cur = pair(i0);
+    nxt = pair(i0 + 2);
+    pend = pair(i0 + 4);
+  }
+  __device__ __forceinline__ u64 operator()(u32 p) {
+    const u32 at = p - i0 * 32u;  // wraps when p precedes the window
+    if (at >= 128) {
+      seek(p);
+    } else if (at >= 64) {
+      cur = nxt;
+      nxt = pend;
+      i0 += 2;
+      pend = pair(i0 + 4);
+    }
+    const u32 sh = p - i0 * 32u;
+    return sh ? (cur >> sh) | (nxt << (64 - sh)) : cur;
+  }
+};
+
 // Fixed-Huffman decode from token start `p` until the first token start at or
 // after `stop`, crossing non-final and final fixed headers, within `body_end`
 // (stage bits past it do not exist).  `in_final`: the decode starts inside the
 // stream's final block, so its first EOB ends the stream.  Positions in the
 // result are relative to `rel0`.  With kMaxTokens, a decode that has taken
 // that many tokens stops as if it had reached `stop` (the probe).
-template <u32 kMaxTokens = 0>
-__device__ __forceinline__ FixSummary fix_scan(const FixPeek& pk, u32 p, u32 stop, u32 body_end, bool in_final,
-                               u32 rel0) {
+template <u32 kMaxTokens = 0, class Peek>
+__device__ __forceinline__ FixSummary fix_scan(Peek& pk, u32 p, u32 stop, u32 body_end,
+                                               bool in_final, u32 rel0) {
   FixSummary s;
   s.bytes = 0;
   s.eob_bytes = 0;
@@ -2536,7 +2571,10 @@ __global__ __launch_bounds__(256) void g_fix_rem(const u8* body, u64 len, const 
     const u32 nwords = u32(end_word > first_word ? end_word - first_word : 0);
     const u32 skew = u32((base + byte0) & 3u) * 8;
     const u32 body_end = u32(min<u64>(len * 8 - tk.tile * kFixTileBits + skew, 0xffffffffull));
-    const FixPeek pk{reinterpret_cast<const u32*>(first_word << 2), nwords};
+    FixStream pk;
+    pk.w = reinterpret_cast<const u32*>(first_word << 2);
+    pk.n = nwords;
+    pk.seek(skew + tk.p);
     const FixSummary r =
         fix_scan(pk, skew + tk.p, skew + kFixTileBits, body_end, tk.in_final != 0, skew);
     for (u32 m = tk.entries; m; m &= m - 1) {
@@ -2599,7 +2637,10 @@ __global__ __launch_bounds__(64) void g_fix_walk(
     u64 slot_base = 0;
     u32 slot_used = 64;
     bool chunk = false;  // slots slot_base .. +63 are this walk's (unused ones marked at the end)
+    FixTile mine;        // lane l: slot l of the chunk, stored when the chunk is done
     u64 batch_k = ~0ull;
+    u64 need_at = ~0ull;  // index of the cached word of the tile marks
+    u32 need_word = 0;
     // Finishes the open run at bit `e_end`: its record, slice groups and FixRun.
     auto close_run = [&](u64 e_end) {
       run_on = false;
@@ -2723,6 +2764,7 @@ __global__ __launch_bounds__(64) void g_fix_walk(
       const u32 e = u32(pos - k * kFixTileBits);
       if (recs_ok && run_id != kNone) {
         if (slot_used == 64) {
+          if (chunk) rt[slot_base + lane] = mine;  // the full chunk, one slot a lane
           slot_base = wave_fetch_add(&st->fix_rt, 64);
           slot_used = 0;
           chunk = slot_base + 64 <= rt_capacity;
@@ -2733,19 +2775,21 @@ __global__ __launch_bounds__(64) void g_fix_walk(
           }
         }
         if (recs_ok) {
-          if (!lane) {
-            FixTile ft;
-            ft.pos = pos;
-            ft.off = u32(out - run_out0);
-            ft.run = run_id;
-            ft.k = k;
-            rt[slot_base + slot_used] = ft;
+          if (lane == slot_used) {
+            mine.pos = pos;
+            mine.off = u32(out - run_out0);
+            mine.run = run_id;
+            mine.k = k;
           }
           ++slot_used;
         }
       }
       FixSummary f;
-      const bool have = e < kFixEntries && k < tiles && ((need[k >> 5] >> (k & 31)) & 1u);
+      if (k < tiles && (k >> 5) != need_at) {  // the walk's tiles advance: one load per 32
+        need_at = k >> 5;
+        need_word = need[need_at];
+      }
+      const bool have = e < kFixEntries && k < tiles && ((need_word >> (k & 31)) & 1u);
       if (have) {
         if (k < batch_k || k >= batch_k + kFixBatch) {
           // The next kFixBatch tiles' summaries, 16 bytes a load.
@@ -2807,8 +2851,11 @@ __global__ __launch_bounds__(64) void g_fix_walk(
         break;
       }
     }
-    // Unused slots of the last chunk.
-    if (chunk && lane >= slot_used) rt[slot_base + lane].run = kNone;
+    // The last chunk: its used slots, and its unused ones marked.
+    if (chunk) {
+      if (lane < slot_used) rt[slot_base + lane] = mine;
+      else rt[slot_base + lane].run = kNone;
+    }
     if (!lane) {
       seg_end[c] = pos;
       seg_size[c] = out;
@@ -2853,6 +2900,12 @@ __global__ __launch_bounds__(256) void g_fix_slices(const u8* body, u64 len, con
     // Windows up to bt; the tile whose decode reaches the run's end also
     // places the windows after it (the run's last EOB may end past the tile).
     const u64 tile_end = (ft.k + 1) * kFixTileBits;
+    // The body read from the tile's first word on (bit p at p - tile + skew).
+    const u64 tile0 = ft.k * kFixTileBits, w0 = tile0 / 32;
+    FixStream in;
+    in.w = words + w0;
+    in.n = u32(min<u64>(nwords > w0 ? nwords - w0 : 0, 0xffffffffull));
+    in.seek(u32(p - tile0 + skew));
     for (u64 b = bf + 1; b <= bl;) {
       if (p >= run.end || (b <= bt && p >= b * kFixSliceBits)) {
         if (p > run.end) p = run.end;
@@ -2863,12 +2916,7 @@ __global__ __launch_bounds__(256) void g_fix_slices(const u8* body, u64 len, con
       }
       if (b > bt && p >= tile_end) break;  // the next tile places the rest
       // 64 body bits at p (bits past the body's words read as zero).
-      const u64 a = p + skew, wi = a >> 5;
-      const u32 sh = u32(a & 31u);
-      const u64 x0 = wi < nwords ? words[wi] : 0u, x1 = wi + 1 < nwords ? words[wi + 1] : 0u,
-                x2 = wi + 2 < nwords ? words[wi + 2] : 0u;
-      const u64 lo = x0 | (x1 << 32);
-      const u64 bits = sh ? (lo >> sh) | (x2 << (64 - sh)) : lo;
+      const u64 bits = in(u32(p - tile0 + skew));
       u32 nb, length, value;
       const u32 kind = fixed_token(bits, nb, length, value);
       if (kind == kKindBad) {
