@@ -1344,13 +1344,30 @@ struct FixRun {
   u32 group;    // first of the run's consecutive slice groups
 };
 
-// One tile of a run: its true entry and the run's output bytes before it.
+// Tiles k .. k + tiles - 1 of a run: the first one's true entry and the
+// run's output bytes before it (the others' follow from the summaries).
 struct FixTile {
   u64 pos;
   u32 off;
-  u32 run;  // kNone: unused slot
-  u64 k;    // tile index
+  u32 run;    // kNone: unused slot
+  u32 k;      // tile index
+  u32 tiles;  // 1, or a group's tiles walked in one step
 };
+
+// The walk's step over a group of kFixGroupTiles marked tiles from one entry
+// state (entry bit e < 32 of the group's first tile, in the final block or
+// not): the tile summaries composed.
+constexpr u32 kFixGroupTiles = 16;
+struct FixGroupSum {
+  u32 bytes;   // output bytes up to the group's end or its terminal
+  u32 blocks;  // block headers crossed
+  u16 exit;    // as a tile summary's, relative to the last tile walked
+  u8 kind;     // as a tile summary's (kFixInFinal: the state after the group)
+  u8 tiles;    // tiles walked (the terminal's included); 0: step tile by tile
+  u8 status;
+  u8 pad[3];
+};
+static_assert(sizeof(FixGroupSum) == 16, "group summary layout");
 
 // 64 bits starting at stage bit p, words past `n` reading as zero.
 struct FixPeek {
@@ -2584,6 +2601,58 @@ __global__ __launch_bounds__(256) void g_fix_rem(const u8* body, u64 len, const 
   }
 }
 
+// Group summaries for the walk: one thread per (group of kFixGroupTiles
+// wholly marked tiles, entry state) composes the group's tile summaries as
+// the walk would step them (in the final block, a tile's first EOB ends the
+// stream).
+__global__ __launch_bounds__(256) void g_fix_groups(const State* st, const u32* need,
+                                                    const FixSummary* sum, u64 tiles,
+                                                    FixGroupSum* groups) {
+  if (st->status || !st->fix_regions) return;
+  const u64 n = tiles / kFixGroupTiles * 64;
+  for (u64 i = u64(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += u64(gridDim.x) * blockDim.x) {
+    const u64 k0 = i / 64 * kFixGroupTiles;
+    if (((need[k0 >> 5] >> (k0 & 31)) & 0xffffu) != 0xffffu) continue;  // stepped tile by tile
+    u32 e = u32(i & 31), bytes = 0, blocks = 0;
+    bool fin = (i & 32) != 0;
+    FixGroupSum r;
+    r.exit = 0;
+    r.kind = 0;
+    r.tiles = 0;
+    r.status = 0;
+    for (u32 j = 0; j < kFixGroupTiles; ++j) {
+      FixSummary f = sum[(k0 + j) * kFixEntries + e];
+      if (fin && f.eob != kFixNoEob) {
+        f.kind = kFixEnd;
+        f.exit = f.eob;
+        f.bytes = f.eob_bytes;
+        f.blocks = 0;
+      }
+      bytes += f.bytes;
+      blocks += f.blocks;
+      if ((f.kind & 15u) != kFixGo) {
+        r.exit = f.exit;
+        r.kind = f.kind;
+        r.tiles = u8(j + 1);
+        r.status = f.status;
+        break;
+      }
+      fin = fin || (f.kind & kFixInFinal) != 0;
+      if (f.exit < kFixTileBits || f.exit - kFixTileBits >= kFixEntries) break;  // no jump (r.tiles 0)
+      if (j + 1 == kFixGroupTiles) {
+        r.exit = f.exit;
+        r.kind = u8(kFixGo | (fin ? kFixInFinal : 0u));
+        r.tiles = u8(kFixGroupTiles);
+      }
+      e = f.exit - kFixTileBits;
+    }
+    r.bytes = bytes;
+    r.blocks = blocks;
+    groups[i] = r;
+  }
+}
+
 
 
 namespace {
@@ -2613,7 +2682,7 @@ __global__ __launch_bounds__(64) void g_fix_walk(
     u64 tiles, u64* seg_end, u64* seg_size, u32* seg_blocks, u32* seg_next, u32* seg_flags,
     u32* seg_rec, const u32* seg_last, const u32* region_cand, BlockRec* recs, u64 rec_capacity,
     FixRun* runs, u64 run_capacity, FixTile* rt, u64 rt_capacity, u32* group_link,
-    u64 group_capacity, u64 out_size) {
+    u64 group_capacity, u64 out_size, const FixGroupSum* groups) {
   __shared__ FixWalkShared sh;
   if (st->status) return;
   const u64 regions = st->fix_regions;
@@ -2762,6 +2831,21 @@ __global__ __launch_bounds__(64) void g_fix_walk(
       if (pos >= len * 8) { status = kTruncated; break; }
       const u64 k = pos / kFixTileBits;
       const u32 e = u32(pos - k * kFixTileBits);
+      if (k < tiles && (k >> 5) != need_at) {  // the walk's tiles advance: one load per 32
+        need_at = k >> 5;
+        need_word = need[need_at];
+      }
+      const bool have = e < kFixEntries && k < tiles && ((need_word >> (k & 31)) & 1u);
+      // At the first tile of a group of marked tiles: the whole group in one
+      // step, unless the output or block limit fails inside it (then tile by
+      // tile, which finds the failing tile).
+      FixGroupSum gs;
+      bool jump = false;
+      if (have && k % kFixGroupTiles == 0 && k + kFixGroupTiles <= tiles &&
+          ((need_word >> (k & 31)) & 0xffffu) == 0xffffu) {
+        gs = groups[k / kFixGroupTiles * 64 + e + (in_final ? 32 : 0)];
+        jump = gs.tiles != 0 && out + gs.bytes <= out_size && blocks + gs.blocks <= kMaxBlocks;
+      }
       if (recs_ok && run_id != kNone) {
         if (slot_used == 64) {
           if (chunk) rt[slot_base + lane] = mine;  // the full chunk, one slot a lane
@@ -2779,17 +2863,33 @@ __global__ __launch_bounds__(64) void g_fix_walk(
             mine.pos = pos;
             mine.off = u32(out - run_out0);
             mine.run = run_id;
-            mine.k = k;
+            mine.k = u32(k);
+            mine.tiles = jump ? gs.tiles : 1u;
           }
           ++slot_used;
         }
       }
-      FixSummary f;
-      if (k < tiles && (k >> 5) != need_at) {  // the walk's tiles advance: one load per 32
-        need_at = k >> 5;
-        need_word = need[need_at];
+      if (jump) {
+        out += gs.bytes;
+        blocks += gs.blocks;
+        pos = (k + gs.tiles - 1) * kFixTileBits + gs.exit;
+        const u32 kind = gs.kind & 15u;
+        if (kind == kFixGo) {
+          in_final = (gs.kind & kFixInFinal) != 0;
+        } else if (kind == kFixEnd) {
+          close_run(pos);
+          final_seg = true;
+          break;
+        } else if (kind == kFixHeader) {
+          close_run(pos);
+          at_header = true;
+        } else {
+          status = gs.status ? gs.status : u32(kBadSymbol);
+          break;
+        }
+        continue;
       }
-      const bool have = e < kFixEntries && k < tiles && ((need_word >> (k & 31)) & 1u);
+      FixSummary f;
       if (have) {
         if (k < batch_k || k >= batch_k + kFixBatch) {
           // The next kFixBatch tiles' summaries, 16 bytes a load.
@@ -2875,7 +2975,8 @@ __global__ __launch_bounds__(64) void g_fix_walk(
 __global__ __launch_bounds__(256) void g_fix_slices(const u8* body, u64 len, const State* st,
                                                     const FixTile* rt, u64 rt_capacity,
                                                     const FixRun* runs, u64 run_capacity,
-                                                    u64* slice_entry, u32* slice_off) {
+                                                    const FixSummary* sum, u64* slice_entry,
+                                                    u32* slice_off) {
   if (st->status || !st->fix_regions) return;
   const u64 used = min<u64>(st->fix_rt, rt_capacity);
   const u64 nruns = min<u64>(st->fix_runs, run_capacity);
@@ -2883,25 +2984,40 @@ __global__ __launch_bounds__(256) void g_fix_slices(const u8* body, u64 len, con
   const u32* words = reinterpret_cast<const u32*>(base & ~uintptr_t(3));
   const u64 skew = u64(base & 3u) * 8;
   const u64 nwords = (u64(base & 3u) + len + 3) / 4;
-  for (u64 i = u64(blockIdx.x) * blockDim.x + threadIdx.x; i < used;
+  for (u64 i = u64(blockIdx.x) * blockDim.x + threadIdx.x; i < used * kFixGroupTiles;
        i += u64(gridDim.x) * blockDim.x) {
-    const FixTile ft = rt[i];
-    if (ft.run == kNone || ft.run >= nruns) continue;
+    // Tile j of slot i / kFixGroupTiles.
+    const FixTile ft = rt[i / kFixGroupTiles];
+    const u32 j = u32(i % kFixGroupTiles);
+    if (ft.run == kNone || ft.run >= nruns || j >= ft.tiles) continue;
     const FixRun run = runs[ft.run];
     if (!run.lanes) continue;
-    const u64 bl = run.b0 + run.lanes - 1;
-    const u64 bf = max<u64>(run.b0, ft.k * kFixTileSlices);
-    const u64 bt = min<u64>(bl, ft.k * kFixTileSlices + kFixTileSlices - 1);
-    const u64 at = u64(run.group) * 64 - run.b0;  // slice index of window b: at + b
-    slice_entry[at + bf] = ft.pos;
-    slice_off[at + bf] = ft.off;
+    // The tile's true entry and offset: through the summaries of the tiles
+    // before it in the group (inside a group every tile but the last is
+    // left at its end, so the final-block rule never applies to them).
+    const u64 k = u64(ft.k) + j;
     u64 p = ft.pos;
     u32 off = ft.off;
+    if (j) {
+      u32 e = u32(ft.pos - u64(ft.k) * kFixTileBits);
+      for (u32 q = 0; q < j; ++q) {
+        const FixSummary f = sum[(u64(ft.k) + q) * kFixEntries + e];
+        off += f.bytes;
+        e = u32(f.exit) - kFixTileBits;
+      }
+      p = k * kFixTileBits + e;
+    }
+    const u64 bl = run.b0 + run.lanes - 1;
+    const u64 bf = max<u64>(run.b0, k * kFixTileSlices);
+    const u64 bt = min<u64>(bl, k * kFixTileSlices + kFixTileSlices - 1);
+    const u64 at = u64(run.group) * 64 - run.b0;  // slice index of window b: at + b
+    slice_entry[at + bf] = p;
+    slice_off[at + bf] = off;
     // Windows up to bt; the tile whose decode reaches the run's end also
     // places the windows after it (the run's last EOB may end past the tile).
-    const u64 tile_end = (ft.k + 1) * kFixTileBits;
+    const u64 tile_end = (k + 1) * kFixTileBits;
     // The body read from the tile's first word on (bit p at p - tile + skew).
-    const u64 tile0 = ft.k * kFixTileBits, w0 = tile0 / 32;
+    const u64 tile0 = k * kFixTileBits, w0 = tile0 / 32;
     FixStream in;
     in.w = words + w0;
     in.n = u32(min<u64>(nwords > w0 ? nwords - w0 : 0, 0xffffffffull));
@@ -4627,13 +4743,20 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_fix_rem, dim3(clamp_grid((task_capacity + 255) / 256, 2048)), dim3(256), 0, stream,
             body, len, st, fix_tasks, task_capacity, fix_sum);
   HZ_TRY(hipGetLastError());
+  FixGroupSum* fix_groups = nullptr;
+  const u64 fix_group_count = tiles / kFixGroupTiles;
+  HZ_TRY(scratch.alloc(&fix_groups, (fix_group_count ? fix_group_count : 1) * 64));
+  HZ_LAUNCH(g_fix_groups, dim3(clamp_grid((fix_group_count * 64 + 255) / 256, 2048)), dim3(256), 0,
+            stream, st, fix_need, fix_sum, tiles, fix_groups);
+  HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_fix_walk, dim3(clamp_grid(cand_capacity, 2048)), dim3(kWave), 0, stream, body, len, st,
             cand, fix_need, fix_sum, tiles, seg_end, seg_size, seg_blocks, seg_next, seg_flags,
             seg_rec, seg_last, region_cand, recs, rec_capacity, fix_runs, run_capacity, fix_rt,
-            rt_capacity, group_link, group_capacity, out_size);
+            rt_capacity, group_link, group_capacity, out_size, fix_groups);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_fix_slices, dim3(clamp_grid((rt_capacity + 255) / 256, 2048)), dim3(256), 0, stream,
-            body, len, st, fix_rt, rt_capacity, fix_runs, run_capacity, slice_entry, slice_off);
+  HZ_LAUNCH(g_fix_slices, dim3(clamp_grid((rt_capacity * kFixGroupTiles + 255) / 256, 2048)),
+            dim3(256), 0, stream, body, len, st, fix_rt, rt_capacity, fix_runs, run_capacity,
+            fix_sum, slice_entry, slice_off);
   HZ_TRY(hipGetLastError());
 
   // Chain selection, then the exact walk if the fast chain declined.
