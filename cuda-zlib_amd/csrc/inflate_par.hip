@@ -3638,8 +3638,20 @@ struct GlobalBytes {
     out[p] = v;
     if (kAdler) acc->add_byte(v, end - p);
   }
+  __device__ __forceinline__ void fill(u64 p, u32 n, u8 v) const {
+    for (u32 j = 0; j < n; ++j) put(p + j, v);
+  }
   __device__ __forceinline__ void zero(u64, u32) const {}
 };
+
+// d[0, n) = v: bytes up to d's first 16-byte boundary, then 16-byte stores.
+__device__ __forceinline__ void fill_bytes(u8* d, u32 n, u8 v) {
+  u32 i = 0;
+  for (; i < n && (reinterpret_cast<uintptr_t>(d + i) & 15); ++i) d[i] = v;
+  const u32 v4 = 0x01010101u * v;
+  for (; i + 16 <= n; i += 16) *reinterpret_cast<uint4*>(d + i) = make_uint4(v4, v4, v4, v4);
+  for (; i < n; ++i) d[i] = v;
+}
 
 struct StagedBytes {
   u8* lds;
@@ -3673,6 +3685,18 @@ struct RoundBytes {
       out[p] = v;
       acc.add_byte_unfolded(v, end - p);  // folded once per round (at most 2^18 bytes a thread)
     }
+  }
+  // out[p, p + n) = v (a run of the byte before it), 16 bytes a store.
+  __device__ __forceinline__ void fill(u64 p, u32 n, u8 v) const {
+    const u32 in_stage = p < split ? u32(min<u64>(split - p, n)) : 0u;
+    if (in_stage) fill_bytes(lds + u32(p - base), in_stage, v);
+    if (in_stage == n) return;
+    const u64 a = p + in_stage;
+    const u64 m = n - in_stage;
+    // The bytes weigh end - a down to end - a - m + 1.
+    acc.s += u64(v) * m;
+    acc.w += u64(v) * (m * (end - a) - m * (m - 1) / 2);
+    fill_bytes(out + a, u32(m), v);
   }
   __device__ __forceinline__ void zero(u64, u32) const {}
 };
@@ -3724,52 +3748,64 @@ __device__ __forceinline__ void copy_periodic(const Sink& out, u64 dst, u64 src0
 // One match of a slice whose output starts at dst0: bytes copied from before
 // dst0 (or from bytes of this slice still unresolved) are marked unresolved
 // with their root; the rest are copied.  `nunres` counts the slice's
-// unresolved bytes so far.
+// unresolved bytes so far.  tail_at / tail_root: the slice offset just past
+// the last match handled, and the root of that match's last byte (kNone when
+// it is resolved): the byte before a match is that byte or a literal.
 template <class Sink>
 __device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u32 distance,
-                                           u32 length, u32* roots, u32* unres, u32& nunres) {
+                                           u32 length, u32* roots, u32* unres, u32& nunres,
+                                           u32& tail_at, u32& tail_root) {
   const u64 src0 = dst - distance;
+  const u32 at = u32(dst - dst0);
   if (src0 + length <= dst0) {
     // Every source precedes the slice: unresolved, rooted at the source.
     roots_fill(roots, dst, length, u32(src0), 1);
     bits_set_range(unres, dst, length);
     out.zero(dst, length);
     nunres += length;
-  } else if (!nunres && src0 >= dst0) {
-    // Every source is this slice's own resolved output.
-    copy_periodic(out, dst, src0, distance, length);
+    tail_root = u32(src0) + length - 1;
   } else if (distance == 1) {
-    // A run of the byte before: resolved, or one root for the whole run.
+    // A run of the byte before: one root for the whole run when that byte
+    // precedes the slice or ends an unresolved match, else resolved.
     const u64 p = dst - 1;
     const bool before = p < dst0;
-    if (before || (nunres && bit_get(unres, p))) {
-      const u32 root = before ? u32(p) : roots[p];
+    if (before || (at == tail_at && tail_root != kNone)) {
+      const u32 root = before ? u32(p) : tail_root;
       roots_fill(roots, dst, length, root, 0);
       bits_set_range(unres, dst, length);
       out.zero(dst, length);
       nunres += length;
+      tail_root = root;
     } else {
-      const u8 v = out.get(p);
-      for (u32 j = 0; j < length; ++j) out.put(dst + j, v);
+      out.fill(dst, length, out.get(p));
+      tail_root = kNone;
     }
+  } else if (!nunres && src0 >= dst0) {
+    // Every source is this slice's own resolved output.
+    copy_periodic(out, dst, src0, distance, length);
+    tail_root = kNone;
   } else {
+    u32 last = kNone;
     for (u32 j = 0; j < length; ++j) {
       const u64 d = dst + j, src = d - distance;
       if (src < dst0) {
-        roots[d] = u32(src);
+        roots[d] = last = u32(src);
         bit_set(unres, d);
         out.zero(d, 1);
         ++nunres;
       } else if (nunres && bit_get(unres, src)) {
-        roots[d] = roots[src];
+        roots[d] = last = roots[src];
         bit_set(unres, d);
         out.zero(d, 1);
         ++nunres;
       } else {
         out.put(d, out.get(src));
+        last = kNone;
       }
     }
+    tail_root = last;
   }
+  tail_at = at + length;
 }
 
 // Matches a slice decode holds back: literals are written as they are
@@ -3795,9 +3831,10 @@ struct MatchQueue {
   // Copies the queued matches in order (the head, then the rest moves up).
   template <class Sink>
   __device__ __forceinline__ void flush(const Sink& out, u64 dst0, u32* roots, u32* unres,
-                                        u32& nunres) {
+                                        u32& nunres, u32& tail_at, u32& tail_root) {
     for (; n; --n) {
-      emit_match(out, dst0, dst0 + at[0], code[0] >> 9, code[0] & 511u, roots, unres, nunres);
+      emit_match(out, dst0, dst0 + at[0], code[0] >> 9, code[0] & 511u, roots, unres, nunres,
+                 tail_at, tail_root);
 #pragma unroll
       for (u32 k = 0; k + 1 < kMatchQueue; ++k) {
         at[k] = at[k + 1];
@@ -3824,6 +3861,7 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
   u64 dst = dst0;
   u32 nunres = 0, err = 0;  // unresolved bytes of this slice
   MatchQueue q;
+  u32 tail_at = 0, tail_root = kNone;  // see emit_match
   bool live = true;
   for (;;) {
     // One copy site for queued matches: when a lane's queue is full, and
@@ -3881,7 +3919,8 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
         }
       }
     }
-    if (!any_live || __ballot(q.n == kMatchQueue)) q.flush(out, dst0, roots, unres, nunres);
+    if (!any_live || __ballot(q.n == kMatchQueue))
+      q.flush(out, dst0, roots, unres, nunres, tail_at, tail_root);
     if (!any_live) break;
   }
   unres_total += nunres;
