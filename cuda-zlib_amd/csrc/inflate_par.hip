@@ -3599,7 +3599,8 @@ struct LaneEmitShared {
   u16 codes[320];
   BlockRec rec;
   u64 first, chunk_end, round_lo, round_hi, unit_q;
-  u32 count, next_g, need, unit_end, unit_more;
+  u64 carry;  // the state of the byte before the next round (kLastInherit: not known)
+  u32 count, next_g, need, unit_end, unit_more, any_lead;
   u64 red[2][kEmitThreads / 64];
   __align__(16) u8 ostage[kOutStage + 16];  // a whole number of 16-byte lines
   // block_header interface
@@ -3751,13 +3752,28 @@ __device__ __forceinline__ void copy_periodic(const Sink& out, u64 dst, u64 src0
 // unresolved bytes so far.  tail_at / tail_root: the slice offset just past
 // the last match handled, and the root of that match's last byte (kNone when
 // it is resolved): the byte before a match is that byte or a literal.
-template <class Sink>
+// With kDefer, a run of the byte before the slice at the slice's start (its
+// leading run, `lead` bytes) is left unwritten and unmarked: once the round
+// is decoded, the workgroup learns that byte's value or root from the slice
+// before (emit_lead).  A match that reads the leading run marks it first.
+template <bool kDefer, class Sink>
 __device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u32 distance,
                                            u32 length, u32* roots, u32* unres, u32& nunres,
-                                           u32& tail_at, u32& tail_root) {
+                                           u32& tail_at, u32& tail_root, u32& lead) {
   const u64 src0 = dst - distance;
   const u32 at = u32(dst - dst0);
-  if (src0 + length <= dst0) {
+  const bool extend = kDefer && distance == 1 && (at == 0 || (lead && at == lead && tail_at == lead));
+  if (kDefer && !extend && lead && src0 < dst0 + lead && src0 + length > dst0) {
+    roots_fill(roots, dst0, lead, u32(dst0 - 1), 0);
+    bits_set_range(unres, dst0, lead);
+    nunres += lead;
+    if (tail_at == lead) tail_root = u32(dst0 - 1);
+    lead = 0;
+  }
+  if (extend) {
+    lead = at + length;  // the leading run, begun or extended
+    tail_root = kNone;   // not read while the tail is the leading run
+  } else if (src0 + length <= dst0) {
     // Every source precedes the slice: unresolved, rooted at the source.
     roots_fill(roots, dst, length, u32(src0), 1);
     bits_set_range(unres, dst, length);
@@ -3808,6 +3824,13 @@ __device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u
   tail_at = at + length;
 }
 
+// The state of a slice's last byte as the slice after it sees it: the slice
+// ended in its leading run (the state of the byte before the slice), or in a
+// resolved byte, or in an unresolved byte with a root.
+constexpr u64 kLastInherit = 0;
+constexpr u64 kLastValue = 1ull << 32;
+constexpr u64 kLastRoot = 2ull << 32;
+
 // Matches a slice decode holds back: literals are written as they are
 // decoded, matches queue here (in order) and are copied when a lane of the
 // wave has kMatchQueue of them and when the slice ends, so that the lanes of
@@ -3829,12 +3852,12 @@ struct MatchQueue {
     ++n;
   }
   // Copies the queued matches in order (the head, then the rest moves up).
-  template <class Sink>
+  template <bool kDefer, class Sink>
   __device__ __forceinline__ void flush(const Sink& out, u64 dst0, u32* roots, u32* unres,
-                                        u32& nunres, u32& tail_at, u32& tail_root) {
+                                        u32& nunres, u32& tail_at, u32& tail_root, u32& lead) {
     for (; n; --n) {
-      emit_match(out, dst0, dst0 + at[0], code[0] >> 9, code[0] & 511u, roots, unres, nunres,
-                 tail_at, tail_root);
+      emit_match<kDefer>(out, dst0, dst0 + at[0], code[0] >> 9, code[0] & 511u, roots, unres,
+                         nunres, tail_at, tail_root, lead);
 #pragma unroll
       for (u32 k = 0; k + 1 < kMatchQueue; ++k) {
         at[k] = at[k + 1];
@@ -3850,10 +3873,12 @@ struct MatchQueue {
 // holds the block's tables and the staged bits.  With `cross` (a run of
 // fixed blocks), an EOB before `stop` is followed by the next block's fixed
 // header, and decoding goes on after it.
-template <bool kChecked, class Shared, class Sink>
+// With kDefer, `lead` returns the slice's deferred leading run and `last` the
+// state of its last byte for the slices after it (emit_lead).
+template <bool kChecked, bool kDefer, class Shared, class Sink>
 __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u64 block_end,
                           u32 window, const Sink& out, u32* roots, u32* unres, u64& unres_total,
-                          u64 floor = 0, bool cross = false) {
+                          u64 floor, bool cross, u32& lead, u64& last) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
   r.limit = blim;
@@ -3862,6 +3887,7 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
   u32 nunres = 0, err = 0;  // unresolved bytes of this slice
   MatchQueue q;
   u32 tail_at = 0, tail_root = kNone;  // see emit_match
+  lead = 0;
   bool live = true;
   for (;;) {
     // One copy site for queued matches: when a lane's queue is full, and
@@ -3920,10 +3946,16 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
       }
     }
     if (!any_live || __ballot(q.n == kMatchQueue))
-      q.flush(out, dst0, roots, unres, nunres, tail_at, tail_root);
+      q.template flush<kDefer>(out, dst0, roots, unres, nunres, tail_at, tail_root, lead);
     if (!any_live) break;
   }
   unres_total += nunres;
+  if (kDefer) {
+    const u32 n = u32(dst - dst0);
+    if (!n || lead == n) last = kLastInherit;
+    else if (tail_at == n && tail_root != kNone) last = kLastRoot | tail_root;
+    else last = kLastValue | out.get(dst - 1);
+  }
   return err;
 }
 }  // namespace
@@ -3970,6 +4002,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
     if (!t) {
       sh.stage.count = 0;
       sh.stage.bit0 = 0;
+      sh.carry = kLastInherit;
     }
     __syncthreads();
     while (ri != kNone) {
@@ -3986,6 +4019,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
       if (rec.type == 0) {
         copy_bytes(out + block_out, body + (rec.data >> 3), rec.size, body + len, t, kEmitThreads,
                    &sums, out_end - block_out);
+        if (!t && rec.size) sh.carry = kLastValue | body[(rec.data >> 3) + rec.size - 1];
       } else {
         if (rec.table == kNone) {
           block_header<true, true, false>(body, len, ~0ull, sh);
@@ -4056,6 +4090,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
             sh.first = entry;
             sh.chunk_end = next_g != kNone ? slice_entry[u64(next_g) * 64] : rec.end;
             sh.need = !staged_covers(sh.stage, body, len, entry, sh.chunk_end);
+            sh.any_lead = 0;
             // The round's output: from its first slice to the next round's.
             sh.round_lo = block_out + off;
             sh.round_hi = block_out + (next_g != kNone ? slice_off[u64(next_g) * 64] : rec.size);
@@ -4072,7 +4107,8 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
           const u64 skew = (reinterpret_cast<uintptr_t>(out) + lo) & 15u;
           const u64 lo16 = lo - skew;
           const u64 split = min<u64>(hi, lo16 + kOutStage);
-          u32 lerr = 0;
+          u32 lerr = 0, lead = 0;
+          u64 last = kLastInherit;
           if (t < count) {
             if (t + 1 >= count) stop = sh.chunk_end;
             const u64 dst0 = block_out + off;
@@ -4087,18 +4123,57 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
             if (dst0 < lo || dst0 > rend || stop < entry || stop - entry > kMaxEmitSlice)
               lerr = kExtent;  // never from a consistent describe or walk
             else if (stop + 64 <= len * 8)
-              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
-                                       unres, unres_total, floor, cross);
+              lerr = emit_slice<false, true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink,
+                                             roots, unres, unres_total, floor, cross, lead, last);
             else
-              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink, roots,
-                                      unres, unres_total, floor, cross);
+              lerr = emit_slice<true, true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink,
+                                            roots, unres, unres_total, floor, cross, lead, last);
             sums.s += sink.acc.s;
             sums.w += sink.acc.w;
+            if (lead) sh.any_lead = 1;
           }
           if (lerr) atomicMax(&st->emit_status, lerr);
+          __syncthreads();
+          if (sh.any_lead) {  // uniform
+            // Leading runs: each slice learns the state of the byte before it
+            // by a scan over the round's slices (the last state that is not
+            // "inherit" before it; before slice 0, the carry of the round
+            // before), then writes its run or marks it unresolved.  The stage
+            // words hold the scan: this round's bits are decoded.
+            u64* scan = reinterpret_cast<u64*>(sh.stage.words);
+            scan[t] = last;
+            __syncthreads();
+            for (u32 d = 1; d < kEmitThreads; d <<= 1) {
+              const u64 own = scan[t], left = t >= d ? scan[t - d] : kLastInherit;
+              __syncthreads();
+              if (own == kLastInherit) scan[t] = left;
+              __syncthreads();
+            }
+            if (lead && !lerr) {
+              const u64 dst0 = block_out + off;
+              const u64 before = t ? scan[t - 1] : sh.carry;
+              if (before >> 32 == kLastValue >> 32) {
+                const RoundBytes sink{sh.ostage, lo16, split, out, out_end, AdlerAcc{}};
+                sink.fill(dst0, lead, u8(before));
+                sums.s += sink.acc.s;
+                sums.w += sink.acc.w;
+              } else {
+                const u32 root = before >> 32 == kLastRoot >> 32 ? u32(before) : u32(dst0 - 1);
+                roots_fill(roots, dst0, lead, root, 0);
+                bits_set_range(unres, dst0, lead);
+                unres_total += lead;
+              }
+            }
+            __syncthreads();
+            if (!t) {
+              if (scan[count - 1] != kLastInherit) sh.carry = scan[count - 1];
+              sh.stage.count = 0;
+            }
+          } else if (t + 1 == count) {
+            sh.carry = last;
+          }
           // The staged part in whole 16-byte lines (bytes of the neighbouring
           // round in its first line one by one), summed on the way.
-          __syncthreads();
           const u64 span = split - lo16;
           for (u64 k = t; 16 * k < span; k += kEmitThreads) {
             const u64 r0 = 16 * k, a = lo16 + r0;
@@ -4255,14 +4330,16 @@ __global__ __launch_bounds__(kDescThreads) void g_batch_wide(
             const u32 blim = stage_limit(sh.stage, len);
             const u32 e_rel = u32(entry - sh.stage.bit0), s_rel = u32(stop - sh.stage.bit0);
             u32 lerr;
+            u32 no_lead;  // a batch file decodes without deferred leading runs
+            u64 no_last;
             if (stop + 64 <= len * 8)
-              lerr = emit_slice<false>(sh, blim, e_rel, s_rel, dst0, block_end, window,
+              lerr = emit_slice<false, false>(sh, blim, e_rel, s_rel, dst0, block_end, window,
                                        GlobalBytes<false>{out, nullptr, 0}, roots,
-                                       unres, unres_total, base);
+                                       unres, unres_total, base, false, no_lead, no_last);
             else
-              lerr = emit_slice<true>(sh, blim, e_rel, s_rel, dst0, block_end, window,
+              lerr = emit_slice<true, false>(sh, blim, e_rel, s_rel, dst0, block_end, window,
                                       GlobalBytes<false>{out, nullptr, 0}, roots,
-                                      unres, unres_total, base);
+                                      unres, unres_total, base, false, no_lead, no_last);
             if (lerr) bad = 1;
           }
           done += count;
