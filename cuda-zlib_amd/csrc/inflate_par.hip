@@ -3378,6 +3378,16 @@ __device__ __forceinline__ bool bit_get(const u32* bits, u64 i) {
   const u32 w = __hip_atomic_load(bits + (i >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return (w >> (i & 31)) & 1u;
 }
+// Resolve groups: the 2048 output bytes of 64 bitmap words, one resolve wave's
+// share.  A byte per group marks a group that may hold unresolved bytes;
+// resolve rounds skip the others.
+constexpr u32 kResolveGroupShift = 11;
+__device__ __forceinline__ void mark_groups(u8* marks, u64 first, u64 n) {
+  if (!marks || !n) return;
+  for (u64 g = first >> kResolveGroupShift; g <= (first + n - 1) >> kResolveGroupShift; ++g)
+    marks[g] = 1;
+}
+
 __device__ __forceinline__ void bit_set(u32* bits, u64 i) {
   atomicOr(bits + (i >> 5), 1u << (i & 31));
 }
@@ -3443,7 +3453,8 @@ __device__ __forceinline__ void adler_block_sum(u64& s, u64& w, u64 (*red)[16]) 
 // payloads and long matches.  Output positions are absolute.
 __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, State* st,
                                                     const Segment* acc, u8* out, u32* roots,
-                                                    u32* unres, u64 out_end, u64* parts) {
+                                                    u32* unres, u64 out_end, u64* parts,
+                                                    u8* marks) {
   __shared__ EmitShared sh;
   __shared__ u64 red[2][16];
   if (st->status) return;
@@ -3519,8 +3530,10 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
           }
           for (u32 j = 0; j < length; ++j) {
             const u64 src = dst - distance + (j % distance);
-            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src, as, aw, out_end))
+            if (copy_byte(out, roots, unres, seg.prefix, dst + j, src, as, aw, out_end)) {
               atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), 1ull);
+              mark_groups(marks, dst + j, 1);
+            }
           }
           produced += length;
         }
@@ -3539,6 +3552,7 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
           if (j < length)
             queued = copy_byte(out, roots, unres, seg.prefix, begin + j, begin - d + (j % d), as,
                                aw, out_end);
+          if (queued) mark_groups(marks, begin + j, 1);
           const u64 bal = __ballot(queued);
           if (!lane && bal)
             atomicAdd(reinterpret_cast<unsigned long long*>(&st->unresolved[0]), u64(__popcll(bal)));
@@ -3878,7 +3892,7 @@ struct MatchQueue {
 template <bool kChecked, bool kDefer, class Shared, class Sink>
 __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u64 block_end,
                           u32 window, const Sink& out, u32* roots, u32* unres, u64& unres_total,
-                          u64 floor, bool cross, u32& lead, u64& last) {
+                          u64 floor, bool cross, u32& lead, u64& last, u8* marks) {
   Win4<kChecked> r;
   r.words = sh.stage.words;
   r.limit = blim;
@@ -3950,6 +3964,7 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
     if (!any_live) break;
   }
   unres_total += nunres;
+  if (nunres) mark_groups(marks, dst0, dst - dst0);
   if (kDefer) {
     const u32 n = u32(dst - dst0);
     if (!n || lead == n) last = kLastInherit;
@@ -3971,7 +3986,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
     const u8* body, u64 len, State* st, const Segment* acc, const BlockRec* recs,
     const u64* slice_entry, const u32* slice_off, const u32* group_link,
     const BlockTables* tables, u8* out, u32* roots, u32* unres, u64 out_end, u64* parts,
-    EmitUnit* units, u64 unit_capacity, u32 unit_pass) {
+    EmitUnit* units, u64 unit_capacity, u32 unit_pass, u8* marks) {
   __shared__ LaneEmitShared sh;
   if (st->status) return;
   const u32 t = threadIdx.x;
@@ -4124,10 +4139,12 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
               lerr = kExtent;  // never from a consistent describe or walk
             else if (stop + 64 <= len * 8)
               lerr = emit_slice<false, true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink,
-                                             roots, unres, unres_total, floor, cross, lead, last);
+                                             roots, unres, unres_total, floor, cross, lead, last,
+                                             marks);
             else
               lerr = emit_slice<true, true>(sh, blim, e_rel, s_rel, dst0, rend, window, sink,
-                                            roots, unres, unres_total, floor, cross, lead, last);
+                                            roots, unres, unres_total, floor, cross, lead, last,
+                                            marks);
             sums.s += sink.acc.s;
             sums.w += sink.acc.w;
             if (lead) sh.any_lead = 1;
@@ -4161,6 +4178,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
                 const u32 root = before >> 32 == kLastRoot >> 32 ? u32(before) : u32(dst0 - 1);
                 roots_fill(roots, dst0, lead, root, 0);
                 bits_set_range(unres, dst0, lead);
+                mark_groups(marks, dst0, lead);
                 unres_total += lead;
               }
             }
@@ -4335,11 +4353,13 @@ __global__ __launch_bounds__(kDescThreads) void g_batch_wide(
             if (stop + 64 <= len * 8)
               lerr = emit_slice<false, false>(sh, blim, e_rel, s_rel, dst0, block_end, window,
                                        GlobalBytes<false>{out, nullptr, 0}, roots,
-                                       unres, unres_total, base, false, no_lead, no_last);
+                                       unres, unres_total, base, false, no_lead, no_last,
+                                       nullptr);
             else
               lerr = emit_slice<true, false>(sh, blim, e_rel, s_rel, dst0, block_end, window,
                                       GlobalBytes<false>{out, nullptr, 0}, roots,
-                                      unres, unres_total, base, false, no_lead, no_last);
+                                      unres, unres_total, base, false, no_lead, no_last,
+                                      nullptr);
             if (lerr) bad = 1;
           }
           done += count;
@@ -4470,7 +4490,7 @@ inline u32 resolve_rounds(u64 span) {
 __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots, u32* bits0,
                                                  u32* bits1, u64* counts, u32 round,
                                                  u32 max_rounds, u64 words, u64 out_end,
-                                                 u64* parts) {
+                                                 u64* parts, u8* marks0, u8* marks1) {
   __shared__ u64 red[2][16];
   if (st->status || st->emit_status) return;
   const u64 n_in = round ? counts[round] : st->unresolved[0];
@@ -4482,30 +4502,53 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
   const u32 lane = lane_id();
   const u64 waves = u64(gridDim.x) * (blockDim.x / 64);
   u32 kept = 0;
-  // A wave reads 64 bitmap words, then takes the non-empty ones two at a
-  // time: lane l follows the root chain of bit (l & 31) of the first (l < 32)
-  // or second word, so 64 chains advance together.
-  for (u64 g = u64(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6); g * 64 < words;
-       g += waves) {
+  // A wave takes a group of 64 bitmap words at a time and lists the group's
+  // unresolved positions in LDS (a prefix sum over the words' bit counts);
+  // its lanes then follow the root chains of the list's entries, 64 at a
+  // time, so that sparse and dense groups alike keep every lane busy.  The
+  // entries still unresolved are gathered into the group's next words in LDS.
+  // With group marks (marks0 for rounds 0, 2, ..., marks1 for the others), a
+  // round reads only the marked groups of its bitmap and marks those it
+  // leaves unresolved bytes in for the next round; the other groups' words
+  // of the next bitmap are never read.
+  __shared__ u16 list[256 / 64][64 * 32];
+  __shared__ u32 left_words[256 / 64][64];
+  const u32 wave = threadIdx.x >> 6;
+  const u8* marks = round & 1 ? marks1 : marks0;
+  u8* next_marks = round & 1 ? marks0 : marks1;
+  const u32 links = resolve_links(round);
+  for (u64 g = u64(blockIdx.x) * (blockDim.x / 64) + wave; g * 64 < words; g += waves) {
+    if (marks && !marks[g]) {  // uniform
+      if (!lane) next_marks[g] = 0;
+      continue;
+    }
     const u64 w = g * 64 + lane;
-    const u32 m = w < words ? bits[w] : 0u;
-    if (!m && w < words) next_bits[w] = 0;
-    u64 nz = __ballot(m != 0);
-    while (nz) {
-      const u32 i0 = u32(__builtin_ctzll(nz));
-      nz &= nz - 1;
-      const u32 i1 = nz ? u32(__builtin_ctzll(nz)) : 64u;
-      if (nz) nz &= nz - 1;
-      const u32 idx = lane < 32 ? i0 : i1;
-      const u32 mw = __shfl(m, int(idx & 63), 64);
-      const u32 b = lane & 31;
-      const bool mine = idx < 64 && ((mw >> b) & 1u);
+    u32 m = w < words ? bits[w] : 0u;
+    const u32 cnt = __popc(m);
+    u32 incl = cnt;
+#pragma unroll
+    for (u32 off = 1; off < 64; off <<= 1) {
+      const u32 y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const u32 total = __shfl(incl, 63, 64);
+    if (!total) {  // uniform
+      if (w < words) next_bits[w] = 0;
+      if (marks && !lane) next_marks[g] = 0;
+      continue;
+    }
+    for (u32 k = incl - cnt; m; m &= m - 1, ++k) list[wave][k] = u16(lane * 32 + __builtin_ctz(m));
+    left_words[wave][lane] = 0;
+    wave_sync();
+    for (u32 base = 0; base < total; base += 64) {
+      const u32 i = base + lane;
+      const bool mine = i < total;
+      const u32 e = mine ? list[wave][i] : 0u;
+      const u32 u = u32(g * 2048 + e);
       bool unres = false;
       if (mine) {
-        const u32 u = u32((g * 64 + idx) * 32 + b);
         u32 r = roots[u];
         unres = (bits[r >> 5] >> (r & 31)) & 1u;
-        const u32 links = resolve_links(round);
         for (u32 k = 0; unres && k < links; ++k) {
           r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           unres = (bits[r >> 5] >> (r & 31)) & 1u;
@@ -4518,14 +4561,19 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
           if (aw >> 62) aw %= kAdlerMod;
         } else {
           __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          atomicOr(&left_words[wave][e >> 5], 1u << (e & 31));
         }
       }
-      const u64 keep = __ballot(unres);
-      if (lane == 0) next_bits[g * 64 + i0] = u32(keep);
-      if (lane == 32 && i1 < 64) next_bits[g * 64 + i1] = u32(keep >> 32);
-      kept += lane == 0 ? u32(__popcll(keep)) : 0u;
     }
+    wave_sync();
+    const u32 nb = left_words[wave][lane];
+    if (w < words) next_bits[w] = nb;
+    kept += __popc(nb);
+    const bool left = __ballot(nb != 0) != 0;
+    if (marks && !lane) next_marks[g] = left ? 1 : 0;
+    wave_sync();  // the list and words are rewritten for the next group
   }
+  for (u32 off = 32; off; off >>= 1) kept += __shfl_down(kept, off, 64);
   if (lane_id() == 0 && kept) atomicAdd(reinterpret_cast<unsigned long long*>(next_count), u64(kept));
   if (parts) {  // uniform
     adler_block_sum(as, aw, red);
@@ -4747,7 +4795,9 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   // first unresolved bitmap are zeroed by g_frame.
   u8* zeroed = nullptr;
   const u64 zero_u64 = 2 * u64(3 * kAdlerSlots) + rounds + 1;
-  const u64 zero_bytes = 8 * zero_u64 + 4 * words + 4 * need_words;
+  // Resolve group marks (emission marks groups in marks0).
+  const u64 mark_groups_n = (words + 63) / 64;
+  const u64 zero_bytes = 8 * zero_u64 + 4 * words + 4 * need_words + (mark_groups_n + 3) / 4 * 4;
   HZ_TRY(scratch.alloc(&zeroed, zero_bytes));
   HZ_LAUNCH(g_frame, dim3(clamp_grid((zero_bytes / 4 + 255) / 256, 2048)), dim3(256), 0, stream,
             in, in_size, fmt.format, fmt.dict, fmt.dict_len, body_off, out_base, st,
@@ -4895,6 +4945,9 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   u32 *roots = nullptr, *bits1 = nullptr;
   HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
   HZ_TRY(scratch.alloc(&bits1, words));
+  u8* marks0 = zeroed + 8 * zero_u64 + 4 * words + 4 * need_words;
+  u8* marks1 = nullptr;
+  HZ_TRY(scratch.alloc(&marks1, mark_groups_n));
   const u64 out_end = out_total;  // a byte at position p is stream byte n - (out_end - p)
   // Emission by segments, then the queued units of long fixed runs.
   EmitUnit* units = nullptr;
@@ -4903,15 +4956,15 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   for (u32 pass = 0; pass < 2; ++pass) {
     HZ_LAUNCH(g_emit_lanes, dim3(emit_grid), dim3(kEmitThreads), 0, stream, body, len, st, acc,
               recs, slice_entry, slice_off, group_link, tables, out, roots, bits0, out_end,
-              adler_parts, units, unit_capacity, pass);
+              adler_parts, units, unit_capacity, pass, marks0);
     HZ_TRY(hipGetLastError());
   }
   HZ_LAUNCH(g_emit_serial, dim3(emit_grid), dim3(kWave), 0, stream, body, len, st, acc, out,
-            roots, bits0, out_end, adler_parts + 2 * kAdlerSlots);
+            roots, bits0, out_end, adler_parts + 2 * kAdlerSlots, marks0);
   HZ_TRY(hipGetLastError());
   for (u32 round = 0; round < rounds; ++round) {
     HZ_LAUNCH(g_resolve, dim3(resolve_grid), dim3(256), 0, stream, st, out, roots, bits0, bits1,
-              counts, round, rounds, words, out_end, adler_parts + 4 * kAdlerSlots);
+              counts, round, rounds, words, out_end, adler_parts + 4 * kAdlerSlots, marks0, marks1);
     HZ_TRY(hipGetLastError());
   }
   u64* parts = nullptr;
@@ -4972,7 +5025,8 @@ hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8
   HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
   for (u32 round = 0; round < rounds; ++round) {
     HZ_LAUNCH(g_resolve, dim3(u32(clamp_grid((words + 255) / 256, 2048))), dim3(256), 0, stream,
-              st, out, roots, bits0, bits1, counts, round, rounds, words, 0ull, nullptr);
+              st, out, roots, bits0, bits1, counts, round, rounds, words, 0ull, nullptr, nullptr,
+              nullptr);
     HZ_TRY(hipGetLastError());
   }
   HZ_LAUNCH(g_batch_wide_finish, dim3(n), dim3(256), 0, stream, files, list, n, out, st, wanted,
