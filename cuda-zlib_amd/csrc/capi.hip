@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -26,21 +27,31 @@ struct PoolEntry {
 };
 
 // A device buffer that calls carve their scratch from, kept between calls:
-// a call takes an idle arena of its device, makes its stream wait for the
-// arena's last use, and records that use again when it ends, so reuse needs
-// no allocation and no host synchronisation.
+// a call takes an idle arena of its device whose last use was on the call's
+// own stream or is already done (so that a call never waits for work on
+// another stream), makes its stream wait for that use, and records its own
+// use when it ends, so reuse needs no allocation and no host synchronisation.
 struct Arena {
   int device;
   u8* base;
   u64 capacity;
   hipEvent_t last_use;
+  hipStream_t last_stream;
   bool busy;
+};
+
+// A pinned host buffer for uploads (upload_to_device).
+struct PinnedStage {
+  void* host;
+  u64 bytes;
+  hipEvent_t done;  // recorded after the last copy out of it
+  bool taken;
 };
 
 struct PoolRegistry {
   std::mutex mutex;
   std::vector<PoolEntry> pools;
-  std::vector<std::pair<int, hipStream_t>> side_streams;
+  std::vector<PinnedStage> stages;
   std::vector<std::unique_ptr<Arena>> arenas;
   u64 retention = 1ull << 30;
 };
@@ -67,59 +78,57 @@ hipError_t get_pool(int device, hipMemPool_t* out) {
   u64 threshold = reg.retention;
   err = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
   if (err != hipSuccess) return err;
+  // No reuse that would make one caller's stream wait for another's work
+  // (memory freed on a stream whose work is still queued is not handed to
+  // another stream).
+  int no_waits = 0;
+  err = hipMemPoolSetAttribute(pool, hipMemPoolReuseAllowInternalDependencies, &no_waits);
+  if (err != hipSuccess) return err;
   reg.pools.push_back({device, pool});
   *out = pool;
   return hipSuccess;
 }
 
-// A second stream of the device, for work that overlaps the caller's stream
-// inside one call (created on first use with the default priority and kept,
-// like the pools, for the process lifetime).
-hipError_t get_side_stream(int device, hipStream_t* out) {
+
+}  // namespace
+
+hipError_t upload_to_device(hipStream_t stream, void* dst, const void* src, u64 bytes) {
+  if (!bytes) return hipSuccess;
   PoolRegistry& reg = registry();
-  std::lock_guard<std::mutex> lock(reg.mutex);
-  for (const auto& e : reg.side_streams)
-    if (e.first == device) { *out = e.second; return hipSuccess; }
-  hipStream_t side = nullptr;
-  hipError_t err = hipStreamCreateWithFlags(&side, hipStreamNonBlocking);
-  if (err != hipSuccess) return err;
-  reg.side_streams.push_back({device, side});
-  *out = side;
-  return hipSuccess;
+  std::unique_lock<std::mutex> lock(reg.mutex);
+  PinnedStage* stage = nullptr;
+  for (PinnedStage& e : reg.stages)
+    if (!e.taken && e.bytes >= bytes && hipEventQuery(e.done) == hipSuccess) {
+      stage = &e;
+      break;
+    }
+  if (!stage) {
+    PinnedStage e = {nullptr, std::max<u64>(bytes, 64 << 10), nullptr, false};
+    hipError_t err = hipHostMalloc(&e.host, e.bytes, hipHostMallocDefault);
+    if (err != hipSuccess) return err;
+    err = hipEventCreateWithFlags(&e.done, hipEventDisableTiming);
+    if (err != hipSuccess) {
+      (void)hipHostFree(e.host);
+      return err;
+    }
+    reg.stages.push_back(e);
+    stage = &reg.stages.back();
+  }
+  stage->taken = true;
+  void* host = stage->host;
+  hipEvent_t done = stage->done;
+  const size_t index = size_t(stage - reg.stages.data());
+  lock.unlock();
+  std::memcpy(host, src, bytes);
+  hipError_t err = hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, stream);
+  if (err == hipSuccess) err = hipEventRecord(done, stream);
+  lock.lock();
+  // Given back only once its copy is ordered before `done` (else kept out of use).
+  if (err == hipSuccess) reg.stages[index].taken = false;
+  return err;
 }
 
-// Work forked from `main` onto `side`: side starts after what main holds at
-// fork(), and main continues past join() (or the destructor, on every path)
-// only once side's work is done.  Events belong to the one call.
-class SideWork {
- public:
-  SideWork(hipStream_t main, hipStream_t side) : main_(main), side_(side) {}
-  hipError_t fork() {
-    hipError_t err = hipEventCreateWithFlags(&fork_, hipEventDisableTiming);
-    if (err == hipSuccess) err = hipEventCreateWithFlags(&join_, hipEventDisableTiming);
-    if (err == hipSuccess) err = hipEventRecord(fork_, main_);
-    if (err == hipSuccess) err = hipStreamWaitEvent(side_, fork_, 0);
-    forked_ = err == hipSuccess;
-    return err;
-  }
-  hipError_t join() {
-    if (!forked_) return hipSuccess;
-    forked_ = false;
-    hipError_t err = hipEventRecord(join_, side_);
-    if (err == hipSuccess) err = hipStreamWaitEvent(main_, join_, 0);
-    return err;
-  }
-  ~SideWork() {
-    (void)join();
-    if (fork_) (void)hipEventDestroy(fork_);
-    if (join_) (void)hipEventDestroy(join_);
-  }
-
- private:
-  hipStream_t main_, side_;
-  hipEvent_t fork_ = nullptr, join_ = nullptr;
-  bool forked_ = false;
-};
+namespace {
 
 bool find_pool(int device, hipMemPool_t* out) {
   PoolRegistry& reg = registry();
@@ -223,11 +232,15 @@ class Workspace final : public Scratch {
     PoolRegistry& reg = registry();
     std::lock_guard<std::mutex> lock(reg.mutex);
     const u64 want = (total_ + kArenaGranule - 1) / kArenaGranule * kArenaGranule;
-    if (!arena_ && want <= reg.retention) {
+    u64 kept_bytes = 0;  // the device's arenas
+    for (const auto& a : reg.arenas)
+      if (a->device == device_) kept_bytes += a->capacity;
+    if (!arena_ && kept_bytes + want <= reg.retention) {
       auto a = std::make_unique<Arena>();
       a->device = device_;
       a->base = nullptr;
       a->capacity = 0;
+      a->last_stream = nullptr;
       a->busy = true;
       keep(hipEventCreateWithFlags(&a->last_use, hipEventDisableTiming));
       if (first != hipSuccess) return first;
@@ -236,10 +249,11 @@ class Workspace final : public Scratch {
     }
     if (arena_ && total_ > arena_->capacity) {
       // Grow for later calls: the old buffer is freed after this call's work.
+      const u64 others = kept_bytes - arena_->capacity;  // the device's other arenas
       if (arena_->base) keep(hipFreeAsync(arena_->base, stream_));
       arena_->base = nullptr;
       arena_->capacity = 0;
-      if (want <= reg.retention) {
+      if (others + want <= reg.retention) {
         void* base = nullptr;
         hipError_t err = hipMallocFromPoolAsync(&base, want, pool_, stream_);
         keep(err);
@@ -251,6 +265,7 @@ class Workspace final : public Scratch {
     }
     if (arena_) {
       keep(hipEventRecord(arena_->last_use, stream_));
+      arena_->last_stream = stream_;
       arena_->busy = false;
     }
     return first;
@@ -263,7 +278,8 @@ class Workspace final : public Scratch {
     PoolRegistry& reg = registry();
     std::lock_guard<std::mutex> lock(reg.mutex);
     for (auto& a : reg.arenas)
-      if (a->device == device_ && !a->busy) {
+      if (a->device == device_ && !a->busy &&
+          (a->last_stream == stream_ || hipEventQuery(a->last_use) == hipSuccess)) {
         a->busy = true;
         arena_ = a.get();
         return hipStreamWaitEvent(stream_, arena_->last_use, 0);
@@ -687,10 +703,8 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
     BatchFile* device_files = nullptr;
     err = ws.alloc(&device_files, files);
     if (err != hipSuccess) return err;
-    // Pageable source: the runtime stages it before returning, so the host
-    // vector may go out of scope immediately afterwards.
-    err = hipMemcpyAsync(device_files, layout.data(), files * sizeof(BatchFile),
-                         hipMemcpyHostToDevice, stream);
+    // Staged before the call returns, so the host vector may go out of scope.
+    err = upload_to_device(stream, device_files, layout.data(), files * sizeof(BatchFile));
     if (err != hipSuccess) return err;
     const u32* encoded = encoded_rows ? encoded_metadata : nullptr;
     // Files of at least kBatchWideBytes go to the parallel route; the rest,
@@ -711,34 +725,24 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
     if (large.empty())
       return launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
                                   metadata, encoded, kBatchWideBytes);
-    // The small files decode on a second stream while the large ones take
-    // the parallel route here (they share no output bytes or metadata rows,
-    // and resolution writes single bytes of large files only); the caller's
-    // stream then waits for both.
-    hipStream_t side_stream = nullptr;
-    err = get_side_stream(ws.device(), &side_stream);
-    if (err != hipSuccess) return err;
-    SideWork side(stream, side_stream);
-    err = side.fork();
-    if (err != hipSuccess) return err;
-    err = launch_inflate_batch(side_stream, input, output, device_files, u32(files), kMaxBlocks,
+    // The small files, then the large ones by the parallel route, all on the
+    // caller's stream: a second stream would share one of the device's few
+    // hardware queues with unrelated streams and wait behind their work.
+    err = launch_inflate_batch(stream, input, output, device_files, u32(files), kMaxBlocks,
                                metadata, encoded, kBatchWideBytes);
     if (err != hipSuccess) return err;
     u32 *device_large = nullptr, *redo = nullptr;
     err = ws.alloc(&device_large, large.size());
     if (err == hipSuccess) err = ws.alloc(&redo, files);
     if (err != hipSuccess) return err;
-    err = hipMemcpyAsync(device_large, large.data(), large.size() * sizeof(u32),
-                         hipMemcpyHostToDevice, stream);
+    err = upload_to_device(stream, device_large, large.data(), large.size() * sizeof(u32));
     if (err != hipSuccess) return err;
     err = run_inflate_batch_wide(stream, ws, input, output, output_size, device_files,
                                  device_large, u32(large.size()), large_bits, encoded, kMaxBlocks,
                                  redo, metadata);
     if (err != hipSuccess) return err;
-    err = launch_inflate_batch(stream, input, output, device_files, u32(large.size()), kMaxBlocks,
-                               metadata, encoded, ~0ull, device_large, redo);
-    if (err != hipSuccess) return err;
-    return side.join();
+    return launch_inflate_batch(stream, input, output, device_files, u32(large.size()),
+                                kMaxBlocks, metadata, encoded, ~0ull, device_large, redo);
   });
 }
 

@@ -1540,13 +1540,9 @@ hipError_t run_deflate_batch(hipStream_t stream, Scratch& scratch, const u8* in,
   }
   HZ_TRY(scratch.alloc(&b.runs, runs.size()));
   b.run_count = parse_grid;
-  // Pageable sources: the runtime copies them before these calls return.
-  HZ_TRY(hipMemcpyAsync(b.runs, runs.data(), runs.size() * sizeof(u32), hipMemcpyHostToDevice,
-                        stream));
-  HZ_TRY(hipMemcpyAsync(b.descs, descs.data(), descs.size() * sizeof(ChunkDesc),
-                        hipMemcpyHostToDevice, stream));
-  HZ_TRY(hipMemcpyAsync(b.files, files.data(), count * sizeof(FileDesc), hipMemcpyHostToDevice,
-                        stream));
+  HZ_TRY(upload_to_device(stream, b.runs, runs.data(), runs.size() * sizeof(u32)));
+  HZ_TRY(upload_to_device(stream, b.descs, descs.data(), descs.size() * sizeof(ChunkDesc)));
+  HZ_TRY(upload_to_device(stream, b.files, files.data(), count * sizeof(FileDesc)));
   return run_chunks(stream, b, in, descs.size(), count, out, chunk_bytes, meta, true);
 }
 

@@ -38,6 +38,11 @@ void profile_record(const char* name, hipEvent_t start, hipEvent_t stop);
   } while (0)
 
 hipError_t launch_fill(hipStream_t stream, void* dst, u8 value, u64 bytes);
+// Host bytes to device memory in stream order, through pinned staging that
+// is reused once the copy is done: the copy neither waits for nor holds up
+// work on other streams (as the runtime's shared staging of pageable memory
+// does), and the host source may be reused when it returns.
+hipError_t upload_to_device(hipStream_t stream, void* dst, const void* src, u64 bytes);
 hipError_t launch_set_meta(hipStream_t stream, u32* meta, u32 first, u32 second);
 hipError_t launch_set_meta_rows(hipStream_t stream, u32* meta, u64 rows, u32 first, u32 second);
 

@@ -151,8 +151,8 @@ def test_small_dynamic_headers_match_the_serial_oracle(gpu, seed):
 
 
 def test_batch_on_a_side_stream_is_complete_when_that_stream_is(gpu):
-    """Small files decode on a second stream beside the large ones; the
-    caller's stream alone must cover both once synchronized."""
+    """A batch called on a non-default stream, with small and large files,
+    is complete once that stream is synchronized."""
     import torch
     from cuda_zlib import decompress_zlib_batch_checked
     rng = random.Random(77)
@@ -174,3 +174,43 @@ def test_batch_on_a_side_stream_is_complete_when_that_stream_is(gpu):
     stream.synchronize()
     assert host_meta.numpy()[:, 0].tolist() == [0] * len(raws)
     assert host_out.numpy().tobytes() == b"".join(raws)
+
+
+def test_batch_calls_on_two_streams_do_not_wait_for_each_other(gpu):
+    """Batches on two caller streams are independent: a batch on stream B must
+    finish while stream A, whose own batch waits behind a long kernel, is
+    still busy."""
+    import time
+    import torch
+    from cuda_zlib import decompress_zlib_batch_checked
+    rng = random.Random(91)
+    raws = []
+    for i in range(64):
+        if i % 4 == 0:
+            raws.append(workloads.text_like(rng.randrange(2000, 20000), np.random.default_rng(i)))
+        else:
+            raws.append(_small_dynamic(rng, rng.randrange(1, 256))[0])
+    packed = [zlib.compress(r, 6) for r in raws]
+    payload = torch.from_numpy(np.frombuffer(b"".join(packed), np.uint8).copy()).cuda()
+    sizes, expected = [len(s) for s in packed], [len(r) for r in raws]
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(b):  # module, pools and side stream in place
+        decompress_zlib_batch_checked(payload, sizes, expected, 0)
+    b.synchronize()
+    with torch.cuda.stream(a):
+        torch.cuda._sleep(1 << 30)  # about half a second of spinning on stream A
+        t0 = time.perf_counter()
+        out_a, meta_a = decompress_zlib_batch_checked(payload, sizes, expected, 0)
+        host_a = time.perf_counter() - t0
+    if host_a > 0.1:
+        pytest.skip("the call on the busy stream waited on the host (%.3f s)" % host_a)
+    with torch.cuda.stream(b):
+        out_b, meta_b = decompress_zlib_batch_checked(payload, sizes, expected, 0)
+    b.synchronize()
+    a_busy = not a.query()
+    a.synchronize()
+    assert a_busy, "stream B's batch finished only after stream A's work"
+    for out, meta in ((out_a, meta_a), (out_b, meta_b)):
+        assert meta.cpu().numpy()[:, 0].tolist() == [0] * len(raws)
+        assert out.cpu().numpy().tobytes() == b"".join(raws)
