@@ -1452,9 +1452,13 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
 // itself is written in full by e_emit and e_wrap.
 __global__ __launch_bounds__(256) void e_zero_tail(u8* out, u64 capacity, const u32* meta) {
   const u64 from = min<u64>(meta[0], capacity);
-  const u64 first16 = (from + 15) & ~u64(15), end16 = capacity & ~u64(15);
+  // Bytes up to the first 16-byte boundary of memory at or after out + from
+  // and after the last one before out + capacity one by one, 16-byte stores
+  // between (out may have any alignment).
+  const uintptr_t base = reinterpret_cast<uintptr_t>(out);
+  const u64 first16 = from + ((16 - ((base + from) & 15)) & 15);
+  const u64 end16 = capacity - ((base + capacity) & 15);
   const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x, stride = u64(gridDim.x) * blockDim.x;
-  // Unaligned bytes at both ends, then 16-byte stores (out is 256-byte aligned).
   if (first16 >= end16) {
     for (u64 i = from + tid; i < capacity; i += stride) out[i] = 0;
     return;
