@@ -32,7 +32,23 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "cuda-zlib_amd"))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0
+HBM_PEAK_GBS = 8000.0  # MI355X's published HBM3E bandwidth
+
+
+def device_hbm_peak_gbs(device=0):
+    """HBM peak from the device's own properties: memory clock (kHz) x bus
+    width (bits) x 4 transfers a clock (HBM3E reports a quarter of its data
+    rate: 2 GHz x 8192 bits x 4 = 8.19 TB/s on MI355X).  Recorded beside the
+    published figure."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    bus, clock = ctypes.c_int(0), ctypes.c_int(0)
+    # hipDeviceAttributeMemoryBusWidth = 59, hipDeviceAttributeMemoryClockRate = 60
+    if hip.hipDeviceGetAttribute(ctypes.byref(bus), 59, device) or \
+            hip.hipDeviceGetAttribute(ctypes.byref(clock), 60, device):
+        return None
+    return {"bus_bits": bus.value, "memory_clock_khz": clock.value,
+            "peak_gbs": round(4.0 * clock.value * 1e3 * bus.value / 8 / 1e9, 1)}
 MAX = 262144
 SAMPLES = 5          # timed repetitions behind every median
 MIB = 1 << 20
@@ -624,7 +640,8 @@ def main():
                      "hbm_fraction": round(gbs(n, v[0]) / HBM_PEAK_GBS, 6)}
                  for k, v in legs.items()},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 3),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "peak": HBM_PEAK_GBS, "peak_from_device": device_hbm_peak_gbs(),
+                     "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 6),
                      "traffic": traffic_from_profiles(dominant),
                      "avg_launch_ms": round(avg_ms, 4)},
