@@ -1154,15 +1154,15 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
 __global__ __launch_bounds__(256) void g_valid_scatter(State* st, const u64* pre,
                                                        const u32* wave_valid, u64* cand,
                                                        u64 cand_capacity, u64 max_candidates) {
-  static_assert(kDiscThreads == 2 * kValPerWave, "a block covers two validation waves");
+  static_assert(kDiscThreads % kValPerWave == 0, "a block covers whole validation waves");
   __shared__ u32 wave_count[kDiscThreads / 64];
   __shared__ u64 red[kDiscThreads / 64];
   if (st->status) return;
   const u64 n = st->precount;
   if (u64(blockIdx.x) * kDiscThreads >= n) return;
   const u32 t = threadIdx.x, wave = t >> 6, lane = lane_id();
-  // Valid entries before the block: waves 0 .. 2 * blockIdx.x - 1.
-  const u64 before_waves = 2 * u64(blockIdx.x);
+  // Valid entries before the block: the validation waves before its first.
+  const u64 before_waves = u64(blockIdx.x) * (kDiscThreads / kValPerWave);
   u64 part = 0;
   for (u64 w = t; w < before_waves; w += 4 * kDiscThreads) {
     const u64 w1 = w + kDiscThreads, w2 = w + 2 * kDiscThreads, w3 = w + 3 * kDiscThreads;
