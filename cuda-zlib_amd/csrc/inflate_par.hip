@@ -3659,15 +3659,6 @@ struct GlobalBytes {
   __device__ __forceinline__ void zero(u64, u32) const {}
 };
 
-// d[0, n) = v: bytes up to d's first 16-byte boundary, then 16-byte stores.
-__device__ __forceinline__ void fill_bytes(u8* d, u32 n, u8 v) {
-  u32 i = 0;
-  for (; i < n && (reinterpret_cast<uintptr_t>(d + i) & 15); ++i) d[i] = v;
-  const u32 v4 = 0x01010101u * v;
-  for (; i + 16 <= n; i += 16) *reinterpret_cast<uint4*>(d + i) = make_uint4(v4, v4, v4, v4);
-  for (; i < n; ++i) d[i] = v;
-}
-
 struct StagedBytes {
   u8* lds;
   u64 base;
@@ -3683,16 +3674,30 @@ struct StagedBytes {
 // the output buffer (summed as they are written).  The stage is all zero
 // when a round starts (the copy-out clears what it read), so the bytes a
 // resolve round provides are zero without a store each.
+// Byte pointers into LDS and into global memory, typed with their address
+// spaces so that the compiler issues LDS or global instructions: a flat one
+// (what a pointer chosen between the two becomes) counts against both wait
+// counters, so every LDS wait after it would also wait for pending stores.
+typedef __attribute__((address_space(3))) u8 lds_byte;
+typedef __attribute__((address_space(1))) u8 global_byte;
+typedef __attribute__((address_space(3))) u32 lds_word;
+typedef __attribute__((address_space(1))) u32 global_word;
+
 struct RoundBytes {
-  u8* lds;
+  lds_byte* lds;
   u64 base, split;  // split = base + stage bytes
-  u8* out;
+  global_byte* out;
   u64 end;
   // Sums of the bytes written straight to the output, held in the sink (not
   // behind a pointer to the caller's sums, which kept those in scratch
   // memory); the caller adds them after the slice.
   mutable AdlerAcc acc;
-  __device__ __forceinline__ u8 get(u64 p) const { return p < split ? lds[u32(p - base)] : out[p]; }
+  __device__ __forceinline__ RoundBytes(u8* stage, u64 base_, u64 split_, u8* out_, u64 end_)
+      : lds((lds_byte*)stage), base(base_), split(split_), out((global_byte*)out_), end(end_) {}
+  __device__ __forceinline__ u8 get(u64 p) const {
+    if (p < split) return lds[u32(p - base)];
+    return out[p];
+  }
   __device__ __forceinline__ void put(u64 p, u8 v) const {
     if (p < split) {
       lds[u32(p - base)] = v;
@@ -3703,15 +3708,32 @@ struct RoundBytes {
   }
   // out[p, p + n) = v (a run of the byte before it), 16 bytes a store.
   __device__ __forceinline__ void fill(u64 p, u32 n, u8 v) const {
+    const u32 v4 = 0x01010101u * v;
     const u32 in_stage = p < split ? u32(min<u64>(split - p, n)) : 0u;
-    if (in_stage) fill_bytes(lds + u32(p - base), in_stage, v);
+    if (in_stage) {  // the stage's byte 0 lies on a 16-byte boundary
+      const u32 k0 = u32(p - base);
+      u32 i = 0;
+      for (; i < in_stage && ((k0 + i) & 15); ++i) lds[k0 + i] = v;
+      for (; i + 16 <= in_stage; i += 16) {
+        lds_word* w = (lds_word*)(lds + k0 + i);
+        w[0] = w[1] = w[2] = w[3] = v4;
+      }
+      for (; i < in_stage; ++i) lds[k0 + i] = v;
+    }
     if (in_stage == n) return;
     const u64 a = p + in_stage;
     const u64 m = n - in_stage;
     // The bytes weigh end - a down to end - a - m + 1.
     acc.s += u64(v) * m;
     acc.w += u64(v) * (m * (end - a) - m * (m - 1) / 2);
-    fill_bytes(out + a, u32(m), v);
+    global_byte* d = out + a;
+    u32 i = 0;
+    for (; i < m && (reinterpret_cast<uintptr_t>((u8*)(d + i)) & 15); ++i) d[i] = v;
+    for (; i + 16 <= m; i += 16) {
+      global_word* w = (global_word*)(d + i);
+      w[0] = w[1] = w[2] = w[3] = v4;
+    }
+    for (; i < m; ++i) d[i] = v;
   }
   __device__ __forceinline__ void zero(u64, u32) const {}
 };
@@ -4132,7 +4154,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
             // Writes stay inside the round: a slice that would pass its end
             // is an extent error.
             const u64 rend = min(block_out + rec.size, hi);
-            const RoundBytes sink{sh.ostage, lo16, split, out, out_end, AdlerAcc{}};
+            const RoundBytes sink(sh.ostage, lo16, split, out, out_end);
             // Unchecked decoding when the slice and a token of overshoot lie
             // before the body end.
             if (dst0 < lo || dst0 > rend || stop < entry || stop - entry > kMaxEmitSlice)
@@ -4170,7 +4192,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
               const u64 dst0 = block_out + off;
               const u64 before = t ? scan[t - 1] : sh.carry;
               if (before >> 32 == kLastValue >> 32) {
-                const RoundBytes sink{sh.ostage, lo16, split, out, out_end, AdlerAcc{}};
+                const RoundBytes sink(sh.ostage, lo16, split, out, out_end);
                 sink.fill(dst0, lead, u8(before));
                 sums.s += sink.acc.s;
                 sums.w += sink.acc.w;
