@@ -3584,22 +3584,25 @@ __global__ __launch_bounds__(64) void g_emit_serial(const u8* body, u64 len, Sta
 
 namespace {
 constexpr u32 kEmitThreads = kDescThreads;
-// A long fixed run is emitted in units of this many slices (two rounds): its
-// segment's workgroup takes the first and queues the others for the unit
-// pass, so that the run spreads over the grid.
-constexpr u32 kUnitLanes = 2 * kEmitThreads;
 // Longest slice emission accepts, in bits (describe's slices are at most
 // 512 bits plus a token, a fixed run's windows 512 bits plus a token and an
 // end of block with its header): a longer one is an extent error.
 constexpr u64 kMaxEmitSlice = 4096;
 
-// Slices first .. first + kUnitLanes - 1 (at most) of the run in record
-// `rec`, whose output starts at block_out.  rec = kNone: a slot reserved
-// past the queue's end, skipped.
+// Below this many accepted segments every block's rounds are spread over the
+// grid as units (a workgroup per round); above it a segment's workgroup emits
+// its blocks' rounds itself, loading each block's tables once.
+constexpr u64 kSpreadSegments = 512;
+
+// One emission round: slices first .. first + 255 (at most) of record `rec`,
+// whose output starts at block_out, in slice groups from `group` on.
+// rec = kNone: a slot reserved past the queue's end, skipped.
 struct EmitUnit {
   u64 block_out;
   u32 rec;
   u32 first;
+  u32 group;
+  u32 pad;
 };
 
 // Output bytes of one round (256 slices) that g_emit_lanes stages in LDS
@@ -3612,9 +3615,9 @@ struct LaneEmitShared {
   Stage stage;
   u16 codes[320];
   BlockRec rec;
-  u64 first, chunk_end, round_lo, round_hi, unit_q;
+  u64 first, chunk_end, round_lo, round_hi;
   u64 carry;  // the state of the byte before the next round (kLastInherit: not known)
-  u32 count, next_g, need, unit_end, unit_more, any_lead;
+  u32 count, next_g, need, unit_end, unit_group, any_lead;
   u64 red[2][kEmitThreads / 64];
   __align__(16) u8 ostage[kOutStage + 16];  // a whole number of 16-byte lines
   // block_header interface
@@ -4013,6 +4016,7 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
   if (st->status) return;
   const u32 t = threadIdx.x;
   const u64 items = unit_pass ? min<u64>(st->emit_units, unit_capacity) : st->accepted;
+  const bool segments_few = st->accepted < kSpreadSegments;
   const u32 window = st->window;
   const u64 floor = st->floor;
   u64 unres_total = 0;  // this thread's unresolved bytes, counted once per wave at the end
@@ -4022,13 +4026,14 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
   for (u32 k = t; 16 * k < sizeof(sh.ostage); k += kEmitThreads)
     *reinterpret_cast<uint4*>(sh.ostage + 16 * k) = make_uint4(0, 0, 0, 0);
   for (u64 si = blockIdx.x; si < items; si += gridDim.x) {
-    u32 ri, first = 0;
+    u32 ri, first = 0, unit_group = kNone;
     u64 block_out;
     if (unit_pass) {
       const EmitUnit u = units[si];
       ri = u.rec;
       block_out = u.block_out;
       first = u.first;
+      unit_group = u.group;
     } else {
       const Segment seg = acc[si];
       ri = seg.rec_first;
@@ -4049,8 +4054,8 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
       }
       __syncthreads();
       const BlockRec rec = sh.rec;
-      if (unit_pass && (rec.type != 1 || !(rec.pad & kRecFixedRun) || first >= rec.lanes)) {
-        error = kExtent;  // never queued: units are slices of fixed runs
+      if (unit_pass && (rec.type == 0 || first >= rec.lanes)) {
+        error = kExtent;  // never queued: units are rounds of coded blocks
         break;
       }
       if (rec.type == 0) {
@@ -4058,46 +4063,57 @@ __global__ __launch_bounds__(kEmitThreads) __attribute__((amdgpu_waves_per_eu(4)
                    &sums, out_end - block_out);
         if (!t && rec.size) sh.carry = kLastValue | body[(rec.data >> 3) + rec.size - 1];
       } else {
-        if (rec.table == kNone) {
-          block_header<true, true, false>(body, len, ~0ull, sh);
-          if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
-        }
-        bool tables_pending = rec.table != kNone;
         const bool cross = (rec.pad & kRecFixedRun) != 0;
         if (!t) {
-          // The slices this workgroup emits: a unit of the unit pass; else the
-          // record's, or only the first unit of a long fixed run, whose other
-          // units are queued (all of them here when they do not fit).
-          u32 end = rec.lanes, more = 0;
-          u64 q = 0;
+          // The slices this workgroup emits: in the unit pass, its unit's
+          // round.  In the segment pass, a fixed run's rounds, and when the
+          // segments are too few to fill the grid every block's rounds, are
+          // queued as units so that they spread over the grid (with the
+          // queue full, emitted here); other blocks are emitted here, round
+          // after round with the tables loaded once.  A round's four slice
+          // groups are consecutive and its last links to the next round's
+          // first (a fixed run's groups are all consecutive).
+          u32 end = rec.lanes, g0 = rec.group;
           if (unit_pass) {
-            end = min(first + kUnitLanes, rec.lanes);
-          } else if (cross && rec.lanes > kUnitLanes) {
-            more = (rec.lanes - 1) / kUnitLanes;
-            q = atomicAdd(reinterpret_cast<unsigned long long*>(&st->emit_units), u64(more));
-            if (q + more <= unit_capacity) end = kUnitLanes;
+            end = min(first + kEmitThreads, rec.lanes);
+            g0 = unit_group;
+          } else if (rec.lanes && (cross || segments_few)) {
+            end = 0;
+            const u32 rounds = (rec.lanes + kEmitThreads - 1) / kEmitThreads;
+            const u64 q =
+                atomicAdd(reinterpret_cast<unsigned long long*>(&st->emit_units), u64(rounds));
+            if (q + rounds <= unit_capacity) {
+              u32 g = rec.group;
+              for (u32 r = 0; r < rounds; ++r) {
+                EmitUnit u;
+                u.block_out = block_out;
+                u.rec = ri;
+                u.first = r * kEmitThreads;
+                u.group = g;
+                u.pad = 0;
+                units[q + r] = u;
+                if (r + 1 < rounds) g = cross ? g + kEmitThreads / 64 : group_link[g + 3];
+              }
+            } else {
+              for (u64 r = q; r < unit_capacity && r < q + rounds; ++r) units[r].rec = kNone;
+              end = rec.lanes;
+            }
           }
           sh.unit_end = end;
-          sh.unit_more = more;
-          sh.unit_q = q;
+          sh.unit_group = g0;
         }
         __syncthreads();
-        if (sh.unit_more) {  // uniform
-          const u64 q = sh.unit_q;
-          const u32 more = sh.unit_more;
-          const bool queued = sh.unit_end < rec.lanes;
-          for (u32 i = t; i < more && q + i < unit_capacity; i += kEmitThreads) {
-            EmitUnit u;
-            u.block_out = block_out;
-            u.rec = queued ? ri : kNone;
-            u.first = (i + 1) * kUnitLanes;
-            units[q + i] = u;
-          }
-        }
         const u32 unit_end = sh.unit_end;
-        // A fixed run's slice groups are consecutive.
-        u32 g = rec.group + first / 64;
+        u32 g = sh.unit_group;
         u32 done = first;
+        bool tables_pending = false;
+        if (done < unit_end) {  // uniform
+          if (rec.table == kNone) {
+            block_header<true, true, false>(body, len, ~0ull, sh);
+            if (sh.status || sh.type != rec.type || sh.d0 != rec.data) { error = kExtent; break; }
+          }
+          tables_pending = rec.table != kNone;
+        }
         while (g != kNone && done < unit_end) {
           // One describe round: up to 256 slices in consecutive groups.  The
           // round's slice entries and offsets, and in the first round the
@@ -4971,7 +4987,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 out_end = out_total;  // a byte at position p is stream byte n - (out_end - p)
   // Emission by segments, then the queued units of long fixed runs.
   EmitUnit* units = nullptr;
-  const u64 unit_capacity = group_capacity * 64 / kUnitLanes + 64;
+  const u64 unit_capacity = group_capacity + 64;  // a round holds at least one slice group
   HZ_TRY(scratch.alloc(&units, unit_capacity));
   for (u32 pass = 0; pass < 2; ++pass) {
     HZ_LAUNCH(g_emit_lanes, dim3(emit_grid), dim3(kEmitThreads), 0, stream, body, len, st, acc,
