@@ -11,7 +11,8 @@ Prints one JSON line on stdout: value = uncompressed GB/s of the round trip
 (wall clock between synchronisations), each leg on its own, a roofline entry
 for the dominant kernel (timed live with HIP events on the codec's stream),
 the other workloads (256 MiB text encode, 4096-file batch, 1 GiB stress
-stream decode, 64 MiB text decode) timed the same way, and CPU baselines
+stream decode, 64 MiB text decode, 16 MiB fixed-Huffman text decode, 64 KiB
+text decode) timed the same way, and CPU baselines
 measured on this host in the same run: Python zlib and libdeflate, one
 thread and one pinned process per available core, and the oracle's serial C
 inflate.  Progress lines go to stderr.
@@ -299,6 +300,22 @@ def _gen(task):
         t = time.perf_counter()
         zlib.decompress(payload)
         out["zlib_decompress_s"] = time.perf_counter() - t
+    elif name == "fixed16":
+        raw = workloads.text_like(16 * MIB, np.random.default_rng(0))
+        c = zlib.compressobj(1, zlib.DEFLATED, 15, 8, zlib.Z_FIXED)
+        payload = c.compress(raw) + c.flush()
+        out["payload"], out["raw"] = _dump(payload), _dump(raw)
+        t = time.perf_counter()
+        zlib.decompress(payload)
+        out["zlib_decompress_s"] = time.perf_counter() - t
+    elif name == "text64k":
+        raw = workloads.text_like(64 * 1024, np.random.default_rng(7))
+        payload = zlib.compress(raw, 6)
+        out["payload"], out["raw"] = _dump(payload), _dump(raw)
+        t = time.perf_counter()
+        for _ in range(100):
+            zlib.decompress(payload)
+        out["zlib_decompress_s"] = (time.perf_counter() - t) / 100
     elif name == "c3":
         files = workloads.c3()
         out["files"] = _dump(b"".join(files))
@@ -478,7 +495,8 @@ def extra_configs(gpu, generated):
             "cpu_zlib_l1_single_gbs": round(total / info["zlib_l1_s"] / 1e9, 4),
             "cpu_zlib_decompress_single_gbs": round(total / info["zlib_decompress_s"] / 1e9, 4)}
         del src, slots, out
-    for key, label in (("c4", "c4_decode_1GiB_stress"), ("text64", "decode_64MiB_text_l6")):
+    for key, label in (("c4", "c4_decode_1GiB_stress"), ("text64", "decode_64MiB_text_l6"),
+                       ("fixed16", "decode_16MiB_text_fixed"), ("text64k", "decode_64KiB_text_l6")):
         if key not in generated:
             continue
         info = generated[key]
@@ -497,6 +515,10 @@ def extra_configs(gpu, generated):
                          "hbm_fraction": round(gbs(n, ms) / HBM_PEAK_GBS, 6),
                          "compressed_bytes": len(payload),
                          "cpu_zlib_single_gbs": round(n / info["zlib_decompress_s"] / 1e9, 4)}
+        if key == "text64k":
+            # Device time of one decode: HIP events around 200 back-to-back calls.
+            result[label]["device_us"] = round(gpu.timed(call, 200)[1] * 1000, 1)
+            result[label]["cpu_zlib_single_us"] = round(info["zlib_decompress_s"] * 1e6, 1)
         del src, out, ref
     return result
 
@@ -534,7 +556,7 @@ def main():
         # The other workloads are generated by CPU workers while the GPU runs
         # the headline; the CPU baselines run afterwards on idle cores.
         pool = mp.get_context("spawn").Pool(min(5, len(cores)))
-        pending = pool.map_async(_gen, ["c2", "c2_l6", "c3", "c4", "text64"])
+        pending = pool.map_async(_gen, ["c2", "c2_l6", "c3", "c4", "text64", "fixed16", "text64k"])
     lib = _native.load()
     gpu = Gpu(lib, _native)
     log("generating the 64 MiB strain stream")
