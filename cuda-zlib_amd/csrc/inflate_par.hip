@@ -4497,16 +4497,18 @@ __global__ __launch_bounds__(256) void g_batch_wide_finish(const BatchFile* file
   }
 }
 
-// Chain links a position follows in resolve round r: 2, 4, 8, and in the
-// last round as many as its chain has (a root always precedes its position,
-// so every chain ends).  Early rounds see nearly every unresolved byte, and a
+// Chain links a position follows in resolve round r: 2, 4, and in the last
+// round as many as its chain has (a root always precedes its position, so
+// every chain ends).  Early rounds see nearly every unresolved byte, and a
 // wave waits for its longest chain, so they take few links (measured on 64 MiB
 // of text: 2, 8, 32 took the rounds 6 % longer); each round leaves every
-// position's root as far along its chain as it got, so after three rounds a
-// chain of n links is n / 64 roots long.
-constexpr u32 kResolveRounds = 4;
+// position's root as far along its chain as it got, so after two rounds a
+// chain of n links is n / 8 roots long.  Schedules of 2, 8 / 4, 16 / 4, 8, 16
+// links before the last round took as long within 3 %.
+constexpr u32 kResolveRounds = 3;
+constexpr u32 kXcds = 8;  // MI355X: 8 accelerator complex dies of 32 CUs
 __host__ __device__ constexpr u32 resolve_links(u32 round) {
-  return round == 0 ? 2u : round == 1 ? 4u : round == 2 ? 8u : 0xffffffffu;
+  return round == 0 ? 2u : round == 1 ? 4u : 0xffffffffu;
 }
 inline u32 resolve_rounds(u64) { return kResolveRounds; }
 
@@ -4536,7 +4538,6 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
   u32* next_bits = round & 1 ? bits0 : bits1;
   u64* next_count = round + 1 == max_rounds ? &st->unresolved[1] : &counts[round + 1];
   const u32 lane = lane_id();
-  const u64 waves = u64(gridDim.x) * (blockDim.x / 64);
   u32 kept = 0;
   // A wave takes a group of 64 bitmap words at a time and lists the group's
   // unresolved positions in LDS (a prefix sum over the words' bit counts);
@@ -4553,7 +4554,17 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
   const u8* marks = round & 1 ? marks1 : marks0;
   u8* next_marks = round & 1 ? marks0 : marks1;
   const u32 links = resolve_links(round);
-  for (u64 g = u64(blockIdx.x) * (blockDim.x / 64) + wave; g * 64 < words; g += waves) {
+  // Workgroups are dealt to the 8 XCDs in turn (workgroup b to XCD b mod 8),
+  // each with its own L2.  XCD x takes the x-th eighth of the groups, its
+  // waves consecutive groups, so that the chains a wave follows back into
+  // the previous 32 KiB mostly read lines its own XCD's waves loaded.
+  const u32 xcds = gridDim.x < kXcds ? gridDim.x : kXcds;
+  const u32 xcd = blockIdx.x % xcds, xcd_block = blockIdx.x / xcds;
+  const u64 xcd_waves = u64(gridDim.x / xcds + (xcd < gridDim.x % xcds ? 1u : 0u)) * (blockDim.x / 64);
+  const u64 ngroups = (words + 63) / 64;
+  const u64 g_end = ngroups * (xcd + 1) / xcds;
+  for (u64 g = ngroups * xcd / xcds + u64(xcd_block) * (blockDim.x / 64) + wave; g < g_end;
+       g += xcd_waves) {
     if (marks && !marks[g]) {  // uniform
       if (!lane) next_marks[g] = 0;
       continue;
