@@ -801,14 +801,33 @@ __device__ __forceinline__ u64 range_offset(const u32* wg_count, const u64* bloc
   return block_base[b] + before;
 }
 
+// Pre-candidates one validation wave takes: the fewest (a power of two up to
+// kValPerWave) that spread them over at most kValResident waves, so that a
+// few pre-candidates get a wave each (a wave then waits for one walk, not
+// for a lane's several), and many take kValPerWave a wave, a lane walking a
+// few headers one after another.  The launch has more than kValResident
+// waves, and enough for n / kValPerWave.
+constexpr u32 kValPerWave = 128;
+constexpr u64 kValResident = 2048;
+__host__ __device__ inline u32 val_chunk(u64 n) {
+  u32 c = 1;
+  while (c < kValPerWave && n > u64(c) * kValResident) c <<= 1;
+  return c;
+}
+
 // Discovery pass 2: one workgroup scans the per-block entry totals into
-// offsets of the dense pre-candidate array.
+// offsets of the dense pre-candidate array.  When validation waves will take
+// fewer than kValPerWave pre-candidates each, several add into one range's
+// valid count, which is cleared here.
 __global__ __launch_bounds__(1024) void g_discover_scan(State* st, const u32* block_total,
                                                         u64* block_base, u64 blocks,
-                                                        u64 pre_capacity) {
+                                                        u64 pre_capacity, u32* range_valid) {
   __shared__ ScanShared sh;
   if (st->status) return;
   const u64 total = wg_exclusive_scan(block_total, ~0u, blocks, block_base, sh);
+  if (total <= pre_capacity && val_chunk(total) < kValPerWave)  // uniform
+    for (u64 i = threadIdx.x; i < (total + kValPerWave - 1) / kValPerWave; i += blockDim.x)
+      range_valid[i] = 0;
   if (threadIdx.x == 0) {
     st->precount = total;
     // Only kind-2 ranges (valid headers alone overflowing a range) can push the
@@ -883,7 +902,6 @@ namespace {
 // are copied into its LDS window and its code-length symbols are decoded
 // arithmetically from the canonical code (no per-candidate table); a walk
 // that reaches the window's end reloads the window from its position.
-constexpr u32 kValPerWave = 128;                    // pre-candidates per wave
 constexpr u32 kValRound = 16;                       // symbols between refills
 constexpr u32 kValWindowWords = 32;                 // LDS window per lane (dwords)
 constexpr u32 kValUsableBits = (kValWindowWords - 3) * 32;  // a read touches words pos/32 .. +2
@@ -1088,15 +1106,18 @@ __device__ __forceinline__ u32 val_step(const ValShared& sh, u32 lane, ValWalk& 
 }  // namespace
 
 // Discovery pass 4 (one wave per workgroup; see above).  Valid entries get
-// kValidBit; wave_valid[w] counts the valid entries of wave w's range.
+// kValidBit; wave_valid[r] counts the valid entries of pre-candidates
+// [kValPerWave r, kValPerWave (r + 1)), written by the wave that takes them
+// all or added by the waves that share them (val_chunk).
 __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre,
                                                  u32* wave_valid) {
   __shared__ ValShared sh;
   if (st->status) return;
   const u64 n = st->precount;
-  const u64 q0 = u64(blockIdx.x) * kValPerWave;
+  const u32 chunk = val_chunk(n);
+  const u64 q0 = u64(blockIdx.x) * chunk;
   if (q0 >= n) return;
-  const u64 q1 = min<u64>(q0 + kValPerWave, n);
+  const u64 q1 = min<u64>(q0 + chunk, n);
   const u32 lane = lane_id();
   u64 cursor = q0;  // next unassigned entry (uniform)
   u64 ci = 0;
@@ -1142,7 +1163,10 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
     }
   }
   for (u32 off = 32; off; off >>= 1) found += __shfl_xor(found, off, 64);
-  if (!lane) wave_valid[blockIdx.x] = found;
+  if (!lane) {
+    if (chunk == kValPerWave) wave_valid[blockIdx.x] = found;
+    else if (found) atomicAdd(&wave_valid[q0 / kValPerWave], found);
+  }
 }
 
 // Discovery pass 5: valid entries in order into the candidate array, one
@@ -4558,19 +4582,31 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
   // each with its own L2.  XCD x takes the x-th eighth of the groups, its
   // waves consecutive groups, so that the chains a wave follows back into
   // the previous 32 KiB mostly read lines its own XCD's waves loaded.
-  const u32 xcds = gridDim.x < kXcds ? gridDim.x : kXcds;
-  const u32 xcd = blockIdx.x % xcds, xcd_block = blockIdx.x / xcds;
-  const u64 xcd_waves = u64(gridDim.x / xcds + (xcd < gridDim.x % xcds ? 1u : 0u)) * (blockDim.x / 64);
   const u64 ngroups = (words + 63) / 64;
-  const u64 g_end = ngroups * (xcd + 1) / xcds;
-  for (u64 g = ngroups * xcd / xcds + u64(xcd_block) * (blockDim.x / 64) + wave; g < g_end;
-       g += xcd_waves) {
-    if (marks && !marks[g]) {  // uniform
-      if (!lane) next_marks[g] = 0;
-      continue;
+  // Follows the chain of entry e of group g; a byte left unresolved sets its
+  // bit in `left` (the group's next words).
+  const auto chase = [&](u64 g, u32 e, u32* left) {
+    const u32 u = u32(g * 2048 + e);
+    u32 r = roots[u];
+    bool unres = (bits[r >> 5] >> (r & 31)) & 1u;
+    for (u32 k = 0; unres && k < links; ++k) {
+      r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unres = (bits[r >> 5] >> (r & 31)) & 1u;
     }
-    const u64 w = g * 64 + lane;
-    u32 m = w < words ? bits[w] : 0u;
+    if (!unres) {
+      const u8 v = out[r];
+      out[u] = v;
+      as += v;
+      aw += (out_end - u) * v;
+      if (aw >> 62) aw %= kAdlerMod;
+    } else {
+      __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      atomicOr(&left[e >> 5], 1u << (e & 31));
+    }
+  };
+  // The group's unresolved positions into the wave's list (a prefix sum over
+  // the words' bit counts); returns their number.
+  const auto list_group = [&](u64 g, u32 m) {
     const u32 cnt = __popc(m);
     u32 incl = cnt;
 #pragma unroll
@@ -4578,47 +4614,72 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
       const u32 y = __shfl_up(incl, off, 64);
       if (lane >= off) incl += y;
     }
-    const u32 total = __shfl(incl, 63, 64);
-    if (!total) {  // uniform
-      if (w < words) next_bits[w] = 0;
-      if (marks && !lane) next_marks[g] = 0;
-      continue;
-    }
     for (u32 k = incl - cnt; m; m &= m - 1, ++k) list[wave][k] = u16(lane * 32 + __builtin_ctz(m));
-    left_words[wave][lane] = 0;
-    wave_sync();
-    for (u32 base = 0; base < total; base += 64) {
-      const u32 i = base + lane;
-      const bool mine = i < total;
-      const u32 e = mine ? list[wave][i] : 0u;
-      const u32 u = u32(g * 2048 + e);
-      bool unres = false;
-      if (mine) {
-        u32 r = roots[u];
-        unres = (bits[r >> 5] >> (r & 31)) & 1u;
-        for (u32 k = 0; unres && k < links; ++k) {
-          r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          unres = (bits[r >> 5] >> (r & 31)) & 1u;
-        }
-        if (!unres) {
-          const u8 v = out[r];
-          out[u] = v;
-          as += v;
-          aw += (out_end - u) * v;
-          if (aw >> 62) aw %= kAdlerMod;
-        } else {
-          __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          atomicOr(&left_words[wave][e >> 5], 1u << (e & 31));
-        }
+    return __shfl(incl, 63, 64);
+  };
+  if (ngroups <= gridDim.x) {  // uniform
+    // Few groups (a small output): a workgroup per group, its four waves
+    // chasing every fourth batch of 64 entries, so that a group's chains are
+    // followed four times as fast.  Each wave lists the group itself.
+    for (u64 g = blockIdx.x; g < ngroups; g += gridDim.x) {
+      if (marks && !marks[g]) {  // uniform
+        if (!threadIdx.x) next_marks[g] = 0;
+        continue;
       }
+      const u64 w = g * 64 + lane;
+      const u32 total = list_group(g, w < words ? bits[w] : 0u);
+      if (!total) {  // uniform
+        if (!wave && w < words) next_bits[w] = 0;
+        if (marks && !threadIdx.x) next_marks[g] = 0;
+        continue;
+      }
+      if (!wave) left_words[0][lane] = 0;
+      __syncthreads();
+      for (u32 i = wave * 64 + lane; i < total; i += 256) chase(g, list[wave][i], left_words[0]);
+      __syncthreads();
+      if (!wave) {
+        const u32 nb = left_words[0][lane];
+        if (w < words) next_bits[w] = nb;
+        kept += __popc(nb);
+        const bool left = __ballot(nb != 0) != 0;
+        if (marks && !lane) next_marks[g] = left ? 1 : 0;
+      }
+      __syncthreads();  // the list and words are rewritten for the next group
     }
-    wave_sync();
-    const u32 nb = left_words[wave][lane];
-    if (w < words) next_bits[w] = nb;
-    kept += __popc(nb);
-    const bool left = __ballot(nb != 0) != 0;
-    if (marks && !lane) next_marks[g] = left ? 1 : 0;
-    wave_sync();  // the list and words are rewritten for the next group
+  } else {
+    // Workgroups are dealt to the 8 XCDs in turn (workgroup b to XCD b mod
+    // 8), each with its own L2.  XCD x takes the x-th eighth of the groups,
+    // its waves consecutive groups, so that the chains a wave follows back
+    // into the previous 32 KiB mostly read lines its own XCD's waves loaded.
+    const u32 xcds = gridDim.x < kXcds ? gridDim.x : kXcds;
+    const u32 xcd = blockIdx.x % xcds, xcd_block = blockIdx.x / xcds;
+    const u64 xcd_waves =
+        u64(gridDim.x / xcds + (xcd < gridDim.x % xcds ? 1u : 0u)) * (blockDim.x / 64);
+    const u64 g_end = ngroups * (xcd + 1) / xcds;
+    for (u64 g = ngroups * xcd / xcds + u64(xcd_block) * (blockDim.x / 64) + wave; g < g_end;
+         g += xcd_waves) {
+      if (marks && !marks[g]) {  // uniform
+        if (!lane) next_marks[g] = 0;
+        continue;
+      }
+      const u64 w = g * 64 + lane;
+      const u32 total = list_group(g, w < words ? bits[w] : 0u);
+      if (!total) {  // uniform
+        if (w < words) next_bits[w] = 0;
+        if (marks && !lane) next_marks[g] = 0;
+        continue;
+      }
+      left_words[wave][lane] = 0;
+      wave_sync();
+      for (u32 i = lane; i < total; i += 64) chase(g, list[wave][i], left_words[wave]);
+      wave_sync();
+      const u32 nb = left_words[wave][lane];
+      if (w < words) next_bits[w] = nb;
+      kept += __popc(nb);
+      const bool left = __ballot(nb != 0) != 0;
+      if (marks && !lane) next_marks[g] = left ? 1 : 0;
+      wave_sync();  // the list and words are rewritten for the next group
+    }
   }
   for (u32 off = 32; off; off >>= 1) kept += __shfl_down(kept, off, 64);
   if (lane_id() == 0 && kept) atomicAdd(reinterpret_cast<unsigned long long*>(next_count), u64(kept));
@@ -4855,13 +4916,16 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   const u64 groups = len ? (len + kDiscRange - 1) / kDiscRange : 1;
   const u64 pre_capacity = groups * kDiscCap + u64(max_candidates) + 1;
   const u64 pre_blocks = (pre_capacity + kDiscThreads - 1) / kDiscThreads;
-  const u64 val_waves = (pre_capacity + kValPerWave - 1) / kValPerWave;
+  // Valid counts per kValPerWave pre-candidates; the launch has a wave for
+  // every val_chunk(n) of them (n <= pre_capacity).
+  const u64 val_ranges = (pre_capacity + kValPerWave - 1) / kValPerWave;
+  const u64 val_waves = std::max(val_ranges, std::min(pre_capacity, kValResident));
   u32 *wg_count = nullptr, *wave_valid = nullptr;
   u64 *wg_list = nullptr, *pre = nullptr, *cand = nullptr;
   HZ_TRY(scratch.alloc(&wg_count, groups));
   HZ_TRY(scratch.alloc(&wg_list, groups * kDiscCap));
   HZ_TRY(scratch.alloc(&pre, pre_capacity));
-  HZ_TRY(scratch.alloc(&wave_valid, val_waves));
+  HZ_TRY(scratch.alloc(&wave_valid, val_ranges));
   const u64 cand_capacity = u64(max_candidates) + 1;
   HZ_TRY(scratch.alloc(&cand, cand_capacity));
   // Each discovery workgroup takes per_block consecutive ranges.
@@ -4877,7 +4941,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
             wg_list, dense, block_total, groups, per_block);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_discover_scan, dim3(1), dim3(1024), 0, stream, st, block_total, block_base, blocks,
-            pre_capacity);
+            pre_capacity, wave_valid);
   HZ_TRY(hipGetLastError());
   HZ_LAUNCH(g_discover_gather, dim3(u32((groups + kDiscThreads / 64 - 1) / (kDiscThreads / 64))),
             dim3(kDiscThreads), 0, stream, st, wg_count, wg_list, block_base, pre, groups,
@@ -4985,7 +5049,9 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
 
   // Emission and cross-segment resolution.
   const u32 emit_grid = clamp_grid(max_blocks, 4096);
-  const u32 resolve_grid = clamp_grid((words + 255) / 256, 2048);
+  // A workgroup per group of 64 words while there are at most 2048 groups
+  // (g_resolve then shares each group among its waves), else 2048.
+  const u32 resolve_grid = clamp_grid((words + 63) / 64, 2048);
   u64* adler_parts = reinterpret_cast<u64*>(zeroed);
   u64* counts = adler_parts + 2 * u64(3 * kAdlerSlots);
   u32* bits0 = reinterpret_cast<u32*>(counts + rounds + 1);
