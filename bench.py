@@ -533,6 +533,9 @@ def main():
                         help="skip the other workloads (256 MiB text, batch, stress, text)")
     parser.add_argument("--legs", choices=("both", "decode", "encode"), default="both",
                         help="restrict the timed step to one leg (profiling runs; implies --no-extra)")
+    parser.add_argument("--only", choices=("c2", "c3", "c4", "text64", "fixed16", "text64k"),
+                        help="time one of the other workloads alone (profiling runs): prints "
+                             "its figures as one JSON line, no headline")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="run one plain 256 MiB device copy first, so that hardware "
                              "counters of a kernel with known traffic sit in the same profile")
@@ -550,6 +553,15 @@ def main():
     from cuda_zlib import _native
 
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    if args.only:
+        lib = _native.load()
+        gpu = Gpu(lib, _native)
+        log("generating workload %s" % args.only)
+        generated = dict([_gen(args.only)])
+        if args.only == "c2":
+            generated.update([_gen("c2_l6")])
+        print(json.dumps({"workload": args.only, "configs": extra_configs(gpu, generated)}), flush=True)
+        return 0
     cores, cpu_info = available_cpus()
     pool = pending = None
     if extras:

@@ -4982,7 +4982,11 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&tables, table_capacity));
   HZ_TRY(scratch.alloc(&hdr_d0, table_capacity));
   HZ_TRY(scratch.alloc(&hdr_info, table_capacity));
-  HZ_LAUNCH(g_headers, dim3(clamp_grid(table_capacity, 8192)), dim3(kWave), 0, stream, body, len, st,
+  // Grid-stride kernels over candidates, segments or units launch at most one
+  // workgroup per 64 body bytes (at least 256): a small stream has few of
+  // them, and idle workgroups of a 4096-wide launch cost their dispatch.
+  const u64 items_cap = std::max<u64>(256, len / 64);
+  HZ_LAUNCH(g_headers, dim3(clamp_grid(std::min(table_capacity, 2 * items_cap), 8192)), dim3(kWave), 0, stream, body, len, st,
             cand, tables, table_capacity, hdr_d0, hdr_info);
   HZ_TRY(hipGetLastError());
   HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
@@ -4992,7 +4996,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(scratch.alloc(&seg_last, cand_capacity));
   HZ_TRY(scratch.alloc(&region_cand, cand_capacity));
   u32* fix_need = reinterpret_cast<u32*>(zeroed + 8 * zero_u64 + 4 * words);
-  HZ_LAUNCH(g_describe, dim3(clamp_grid(cand_capacity, 4096)), dim3(kDescThreads), 0, stream, body, len,
+  HZ_LAUNCH(g_describe, dim3(clamp_grid(std::min(cand_capacity, items_cap), 4096)), dim3(kDescThreads), 0, stream, body, len,
             cand, st, out_size, seg_end, seg_size, seg_blocks, seg_next, seg_flags, seg_rec, recs,
             rec_capacity, slice_entry, slice_off, group_link, group_capacity, tables,
             table_capacity, hdr_d0, hdr_info, seg_last, region_cand);
@@ -5026,7 +5030,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_LAUNCH(g_fix_groups, dim3(clamp_grid((fix_group_count * 64 + 255) / 256, 2048)), dim3(256), 0,
             stream, st, fix_need, fix_sum, tiles, fix_groups);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(g_fix_walk, dim3(clamp_grid(cand_capacity, 2048)), dim3(kWave), 0, stream, body, len, st,
+  HZ_LAUNCH(g_fix_walk, dim3(clamp_grid(std::min(cand_capacity, items_cap), 2048)), dim3(kWave), 0, stream, body, len, st,
             cand, fix_need, fix_sum, tiles, seg_end, seg_size, seg_blocks, seg_next, seg_flags,
             seg_rec, seg_last, region_cand, recs, rec_capacity, fix_runs, run_capacity, fix_rt,
             rt_capacity, group_link, group_capacity, out_size, fix_groups);
@@ -5048,7 +5052,7 @@ hipError_t run_inflate_general(hipStream_t stream, Scratch& scratch, const u8* i
   HZ_TRY(hipGetLastError());
 
   // Emission and cross-segment resolution.
-  const u32 emit_grid = clamp_grid(max_blocks, 4096);
+  const u32 emit_grid = clamp_grid(std::min<u64>(max_blocks, items_cap), 4096);
   // A workgroup per group of 64 words while there are at most 2048 groups
   // (g_resolve then shares each group among its waves), else 2048.
   const u32 resolve_grid = clamp_grid((words + 63) / 64, 2048);
