@@ -4,7 +4,8 @@ Checked through the C ABI against HipZlibCompress on two calls in a row, the
 second with a smaller input (the fixed scratch keeps the first call's
 contents), plus CPU zlib round trips; an input whose scratch would not fit is
 refused with a clear error; in a fresh process the entry point never creates
-the scratch pool.
+the scratch pool; one call captured in a HIP graph (torch.cuda.graph) and
+replayed over inputs rewritten in place gives HipZlibCompress's streams.
 """
 
 import ctypes
@@ -102,3 +103,47 @@ def test_fresh_process_never_creates_the_pool(gpu):
     proc = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True,
                           timeout=300)
     assert proc.returncode == 0 and "CHILD OK" in proc.stdout, proc.stderr[-3000:]
+
+
+def test_no_alloc_captured_in_a_graph_replays_over_new_inputs(gpu):
+    """Capture one call, then replay it several times, the input rewritten in
+    place between replays (eager work and a synchronisation around each), and
+    check every replay against HipZlibCompress on the same bytes."""
+    import torch
+    from cuda_zlib import _native
+    lib = _native.load()
+    dev = torch.device("cuda", 0)
+    n, chunk = 1 << 20, 32768
+    capacity = n + 5 * (n // chunk) + 6
+    inputs = [workloads.text_like(n, np.random.default_rng(31)), workloads.strain(n // 4, 32),
+              bytes(np.random.default_rng(33).integers(0, 256, n, dtype=np.uint8))]
+    src = torch.empty(n, dtype=torch.uint8, device=dev)
+    out = torch.empty(capacity, dtype=torch.uint8, device=dev)
+    meta = torch.empty(2, dtype=torch.uint32, device=dev)
+
+    def call():
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        return lib.HipZlibCompressNoAlloc(stream, chunk, _ptr(src), n, _ptr(out), capacity,
+                                          _ptr(meta), 2)
+
+    src.copy_(torch.frombuffer(bytearray(inputs[0]), dtype=torch.uint8))
+    assert call() == 0  # eager first call: the device's scratch address is looked up here
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = call()
+    assert rc == 0
+    for data in inputs + inputs[::-1]:
+        host = torch.frombuffer(bytearray(data), dtype=torch.uint8)
+        src.copy_(host)
+        out.fill_(0xA5)
+        meta.fill_(0xDEAD)
+        torch.cuda.synchronize(dev)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        length, status = (int(v) for v in meta.cpu().numpy())
+        assert status == 0
+        got = out.cpu().numpy().tobytes()
+        assert zlib.decompress(got[:length]) == data
+        rc, slot, meta_a = _compress(lib, "HipZlibCompress", data, chunk)
+        assert rc == 0 and meta_a == [length, 0] and slot == got
