@@ -63,9 +63,13 @@ int HipZlibDecompress(hipStream_t stream, int64_t max_candidates, int64_t max_bl
  * statuses: 24 (gzip CRC-32 or ISIZE mismatch; output kept, as for 21) and 25
  * (dictionary Adler-32 differs from the DICTID).  Bytes after the stream's end
  * (such as a second gzip member) give status 12.  Format 0 without a
- * dictionary is exactly HipZlibDecompress.  No counterpart in the reference,
- * which rejects gzip with status 16 and dictionaries with 17
- * (src/cuda_zlib/_codec.py:105-111).
+ * dictionary is exactly HipZlibDecompress.  With a dictionary, an output
+ * above 64 KiB (or any output under non-default limits) is decoded into
+ * scratch behind the dictionary's last 32 KiB and then copied to `output`:
+ * the call needs about output_size more scratch, and one more pass over the
+ * output, than the same stream without a dictionary.  No
+ * counterpart in the reference, which rejects gzip with status 16 and
+ * dictionaries with 17 (src/cuda_zlib/_codec.py:105-111).
  *
  * format | HIP_ZLIB_FORMAT_MEMBERS (zlib or gzip, no dictionary) decodes a
  * concatenation: one member after another (each zlib stream or gzip member
