@@ -1048,8 +1048,13 @@ __host__ __device__ inline u32 crc_finish(u32 linear, u64 n) {
 // whether the caller supplied a preset dictionary.  Statuses follow the zlib
 // route's order: truncated wrapper 14, bad header 15, gzip magic under zlib 16,
 // a preset dictionary nobody supplied 17.
+// With `fields_at`, a gzip header's FNAME, FCOMMENT and FHCRC fields are
+// left to the caller: *fields_at is where they start (0 when the header has
+// none), and f holds everything else (f.body and f.body_len are set once
+// the fields are parsed).  Without it, they are parsed here, byte by byte.
 __host__ __device__ inline u32 parse_frame(const u8* in, u64 size, u32 format, bool have_dict,
-                                           Frame& f) {
+                                           Frame& f, u64* fields_at = nullptr) {
+  if (fields_at) *fields_at = 0;
   f.body = 0;
   f.body_len = 0;
   f.window = 32768;
@@ -1093,6 +1098,15 @@ __host__ __device__ inline u32 parse_frame(const u8* in, u64 size, u32 format, b
     p += 2 + (u64(in[p]) | (u64(in[p + 1]) << 8));
     if (p > limit) return kTruncatedZlib;
   }
+  f.check = kCheckCrc;
+  f.wanted = u32(in[size - 8]) | (u32(in[size - 7]) << 8) | (u32(in[size - 6]) << 16) |
+             (u32(in[size - 5]) << 24);
+  f.isize = u32(in[size - 4]) | (u32(in[size - 3]) << 8) | (u32(in[size - 2]) << 16) |
+            (u32(in[size - 1]) << 24);
+  if (fields_at && (flg & (2 | 8 | 16))) {
+    *fields_at = p;
+    return kOk;
+  }
   for (u32 field = 8; field <= 16; field <<= 1) {  // FNAME, then FCOMMENT
     if (!(flg & field)) continue;
     while (p < limit && in[p]) ++p;
@@ -1108,11 +1122,6 @@ __host__ __device__ inline u32 parse_frame(const u8* in, u64 size, u32 format, b
   }
   f.body = p;
   f.body_len = limit - p;
-  f.check = kCheckCrc;
-  f.wanted = u32(in[size - 8]) | (u32(in[size - 7]) << 8) | (u32(in[size - 6]) << 16) |
-             (u32(in[size - 5]) << 24);
-  f.isize = u32(in[size - 4]) | (u32(in[size - 3]) << 8) | (u32(in[size - 2]) << 16) |
-            (u32(in[size - 1]) << 24);
   return kOk;
 }
 

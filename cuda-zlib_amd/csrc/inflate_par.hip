@@ -567,6 +567,68 @@ __device__ u64 wg_exclusive_scan(const u32* in, u32 mask, u64 count, u64* out, S
 
 }  // namespace
 
+// A gzip header's FNAME, FCOMMENT and FHCRC fields from `p` (RFC 1952 2.3.1),
+// by the whole 256-thread workgroup, with the statuses parse_frame gives:
+// each field's terminating zero is searched 4 KiB at a time (16 bytes a
+// thread), and the header's CRC-32 (for FHCRC) is summed a piece per thread
+// and the pieces joined by GF(2) shifts, so that a hostile header as long as
+// the input costs a parallel pass, not a serial one.  Returns the status;
+// f.body and f.body_len on success.
+__device__ u32 gzip_fields_group(const u8* in, u64 size, u64 p, Frame& f, u64& zmin, u32* table,
+                                 u32* piece) {
+  const u32 t = threadIdx.x;
+  const u32 flg = in[3];
+  const u64 limit = size - 8;
+  for (u32 field = 8; field <= 16; field <<= 1) {  // FNAME, then FCOMMENT
+    if (!(flg & field)) continue;
+    u64 zero_at = limit;
+    for (u64 base = p; base < limit; base += 16 * 256) {  // uniform
+      if (!t) zmin = limit;
+      __syncthreads();
+      const u64 q = base + 16 * u64(t);
+      for (u32 j = 0; j < 16 && q + j < limit; ++j)
+        if (!in[q + j]) {
+          atomicMin(reinterpret_cast<unsigned long long*>(&zmin), q + j);
+          break;
+        }
+      __syncthreads();
+      zero_at = zmin;
+      __syncthreads();  // every thread has read zmin before it is reset
+      if (zero_at < limit) break;  // uniform
+    }
+    if (zero_at >= limit) return kTruncatedZlib;
+    p = zero_at + 1;
+  }
+  if (flg & 2) {
+    if (p + 2 > limit) return kTruncatedZlib;
+    table[t] = crc_byte_update(0, t);
+    __syncthreads();
+    // Thread t: the register (from 0) of bytes [t c, (t + 1) c) of [0, p).
+    const u64 c = (p + 255) / 256, lo = min(p, u64(t) * c), hi = min(p, lo + c);
+    u32 reg = 0;
+    for (u64 i = lo; i < hi; ++i) reg = table[(reg ^ in[i]) & 255u] ^ (reg >> 8);
+    piece[t] = reg;
+    __syncthreads();
+    if (!t) {
+      const u32 shift = crc_shift_bytes(c);
+      u32 all = 0;
+      for (u32 k = 0; k < 256 && u64(k) * c < p; ++k) {
+        const u64 len = min(p, u64(k + 1) * c) - u64(k) * c;
+        all = crc_mul(all, len == c ? shift : crc_shift_bytes(len)) ^ piece[k];
+      }
+      piece[0] = crc_finish(all, p);
+    }
+    __syncthreads();
+    if ((piece[0] & 0xffffu) != (u32(in[p]) | (u32(in[p + 1]) << 8))) return kInvalidHeader;
+    p += 2;
+  }
+  if (!t) {
+    f.body = p;
+    f.body_len = limit - p;
+  }
+  return kOk;
+}
+
 // Wrapper checks and the state's initial values.  `body_off` is where the
 // host-side launches place the body (2 for zlib, 10 for gzip, 0 for raw); a
 // wrapper field between it and the first block (a zlib DICTID, gzip's
@@ -582,14 +644,22 @@ __global__ __launch_bounds__(256) void g_frame(const u8* in, u64 in_size, u32 fo
   __shared__ Frame frame;
   __shared__ u32 status;
   __shared__ u64 red[2][4];
+  __shared__ u64 fields_at, zmin;
+  __shared__ u32 crc_table[256], crc_piece[256];
   const u32 t = threadIdx.x, lane = lane_id(), wave = t >> 6;
   {
     const u64 stride = u64(gridDim.x) * blockDim.x;
     for (u64 i = u64(blockIdx.x) * blockDim.x + t; i < zero_words; i += stride) zero[i] = 0;
   }
   if (blockIdx.x) return;
-  if (!t) status = parse_frame(in, in_size, format, dict_len > 0, frame);
+  if (!t) status = parse_frame(in, in_size, format, dict_len > 0, frame, &fields_at);
   __syncthreads();
+  if (!status && fields_at) {  // uniform: gzip's optional fields, by the workgroup
+    const u32 s = gzip_fields_group(in, in_size, fields_at, frame, zmin, crc_table, crc_piece);
+    __syncthreads();
+    if (!t) status = s;
+    __syncthreads();
+  }
   if (!status && frame.needs_dict) {  // uniform
     u64 s = 0, w = 0;
     for (u64 i = t; i < dict_len; i += 256) {

@@ -112,6 +112,30 @@ def test_wrapper_parsing_of_every_truncation(harness, stream_files, tmp_path):
         assert got[p]["f0"] == "0" and got[p]["f1"] == "0" and got[p]["f2"] == "15"
 
 
+def test_gzip_long_header_fields_every_truncation(harness, tmp_path):
+    """A 3000-byte FNAME (terminated, with a comment and FHCRC; and one that
+    runs into the trailer) parsed at every truncation from guarded buffers:
+    no read past the end, and the full files give 0 and 14."""
+    import struct
+    name = bytes(range(1, 256)) * 12 + b"abcdefghijklmno"
+    data = b"header fields " * 40
+    header = bytes((0x1F, 0x8B, 8, 8 | 16 | 2)) + bytes(6) + name + b"\0" + b"comment\0"
+    header += struct.pack("<H", zlib.crc32(header) & 0xFFFF)
+    c = zlib.compressobj(6, zlib.DEFLATED, -15)
+    good = header + c.compress(data) + c.flush() + struct.pack("<II", zlib.crc32(data), len(data))
+    assert zlib.decompress(good, 31) == data
+    runs_on = bytes((0x1F, 0x8B, 8, 8)) + bytes(6) + name + bytes(8)
+    paths = []
+    for label, blob in (("long_name.gz", good), ("runs_on.gz", runs_on)):
+        path = tmp_path / label
+        path.write_bytes(blob)
+        paths.append(str(path))
+    proc = _run(harness, "frame", paths)
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    got = _parse(proc.stdout)
+    assert got[paths[0]]["f2"] == "0" and got[paths[1]]["f2"] == "14"
+
+
 def test_literal_pairs_match_single_tokens(harness, stream_files):
     """quick_pair (two literals per step) and quick_triple (three) stop at
     every slice end where quick_token does, end every step at one of its token

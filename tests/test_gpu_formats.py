@@ -105,6 +105,27 @@ def _gzip_cases():
     ]
 
 
+def test_gzip_long_header_fields_on_the_general_route(gpu, no_cpu_codec):
+    """A 300 KB FNAME, a comment and FHCRC before a 200 KB body: the general
+    route's frame pass finds the terminators and the header CRC-32 with its
+    whole workgroup, with parse_frame's statuses (0, 15 for a header CRC that
+    does not match, 14 for a name that runs into the trailer)."""
+    import cuda_zlib
+    data = _text(200000, 41)
+    name = bytes(np.random.default_rng(42).integers(1, 256, 300000, dtype=np.uint8))
+    good = _gzip_member(data, name=name, comment=b"c" * 5000, hcrc=True)
+    assert zlib.decompress(good, 31) == data
+    bad_hcrc = bytearray(good)
+    bad_hcrc[150000] = 1 if bad_hcrc[150000] != 1 else 2  # inside the name, still not zero
+    runs_on = bytes((0x1F, 0x8B, 8, 8)) + bytes(6) + name + bytes(8)  # no zero before the trailer
+    for stream, status in ((good, 0), (bytes(bad_hcrc), 15), (runs_on, 14)):
+        with no_cpu_codec:
+            out, meta = cuda_zlib.decompress_gzip_checked(stream, len(data), 0)
+            assert _status(meta) == status
+        got = out.cpu().numpy().tobytes()
+        assert got == (data if status == 0 else bytes(len(data)))
+
+
 @pytest.mark.parametrize("case", _gzip_cases(), ids=lambda c: c[0])
 def test_gzip_wrapper_failures(gpu, no_cpu_codec, case):
     import cuda_zlib
