@@ -3880,8 +3880,8 @@ __device__ __forceinline__ void copy_periodic(const Sink& out, u64 dst, u64 src0
 }
 
 // One match of a slice whose output starts at dst0: bytes copied from before
-// dst0 (or from bytes of this slice still unresolved) are marked unresolved
-// with their root; the rest are copied.  `nunres` counts the slice's
+// dst0 (and, once the slice has an unresolved byte, every byte it copies from
+// its own output) are marked unresolved with their root; the rest are copied.  `nunres` counts the slice's
 // unresolved bytes so far.  tail_at / tail_root: the slice offset just past
 // the last match handled, and the root of that match's last byte (kNone when
 // it is resolved): the byte before a match is that byte or a literal.
@@ -3937,13 +3937,13 @@ __device__ __forceinline__ void emit_match(const Sink& out, u64 dst0, u64 dst, u
     u32 last = kNone;
     for (u32 j = 0; j < length; ++j) {
       const u64 d = dst + j, src = d - distance;
-      if (src < dst0) {
+      // Once the slice has an unresolved byte, a byte copied from its own
+      // output is rooted at its source without checking whether that is
+      // resolved: a load of the bitmap (or of the source's root) here would
+      // wait for every store the wave has pending.  A resolved source only
+      // costs the resolve rounds one link.
+      if (src < dst0 || nunres) {
         roots[d] = last = u32(src);
-        bit_set(unres, d);
-        out.zero(d, 1);
-        ++nunres;
-      } else if (nunres && bit_get(unres, src)) {
-        roots[d] = last = roots[src];
         bit_set(unres, d);
         out.zero(d, 1);
         ++nunres;
