@@ -4654,7 +4654,17 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
   // the previous 32 KiB mostly read lines its own XCD's waves loaded.
   const u64 ngroups = (words + 63) / 64;
   // Follows the chain of entry e of group g; a byte left unresolved sets its
-  // bit in `left` (the group's next words).
+  // bit in `left` (the group's next words).  The lane's stores (the byte, or
+  // the root reached) wait in `pend` until its next entry's loads have
+  // returned: a load waits for every store issued before it, so each entry's
+  // chain would otherwise wait for the previous entry's stores.
+  u32 pend_u = 0, pend_v = 0, pend_kind = 0;  // kind 1: out[u] = v; 2: roots[u] = v
+  const auto commit = [&]() {
+    if (pend_kind == 1) out[pend_u] = u8(pend_v);
+    else if (pend_kind == 2)
+      __hip_atomic_store(roots + pend_u, pend_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    pend_kind = 0;
+  };
   const auto chase = [&](u64 g, u32 e, u32* left) {
     const u32 u = u32(g * 2048 + e);
     u32 r = roots[u];
@@ -4663,14 +4673,16 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
       r = __hip_atomic_load(roots + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       unres = (bits[r >> 5] >> (r & 31)) & 1u;
     }
+    const u32 v = unres ? r : u32(out[r]);
+    commit();
+    pend_u = u;
+    pend_v = v;
+    pend_kind = unres ? 2u : 1u;
     if (!unres) {
-      const u8 v = out[r];
-      out[u] = v;
       as += v;
       aw += (out_end - u) * v;
       if (aw >> 62) aw %= kAdlerMod;
     } else {
-      __hip_atomic_store(roots + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       atomicOr(&left[e >> 5], 1u << (e & 31));
     }
   };
@@ -4706,6 +4718,7 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
       if (!wave) left_words[0][lane] = 0;
       __syncthreads();
       for (u32 i = wave * 64 + lane; i < total; i += 256) chase(g, list[wave][i], left_words[0]);
+      commit();
       __syncthreads();
       if (!wave) {
         const u32 nb = left_words[0][lane];
@@ -4742,6 +4755,7 @@ __global__ __launch_bounds__(256) void g_resolve(State* st, u8* out, u32* roots,
       left_words[wave][lane] = 0;
       wave_sync();
       for (u32 i = lane; i < total; i += 64) chase(g, list[wave][i], left_words[wave]);
+      commit();
       wave_sync();
       const u32 nb = left_words[wave][lane];
       if (w < words) next_bits[w] = nb;
