@@ -1160,8 +1160,9 @@ __device__ __forceinline__ u32 stage_bits(const u32* words, u32 q) {
 // limit there) / nl / nd describe the walk over the lengths.  Lane s < 19 holds symbol s: its length, its rank among the
 // symbols of that length (ballots) and so its canonical code, whose LUT
 // entries it fills.
+template <class Tables>  // DecodeTables, or any type with its `cl` table and `lens`
 __device__ inline bool header_prelude_wave(const u32* words, u64 bit0, u32 count,
-                                           DecodeTables& tables, u64 len, u64 start, u32& nl,
+                                           Tables& tables, u64 len, u64 start, u32& nl,
                                            u32& nd, u32& err, u64& after, u32& p, u32& lim32) {
   const u32 lane = lane_id();
   // A read of bit q touches words q/32 and q/32 + 1.
@@ -1226,7 +1227,8 @@ __device__ inline bool header_prelude_wave(const u32* words, u64 bit0, u32 count
 // Returns kOk, an error status (the one parse_dynamic_lengths gives: every
 // read on the path lies before the limit), or kHeaderWalkStuck when the walk
 // would read past it.  `p` advances to the bit after the lengths.
-__device__ inline u32 header_lengths_wave(const u32* words, DecodeTables& tables, u32* runs, u32 total,
+template <class Tables>
+__device__ inline u32 header_lengths_wave(const u32* words, Tables& tables, u32* runs, u32 total,
                                    u32& p, u32 lim) {
   const u32 lane = lane_id();
   u32 i = 0, prev = 0, nruns = 0;

@@ -1175,13 +1175,70 @@ __device__ __forceinline__ u32 val_step(const ValShared& sh, u32 lane, ValWalk& 
 
 }  // namespace
 
+// What the wave-wide header walk of g_validate needs: the code-length code,
+// the lengths, the staged header and the walk's runs.
+struct ValHeadTables {
+  HuffTable<19, 7> cl;
+  u8 lens[320];
+};
+struct ValWaveShared {
+  ValHeadTables tables;
+  StageT<kHeaderWords> stage;
+  u32 runs[320];
+};
+
+// A wave's single pre-candidate at bit `pos` (its BTYPE known to be 2, its
+// header staged whole before the body end): walked by the whole wave as
+// g_headers walks a header (lanes decode speculatively, the true path taken
+// by scalar hops), then the verdict val_step gives: the code-length code
+// complete, every run inside the lengths, a code for symbol 256, and
+// literal/length and distance codes complete (or a single code of length 1;
+// no distance codes at all is allowed too).
+__device__ bool val_wave(const u8* body, u64 len, u64 pos, ValWaveShared& w) {
+  const u32 lane = lane_id();
+  stage_range(body, len, pos, pos + 8, w.stage, kHeaderBytes);
+  __syncthreads();
+  u32 nl = 0, nd = 0, err = kOk, p = 0, lim = 0;
+  u64 after = 0;
+  if (!header_prelude_wave(w.stage.words, w.stage.bit0, w.stage.count, w.tables, len, pos + 3, nl,
+                           nd, err, after, p, lim) ||
+      err)
+    return false;
+  if (header_lengths_wave(w.stage.words, w.tables, w.runs, nl + nd, p, lim)) return false;
+  u32 llk = 0, lln = 0, dk = 0, dn = 0;  // Kraft sums in units of 2^-15, nonzero counts
+  for (u32 k = lane; k < nl + nd; k += 64) {
+    const u32 l = w.tables.lens[k];
+    const u32 wt = l ? 1u << (15 - l) : 0u;
+    if (k < nl) {
+      llk += wt;
+      lln += l != 0;
+    } else {
+      dk += wt;
+      dn += l != 0;
+    }
+  }
+  for (u32 off = 32; off; off >>= 1) {
+    llk += __shfl_xor(llk, off, 64);
+    lln += __shfl_xor(lln, off, 64);
+    dk += __shfl_xor(dk, off, 64);
+    dn += __shfl_xor(dn, off, 64);
+  }
+  const bool ll_ok = llk == (1u << 15) || (lln == 1 && llk == (1u << 14));
+  const bool d_ok = dn == 0 || dk == (1u << 15) || (dn == 1 && dk == (1u << 14));
+  return ll_ok && d_ok;
+}
+
 // Discovery pass 4 (one wave per workgroup; see above).  Valid entries get
 // kValidBit; wave_valid[r] counts the valid entries of pre-candidates
 // [kValPerWave r, kValPerWave (r + 1)), written by the wave that takes them
 // all or added by the waves that share them (val_chunk).
 __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State* st, u64* pre,
                                                  u32* wave_valid) {
-  __shared__ ValShared sh;
+  __shared__ union {
+    ValShared lanes;
+    ValWaveShared wave;
+  } shu;
+  ValShared& sh = shu.lanes;
   if (st->status) return;
   const u64 n = st->precount;
   const u32 chunk = val_chunk(n);
@@ -1189,6 +1246,20 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
   if (q0 >= n) return;
   const u64 q1 = min<u64>(q0 + chunk, n);
   const u32 lane = lane_id();
+  if (chunk == 1) {  // uniform
+    // A wave per pre-candidate: the whole wave walks the header (one lane's
+    // walk would take a symbol a step), unless its header could reach the
+    // body end, where the lane walk's exact limits apply.
+    const u64 e = pre[q0], pos = e & kPosMask;
+    if (!(e & kValidBit) && pos / 8 + kHeaderBytes + 16 <= len) {
+      const bool valid = val_wave(body, len, pos, shu.wave);
+      if (!lane && valid) {
+        pre[q0] = e | kValidBit;
+        atomicAdd(&wave_valid[q0 / kValPerWave], 1u);
+      }
+      return;
+    }
+  }
   u64 cursor = q0;  // next unassigned entry (uniform)
   u64 ci = 0;
   bool active = false;
