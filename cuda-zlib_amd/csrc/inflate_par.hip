@@ -879,6 +879,9 @@ __device__ __forceinline__ u64 range_offset(const u32* wg_count, const u64* bloc
 // waves, and enough for n / kValPerWave.
 constexpr u32 kValPerWave = 128;
 constexpr u64 kValResident = 2048;
+// Up to this many pre-candidates a wave, the wave walks each header with all
+// its lanes (val_wave) rather than a lane a header.
+constexpr u32 kValWaveChunk = 4;
 __host__ __device__ inline u32 val_chunk(u64 n) {
   u32 c = 1;
   while (c < kValPerWave && n > u64(c) * kValResident) c <<= 1;
@@ -1246,19 +1249,21 @@ __global__ __launch_bounds__(64) void g_validate(const u8* body, u64 len, State*
   if (q0 >= n) return;
   const u64 q1 = min<u64>(q0 + chunk, n);
   const u32 lane = lane_id();
-  if (chunk == 1) {  // uniform
-    // A wave per pre-candidate: the whole wave walks the header (one lane's
-    // walk would take a symbol a step), unless its header could reach the
-    // body end, where the lane walk's exact limits apply.
-    const u64 e = pre[q0], pos = e & kPosMask;
-    if (!(e & kValidBit) && pos / 8 + kHeaderBytes + 16 <= len) {
-      const bool valid = val_wave(body, len, pos, shu.wave);
-      if (!lane && valid) {
-        pre[q0] = e | kValidBit;
-        atomicAdd(&wave_valid[q0 / kValPerWave], 1u);
-      }
-      return;
+  if (chunk <= kValWaveChunk && (pre[q1 - 1] & kPosMask) / 8 + kHeaderBytes + 16 <= len) {
+    // Few pre-candidates a wave: the whole wave walks each header in turn
+    // (one lane's walk would take a symbol a step), unless a header could
+    // reach the body end, where the lane walk's exact limits apply (the
+    // entries are in order, so the last one is the one to check).
+    u32 found_here = 0;
+    for (u64 q = q0; q < q1; ++q) {
+      const u64 e = pre[q];
+      const bool valid = (e & kValidBit) || val_wave(body, len, e & kPosMask, shu.wave);
+      if (valid && !(e & kValidBit) && !lane) pre[q] = e | kValidBit;
+      found_here += valid ? 1u : 0u;
+      __syncthreads();  // the next header reuses the stage
     }
+    if (!lane && found_here) atomicAdd(&wave_valid[q0 / kValPerWave], found_here);
+    return;
   }
   u64 cursor = q0;  // next unassigned entry (uniform)
   u64 ci = 0;
