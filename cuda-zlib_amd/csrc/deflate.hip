@@ -1316,16 +1316,55 @@ __global__ __launch_bounds__(1024) void e_scan(const ChunkResult* results, u32 c
 }
 
 // Per file: status, wrapper and metadata [length, status].
+// Zeroes out[from, capacity) with every thread of the grid: bytes up to the
+// first 16-byte boundary of memory at or after out + from and after the last
+// one before out + capacity one by one, 16-byte stores between (out may have
+// any alignment).
+__device__ void zero_tail(u8* out, u64 capacity, u64 from) {
+  from = min<u64>(from, capacity);
+  const uintptr_t base = reinterpret_cast<uintptr_t>(out);
+  const u64 first16 = from + ((16 - ((base + from) & 15)) & 15);
+  const u64 end16 = capacity - ((base + capacity) & 15);
+  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x, stride = u64(gridDim.x) * blockDim.x;
+  if (first16 >= end16) {
+    for (u64 i = from + tid; i < capacity; i += stride) out[i] = 0;
+    return;
+  }
+  for (u64 i = from + tid; i < first16; i += stride) out[i] = 0;
+  for (u64 i = end16 + tid; i < capacity; i += stride) out[i] = 0;
+  uint4* o = reinterpret_cast<uint4*>(out + first16);
+  const u64 n16 = (end16 - first16) / 16;
+  for (u64 i = tid; i < n16; i += stride) o[i] = uint4{0u, 0u, 0u, 0u};
+}
+
+
+// File fi's status and stream length (total) from the chunk scans.
+__device__ __forceinline__ u32 wrap_status(const FileDesc& f, u32 fi, const u64* sums,
+                                           const u32* file_bad, u64& total) {
+  const u64 a0 = f.first_chunk, a1 = f.first_chunk + f.chunks;
+  u32 status = sums[4 * a1 + 3] != sums[4 * a0 + 3] || file_bad[fi] ? kCompressionOverflow : 0u;
+  total = sums[4 * a1] - sums[4 * a0] + 6;
+  if (total > f.capacity) status = kCompressionOverflow;
+  return status;
+}
+
+// The zlib header and Adler-32 trailer of every file, its metadata row and
+// its ok flag.  With `tail` (a single stream, count 1), the whole grid also
+// zeroes the slot after the stream, [total, tail), or all of it when the
+// stream failed.
 __global__ void e_wrap(const FileDesc* files, u32 count, const u64* sums, u8* out, u32* meta,
-                       u32* file_ok, const u32* file_bad) {
+                       u32* file_ok, const u32* file_bad, u64 tail) {
   const u32 tid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (tail) {
+    u64 total = 0;
+    const u32 status = wrap_status(files[0], 0, sums, file_bad, total);
+    zero_tail(out, tail, status ? 0 : total);
+  }
   for (u32 fi = tid; fi < count; fi += gridDim.x * blockDim.x) {
     const FileDesc f = files[fi];
     const u64 a0 = f.first_chunk, a1 = f.first_chunk + f.chunks;
-    u32 status = sums[4 * a1 + 3] != sums[4 * a0 + 3] || file_bad[fi] ? kCompressionOverflow : 0u;
-    const u64 body = sums[4 * a1] - sums[4 * a0];
-    const u64 total = body + 6;
-    if (total > f.capacity) status = kCompressionOverflow;
+    u64 total = 0;
+    const u32 status = wrap_status(f, fi, sums, file_bad, total);
     file_ok[fi] = status ? 0u : 1u;
     if (status) {
       meta[2 * u64(fi)] = 0;
@@ -1412,7 +1451,8 @@ hipError_t parse_grid_size(u64 chunks, u32 chunk_bytes, u32* grid) {
 }
 
 hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u64 chunks,
-                      u32 file_count, u8* out, u32 chunk_bytes, u32* meta, bool clear_failed) {
+                      u32 file_count, u8* out, u32 chunk_bytes, u32* meta, bool clear_failed,
+                      u64 tail = 0) {
   const u32 parse_lds = kParseShared + history_limit(chunk_bytes) + chunk_bytes + 32;
 
   HZ_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(e_parse),
@@ -1435,8 +1475,11 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
   HZ_LAUNCH(e_emit, dim3(grid), dim3(kEmitThreads), 0, stream, in, b.descs, b.files, u32(chunks),
             b.tokens, b.stats, b.tables, b.sums, out, b.file_bad);
   HZ_TRY(hipGetLastError());
-  HZ_LAUNCH(e_wrap, dim3((file_count + 255) / 256), dim3(256), 0, stream, b.files, file_count,
-            b.sums, out, meta, b.file_ok, b.file_bad);
+  // A single stream's slot after the stream is zeroed by the same launch.
+  const u32 wrap_grid = tail ? u32(std::min<u64>(1024, (tail / 16 + 255) / 256 + 1))
+                             : (file_count + 255) / 256;
+  HZ_LAUNCH(e_wrap, dim3(wrap_grid), dim3(256), 0, stream, b.files, file_count, b.sums, out, meta,
+            b.file_ok, b.file_bad, tail);
   HZ_TRY(hipGetLastError());
   if (clear_failed) {
     HZ_LAUNCH(e_clear_failed, dim3(std::min<u32>(file_count, 65536)), dim3(256), 0, stream,
@@ -1447,29 +1490,6 @@ hipError_t run_chunks(hipStream_t stream, const ChunkBuffers& b, const u8* in, u
 
 }  // namespace
 
-// Zeros the single stream's slot after its stream: [meta[0], capacity), which
-// is the whole slot when compression failed (meta[0] is then 0).  The stream
-// itself is written in full by e_emit and e_wrap.
-__global__ __launch_bounds__(256) void e_zero_tail(u8* out, u64 capacity, const u32* meta) {
-  const u64 from = min<u64>(meta[0], capacity);
-  // Bytes up to the first 16-byte boundary of memory at or after out + from
-  // and after the last one before out + capacity one by one, 16-byte stores
-  // between (out may have any alignment).
-  const uintptr_t base = reinterpret_cast<uintptr_t>(out);
-  const u64 first16 = from + ((16 - ((base + from) & 15)) & 15);
-  const u64 end16 = capacity - ((base + capacity) & 15);
-  const u64 tid = u64(blockIdx.x) * blockDim.x + threadIdx.x, stride = u64(gridDim.x) * blockDim.x;
-  if (first16 >= end16) {
-    for (u64 i = from + tid; i < capacity; i += stride) out[i] = 0;
-    return;
-  }
-  for (u64 i = from + tid; i < first16; i += stride) out[i] = 0;
-  for (u64 i = end16 + tid; i < capacity; i += stride) out[i] = 0;
-  uint4* o = reinterpret_cast<uint4*>(out + first16);
-  const u64 n16 = (end16 - first16) / 16;
-  for (u64 i = tid; i < n16; i += stride) o[i] = uint4{0u, 0u, 0u, 0u};
-}
-
 hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 in_size, u8* out,
                        u64 capacity, u32 chunk_bytes, u32* meta, bool independent) {
   const u64 chunks = in_size ? (in_size + chunk_bytes - 1) / chunk_bytes : 1;
@@ -1479,10 +1499,7 @@ hipError_t run_deflate(hipStream_t stream, Scratch& scratch, const u8* in, u64 i
             stream, in_size, chunk_bytes, u32(chunks), independent ? 0u : history_limit(chunk_bytes),
             capacity, b.descs, b.files);
   HZ_TRY(hipGetLastError());
-  HZ_TRY(run_chunks(stream, b, in, chunks, 1, out, chunk_bytes, meta, false));
-  HZ_LAUNCH(e_zero_tail, dim3(u32(std::min<u64>(1024, (capacity / 16 + 255) / 256 + 1))), dim3(256),
-            0, stream, out, capacity, meta);
-  return hipGetLastError();
+  return run_chunks(stream, b, in, chunks, 1, out, chunk_bytes, meta, false, capacity);
 }
 
 u64 deflate_scratch_bytes(u64 in_size, u32 chunk_bytes) {
