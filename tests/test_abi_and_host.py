@@ -23,9 +23,19 @@ def _declared():
     return re.findall(r"^\s*(?:int|uint64_t|const char\s*\*)\s*(HipZlib\w+)\s*\(", text, re.M)
 
 
+def _torch_first():
+    """torch brings its own HIP runtime: it must be loaded before the codec
+    library, or a later GPU test in this process finds no device."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def test_library_exports_every_declared_entry_point():
     from cuda_zlib import _native
     assert os.path.exists(_native.LIBRARY_PATH), "build the library first (__graft_entry__.build())"
+    _torch_first()
     lib = ctypes.CDLL(_native.LIBRARY_PATH)
     names = _declared()
     assert len(names) >= 10
@@ -36,6 +46,7 @@ def test_library_exports_every_declared_entry_point():
 
 def test_error_strings_need_no_device():
     from cuda_zlib import _native
+    _torch_first()
     lib = _native._bind(ctypes.CDLL(_native.LIBRARY_PATH))
     assert lib.HipZlibErrorString(1)  # a HIP error code maps to its runtime message
     assert lib.HipZlibErrorString(-1) is not None

@@ -1,6 +1,6 @@
 """Batch decode parity: every file against the oracle's serial inflate.
 
-Batch files of at least 256 B of output decode by parallel slices, one
+Batch files of at least 32 B of output decode by parallel slices, one
 workgroup per file; a file that does not decode cleanly there is handed to the
 serial per-file decoder.  Either way each file's [status, 0] row and output
 (decoded prefix then zeros on failure, the reference's DecodeOneFile,
@@ -118,7 +118,8 @@ def test_encoded_rows_route_large_files_like_small_ones(gpu):
 
 
 def _small_dynamic(rng, n):
-    """A stream of under 256 B of output in one dynamic-Huffman block."""
+    """A stream of under 256 B of output in one dynamic-Huffman block (most of
+    them take the parallel route, those under 32 B the serial one)."""
     raw = bytes(rng.choice(b"abcdefg"[:rng.randrange(2, 8)]) for _ in range(n))
     c = zlib.compressobj(9, zlib.DEFLATED, 15, 9, zlib.Z_HUFFMAN_ONLY)
     return raw, c.compress(raw) + c.flush()
@@ -126,9 +127,10 @@ def _small_dynamic(rng, n):
 
 @pytest.mark.parametrize("seed", range(3))
 def test_small_dynamic_headers_match_the_serial_oracle(gpu, seed):
-    """Files under 256 B decode one wave per file, staged in LDS, their
-    dynamic headers read by the wave walk (lane 0's serial parse where the
-    walk stops); valid, header-corrupted and truncated ones against the
+    """Small files: under 32 B one wave per file, staged in LDS, their dynamic
+    headers read by the wave walk (lane 0's serial parse where the walk
+    stops), and above that by parallel slices with the serial decoder for
+    any that fail; valid, header-corrupted and truncated ones against the
     oracle, beside large files so both routes run together."""
     rng = random.Random(40 + seed)
     streams, expected = [], []
