@@ -236,16 +236,42 @@ __device__ __forceinline__ void wave_sync() {
 
 // ---- canonical Huffman decode tables ---------------------------------------
 // Primary LUT entry (u32): bits 0..3 code length (0 = no short code here),
-// bits 16..31 symbol.  Codes longer than the primary width use the canonical
-// count/first walk.  `maximum` is the longest code length (0 for an empty tree).
+// bits 16..31 symbol.  Codes longer than the primary width are decoded from
+// the per-length bounds (long_code).  `maximum` is the longest code length
+// (0 for an empty tree).
+//
+// With v the next 15 bits read as an MSB-first code value and first[l] the
+// first canonical code of length l, limit[l] = (first[l] + count[l]) << (15 - l)
+// is the first 15-bit value past the length-l codes.  The limits never
+// decrease with l (lengths past `maximum` repeat the last one), so the code
+// length is the least l with v < limit[l], and its symbol is
+// symbols[base[l] + (v >> (15 - l))] with base[l] = (symbols before length l)
+// - first[l], modulo 2^16.
 template <int N, int P>
 struct HuffTable {
   u16 count[16];
-  u16 offs[16];   // build scratch (kept in the table so builds use no private arrays)
+  u16 limit[16];  // also the serial build's scratch until the bounds are set
+  u16 base[16];
   u16 symbols[N];
   u32 primary[1 << P];
   u32 maximum;
 };
+
+// limit and base from count (lengths 1..15; entry 0 unused).  Only the
+// tables a build accepts are decoded, so over-subscribed counts may wrap.
+template <int N, int P>
+__host__ __device__ inline void huff_bounds(HuffTable<N, P>& t) {
+  u32 first = 0, index = 0;
+  t.limit[0] = 0;
+  t.base[0] = 0;
+  for (u32 l = 1; l < 16; ++l) {
+    const u32 c = t.count[l];
+    t.limit[l] = u16((first + c) << (15 - l));
+    t.base[l] = u16(index - first);
+    index += c;
+    first = (first + c) << 1;
+  }
+}
 
 // Code-length alphabet order (RFC 1951 3.2.7), 5 bits per entry, packed so
 // device code indexes registers rather than a private array.
@@ -270,17 +296,22 @@ __host__ __device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bo
     ++t.count[l];
     if (l > t.maximum) t.maximum = l;
   }
-  if (!t.maximum) return empty_ok ? 0u : u32(kBadTree);
+  if (!t.maximum) {
+    huff_bounds(t);
+    return empty_ok ? 0u : u32(kBadTree);
+  }
   i32 left = 1;
   for (u32 l = 1; l <= limit; ++l) {
     left = (left << 1) - i32(t.count[l]);
     if (left < 0) return kBadTree;
   }
   if (left && !(single_ok && t.maximum == 1 && t.count[1] == 1)) return kBadTree;
-  t.offs[1] = 0;
-  for (u32 l = 1; l < 15; ++l) t.offs[l + 1] = t.offs[l] + t.count[l];
+  u16* slot = t.limit;  // next symbol slot of each length
+  slot[1] = 0;
+  for (u32 l = 1; l < 15; ++l) slot[l + 1] = slot[l] + t.count[l];
   for (u32 i = 0; i < n; ++i)
-    if (lens[i]) t.symbols[t.offs[lens[i]]++] = u16(i);
+    if (lens[i]) t.symbols[slot[lens[i]]++] = u16(i);
+  huff_bounds(t);
   for (u32 i = 0; i < (1u << P); ++i) t.primary[i] = 0;
   u32 code = 0, index = 0;
   for (u32 l = 1; l <= u32(P); ++l) {
@@ -293,6 +324,34 @@ __host__ __device__ u32 huff_build(HuffTable<N, P>& t, const u8* lens, u32 n, bo
     code = (code + t.count[l]) << 1;
   }
   return 0;
+}
+
+// A code longer than the primary LUT (or none) at the next bits `b` (LSB
+// first), after a LUT miss.  Returns the symbol and its length, or -1 with
+// `err`: kTruncated when the code, or any code up to `maximum` bits when none
+// matches, needs more than `avail` bits; kBadSymbol when no code matches.
+// A LUT miss leaves v >= limit[l] for every l <= P (P >= 7), so only lengths
+// 8..15 are compared; a length is decided by its own first l bits, so bits
+// past `avail` never change a result that fits in `avail`.
+template <int N, int P>
+__host__ __device__ __forceinline__ i32 long_code(const HuffTable<N, P>& t, u32 b, u32 avail,
+                                                  u32& len_out, u32& err) {
+  static_assert(P >= 7, "long_code compares lengths 8..15 only");
+  const u32 v = bit_reverse(b & 0x7fffu, 15);
+  u32 n = 0;
+#pragma unroll
+  for (u32 l = 8; l < 16; ++l) n += u32(t.limit[l]) <= v ? 1u : 0u;
+  if (n == 8) {
+    err = t.maximum > avail ? kTruncated : kBadSymbol;
+    return -1;
+  }
+  const u32 len = 8 + n;
+  if (len > avail) {
+    err = kTruncated;
+    return -1;
+  }
+  len_out = len;
+  return i32(t.symbols[(u32(t.base[len]) + (v >> (15 - len))) & 0xffffu]);
 }
 
 // Decode one symbol.  Returns the symbol (>= 0), or -1 with `err` set to
@@ -308,23 +367,12 @@ __host__ __device__ __forceinline__ i32 huff_decode(const HuffTable<N, P>& t, Re
     r.drop(l);
     return i32(e >> 16);
   }
-  // Canonical walk for long codes and invalid prefixes.
-  u32 code = 0, first = 0, index = 0;
+  // Long codes and invalid prefixes.
   const u64 avail = r.avail();
-  for (u32 len = 1; len <= t.maximum; ++len) {
-    if (u64(len) > avail) { err = kTruncated; return -1; }
-    code |= u32((r.buf >> (len - 1)) & 1ull);
-    const u32 c = t.count[len];
-    if (code < first + c) {
-      r.drop(len);
-      return i32(t.symbols[index + code - first]);
-    }
-    index += c;
-    first = (first + c) << 1;
-    code <<= 1;
-  }
-  err = kBadSymbol;
-  return -1;
+  u32 len = 0;
+  const i32 sym = long_code(t, u32(r.buf), avail > 0xffffffffull ? 0xffffffffu : u32(avail), len, err);
+  if (sym >= 0) r.drop(len);
+  return sym;
 }
 
 struct DecodeTables {
@@ -358,6 +406,7 @@ __host__ __device__ inline u32 build_cl_table(HuffTable<19, 7>& t, u64 pack) {
   for (u32 l = 0; l < 16; ++l) t.count[l] = l < 8 ? u16((cnt >> (8 * l)) & 0xff) : 0;
   t.maximum = maximum;
   if (kraft != 128) return kBadTree;
+  huff_bounds(t);
   u64 next = 0, offs = 0;  // byte l: next code / next symbol slot for length l
   u32 code = 0, slot = 0;
   for (u32 l = 1; l < 8; ++l) {
@@ -489,8 +538,16 @@ __device__ u32 huff_build_wave(HuffTable<N, P>& t, const u8* lens, u32 n, bool e
     const u32 maximum = lens_used ? 63u - u32(__builtin_clzll(lens_used)) : 0u;
     const u32 ones = u32(__builtin_amdgcn_readlane(int(cnt), 1));
     if (lane >= 1 && lane < 16) {
+      const u32 first = (wsum - (c << (15 - lane))) >> (15 - lane);
       offs[lane] = u16(csum - c);
-      next[lane] = u16((wsum - (c << (15 - lane))) >> (15 - lane));
+      next[lane] = u16(first);
+      // The inclusive weighted sum is the length's limit (see HuffTable).
+      t.limit[lane] = u16(wsum);
+      t.base[lane] = u16(csum - c - first);
+    }
+    if (!lane) {
+      t.limit[0] = 0;
+      t.base[0] = 0;
     }
     if (!lane) {
       u32 st = kOk;
@@ -636,28 +693,6 @@ struct WordBits {
   }
 };
 
-// Canonical walk over the next bits `b` (LSB first), as huff_decode does on a
-// LUT miss.  Returns the symbol and its length, or -1 with `err`.
-template <int N, int P>
-__host__ __device__ __forceinline__ i32 canon_walk(const HuffTable<N, P>& t, u32 b, u32 avail, u32& len_out,
-                                          u32& err) {
-  u32 code = 0, first = 0, index = 0;
-  for (u32 len = 1; len <= t.maximum; ++len) {
-    if (len > avail) { err = kTruncated; return -1; }
-    code |= (b >> (len - 1)) & 1u;
-    const u32 c = t.count[len];
-    if (code < first + c) {
-      len_out = len;
-      return i32(t.symbols[index + code - first]);
-    }
-    index += c;
-    first = (first + c) << 1;
-    code <<= 1;
-  }
-  err = kBadSymbol;
-  return -1;
-}
-
 // One token with fast-format tables; same results and error order as
 // decode_token over the standard format (a distance is at most 32768).
 template <class R>
@@ -670,7 +705,7 @@ __host__ __device__ __forceinline__ u32 fast_token(const HuffTable<288, 10>& ll,
   u32 l = e & 15u;
   if (!l) {
     u32 err = 0;
-    const i32 sym = canon_walk(ll, b, r.avail(), l, err);
+    const i32 sym = long_code(ll, b, r.avail(), l, err);
     if (sym < 0) return err;
     e = fast_ll_entry(u32(sym), l);
   }
@@ -694,7 +729,7 @@ __host__ __device__ __forceinline__ u32 fast_token(const HuffTable<288, 10>& ll,
   u32 dl = d & 15u;
   if (!dl) {
     u32 err = 0;
-    const i32 sym = canon_walk(dd, b, r.avail(), dl, err);
+    const i32 sym = long_code(dd, b, r.avail(), dl, err);
     if (sym < 0) return err;
     d = fast_d_entry(u32(sym), dl);
   }

@@ -16,6 +16,9 @@
 //   frame  parse_frame on every truncation, in each format
 //   pairs  quick_pair (literal pairs) and quick_triple (three literals)
 //          against quick_token over guarded words
+//   longcodes  long_code (per-length bounds) against a bit-by-bit canonical
+//          walk on random complete, single-code and empty tables, every
+//          15-bit prefix the primary LUT misses and every bit budget
 //   guard  reads one byte past a guarded buffer (must crash: checks the guard)
 #include <sys/mman.h>
 #include <unistd.h>
@@ -403,6 +406,115 @@ int mode_frame(int argc, char** argv) {
   return 0;
 }
 
+// Bit-by-bit canonical decode (RFC 1951 3.2.2 order): the code value grows
+// one bit at a time and is compared with the length's code range.
+template <int N, int P>
+i32 walk_code(const HuffTable<N, P>& t, u32 b, u32 avail, u32& len_out, u32& err) {
+  u32 code = 0, first = 0, index = 0;
+  for (u32 len = 1; len <= t.maximum; ++len) {
+    if (len > avail) { err = kTruncated; return -1; }
+    code |= (b >> (len - 1)) & 1u;
+    const u32 c = t.count[len];
+    if (code < first + c) {
+      len_out = len;
+      return i32(t.symbols[index + code - first]);
+    }
+    index += c;
+    first = (first + c) << 1;
+    code <<= 1;
+  }
+  err = kBadSymbol;
+  return -1;
+}
+
+u64 rng_state = 0x9e3779b97f4a7c15ull;
+u32 rnd(u32 n) {
+  rng_state ^= rng_state << 13;
+  rng_state ^= rng_state >> 7;
+  rng_state ^= rng_state << 17;
+  return u32((rng_state >> 11) % n);
+}
+
+// Lengths of a random complete code over `used` of n symbols (leaves split
+// until there are `used`; `deep` favours splitting the deepest leaf, which
+// makes codes up to 15 bits), or one length-1 code, or none.
+void random_lengths(u8* lens, u32 n, u32 kind) {
+  for (u32 i = 0; i < n; ++i) lens[i] = 0;
+  if (kind == 1) { lens[rnd(n)] = 1; return; }
+  if (kind == 2) return;
+  const u32 used = 2 + rnd(n - 1);
+  std::vector<u32> depth(1, 0);
+  const bool deep = rnd(2);
+  while (depth.size() < used) {
+    u32 pick = rnd(u32(depth.size()));
+    if (deep && rnd(4)) {
+      for (u32 i = 0; i < depth.size(); ++i)
+        if (depth[i] > depth[pick] && depth[i] < 15) pick = i;
+    }
+    if (depth[pick] >= 15) {
+      bool any = false;
+      for (u32 i = 0; i < depth.size(); ++i)
+        if (depth[i] < 15) { pick = i; any = true; break; }
+      if (!any) break;
+    }
+    const u32 d = depth[pick] + 1;
+    depth[pick] = d;
+    depth.push_back(d);
+  }
+  std::vector<u32> syms(n);
+  for (u32 i = 0; i < n; ++i) syms[i] = i;
+  for (u32 i = n - 1; i > 0; --i) std::swap(syms[i], syms[rnd(i + 1)]);
+  for (u32 i = 0; i < depth.size(); ++i) lens[syms[i]] = u8(depth[i]);
+}
+
+template <int N, int P>
+u64 check_long_codes(u32 trials, u32& bad) {
+  static HuffTable<N, P> t;
+  u8 lens[N];
+  u64 checked = 0;
+  for (u32 trial = 0; trial < trials; ++trial) {
+    const u32 kind = trial % 16 == 1 ? 1u : trial % 16 == 2 ? 2u : 0u;
+    random_lengths(lens, N, kind);
+    if (huff_build(t, lens, N, true, true, 15)) { ++bad; continue; }
+    // The wave build's per-lane bounds: inclusive weighted sums of the counts.
+    u32 wsum = 0, csum = 0;
+    for (u32 l = 1; l < 16; ++l) {
+      const u32 c = t.count[l];
+      wsum += c << (15 - l);
+      csum += c;
+      const u32 first = (wsum - (c << (15 - l))) >> (15 - l);
+      if (t.limit[l] != u16(wsum) || t.base[l] != u16(csum - c - first)) ++bad;
+    }
+    for (u32 v = 0; v < (1u << 15); ++v) {
+      const u32 b = bit_reverse(v, 15) | (rnd(1u << 17) << 15);  // bits past 15: noise
+      if (t.primary[b & ((1u << P) - 1)] & 15u) continue;
+      for (u32 avail = 0; avail <= 17; ++avail) {
+        const u32 a = avail == 17 ? 0xffffffffu : avail;
+        u32 l1 = 99, l2 = 99, e1 = 0, e2 = 0;
+        const i32 s1 = walk_code(t, b, a, l1, e1);
+        const i32 s2 = long_code(t, b, a, l2, e2);
+        if (s1 != s2 || (s1 >= 0 ? l1 != l2 : e1 != e2)) {
+          if (bad < 10)
+            printf("mismatch N=%d trial=%u v=%u avail=%u: walk %d/%u/%u long %d/%u/%u\n", N,
+                   trial, v, a, s1, l1, e1, s2, l2, e2);
+          ++bad;
+        }
+        ++checked;
+      }
+    }
+  }
+  return checked;
+}
+
+int mode_long_codes() {
+  u32 bad = 0;
+  const u64 a = check_long_codes<288, 10>(400, bad);
+  const u64 b = check_long_codes<32, 8>(400, bad);
+  const u64 c = check_long_codes<19, 7>(100, bad);
+  printf("longcodes checked=%llu bad=%u\n", (unsigned long long)(a + b + c), bad);
+  return bad ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -413,6 +525,7 @@ int main(int argc, char** argv) {
   if (!strcmp(mode, "copy")) return mode_copy();
   if (!strcmp(mode, "frame")) return mode_frame(argc - 2, argv + 2);
   if (!strcmp(mode, "pairs")) return mode_pairs(argc - 2, argv + 2);
+  if (!strcmp(mode, "longcodes")) return mode_long_codes();
   if (!strcmp(mode, "guard")) {
     const u8 byte = 1;
     Guarded g(&byte, 1);

@@ -152,6 +152,19 @@ def test_literal_pairs_match_single_tokens(harness, stream_files):
             assert int(got[path]["adler%d" % slice_bits]) == zlib.adler32(raw), name
 
 
+def test_long_codes_match_a_bitwise_canonical_walk(harness):
+    """Codes longer than the primary LUT are decoded from per-length bounds
+    (deflate_common.h long_code); a bit-by-bit canonical walk must give the
+    same symbol, length and error for every prefix the LUT misses, at every
+    bit budget, on random complete (up to 15-bit), single-code and empty
+    tables.  The wave build's per-lane bound formula is checked against the
+    serial one on the same tables."""
+    proc = _run(harness, "longcodes")
+    assert proc.returncode == 0, proc.stdout[-3000:] + proc.stderr[-2000:]
+    checked = int(proc.stdout.split("checked=")[1].split()[0])
+    assert checked > 1000000 and "bad=0" in proc.stdout
+
+
 def test_copy_bytes_every_length_and_alignment(harness):
     proc = _run(harness, "copy")
     assert proc.returncode == 0, proc.stdout + proc.stderr[-2000:]
