@@ -863,6 +863,62 @@ __host__ __device__ __forceinline__ u32 quick_pair(const HuffTable<288, 10>& ll,
   return ok ? (pair ? 2u : 1u) : 0u;
 }
 
+// fast_token over the window's registers: the same results, errors and
+// error order, but every bit comes from bits64() (a token takes at most 48
+// bits), so a token that misses quick_pair costs its table reads only, not
+// the word loads of a second reader.  On success the window moves past the
+// token (an EOB included); on an error it stays where it was.
+template <bool kChecked>
+__host__ __device__ __forceinline__ u32 window_token(const HuffTable<288, 10>& ll,
+                                                    const HuffTable<32, 8>& dd, Win4<kChecked>& r,
+                                                    u32& lit, u32& length, u32& distance) {
+  length = 0;
+  distance = 0;
+  const u64 b = r.bits64();
+  const u32 avail = r.avail();
+  u32 e = ll.primary[u32(b) & 1023u];
+  u32 l = e & 15u;
+  if (!l) {
+    u32 err = 0;
+    const i32 sym = long_code(ll, u32(b), avail, l, err);
+    if (sym < 0) return err;
+    e = fast_ll_entry(u32(sym), l);
+  }
+  if (l > avail) return kTruncated;
+  u32 used = l;
+  const u32 kind = (e >> 4) & 3u;
+  if (kind == kKindLit || kind == kKindEob) {
+    if (kind == kKindLit) {
+      lit = (e >> 8) & 0xffu;
+      length = 1;
+    }
+    r.advance(used);
+    return kOk;
+  }
+  if (kind == kKindBad) return kBadSymbol;
+  const u32 nx = (e >> 8) & 15u;
+  if (nx > avail - used) return kTruncated;
+  length = (e >> 16) + (u32(b >> used) & ((1u << nx) - 1u));
+  used += nx;
+  const u32 bd = u32(b >> used);
+  u32 d = dd.primary[bd & 255u];
+  u32 dl = d & 15u;
+  if (!dl) {
+    u32 err = 0;
+    const i32 sym = long_code(dd, bd, avail - used, dl, err);
+    if (sym < 0) return err;
+    d = fast_d_entry(u32(sym), dl);
+  }
+  if (dl > avail - used) return kTruncated;
+  used += dl;
+  if (d & 0x100u) return kBadSymbol;
+  const u32 dx = (d >> 4) & 15u;
+  if (dx > avail - used) return kTruncated;
+  distance = (d >> 16) + (u32(b >> used) & ((1u << dx) - 1u));
+  r.advance(used + dx);
+  return kOk;
+}
+
 // quick_pair extended to a third literal after a pair (a third lookup in
 // the same window bits, taken when that code too is a literal in the primary
 // table and starts before `stop`): returns 0-3 tokens taken; with 3, lit3 is

@@ -1744,13 +1744,7 @@ __device__ __forceinline__ Win4<kChecked> win4(const Stage& sg, u32 limit, u32 p
 template <bool kChecked>
 __device__ __forceinline__ u32 full_token(const DecodeTables& t, Win4<kChecked>& r, u32& length,
                                        u32& lit, u32& distance) {
-  WordBits<kChecked> q;
-  q.words = r.words;
-  q.limit = r.limit;
-  q.seek(r.pos());
-  const u32 err = fast_token(t.ll, t.dd, q, lit, length, distance);
-  if (!err) r.seek(q.pos());
-  return err;
+  return window_token<kChecked>(t.ll, t.dd, r, lit, length, distance);
 }
 
 // Token-level decode from r.pos() until it reaches `stop`.  An event (an EOB
@@ -4110,28 +4104,23 @@ __device__ u32 emit_slice(Shared& sh, u32 blim, u32 entry, u32 stop, u64 dst0, u
         live = false;
       } else if (!(got = quick_triple<kChecked>(sh.tables.ll, sh.tables.dd, r, stop, length, x, x2,
                                                 x3, l1, l12))) {
-        WordBits<kChecked> w;
-        w.words = r.words;
-        w.limit = r.limit;
-        w.seek(r.pos());
         u32 lit, distance;
-        if (fast_token(sh.tables.ll, sh.tables.dd, w, lit, length, distance)) {
+        if (window_token<kChecked>(sh.tables.ll, sh.tables.dd, r, lit, length, distance)) {
           err = kExtent;
           live = false;
         } else if (!length) {
           live = false;
-          if (cross && w.pos() < stop) {
+          if (cross && r.pos() < stop) {
             // The run's next block: a non-final or final fixed header.
-            if (w.avail() < 3 || ((w.bits32() >> 1) & 3u) != 1u) {
+            if (r.avail() < 3 || ((r.bits32() >> 1) & 3u) != 1u) {
               err = kExtent;
             } else {
-              r.seek(w.pos() + 3);
+              r.advance(3);
               live = true;
               got = 0;  // no token to emit this step
             }
           }
         } else {
-          r.seek(w.pos());
           x = length == 1 ? lit : distance;
           got = 1;
         }

@@ -16,6 +16,9 @@
 //   frame  parse_frame on every truncation, in each format
 //   pairs  quick_pair (literal pairs) and quick_triple (three literals)
 //          against quick_token over guarded words
+//   window window_token (one token from the Win4 registers) against
+//          fast_token over WordBits at every bit of every block body, at the
+//          body end and at a varying nearer limit
 //   longcodes  long_code (per-length bounds) against a bit-by-bit canonical
 //          walk on random complete, single-code and empty tables, every
 //          15-bit prefix the primary LUT misses and every bit budget
@@ -406,6 +409,88 @@ int mode_frame(int argc, char** argv) {
   return 0;
 }
 
+// window_token against fast_token at every bit position of each dynamic or
+// fixed block's body (and past it, into the next header and garbage), with
+// the body end as the limit and with a nearer limit that varies with the
+// position: the status, the token and, on success, the end position must
+// agree.  Prints "window <file> positions=<n> bad=<k>".
+int mode_window(int argc, char** argv) {
+  static DecodeTables t;
+  int rc = 0;
+  for (int i = 0; i < argc; ++i) {
+    const std::vector<u8> s = read_file(argv[i]);
+    Frame f;
+    if (parse_frame(s.data(), s.size(), kFormatZlib, false, f) || !f.body_len) continue;
+    const u8* body = s.data() + f.body;
+    const u64 len = f.body_len;
+    const u64 words = (len + 3) / 4 + 16;
+    std::vector<u32> host(words, 0u);
+    memcpy(host.data(), body, len);
+    Guarded g(reinterpret_cast<const u8*>(host.data()), words * 4);
+    const u32* w = reinterpret_cast<const u32*>(g.data);
+    BitIn hdr;
+    hdr.init(body, len, 0);
+    u64 positions = 0, bad = 0;
+    for (u32 blocks = 0; blocks < 1000; ++blocks) {
+      u32 final_block, type;
+      if (!hdr.take(1, final_block) || !hdr.take(2, type) || type == 0 || type == 3) break;
+      const u32 err = type == 1 ? build_fixed_tables(t) : build_dynamic_tables(t, hdr);
+      if (err) break;
+      fast_format(t.ll, true, 0, 1);
+      fast_format(t.dd, false, 0, 1);
+      const u32 from = u32(hdr.pos);
+      const u32 end = u32(len * 8);
+      u32 next = end;
+      for (u32 p = from; p < end; ++p) {
+        for (u32 near = 0; near < 2; ++near) {
+          const u32 limit = near ? p + (p * 7 + 3) % 53 : end;
+          if (limit > end) continue;
+          WordBits<true> q;
+          q.words = w;
+          q.limit = limit;
+          q.seek(p);
+          Win4<true> r;
+          r.words = w;
+          r.limit = limit;
+          r.seek(p);
+          u32 lit1 = 0, len1 = 0, d1 = 0, lit2 = 0, len2 = 0, d2 = 0;
+          const u32 e1 = fast_token(t.ll, t.dd, q, lit1, len1, d1);
+          const u32 e2 = window_token<true>(t.ll, t.dd, r, lit2, len2, d2);
+          bool same = e1 == e2;
+          if (same && !e1) {
+            same = len1 == len2 && q.pos() == r.pos() && (len1 != 1 || lit1 == lit2) &&
+                   (len1 < 3 || d1 == d2);
+            if (!near && !len1 && next == end) next = q.pos();  // first EOB
+          }
+          if (!same) {
+            if (bad < 5)
+              printf("mismatch %s p=%u limit=%u: fast %u/%u/%u/%u@%u window %u/%u/%u/%u@%u\n",
+                     argv[i], p, limit, e1, len1, lit1, d1, q.pos(), e2, len2, lit2, d2, r.pos());
+            ++bad;
+          }
+          ++positions;
+        }
+      }
+      // The next block: follow the true parse to this block's end.
+      Win4<true> r;
+      r.words = w;
+      r.limit = end;
+      r.seek(from);
+      for (;;) {
+        u32 lit, length, distance;
+        if (window_token<true>(t.ll, t.dd, r, lit, length, distance)) { final_block = 1; break; }
+        if (!length) break;
+      }
+      hdr.seek(r.pos());
+      if (final_block) break;
+    }
+    printf("window %s positions=%llu bad=%llu\n", argv[i], (unsigned long long)positions,
+           (unsigned long long)bad);
+    if (bad) rc = 1;
+  }
+  return rc;
+}
+
 // Bit-by-bit canonical decode (RFC 1951 3.2.2 order): the code value grows
 // one bit at a time and is compared with the length's code range.
 template <int N, int P>
@@ -526,6 +611,7 @@ int main(int argc, char** argv) {
   if (!strcmp(mode, "frame")) return mode_frame(argc - 2, argv + 2);
   if (!strcmp(mode, "pairs")) return mode_pairs(argc - 2, argv + 2);
   if (!strcmp(mode, "longcodes")) return mode_long_codes();
+  if (!strcmp(mode, "window")) return mode_window(argc - 2, argv + 2);
   if (!strcmp(mode, "guard")) {
     const u8 byte = 1;
     Guarded g(&byte, 1);

@@ -152,6 +152,17 @@ def test_literal_pairs_match_single_tokens(harness, stream_files):
             assert int(got[path]["adler%d" % slice_bits]) == zlib.adler32(raw), name
 
 
+def test_window_token_matches_fast_token_at_every_bit(harness, stream_files):
+    """The slow-path token decode from the window's registers (window_token)
+    gives fast_token's status, token and end position at every bit of every
+    block body, with the body end and with nearer limits as the bound."""
+    proc = _run(harness, "window", [p for _, p, _ in stream_files])
+    assert proc.returncode == 0, proc.stdout[-3000:] + proc.stderr[-2000:]
+    lines = [l for l in proc.stdout.splitlines() if l.startswith("window ")]
+    assert lines and all(l.endswith("bad=0") for l in lines)
+    assert sum(int(l.split("positions=")[1].split()[0]) for l in lines) > 100000
+
+
 def test_long_codes_match_a_bitwise_canonical_walk(harness):
     """Codes longer than the primary LUT are decoded from per-length bounds
     (deflate_common.h long_code); a bit-by-bit canonical walk must give the
