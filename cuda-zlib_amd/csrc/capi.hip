@@ -700,12 +700,17 @@ extern "C" int HipZlibDecompressBatch(hipStream_t stream, const int64_t* input_s
     return invalid("invalid argument: batch layout differs from buffer sizes");
   const u64 files = input_count;
   return execute(stream, [&](Workspace& ws) -> hipError_t {
-    hipError_t err = launch_fill(stream, output, 0, output_size);
-    if (err != hipSuccess) return err;
-    if (files > kMaxBlocks || in_total > kMaxBytes || out_total > kMaxBytes)
+    if (files > kMaxBlocks || in_total > kMaxBytes || out_total > kMaxBytes) {
+      hipError_t err = launch_fill(stream, output, 0, output_size);
+      if (err != hipSuccess) return err;
       return launch_set_meta_rows(stream, metadata, files, kInvalidBounds, 0);
+    }
+    // No fill of the output first: every file's bytes are written by its
+    // decoder.  The serial one zeroes a file's slot before decoding (and a
+    // slot with a bad encoded row); the parallel route writes all of a file
+    // it accepts and hands every other file to the serial one.
     BatchFile* device_files = nullptr;
-    err = ws.alloc(&device_files, files);
+    hipError_t err = ws.alloc(&device_files, files);
     if (err != hipSuccess) return err;
     // Staged before the call returns, so the host vector may go out of scope.
     err = upload_to_device(stream, device_files, layout.data(), files * sizeof(BatchFile));

@@ -5262,33 +5262,35 @@ hipError_t run_inflate_batch_wide(hipStream_t stream, Scratch& scratch, const u8
                                   u32 n, u64 in_bits, const u32* encoded, u32 max_blocks,
                                   u32* redo, u32* meta) {
   if (!n) return hipSuccess;
-  State* st = nullptr;
-  HZ_TRY(scratch.alloc(&st, 1));
-  HZ_TRY(launch_fill(stream, st, 0, sizeof(State)));
   // Slice groups: at most one per 64 slices of >= kDescMinSlice bits, plus
   // the partly filled last group of every describe round.
   const u64 group_capacity = in_bits / (u64(kDescMinSlice) * 64) +
                              in_bits / (u64(kDescThreads) * kDescMinSlice) + 8 * u64(n) + 64;
+  const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
+  const u64 words = (out_total + 31) / 32 + 1;
+  // The state, the resolve counts and the first bitmap start zeroed: one
+  // allocation, cleared by one fill.
+  const u64 st_bytes = scratch_round(sizeof(State));
+  const u64 counts_bytes = scratch_round((rounds + 1) * sizeof(u64));
+  u8* zeroed = nullptr;
+  HZ_TRY(scratch.alloc(&zeroed, st_bytes + counts_bytes + words * 4));
+  HZ_TRY(launch_fill(stream, zeroed, 0, st_bytes + counts_bytes + words * 4));
+  State* st = reinterpret_cast<State*>(zeroed);
+  u64* counts = reinterpret_cast<u64*>(zeroed + st_bytes);
+  u32* bits0 = reinterpret_cast<u32*>(zeroed + st_bytes + counts_bytes);
   u64* slice_entry = nullptr;
   u32 *slice_off = nullptr, *group_link = nullptr, *wanted = nullptr;
   HZ_TRY(scratch.alloc(&slice_entry, group_capacity * 64));
   HZ_TRY(scratch.alloc(&slice_off, group_capacity * 64));
   HZ_TRY(scratch.alloc(&group_link, group_capacity));
   HZ_TRY(scratch.alloc(&wanted, u64(n) + 1));
-  const u64 words = (out_total + 31) / 32 + 1;
-  u32 *roots = nullptr, *bits0 = nullptr, *bits1 = nullptr;
+  u32 *roots = nullptr, *bits1 = nullptr;
   HZ_TRY(scratch.alloc(&roots, out_total ? out_total : 1));
-  HZ_TRY(scratch.alloc(&bits0, words));
   HZ_TRY(scratch.alloc(&bits1, words));
-  HZ_TRY(launch_fill(stream, bits0, 0, words * 4));
   HZ_LAUNCH(g_batch_wide, dim3(n), dim3(kDescThreads), 0, stream, in, out, files, list, n,
             encoded, max_blocks, st, slice_entry, slice_off, group_link, group_capacity, roots,
             bits0, redo, wanted);
   HZ_TRY(hipGetLastError());
-  const u32 rounds = resolve_rounds(group_capacity * 64 + u64(max_blocks));
-  u64* counts = nullptr;
-  HZ_TRY(scratch.alloc(&counts, rounds + 1));
-  HZ_TRY(launch_fill(stream, counts, 0, (rounds + 1) * sizeof(u64)));
   for (u32 round = 0; round < rounds; ++round) {
     HZ_LAUNCH(g_resolve, dim3(u32(clamp_grid((words + 255) / 256, 2048))), dim3(256), 0, stream,
               st, out, roots, bits0, bits1, counts, round, rounds, words, 0ull, nullptr, nullptr,
