@@ -92,6 +92,56 @@ def test_corrupted_files_match_the_serial_oracle(gpu, seed):
     _check(streams, expected)
 
 
+def test_stale_output_bytes_never_survive(gpu):
+    """The batch decoders write every byte of every slot (the output is not
+    cleared first): into an output buffer holding 0xA5 everywhere, valid,
+    corrupted and size-mismatched files of both routes decode to the oracle's
+    bytes (decoded prefix then zeros on failure), and the same buffer reused
+    for a second batch keeps nothing of the first."""
+    import ctypes
+    import torch
+    from cuda_zlib import _native
+    from cuda_zlib._native import int64_array
+    lib = _native.load()
+    dev = torch.device("cuda", 0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    rng = random.Random(41)
+    batches = []
+    for seed in (300, 301):
+        streams, expected = [], []
+        for raw, payload in _files(seed, 36):
+            if rng.random() < 0.5:
+                payload = _mutate(payload, rng)
+            n = len(raw)
+            if rng.random() < 0.1:
+                n += rng.choice([-1, 1]) if n else 1
+            streams.append(payload)
+            expected.append(n)
+        batches.append((streams, expected))
+    total = max(sum(e) for _, e in batches)
+    out = torch.full((total,), 0xA5, dtype=torch.uint8, device=dev)
+    for streams, expected in batches:
+        payload = b"".join(streams)
+        src = torch.from_numpy(np.frombuffer(payload, np.uint8).copy()).to(dev)
+        n = sum(expected)
+        meta = torch.empty((len(streams), 2), dtype=torch.uint32, device=dev)
+        rc = lib.HipZlibDecompressBatch(stream, int64_array([len(s) for s in streams]),
+                                        len(streams), int64_array(expected), len(expected),
+                                        ptr(src), len(payload), ctypes.c_void_p(0), 0, 0,
+                                        ptr(out), n, ptr(meta), len(streams), 2)
+        assert rc == 0
+        torch.cuda.synchronize()
+        host = out[:n].cpu().numpy().tobytes()
+        rows = meta.cpu().numpy()
+        at = 0
+        for i, (s, k) in enumerate(zip(streams, expected)):
+            want, want_status = oracle.inflate_serial(s, k)
+            assert int(rows[i, 0]) == want_status and int(rows[i, 1]) == 0, i
+            assert host[at:at + k] == want, "file %d output differs" % i
+            at += k
+
+
 def test_encoded_rows_route_large_files_like_small_ones(gpu):
     """Bad [length, status] rows give 22 / 23 and zeroed outputs, large files too."""
     import torch
