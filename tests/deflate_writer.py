@@ -196,6 +196,57 @@ def literal_only_block(w, data, final=True, long_codes=False, single_eob=False):
     return blk.literals(data).end()
 
 
+def _deep_lengths(rng, count):
+    """Lengths of a complete code over `count` symbols with codes of up to 15
+    bits: leaves are split (often the deepest one that can still grow) until
+    there are `count`, so many codes are 11-15 bits long."""
+    depth = [0]
+    while len(depth) < count:
+        growable = [i for i, d in enumerate(depth) if d < 15]
+        if rng.random() < 0.4:
+            pick = max(growable, key=lambda i: (depth[i], i))
+        else:
+            pick = rng.choice(growable)
+        depth[pick] += 1
+        depth.append(depth[pick])
+    rng.shuffle(depth)
+    return depth
+
+
+def long_code_mix_stream(blocks=3, tokens=12000, seed=5150):
+    """Dynamic blocks whose literal/length and distance codes run up to 15 bits
+    (literal/length codes of most lengths from 9 to 15), with tokens drawn
+    uniformly over the symbols, so that most literals, lengths and distances
+    take codes longer than a decoder's primary table."""
+    rng = random.Random(seed)
+    w = BitWriter()
+    out = bytearray()
+    for b in range(blocks):
+        ll = _deep_lengths(rng, 286)
+        d = _deep_lengths(rng, 30)
+        assert max(ll) == 15 and max(d) >= 12
+        blk = Block(w, b == blocks - 1, ll, d)
+        for _ in range(tokens):
+            if len(out) < 64 or rng.random() < 0.6:
+                byte = rng.randrange(256)
+                blk.literal(byte)
+                out.append(byte)
+                continue
+            li = rng.randrange(29)
+            length = LENGTH_BASE[li] + rng.randrange(1 << LENGTH_EXTRA[li])
+            if li == 28:
+                length = 258
+            top = min(len(out), 32768)
+            di = rng.randrange(max(i for i, base in enumerate(DIST_BASE) if base <= top) + 1)
+            span = min(DIST_BASE[di] + (1 << DIST_EXTRA[di]) - 1, top) - DIST_BASE[di] + 1
+            distance = DIST_BASE[di] + rng.randrange(span)
+            blk.match(length, distance)
+            for _ in range(length):
+                out.append(out[-distance])
+        blk.end()
+    return wrap(w.getvalue(), bytes(out)), bytes(out)
+
+
 def literal_only_stream(data, **kwargs):
     w = BitWriter()
     literal_only_block(w, data, **kwargs)
@@ -544,6 +595,8 @@ def valid_streams():
     out.append(("embedded", p, r))
     raw = bytes((14,)) * 65536
     out.append(("long-codes", literal_only_stream(raw, long_codes=True), raw))
+    p, r = long_code_mix_stream()
+    out.append(("long-code-mix", p, r))
     for blocks in (257, 1050):
         p, r = deep_reference_stream(blocks)
         out.append(("deep-%d" % blocks, p, r))
