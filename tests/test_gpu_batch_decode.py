@@ -92,6 +92,20 @@ def test_corrupted_files_match_the_serial_oracle(gpu, seed):
     _check(streams, expected)
 
 
+def test_codes_up_to_15_bits_on_both_batch_routes(gpu):
+    """Files whose literal/length and distance codes run to 15 bits (most
+    tokens miss the primary tables): large ones take the parallel route, the
+    tiny ones the serial decoder; all must equal the oracle."""
+    import deflate_writer as dw
+    streams, expected = [], []
+    for seed in range(6):
+        payload, raw = dw.long_code_mix_stream(blocks=1 + seed % 3, tokens=[20, 400, 3000][seed % 3],
+                                               seed=900 + seed)
+        streams.append(payload)
+        expected.append(len(raw))
+    _check(streams, expected)
+
+
 def test_stale_output_bytes_never_survive(gpu):
     """The batch decoders write every byte of every slot (the output is not
     cleared first): into an output buffer holding 0xA5 everywhere, valid,
